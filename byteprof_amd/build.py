@@ -1,0 +1,84 @@
+"""Build recipe of libbyteprof_amd.so: hipcc for gfx950, one object per source (the skinny kernel menu is compiled in
+ten slices, one per weight kind x activation-row bucket), objects compiled in parallel, then linked into the shared
+library next to this file. `python -m byteprof_amd.build` runs it."""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+INCLUDE = ROOT / "include"
+BUILD_DIR = PKG / "_build"
+LIB_NAME = "libbyteprof_amd.so"
+LIB_PATH = PKG / LIB_NAME
+ARCH = "gfx950"
+
+KINDS = (0, 1)  # bf16, int8 weights
+ROW_BUCKETS = (1, 2, 4, 8, 16)
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    path = Path(rocm) / "bin" / "hipcc"
+    if path.exists():
+        return str(path)
+    found = shutil.which("hipcc")
+    if found is None:
+        raise RuntimeError("hipcc not found (ROCM_PATH or PATH)")
+    return found
+
+
+def common_flags() -> list[str]:
+    return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", f"-I{INCLUDE}", f"-I{CSRC}",
+            # no packed-fp32 VALU instructions in device code
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def units() -> list[tuple[Path, list[str], Path]]:
+    """(source, extra flags, object) for every translation unit."""
+    out = [(CSRC / "skinny.hip", [], BUILD_DIR / "skinny.o"),
+           (CSRC / "mlstm.hip", [], BUILD_DIR / "mlstm.o")]
+    for kind in KINDS:
+        for mt in ROW_BUCKETS:
+            out.append((CSRC / "skinny_inst.hip", [f"-DBP_KIND={kind}", f"-DBP_MT={mt}"],
+                        BUILD_DIR / f"skinny_inst_k{kind}_m{mt}.o"))
+    return out
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the device-only target feature; that warning is expected
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in r.stderr.splitlines() if noise not in line)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every HIP source and link the library; always rebuilds. Returns the library path."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    cc = hipcc()
+    cmds = [[cc, *common_flags(), *extra, "-c", str(src), "-o", str(obj)] for src, extra, obj in units()]
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        for cmd, _ in zip(cmds, ex.map(_run, cmds)):
+            if verbose:
+                print(" ".join(cmd))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    link = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *[str(o) for _, _, o in units()]]
+    _run(link)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

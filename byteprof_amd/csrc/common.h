@@ -1,0 +1,79 @@
+// Device helpers shared by the gfx950 kernels: bf16/fp16 conversions, packed bf16 dot products and wave-level
+// reductions. Wavefronts are 64 lanes wide on CDNA; every reduction here assumes that.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bp {
+
+constexpr int kWave = 64;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// bf16 -> fp32 is exact: the bf16 bits are the top half of the fp32 pattern.
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (what torch's .to(torch.bfloat16) does); NaN stays NaN.
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+__device__ __forceinline__ float round_to_bf16(float f) { return bf16_bits_to_float(float_to_bf16_bits(f)); }
+__device__ __forceinline__ float round_to_f16(float f) { return static_cast<float>(static_cast<_Float16>(f)); }
+
+// acc + a.lo * b.lo + a.hi * b.hi with a, b two packed bf16 values (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
+}
+
+// Two signed bytes of d (at bit offsets sh and sh + 8) as a packed pair of bf16 values; exact for |q| <= 128.
+__device__ __forceinline__ uint32_t i8pair_to_bf16x2(uint32_t d, int sh) {
+  const float lo = static_cast<float>(static_cast<int8_t>(d >> sh));
+  const float hi = static_cast<float>(static_cast<int8_t>(d >> (sh + 8)));
+  // bytes 2,3 of lo then bytes 2,3 of hi (v_perm_b32 selector: sources are {hi: bytes 4-7, lo: bytes 0-3})
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// Load a scale element of the given dtype code as fp32 (0 = bf16, 1 = fp16, 2 = fp32).
+__device__ __forceinline__ float load_scale(const void* p, int64_t i, int dt) {
+  if (dt == 0) return bf16_bits_to_float(static_cast<const uint16_t*>(p)[i]);
+  if (dt == 1) return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  return static_cast<const float*>(p)[i];
+}
+
+// Sum of v over the 64 lanes of the wave, for P values at once (P a power of two). Butterfly stages pair lanes
+// l and l ^ d for d = 32, 16, ..., 1; while more than one value is left, each stage also halves the values a lane
+// keeps (the lane with bit d set keeps the upper half). On return:
+//   P >= 64: lane l holds, in v[0 .. P/64), the totals of indices [l * P/64, (l + 1) * P/64);
+//   P <  64: v[0] of lane l holds the total of index l / (64 / P) (all 64/P lanes of a group hold the same).
+// The addition tree of every index is the same for every P (pairs by lane bit 5, then 4, ..., then 0), so a total
+// does not depend on how many other values were reduced with it.
+template <int P, int D>
+__device__ __forceinline__ void reduce_stage(float* v, int lane) {
+  if constexpr (P > 1) {
+    const bool hi = (lane & D) != 0;
+#pragma unroll
+    for (int j = 0; j < P / 2; ++j) {
+      const float keep = hi ? v[j + P / 2] : v[j];
+      const float send = hi ? v[j] : v[j + P / 2];
+      v[j] = keep + __shfl_xor(send, D);
+    }
+  } else {
+    v[0] += __shfl_xor(v[0], D);
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void wave_transpose_reduce(float* v, int lane) {
+  static_assert((P & (P - 1)) == 0, "P must be a power of two");
+  reduce_stage<P, 32>(v, lane);
+  reduce_stage<(P > 2 ? P / 2 : 1), 16>(v, lane);
+  reduce_stage<(P > 4 ? P / 4 : 1), 8>(v, lane);
+  reduce_stage<(P > 8 ? P / 8 : 1), 4>(v, lane);
+  reduce_stage<(P > 16 ? P / 16 : 1), 2>(v, lane);
+  reduce_stage<(P > 32 ? P / 32 : 1), 1>(v, lane);
+}
+
+}  // namespace bp

@@ -1,0 +1,193 @@
+"""Skinny weight-only matmul y[M, N] = x[M, K] @ W[N, K]^T on gfx950 (MI355X), through libbyteprof_amd.so.
+
+Drop-in for byteprof/optim/skinny.py: same names (`skinny_mm`, `get_cfg`, `dequantize`, `MAX_M`, `GROUP`), same
+argument meaning, same ValueError validation (skinny.py:136-166). bf16 activations, fp32 accumulation, bf16 output;
+weights bf16 [N, K] or int8 [N, K] with one scale per output row (bf16, fp16 or fp32).
+
+Differences from the reference, each forced by the hardware mapping or by raw-pointer kernels:
+  - one launch handles up to ROWS_PER_LAUNCH = 16 activation rows (the reference: 64); larger M is chunked here,
+    and `SkinnyLinear` still sends every input of 1..MAX_M rows to the kernel;
+  - x must be bfloat16 and on the GPU, w and scale contiguous (the reference assumes the latter silently);
+  - `cfg` is (rows, waves, split) for this kernel (rows: weight rows per workgroup; waves: wavefronts sharing the
+    K range of a workgroup; split: K ranges in separate workgroups, added in fixed order). The reference's
+    (BN, BK, num_warps, num_stages[, split]) tuples are accepted and mapped to (BN, num_warps, split);
+  - the row buckets that share one K order (bitwise row independence, test_skinny.py:114-121) are the whole
+    range M = 1..16: the K order depends only on (N, K, waves, split);
+  - int4 group-128 weights (uint8 tile-major) are not implemented yet: they raise NotImplementedError.
+"""
+
+from __future__ import annotations
+
+import functools
+import json
+from pathlib import Path
+
+import torch
+
+from .. import _lib
+
+GROUP = 128
+MAX_M = 64  # rows for which SkinnyLinear uses the kernel (skinny_linear.py:60); interface parity with the reference
+ROWS_PER_LAUNCH = 16  # activation rows per kernel launch on gfx950
+
+_ROW_BUCKETS = (1, 2, 4, 8, 16)
+_ROWS_MENU = (2, 4, 8, 16, 32)
+_WAVES_MENU = (1, 2, 4, 8, 16)
+_KIND_CODE = {"bf16": 0, "int8": 1}
+_CHUNK = {"bf16": 512, "int8": 1024}  # K elements per wave-wide 16-byte load
+
+# Tuned (waves, split) per (kind, N, K) and rows per activation-row bucket; see skinny_cfg.json.
+_CFG_FILE = Path(__file__).with_name("skinny_cfg.json")
+_TABLE: dict[tuple[str, int, int], dict] = {}
+if _CFG_FILE.exists():
+    for _key, _v in json.loads(_CFG_FILE.read_text(encoding="utf-8")).items():
+        if _key.startswith("_"):
+            continue
+        _kind, _n, _k = _key.split("|")
+        _TABLE[(_kind, int(_n), int(_k))] = _v
+
+
+def _bm(m: int) -> int:
+    """Activation-row bucket of a launch (M rounded up to 1, 2, 4, 8 or 16)."""
+    for b in _ROW_BUCKETS:
+        if m <= b:
+            return b
+    return ROWS_PER_LAUNCH
+
+
+@functools.lru_cache(maxsize=None)
+def _supported(kind: str, bm: int, rows: int, waves: int) -> bool:
+    return bool(_lib.lib().bp_skinny_config_supported(_KIND_CODE[kind], bm, rows, waves))
+
+
+def _default_waves(kind: str, k: int) -> int:
+    nch = -(-k // _CHUNK[kind])
+    waves = 1
+    while waves * 2 <= min(nch, 8):
+        waves *= 2
+    return waves
+
+
+def _default_rows(n: int, bm: int) -> int:
+    rows = {1: 8, 2: 8, 4: 4, 8: 4, 16: 2}[bm]
+    while rows > 2 and -(-n // rows) < 512:  # keep at least ~2 workgroups per CU on 256 CUs
+        rows //= 2
+    return rows
+
+
+def get_cfg(kind: str, n: int, k: int, bm: int) -> tuple[int, int, int]:
+    """(rows, waves, split) for a launch of `bm` activation rows; tuned table first, then the heuristic."""
+    entry = _TABLE.get((kind, n, k))
+    if entry is not None:
+        rows = int(entry.get("rows", {}).get(str(bm), _default_rows(n, bm)))
+        return rows, int(entry["waves"]), int(entry.get("split", 1))
+    return _default_rows(n, bm), _default_waves(kind, k), 1
+
+
+def _resolve(kind: str, n: int, k: int, bm: int, cfg) -> tuple[int, int, int]:
+    """Map a user / table configuration onto the compiled menu (largest supported rows <= requested)."""
+    if cfg is None:
+        rows, waves, split = get_cfg(kind, n, k, bm)
+    elif len(cfg) == 3:
+        rows, waves, split = (int(c) for c in cfg)
+    elif len(cfg) in (4, 5):  # the reference's (BN, BK, num_warps, num_stages[, split])
+        rows, waves, split = int(cfg[0]), int(cfg[2]), int(cfg[4]) if len(cfg) == 5 else 1
+    else:
+        raise ValueError(f"cfg must be (rows, waves, split) or (BN, BK, warps, stages[, split]), got {cfg!r}")
+    waves = max(w for w in _WAVES_MENU if w <= max(waves, 1))
+    split = max(1, split)
+    cands = [r for r in _ROWS_MENU if r <= max(rows, 2)]
+    for r in sorted(cands, reverse=True):
+        if _supported(kind, bm, r, waves):
+            return r, waves, split
+    for w in sorted((w for w in _WAVES_MENU if w < waves), reverse=True):
+        for r in sorted(_ROWS_MENU, reverse=True):
+            if _supported(kind, bm, r, w):
+                return r, w, split
+    raise ValueError(f"no compiled kernel for {kind} rows<={rows} waves<={waves} at {bm} activation rows")
+
+
+def _launch(kind: str, x: torch.Tensor, w: torch.Tensor, scale, y: torch.Tensor, cfg=None) -> None:
+    m, k = x.shape
+    n = w.shape[0]
+    bm = _bm(m)
+    rows, waves, split = _resolve(kind, n, k, bm, cfg)
+    split = min(split, -(-k // _CHUNK[kind]))
+    L = _lib.lib()
+    ws = None
+    ws_bytes = 0
+    if split > 1:
+        ws_bytes = L.bp_skinny_workspace_bytes(m, n, split)
+        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=x.device)
+    stream = _lib.stream_ptr(x.device)
+    if kind == "bf16":
+        rc = L.bp_skinny_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, rows, waves, split,
+                              _lib.ptr(ws), ws_bytes, stream)
+    else:
+        rc = L.bp_skinny_int8(x.data_ptr(), w.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype],
+                              y.data_ptr(), m, n, k, rows, waves, split, _lib.ptr(ws), ws_bytes, stream)
+    _lib.check(rc, f"bp_skinny_{kind}")
+
+
+def _check_device(x: torch.Tensor, *others: torch.Tensor | None) -> None:
+    if not x.is_cuda:
+        raise ValueError("x must be on a GPU (the skinny kernels have no CPU path)")
+    for t in others:
+        if t is not None and t.device != x.device:
+            raise ValueError(f"all tensors must be on {x.device}, got {t.device}")
+
+
+def skinny_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None = None,
+              zero: torch.Tensor | None = None, out: torch.Tensor | None = None,
+              cfg: tuple[int, ...] | None = None) -> torch.Tensor:
+    """x: [M, K] bf16 (contiguous); w: bf16 [N, K] | int8 [N, K] + scale [N]. Returns y [M, N] in x.dtype.
+
+    Validation and empty-shape behaviour follow byteprof/optim/skinny.py:136-166."""
+    if x.dim() != 2 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous [M, K] tensor")
+    m, k = x.shape
+    if w.dtype == torch.bfloat16:
+        kind, n = "bf16", w.shape[0]
+        if w.shape[1] != k:
+            raise ValueError("K mismatch")
+    elif w.dtype == torch.int8:
+        kind, n = "int8", w.shape[0]
+        if scale is None or w.shape[1] != k:
+            raise ValueError("int8 needs scale [N] and K to match")
+        if scale.dim() != 1 or scale.shape[0] != n or not scale.is_contiguous() or scale.dtype not in (
+                torch.bfloat16, torch.float16, torch.float32):
+            raise ValueError("int8 scale must be a contiguous [N] bf16 / fp16 / fp32 tensor")
+    elif w.dtype == torch.uint8:
+        if scale is None or zero is None or w.dim() != 4 or k % GROUP or w.shape[1] * GROUP != k or \
+                scale.shape[0] != w.shape[1]:
+            raise ValueError("int4 needs packed [N/R, K/128, R, 64], scale/zero [K/128, N] and K % 128 == 0")
+        raise NotImplementedError("int4 group-128 weights are not implemented by the gfx950 kernels yet")
+    else:
+        raise ValueError(f"unsupported weight dtype {w.dtype}")
+    if w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("w must be a contiguous [N, K] tensor")
+    if x.dtype != torch.bfloat16:
+        raise ValueError("x must be bfloat16")
+    _check_device(x, w, scale, out)
+    if out is not None:
+        if out.shape != (m, n) or out.dtype != x.dtype or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous [{m}, {n}] {x.dtype} tensor")
+        y = out
+    else:
+        y = torch.empty(m, n, dtype=x.dtype, device=x.device)
+    if m == 0 or n == 0 or k == 0:
+        if k == 0:
+            y.zero_()
+        return y
+    for r0 in range(0, m, ROWS_PER_LAUNCH):
+        _launch(kind, x[r0:r0 + ROWS_PER_LAUNCH], w, scale, y[r0:r0 + ROWS_PER_LAUNCH], cfg)
+    return y
+
+
+def dequantize(kind: str, w: torch.Tensor, scale=None, zero=None) -> torch.Tensor:
+    """fp32 weights [N, K] of a stored format (byteprof/optim/skinny.py:209-217)."""
+    if kind == "bf16":
+        return w.float()
+    if kind == "int8":
+        return w.float() * scale.float()[:, None]
+    raise NotImplementedError("int4 group-128 weights are not implemented by the gfx950 kernels yet")

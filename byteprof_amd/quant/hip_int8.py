@@ -1,0 +1,64 @@
+"""Fused int8 weight-only products on gfx950 and the per-row int8 quantizer.
+
+Drop-in for byteprof/quant/triton_int8.py: `gemv_int8(x, w, scale, cfg=None, out=None)` computes
+y[1, n] = scale[n] * sum_k float(w[n, k]) * float(x[k]) with the int8 -> float conversion fused into the weight
+stream (triton_int8.py:16-47); `quantize_rowwise_int8(w)` is the symmetric per-row quantizer (triton_int8.py:50-55),
+restated in torch so its bytes are those of the reference.
+
+`cfg` is (rows, waves) for the gfx950 kernel; the reference's (BN, BK, num_warps) triples are accepted and mapped to
+(BN, num_warps). Like the reference, gemv_int8 does not validate beyond what raw-pointer kernels need (one row,
+shapes that agree, GPU tensors).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..optim import skinny
+
+DEFAULT_CFG = None  # chosen per shape by byteprof_amd.optim.skinny.get_cfg (tuned table / heuristic)
+
+
+def default_cfg(n_out: int, k: int = 2048) -> tuple[int, int]:
+    rows, waves, _ = skinny.get_cfg("int8", n_out, k, 1)
+    return rows, waves
+
+
+def gemv_int8(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, cfg: tuple[int, ...] | None = None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """x: [1, K] bf16, w: [N, K] int8, scale: [N] (bf16 / fp16 / fp32) -> [1, N] bf16."""
+    N, K = w.shape
+    if x.numel() != K or not x.is_contiguous() or x.dtype != torch.bfloat16 or not x.is_cuda:
+        raise ValueError("x must be a contiguous [1, K] bfloat16 GPU tensor")
+    if not w.is_contiguous() or scale.shape != (N,) or not scale.is_contiguous():
+        raise ValueError("w must be a contiguous [N, K] int8 tensor and scale a contiguous [N] tensor")
+    y = out if out is not None else torch.empty(1, N, dtype=x.dtype, device=x.device)
+    if N == 0:
+        return y
+    if K == 0:
+        y.zero_()
+        return y
+    if cfg is None:
+        rows, waves = default_cfg(N, K)
+    else:
+        rows, waves = int(cfg[0]), int(cfg[-1] if len(cfg) == 2 else cfg[2])
+    rows, waves, _ = skinny._resolve("int8", N, K, 1, (rows, waves, 1))
+    L = _lib.lib()
+    rc = L.bp_gemv_int8(x.data_ptr(), w.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype], y.data_ptr(), N, K,
+                        rows, waves, _lib.stream_ptr(x.device))
+    _lib.check(rc, "bp_gemv_int8")
+    return y
+
+
+def quantize_rowwise_int8(w: torch.Tensor, scale_dtype: torch.dtype | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-output-row int8: w ~ q * scale[:, None], scale stored in `scale_dtype` (default: w.dtype, as in
+    the reference; fp16 is the other 2-byte option).
+
+    The scale is rounded to the stored dtype first and q is computed against that stored value; torch.round is
+    round-half-to-even (triton_int8.py:50-55)."""
+    sdt = scale_dtype or w.dtype
+    floor = 2.0 ** -24 if sdt == torch.float16 else 1e-12  # fp16: its smallest subnormal, never a zero scale
+    scale = (w.float().abs().amax(dim=1) / 127.0).clamp_min(floor).to(sdt)
+    q = torch.round(w.float() / scale.float()[:, None]).clamp_(-127, 127).to(torch.int8)
+    return q.contiguous(), scale

@@ -1,0 +1,121 @@
+/*
+ * byteprof_amd.h — C ABI of libbyteprof_amd.so, the gfx950 (MI355X) kernels of the batch-1 decode hot path:
+ * skinny weight-only matmul (bf16 / int8 weights, 1..64 activation rows), the int8 matrix-vector product, and the
+ * fused multi-step mLSTM recurrence of the drafting path.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers (HBM) owned by the caller; the library never allocates, frees, retains or
+ *     synchronises, and never reads device memory from the host, so every call can be captured in a HIP graph.
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream). Work is enqueued on it and nothing else.
+ *   - Matrices are row-major and dense: x [M, K], w [N, K], y [M, N] (leading dimension = the column count).
+ *   - Return value: BP_OK (0) on success; a positive value is the hipError_t of the failed launch; a negative value
+ *     is one of the BP_E_* codes below (checked before anything is enqueued).
+ *   - Numerics: fp32 accumulation; the per-row int8 scale is applied to the fp32 sum; output rounded to nearest-even
+ *     bf16; the K order of every sum depends only on (N, K, waves, split), never on M, so output row i does not
+ *     change with the number of rows in the call (bitwise).
+ *
+ * The reference interfaces these replace are cited per function (paths relative to the byteprof repository).
+ */
+#ifndef BYTEPROF_AMD_H
+#define BYTEPROF_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BP_OK 0
+#define BP_E_INVALID_ARG (-1)    /* a null pointer, a negative size or an inconsistent shape */
+#define BP_E_UNSUPPORTED (-2)    /* a tile configuration or dtype that no compiled kernel implements */
+#define BP_E_WORKSPACE (-3)      /* split > 1 and the workspace is null or smaller than bp_skinny_workspace_bytes() */
+
+/* Element type codes. */
+#define BP_DT_BF16 0
+#define BP_DT_F16 1
+#define BP_DT_F32 2
+#define BP_DT_I8 3
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int bp_version(void);
+
+/* Short static description of a status code returned by any bp_* function (BP_* and hipError_t codes). */
+const char* bp_status_string(int status);
+
+/*
+ * Tile configuration menu of the skinny kernels. A call chooses
+ *   rows  : weight rows (output channels) per workgroup, one of {2, 4, 8, 16, 32};
+ *   waves : wavefronts per workgroup; the K dimension is dealt out to them in chunks of 512 (bf16) / 1024 (int8)
+ *           elements and their partial sums are added in LDS, one of {1, 2, 4, 8, 16};
+ *   split : K ranges computed by separate workgroups (1..1024); with split > 1 the partial sums go to an fp32
+ *           workspace and a second kernel adds them in split order (deterministic).
+ * bp_skinny_config_supported() tells whether a (kind, mt, rows, waves) combination is compiled; mt is the row
+ * bucket of the activations (1, 2, 4, 8 or 16; M is rounded up to it).
+ */
+int bp_skinny_config_supported(int wkind, int mt, int rows, int waves);
+
+/* Bytes of fp32 workspace a skinny call with this split needs: split * M * N * 4 when split > 1, else 0. */
+size_t bp_skinny_workspace_bytes(int64_t M, int64_t N, int split);
+
+/*
+ * y[M, N] (bf16) = x[M, K] (bf16) . w[N, K]^T (bf16), fp32 accumulation. 1 <= M <= 16 per call (the Python layer
+ * chunks larger M). M = 0 or N = 0 is a no-op; K = 0 writes zeros.
+ * Replaces: byteprof/optim/skinny.py:111-129 (_launch, kind "bf16") + :36-45,64-72,76-80 (_skinny_kernel MODE 0)
+ *           + :84-90 (_split_reduce), called from skinny_mm (skinny.py:136-166).
+ */
+int bp_skinny_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
+                   int rows, int waves, int split, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * y[M, N] (bf16) = (x[M, K] (bf16) . q[N, K]^T (int8)) * scale[N], the int8 -> float conversion fused into the
+ * weight stream and the scale applied to the fp32 sum. scale_dtype: BP_DT_BF16, BP_DT_F16 or BP_DT_F32.
+ * Replaces: byteprof/optim/skinny.py:64-75 (_skinny_kernel MODE 1) via skinny_mm with an int8 weight.
+ */
+int bp_skinny_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y,
+                   int64_t M, int64_t N, int64_t K, int rows, int waves, int split,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * One-row int8 product: y[1, N] (bf16) = scale[n] * sum_k float(q[n, k]) * float(x[k]).
+ * Replaces: byteprof/quant/triton_int8.py:40-47 (gemv_int8) and :16-28 (_gemv_int8).
+ */
+int bp_gemv_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y,
+                 int64_t N, int64_t K, int rows, int waves, void* stream);
+
+/*
+ * Fixed-order reduction of split-K partial sums: y[M, N] = bf16(scale[n] * sum_{s < split} ws[s, M, N]);
+ * scale may be null (bf16 weights). bp_skinny_* call it themselves when split > 1; it is exported for callers
+ * that produce partial sums of their own.
+ * Replaces: byteprof/optim/skinny.py:84-90 (_split_reduce).
+ */
+int bp_splitk_reduce(const void* workspace, void* y, const void* scale, int scale_dtype,
+                     int64_t M, int64_t N, int split, void* stream);
+
+/*
+ * Fused mLSTM recurrence over T positions from a read-only start state (batch 1).
+ *   c [NH, DQ, DV], n [NH, DQ], m [NH]: start state, fp32, contiguous; never written.
+ *   q, k [T, NH, DQ]; v [T, NH, DV]: io_dtype (BP_DT_BF16, BP_DT_F16 or BP_DT_F32); i, f [T, NH]: gate_dtype.
+ *   h [>= T, NH, DV]: io_dtype, receives the cell outputs.
+ *   nstart [NH, DQ], mstart [NH]: fp32, receive copies of the start n and m (for a later commit).
+ *   str_*: element strides along T of q/k, v, i/f and h; the inner dimensions are contiguous.
+ * Per position (f and i are pre-activations):
+ *   m' = max(logsigmoid(f) + m, i); fa = exp(logsigmoid(f) + m - m'); ia = exp(i - m'); mv = exp(-m'),
+ *   the three rounded to io_dtype; C <- fa C + ia k v^T; n <- fa n + ia k (fp32 state);
+ *   h = (qs . io(C)) / (max(|qs . io(n)|, mv) + eps) with qs = q * qk_scale, stored as io_dtype.
+ * bv: value columns per workgroup (4, 8 or 16); dq must be a multiple of 64, at most 512.
+ * Replaces: byteprof/optim/draft_fused.py:27-40 (multistep_fw) and byteprof/optim/mlstm_multistep.py:21-86
+ *           (_gates, multistep_fw_kernel).
+ */
+int bp_mlstm_multistep(const void* c, const void* n, const void* m,
+                       const void* q, const void* k, const void* v, const void* i, const void* f,
+                       void* h, void* nstart, void* mstart,
+                       int T, int NH, int DQ, int DV,
+                       int64_t str_t_qk, int64_t str_t_v, int64_t str_t_if, int64_t str_t_h,
+                       int io_dtype, int gate_dtype, float qk_scale, float eps, int bv, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BYTEPROF_AMD_H */

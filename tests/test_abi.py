@@ -1,0 +1,93 @@
+"""The C ABI: libbyteprof_amd.so loads (sharing torch's HIP runtime), exports every function include/byteprof_amd.h
+declares, and rejects bad arguments before touching the GPU. CPU only: no call here launches a kernel."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "byteprof_amd.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(bp_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from byteprof_amd import _lib
+
+    return _lib.lib()
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_functions()
+    for required in ("bp_skinny_bf16", "bp_skinny_int8", "bp_gemv_int8", "bp_splitk_reduce", "bp_mlstm_multistep",
+                     "bp_skinny_workspace_bytes", "bp_skinny_config_supported", "bp_version", "bp_status_string"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(L):
+    for name in declared_functions():
+        assert hasattr(L, name), name
+
+
+def test_python_binding_covers_every_declared_symbol():
+    from byteprof_amd import _lib
+
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+
+
+def test_one_hip_runtime_is_mapped(L):
+    from byteprof_amd import _lib
+
+    assert len(_lib._mapped_hip_runtimes()) <= 1
+
+
+def test_version_and_status_strings(L):
+    assert L.bp_version() >= 100
+    for code in (0, -1, -2, -3):
+        assert L.bp_status_string(code)
+    assert b"workspace" in L.bp_status_string(-3)
+
+
+def test_workspace_bytes(L):
+    assert L.bp_skinny_workspace_bytes(4, 100, 1) == 0
+    assert L.bp_skinny_workspace_bytes(4, 100, 3) == 3 * 4 * 100 * 4
+    assert L.bp_skinny_workspace_bytes(0, 100, 3) == 0
+
+
+def test_config_menu(L):
+    # rows = 2 exists at every waves <= 8 for every row bucket and kind (one K order serves all buckets)
+    for kind in (0, 1):
+        for mt in (1, 2, 4, 8, 16):
+            for waves in (1, 2, 4, 8):
+                assert L.bp_skinny_config_supported(kind, mt, 2, waves), (kind, mt, waves)
+    assert not L.bp_skinny_config_supported(0, 1, 3, 4)  # rows must be a power of two in the menu
+    assert not L.bp_skinny_config_supported(0, 3, 2, 4)  # row buckets are 1, 2, 4, 8, 16
+    assert not L.bp_skinny_config_supported(2, 1, 2, 4)  # kinds are 0 (bf16) and 1 (int8)
+
+
+def test_invalid_arguments_are_rejected_before_any_launch(L):
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below returns before enqueueing anything
+    assert L.bp_skinny_bf16(None, p, p, 1, 1, 1, 4, 4, 1, None, 0, None) == -1       # null x
+    assert L.bp_skinny_bf16(p, p, p, -1, 1, 1, 4, 4, 1, None, 0, None) == -1          # negative M
+    assert L.bp_skinny_bf16(p, p, p, 17, 1, 1, 4, 4, 1, None, 0, None) == -1          # more than 16 rows
+    assert L.bp_skinny_bf16(p, p, p, 0, 5, 5, 4, 4, 1, None, 0, None) == 0            # M = 0: no-op
+    assert L.bp_skinny_bf16(p, p, p, 3, 0, 5, 4, 4, 1, None, 0, None) == 0            # N = 0: no-op
+    assert L.bp_skinny_bf16(p, p, p, 1, 8, 1024, 3, 4, 1, None, 0, None) == -2        # rows not in the menu
+    assert L.bp_skinny_bf16(p, p, p, 1, 8, 4096, 4, 4, 2, None, 0, None) == -3        # split without workspace
+    assert L.bp_skinny_int8(p, p, None, 0, p, 1, 8, 64, 4, 4, 1, None, 0, None) == -1  # int8 without scale
+    assert L.bp_skinny_int8(p, p, p, 7, p, 1, 8, 64, 4, 4, 1, None, 0, None) == -1     # bad scale dtype
+    assert L.bp_splitk_reduce(None, p, None, 0, 2, 2, 2, None) == -1
+    # mLSTM: DQ not a multiple of 64, bad value block, DV not a multiple of it
+    args = [p] * 11
+    assert L.bp_mlstm_multistep(*args, 4, 2, 48, 16, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 8, None) == -2
+    assert L.bp_mlstm_multistep(*args, 4, 2, 64, 16, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 5, None) == -2
+    assert L.bp_mlstm_multistep(*args, 4, 2, 64, 12, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 8, None) == -2
+    assert L.bp_mlstm_multistep(*args, 4, 0, 64, 16, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 8, None) == 0  # NH = 0: no-op

@@ -1,0 +1,242 @@
+"""Host-side logic of the drop-in modules on the CPU: module selection, byte accounting, the quantizer's bytes,
+argument validation, configuration resolution and the CPU (dequantized) paths of the nn.Module drop-ins.
+Selection / accounting cases follow byteprof tests/test_quant_accounting.py; validation follows
+tests/test_skinny.py:125-132."""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from byteprof_amd.optim import skinny as S
+from byteprof_amd.quant import accounting as A
+from byteprof_amd.quant import select as SEL
+from byteprof_amd.quant.hip_int8 import quantize_rowwise_int8
+from oracle import numerics as ON
+from oracle import skinny as OS
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---- selection (names in, bool out) -----------------------------------------------------------------------------
+
+
+def test_select_local_exactly():
+    enc = "model.local_encoder.layers.0."
+    dec = "model.local_decoder.layers.3."
+    yes = [enc + s for s in ("xlstm.q", "xlstm.k", "xlstm.v", "xlstm.ogate_preact", "xlstm.out_proj",
+                              "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")]
+    yes += [dec + s for s in ("xlstm.q", "mlp.down_proj")]
+    yes += ["model.local_encoder.out_projection", "model.local_decoder.in_projection"]
+    no = ["lm_head", "model.local_encoder.byte_embedding", "model.local_encoder.subword_embedding",
+          "model.local_encoder.boundary_predictor_module.q_proj_layer", enc + "xlstm.igate_preact",
+          enc + "xlstm.fgate_preact", "model.local_decoder.layers", "model.local_encoder.layers.0.mlp",
+          enc + "pre_xlstm_layernorm"]
+    for n in yes:
+        assert SEL.should_quantize(n, "local") and not SEL.should_quantize(n, "global") and SEL.should_quantize(n, "all")
+        assert not SEL.should_quantize(n, "none")
+    assert not SEL.should_quantize("model.layers.0.self_attn.q_proj", "local")
+    for n in no:
+        assert not any(SEL.should_quantize(n, t) for t in ("none", "local", "global", "all")), n
+
+
+def test_select_global_and_olmo_targets():
+    blocks = [f"model.layers.{i}.{s}" for i in (0, 15) for s in (
+        "self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+        "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")]
+    for n in blocks:
+        assert SEL.group_of(n) == "global" and SEL.should_quantize(n, "global")
+        assert SEL.olmo_group_of(n) == "blocks"
+        assert SEL.olmo_should_quantize(n, "blocks") and SEL.olmo_should_quantize(n, "blocks+head")
+        assert not SEL.olmo_should_quantize(n, "none")
+    assert SEL.olmo_group_of("lm_head") == "head"
+    assert not SEL.olmo_should_quantize("lm_head", "blocks") and SEL.olmo_should_quantize("lm_head", "blocks+head")
+    for n in ("model.layers.0.self_attn.q_norm", "model.layers.0", "model.embed_tokens", "model.layers.0.self_attn"):
+        assert SEL.group_of(n) is None and SEL.olmo_group_of(n) is None
+    with pytest.raises(ValueError):
+        SEL.should_quantize("lm_head", "everything")
+    with pytest.raises(ValueError):
+        SEL.olmo_should_quantize("lm_head", "all")
+    assert SEL.selects("blocks+head", "head") and not SEL.selects("blocks", "head") and not SEL.selects("none", "local")
+
+
+# ---- byte accounting ----------------------------------------------------------------------------------------------
+
+
+def test_linear_bytes_schemes():
+    lin = A.Linear(8, 256, "local")
+    assert A.linear_bytes(lin, None) == 8 * 256 * 2
+    assert A.linear_bytes(lin, "int8_wo") == 8 * 256 + 8 * 2
+    assert A.linear_bytes(lin, "int4_wo", 128) == 8 * 256 * 0.5 + 8 * 2 * 4
+    with pytest.raises(ValueError):
+        A.linear_bytes(A.Linear(8, 100), "int4_wo", 128)
+
+
+def test_decode_set_byte_totals():
+    """The algorithmic bytes of the OLMo-2-1B-shaped decode-step set at M = 1 (weights + activations + outputs)."""
+    lins = [A.Linear(2048, 2048)] * 4 + [A.Linear(8192, 2048)] * 2 + [A.Linear(2048, 8192)]
+    blocks = 16 * sum(A.call_bytes(l, None, 1) for l in lins)
+    head = A.call_bytes(A.Linear(100352, 2048), None, 1)
+    assert blocks + head == 2_560_237_568
+    assert A.call_bytes(A.Linear(8192, 2048), None, 1) == 33_574_912
+    int8 = 16 * sum(A.call_bytes(l, "int8_wo", 1) for l in lins) + A.call_bytes(A.Linear(100352, 2048), "int8_wo", 1)
+    assert int8 == 1_282_027_520
+
+
+# ---- quantizer bytes ----------------------------------------------------------------------------------------------
+
+
+def test_quantizer_matches_the_exact_fixture():
+    cases = json.loads((GOLDEN / "quantizer_kat.json").read_text())["cases"]
+    for c in cases:
+        w = torch.tensor([c["w"]], dtype=torch.bfloat16)
+        sdt = torch.bfloat16 if c["scale_dtype"] == "bf16" else torch.float16
+        q, s = quantize_rowwise_int8(w, sdt)
+        assert q[0].tolist() == c["q"] and float(s[0]) == c["scale"] and s.dtype == sdt, c
+
+
+def test_quantizer_matches_the_oracle_bit_for_bit():
+    torch.manual_seed(0)
+    w = (torch.randn(64, 512) * 0.02).to(torch.bfloat16)
+    q, s = quantize_rowwise_int8(w)
+    oq, os_ = OS.quantize_rowwise_int8(w.float().numpy(), "bf16")
+    assert np.array_equal(q.numpy(), oq) and np.array_equal(s.float().numpy(), os_)
+    assert q.dtype == torch.int8 and s.dtype == torch.bfloat16 and q.is_contiguous()
+
+
+# ---- validation and configuration ---------------------------------------------------------------------------------
+
+
+def test_skinny_mm_validation_errors():
+    w = torch.zeros(8, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        S.skinny_mm(torch.zeros(2, 64, dtype=torch.bfloat16), w)  # K mismatch
+    with pytest.raises(ValueError):
+        S.skinny_mm(torch.zeros(2, 128, dtype=torch.bfloat16)[:, ::2], w)  # not contiguous
+    with pytest.raises(ValueError):
+        S.skinny_mm(torch.zeros(2, 128, dtype=torch.bfloat16), torch.zeros(8, 128, dtype=torch.int8))  # no scale
+    with pytest.raises(ValueError):
+        S.skinny_mm(torch.zeros(2, 128, dtype=torch.bfloat16), torch.zeros(8, 128, dtype=torch.float64))
+    with pytest.raises(ValueError):
+        S.skinny_mm(torch.zeros(2, 128, dtype=torch.bfloat16), w)  # on the CPU: no CPU path
+    with pytest.raises(NotImplementedError):
+        S.skinny_mm(torch.zeros(2, 256, dtype=torch.bfloat16), torch.zeros(1, 2, 32, 64, dtype=torch.uint8),
+                    torch.zeros(2, 32, dtype=torch.bfloat16), torch.zeros(2, 32, dtype=torch.float16))
+
+
+def test_configuration_keeps_one_k_order_per_shape():
+    """waves and split (the K order) must not depend on the activation-row bucket."""
+    for kind in ("bf16", "int8"):
+        for n, k in ((2048, 2048), (8192, 2048), (2048, 8192), (100352, 2048), (37, 256), (129, 640), (8, 5000)):
+            orders = {S._resolve(kind, n, k, bm, None)[1:] for bm in (1, 2, 4, 8, 16)}
+            assert len(orders) == 1, (kind, n, k, orders)
+
+
+def test_reference_cfg_tuples_are_mapped():
+    assert S._resolve("bf16", 192, 1024, 1, (32, 128, 4, 3, 4)) == (32, 4, 4)
+    assert S._resolve("bf16", 192, 1024, 16, (64, 64, 2, 2, 1)) == (4, 2, 1)  # rows clamped to the menu
+    assert S._resolve("int8", 192, 1024, 1, (16, 256, 4, 3, 3)) == (16, 4, 3)
+    assert S._resolve("bf16", 192, 1024, 1, (4, 8, 2)) == (4, 8, 2)
+    with pytest.raises(ValueError):
+        S._resolve("bf16", 192, 1024, 1, (1, 2))
+
+
+# ---- CPU paths of the drop-in modules (the reference's dequantized F.linear path) -------------------------------
+
+
+def test_skinny_linear_cpu_inputs_use_the_dequantized_weights():
+    from byteprof_amd.optim.skinny_linear import SkinnyLinear
+
+    torch.manual_seed(1)
+    lin = nn.Linear(256, 64, bias=True, dtype=torch.float32)
+    m = SkinnyLinear(lin, "int8_wo")
+    assert m.weight.numel() == 0 and m.weight.dtype == torch.float32
+    x = torch.randn(3, 256)
+    y = m(x)
+    assert torch.allclose(y, x @ m.dequantized(torch.float32).T + lin.bias, atol=1e-5, rtol=1e-5)
+    assert m(x.new_empty(0, 256)).shape == (0, 64)
+    with pytest.raises(ValueError):
+        SkinnyLinear(lin, "int3_wo")
+    with pytest.raises(NotImplementedError):
+        SkinnyLinear(lin, "int4_wo")
+
+
+class _Block(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.self_attn = nn.ModuleDict({n: nn.Linear(d, d, bias=False) for n in ("q_proj", "k_proj", "v_proj", "o_proj")})
+        self.mlp = nn.ModuleDict({"gate_proj": nn.Linear(d, 2 * d, bias=False), "up_proj": nn.Linear(d, 2 * d, bias=False),
+                                  "down_proj": nn.Linear(2 * d, d, bias=False)})
+
+
+class _Toy(nn.Module):
+    def __init__(self, d=256):
+        super().__init__()
+        self.model = nn.Module()
+        self.model.layers = nn.ModuleList([_Block(d) for _ in range(2)])
+        self.lm_head = nn.Linear(d, 64, bias=False)
+
+
+@pytest.mark.parametrize("scheme,kernel", [("bf16_wo", "skinny"), ("int8_wo", "skinny"), ("int8_wo", "default")])
+def test_apply_quantization_swaps_the_selected_linears(scheme, kernel):
+    from byteprof_amd.optim.skinny_linear import SkinnyLinear
+    from byteprof_amd.quant.integrate import Int8Linear, apply_quantization
+
+    torch.manual_seed(0)
+    m = _Toy().to(torch.bfloat16)
+    stats = apply_quantization(m, "blocks", scheme, 128, None, None, kernel)
+    cls = SkinnyLinear if kernel == "skinny" else Int8Linear
+    assert stats["n_linears"] == 14 and sum(isinstance(x, cls) for x in m.modules()) == 14
+    assert isinstance(m.lm_head, nn.Linear)
+    assert ("kernel" in stats) == (kernel != "default")
+    m2 = _Toy().to(torch.bfloat16)
+    assert apply_quantization(m2, "blocks+head", scheme, 128, None, None, kernel)["n_linears"] == 15
+
+
+def test_default_kernel_rejects_the_skinny_only_scheme():
+    from byteprof_amd.quant.integrate import apply_quantization
+
+    with pytest.raises(ValueError):
+        apply_quantization(_Toy(), "blocks", "bf16_wo")
+
+
+def test_int8linear_cpu_path_matches_dequantized_reference():
+    from byteprof_amd.quant.integrate import Int8Linear
+
+    torch.manual_seed(2)
+    lin = nn.Linear(128, 32, bias=True, dtype=torch.bfloat16)
+    mod = Int8Linear(lin)
+    x = torch.randn(2, 1, 128, dtype=torch.bfloat16)
+    y = mod(x)
+    ref = torch.nn.functional.linear(x.reshape(2, 128), mod.q.to(torch.bfloat16) * mod.scale[:, None], lin.bias)
+    assert y.shape == (2, 1, 32) and torch.equal(y.reshape(2, 32), ref)
+
+
+def test_multistep_fw_validation():
+    from byteprof_amd.optim import draft_fused as F
+
+    nh, dq, dv, t = 2, 48, 16, 3
+    cur = (torch.zeros(1, nh, dq, dv), torch.zeros(1, nh, dq), torch.zeros(1, nh, 1))
+    q = torch.zeros(t, nh, dq)
+    v = torch.zeros(t, nh, dv)
+    g = torch.zeros(t, nh, 1)
+    with pytest.raises(NotImplementedError):  # DQ not a multiple of 64
+        F.multistep_fw(cur, q, q, v, g, g, torch.zeros(t, nh, dv), torch.zeros(nh, dq), torch.zeros(nh), 1e-6)
+    dq = 64
+    cur = (torch.zeros(1, nh, dq, dv), torch.zeros(1, nh, dq), torch.zeros(1, nh, 1))
+    q = torch.zeros(t, nh, dq)
+    with pytest.raises(ValueError):  # GPU only
+        F.multistep_fw(cur, q, q, v, g, g, torch.zeros(t, nh, dv), torch.zeros(nh, dq), torch.zeros(nh), 1e-6)
+    with pytest.raises(ValueError):  # h too short
+        F.multistep_fw(cur, q, q, v, g, g, torch.zeros(t - 1, nh, dv), torch.zeros(nh, dq), torch.zeros(nh), 1e-6)
+
+
+def test_bf16_of_torch_matches_the_oracle_rounding():
+    """torch's .to(bfloat16) (what every drop-in output is compared in) rounds like the oracle."""
+    x = torch.randn(5000) * 10
+    assert np.array_equal(x.to(torch.bfloat16).float().numpy(), ON.bf16_round(x.numpy()))

@@ -1,0 +1,229 @@
+"""Pins the CPU oracle (oracle/) against things other than itself: exact rational arithmetic, the committed
+known-answer fixtures of tests/golden/, the reference's own bounds, closed forms and invariants. CPU only."""
+
+from __future__ import annotations
+
+import json
+import math
+import struct
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import mlstm as OM
+from oracle import numerics as ON
+from oracle import skinny as OS
+from tests.exact import BF16, FP16, bf16_bits_exact, exact_round
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---- bf16 / fp16 rounding ---------------------------------------------------------------------------------------
+
+
+def _f32(bits: int) -> float:
+    return struct.unpack("<f", struct.pack("<I", bits))[0]
+
+
+@pytest.mark.parametrize("bits,expect", [
+    (0x3F800000, 0x3F80),  # 1.0
+    (0x3F808000, 0x3F80),  # 1 + 2^-8: exact tie, even mantissa stays
+    (0x3F818000, 0x3F82),  # 1 + 3 * 2^-8: tie, odd mantissa rounds up
+    (0x3F808001, 0x3F81),  # just above the tie
+    (0x3FFF8000, 0x4000),  # carry into the exponent: 1.99609375 -> 2.0
+    (0x7F7FFFFF, 0x7F80),  # float max rounds to inf
+    (0xFF7FFFFF, 0xFF80),  # -float max -> -inf
+    (0x80000000, 0x8000),  # -0.0
+    (0x00000001, 0x0000),  # smallest subnormal rounds to +0
+    (0x00018000, 0x0002),  # subnormal tie with odd mantissa -> rounds up
+    (0x7F800000, 0x7F80),  # inf
+])
+def test_bf16_rounding_known_answers(bits, expect):
+    assert int(ON.bf16_bits(np.array([_f32(bits)], np.float32))[0]) == expect
+    assert bf16_bits_exact(_f32(bits)) == expect
+
+
+def test_bf16_rounding_nan_stays_nan():
+    out = ON.bf16_round(np.array([np.nan, -np.nan], np.float32))
+    assert np.isnan(out).all()
+
+
+def test_bf16_rounding_matches_exact_rounding_on_sampled_patterns():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2**32, size=4000, dtype=np.uint64).astype(np.uint32)
+    # add patterns near ties: low 16 bits = 0x8000 +- 1
+    hi = rng.integers(0, 2**16, size=600, dtype=np.uint64).astype(np.uint32) << 16
+    bits = np.concatenate([bits, hi | 0x8000, hi | 0x7FFF, hi | 0x8001])
+    vals = bits.view(np.float32)
+    got = ON.bf16_bits(vals)
+    for v, g in zip(vals, got):
+        if math.isnan(v):
+            continue
+        assert bf16_bits_exact(float(v)) == int(g), hex(struct.unpack('<I', struct.pack('<f', float(v)))[0])
+
+
+def test_f16_rounding_matches_exact_rounding():
+    rng = np.random.default_rng(1)
+    vals = (rng.standard_normal(2000) * rng.choice([1e-6, 1e-3, 1.0, 100.0, 6e4], 2000)).astype(np.float32)
+    got = ON.f16_round(vals)
+    for v, g in zip(vals, got):
+        r = exact_round(Fraction(float(v)), FP16)
+        assert (float(r) if not isinstance(r, float) else r) == float(g)
+
+
+# ---- matmul oracle ----------------------------------------------------------------------------------------------
+
+
+def test_matmul_oracle_against_exact_rational_sum():
+    rng = np.random.default_rng(2)
+    x = ON.bf16_round(rng.standard_normal((3, 40)).astype(np.float32))
+    w = ON.bf16_round((rng.standard_normal((5, 40)) * 0.02).astype(np.float32))
+    y = OS.matmul(x, w)
+    for a in range(3):
+        for b in range(5):
+            exact = sum(Fraction(float(p)) * Fraction(float(q)) for p, q in zip(x[a], w[b]))
+            assert abs(Fraction(float(y[a, b])) - exact) <= abs(exact) * Fraction(1, 2**48) + Fraction(1, 2**100)
+
+
+def test_skinny_oracle_against_committed_exact_fixture():
+    cases = json.loads((GOLDEN / "skinny_kat.json").read_text())["cases"]
+    for c in cases:
+        x = np.array(c["x"], np.float32)
+        w = np.array(c["w"], np.float32)
+        got = ON.bf16_bits(OS.skinny_bf16(x, w))
+        want = np.array(c["y_bf16_bits"], np.uint16)
+        # the oracle rounds float64 -> float32 -> bf16; the fixture rounds the exact sum once. They may differ only
+        # where the exact value sits within float64 error of a bf16 tie; none of these cases does.
+        assert np.array_equal(got, want), (c["m"], c["n"], c["k"])
+
+
+def test_skinny_oracle_known_answer_by_hand():
+    x = np.array([[1.0, 2.0, -1.0, 0.5]], np.float32)
+    w = np.array([[1.0, 1.0, 1.0, 1.0], [0.5, -0.25, 2.0, 4.0], [0.0, 0.0, 0.0, 0.0]], np.float32)
+    assert OS.skinny_bf16(x, w).tolist() == [[2.5, 0.0, 0.0]]
+    q = np.array([[1, -2, 3, 127]], np.int8)
+    assert OS.skinny_int8(x, q, np.array([0.5], np.float32)).tolist() == [[0.5 * (1 - 4 - 3 + 63.5)]]
+
+
+def test_dequantize_known_answer():
+    q = np.array([[1, -127], [64, 0]], np.int8)
+    s = np.array([0.25, 2.0 ** -7], np.float32)
+    assert OS.dequantize("int8", q, s).tolist() == [[0.25, -31.75], [0.5, 0.0]]
+
+
+# ---- int8 quantizer ---------------------------------------------------------------------------------------------
+
+
+def test_quantizer_against_committed_exact_fixture():
+    cases = json.loads((GOLDEN / "quantizer_kat.json").read_text())["cases"]
+    assert len(cases) >= 16
+    for c in cases:
+        q, s = OS.quantize_rowwise_int8(np.array([c["w"]], np.float32), c["scale_dtype"])
+        assert q[0].tolist() == c["q"], c
+        assert float(s[0]) == c["scale"], c
+
+
+def test_quantizer_error_bound_of_the_reference_test():
+    """byteprof tests/test_quant_int8.py:10-16: per-row error <= 0.51 step + 1e-3, |q| <= 127."""
+    rng = np.random.default_rng(3)
+    w = ON.bf16_round(rng.standard_normal((16, 256)).astype(np.float32))
+    q, s = OS.quantize_rowwise_int8(w)
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    deq = q.astype(np.float32) * s[:, None]
+    assert (np.abs(deq - w).max(axis=1) <= s * 0.51 + 1e-3).all()
+    # the row maximum maps to +-127 (within one step of the bf16-rounded scale)
+    am = np.abs(w).argmax(axis=1)
+    assert (np.abs(q[np.arange(16), am].astype(np.int32)) >= 126).all()
+
+
+# ---- mLSTM oracle -----------------------------------------------------------------------------------------------
+
+
+def _mlstm_inputs(t, nh, dq, dv, seed, m_scale=1.0):
+    rng = np.random.default_rng(seed)
+    c = rng.standard_normal((nh, dq, dv)) * 0.1
+    n = rng.standard_normal((nh, dq)) * 0.1
+    m = rng.standard_normal(nh) * m_scale
+    q = rng.standard_normal((t, nh, dq))
+    k = rng.standard_normal((t, nh, dq))
+    v = rng.standard_normal((t, nh, dv))
+    i = rng.standard_normal((t, nh))
+    f = rng.standard_normal((t, nh)) + 3.0
+    return c, n, m, q, k, v, i, f
+
+
+@pytest.mark.parametrize("t", [1, 2, 5, 9])
+def test_mlstm_stabilised_equals_unstabilised_closed_form(t):
+    """The stabiliser only rescales C, n by exp(-m_t): with no roundings and eps = 0 both formulas agree."""
+    c, n, m, q, k, v, i, f = _mlstm_inputs(t, 3, 8, 5, seed=t)
+    h, _ = OM.multistep(c, n, m, q, k, v, i, f, eps=0.0, io="f64")
+    ref = OM.unstabilised(c, n, m, q, k, v, i, f)
+    assert np.allclose(h, ref, rtol=1e-11, atol=1e-13)
+
+
+def test_mlstm_composition_of_steps():
+    c, n, m, q, k, v, i, f = _mlstm_inputs(7, 2, 8, 4, seed=11)
+    h_all, st_all = OM.multistep(c, n, m, q, k, v, i, f, eps=1e-6, io="bf16")
+    h1, st1 = OM.multistep(c, n, m, q[:3], k[:3], v[:3], i[:3], f[:3], eps=1e-6, io="bf16")
+    h2, st2 = OM.multistep(*st1, q[3:], k[3:], v[3:], i[3:], f[3:], eps=1e-6, io="bf16")
+    assert np.array_equal(h_all, np.concatenate([h1, h2]))
+    for a, b in zip(st_all, st2):
+        assert np.array_equal(a, b)
+
+
+def test_mlstm_pure_decay_when_the_input_gate_is_closed():
+    """i -> -inf: C_T = C_0 exp(sum logsigmoid(f) + m_0 - m_T), no k v^T contribution."""
+    c, n, m, q, k, v, i, f = _mlstm_inputs(4, 2, 8, 4, seed=5)
+    i = np.full_like(i, -1e4)
+    _, (C, N, M) = OM.multistep(c, n, m, q, k, v, i, f, eps=0.0, io="f64")
+    decay = np.exp(OM.logsigmoid(f).sum(axis=0) + m - M)
+    assert np.allclose(C, c * decay[:, None, None], rtol=1e-12)
+    assert np.allclose(N, n * decay[:, None], rtol=1e-12)
+    assert np.allclose(M, m + OM.logsigmoid(f).sum(axis=0), rtol=1e-12)
+
+
+def test_mlstm_single_step_from_an_empty_state():
+    """T = 1 from C = n = 0 and m_0 = -inf-like: m_1 = i, C_1 = k v^T, n_1 = k, h = qs.(k v^T) / max(|qs.k|, e^-i)."""
+    rng = np.random.default_rng(7)
+    dq, dv = 8, 3
+    q = rng.standard_normal((1, 1, dq))
+    k = rng.standard_normal((1, 1, dq))
+    v = rng.standard_normal((1, 1, dv))
+    i = np.array([[0.3]])
+    f = np.array([[2.0]])
+    h, (C, N, M) = OM.multistep(np.zeros((1, dq, dv)), np.zeros((1, dq)), np.array([-1e9]), q, k, v, i, f,
+                                eps=0.0, io="f64")
+    qs = q[0, 0] / math.sqrt(dq)
+    want = (qs @ k[0, 0]) * v[0, 0] / max(abs(qs @ k[0, 0]), math.exp(-0.3))
+    assert np.allclose(h[0, 0], want, rtol=1e-12)
+    assert np.allclose(C[0], np.outer(k[0, 0], v[0, 0]), rtol=1e-12) and M[0] == pytest.approx(0.3)
+
+
+def test_mlstm_io_rounding_is_applied_to_h():
+    c, n, m, q, k, v, i, f = _mlstm_inputs(3, 2, 8, 4, seed=9)
+    h, _ = OM.multistep(c, n, m, q, k, v, i, f, eps=1e-6, io="bf16")
+    assert np.array_equal(h, ON.bf16_round(h.astype(np.float32)).astype(np.float64))
+    h32, _ = OM.multistep(c, n, m, q, k, v, i, f, eps=1e-6, io="f32")
+    assert ON.normwise_error(h, h32) < 1e-2  # bf16 roundings stay inside the reference's bf16 tolerance
+
+
+def test_literal_gate_reading_differs_from_the_reference_reading():
+    """BASELINE writes m_t = max(f + m, i) with f ~ N(3, 1); the reference applies logsigmoid(f) first
+    (mlstm_multistep.py:25-26). With f taken literally as a log forget gate the state grows ~e^3 per step
+    (in the stabilised form: m grows by ~3 per step while C keeps its scale), so the two readings give different h."""
+    c, n, m, q, k, v, i, f = _mlstm_inputs(6, 2, 8, 4, seed=13)
+    h_ref, st_ref = OM.multistep(c, n, m, q, k, v, i, f, eps=1e-6, io="f64")
+    h_lit, st_lit = OM.multistep(c, n, m, q, k, v, i, f, eps=1e-6, io="f64", literal_gate=True)
+    assert ON.normwise_error(h_lit, h_ref) > 1e-2
+    assert (st_lit[2] - m).min() > 6 * 2.0  # m grew by about f per step (f ~ 3)
+    assert (st_ref[2] - m).max() < 6 * 0.5  # logsigmoid(f) ~ -0.05: m barely moves
+
+
+def test_error_metrics():
+    y = np.array([[1.0, 2.0]])
+    assert ON.normwise_error(y, np.array([[1.0, 2.5]])) == pytest.approx(0.2)
+    x = np.array([[1.0, -1.0]])
+    w = np.array([[1.0, 1.0]])  # exact output 0 (cancelling): componentwise error normalises by |x||w| = 2
+    assert ON.componentwise_error(np.array([[0.01]]), x, w) == pytest.approx(0.005)
