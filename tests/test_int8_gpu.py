@@ -19,14 +19,14 @@ pytestmark = pytest.mark.gpu
 def _oracle(x, q, s, bias=None):
     y = OS.matmul(x.float().cpu().numpy(), OS.dequantize("int8", q.cpu().numpy(), s.float().cpu().numpy()))
     if bias is not None:
-        y = y + bias.float().cpu().numpy()[None, :]
+        y = y + bias.detach().float().cpu().numpy()[None, :]
     return y
 
 
 def _close(y, ref):
     """max |y - ref| <= 0.01 max |ref| + 1e-3 (tests/test_quant_int8.py:53-56)."""
     assert y.dtype == torch.bfloat16
-    err = float(abs(y.float().cpu().numpy() - ref).max())
+    err = float(abs(y.detach().float().cpu().numpy() - ref).max())
     assert err <= 0.01 * float(abs(ref).max()) + 1e-3, err
 
 
