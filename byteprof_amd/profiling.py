@@ -1,0 +1,139 @@
+"""Short GPU programs to run under rocprofv3 (kernel trace, HBM counters).
+
+  python -m byteprof_amd.profiling set  [--kind bf16|int8] [--replays R]   the decode-step set graph, R replays
+  python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
+  python -m byteprof_amd.profiling summarize TRACE_DB [--fetch DB --write DB --fetch-copy DB --write-copy DB
+                                             --copy-mib 256]               text summary of rocprofv3 databases
+
+The copy is the calibration reference for the FETCH_SIZE / WRITE_SIZE counters: it reads and writes exactly
+`mib` MiB per dispatch, so expected / counter is the factor that turns a counter reading into HBM bytes.
+`summarize` needs no GPU: it reads the SQLite databases rocprofv3 writes (kernels / counters_collection views).
+"""
+
+from __future__ import annotations
+
+import argparse
+import sys
+
+import torch
+
+
+def _kernel_stats(db_path: str) -> list[tuple[str, int, int, float, float]]:
+    """(kernel name, grid threads, calls, total us, average us) from a kernel-trace database, longest total first;
+    the grid size tells the launches of one kernel instantiation on different shapes apart."""
+    import sqlite3
+
+    cur = sqlite3.connect(db_path).cursor()
+    rows = cur.execute("select name, grid_x * grid_y * grid_z, count(*), sum(duration), avg(duration) from kernels "
+                       "group by name, grid_x, grid_y, grid_z order by sum(duration) desc").fetchall()
+    return [(n, int(gs), int(c), tot / 1e3, avg / 1e3) for n, gs, c, tot, avg in rows]
+
+
+def _counter_avgs(db_path: str) -> dict[tuple[str, int], tuple[str, int, float]]:
+    """(kernel name, grid size) -> (counter, dispatches, average value in KiB per dispatch). The grid size tells the
+    launches of one kernel instantiation on different shapes apart."""
+    import sqlite3
+
+    cur = sqlite3.connect(db_path).cursor()
+    rows = cur.execute("select kernel_name, grid_size, counter_name, count(*), avg(value) from counters_collection "
+                       "group by kernel_name, grid_size, counter_name").fetchall()
+    return {(n, int(gs)): (c, int(k), v) for n, gs, c, k, v in rows}
+
+
+def _short(name: str) -> str:
+    return name.split("(")[0].replace("void ", "")
+
+
+def summarize(a) -> int:
+    print("## kernel trace (rocprofv3 --kernel-trace --stats)")
+    print(f"{'kernel':<48} {'grid threads':>12} {'calls':>7} {'total us':>11} {'avg us':>9}")
+    for name, grid, calls, tot, avg in _kernel_stats(a.db):
+        if a.all or "bp::" in name:
+            print(f"{_short(name)[:48]:<48} {grid:>12} {calls:>7} {tot:>11.1f} {avg:>9.3f}")
+    if not a.fetch:
+        return 0
+    expected_kib = a.copy_mib * 1024
+    fetch_copy = [v for (n, _), v in _counter_avgs(a.fetch_copy).items() if "copy" in n.lower()][0][2]
+    write_copy = [v for (n, _), v in _counter_avgs(a.write_copy).items() if "copy" in n.lower()][0][2]
+    f_scale, w_scale = expected_kib / fetch_copy, expected_kib / write_copy
+    print()
+    print(f"## HBM counters (KiB per dispatch), calibrated on a {a.copy_mib} MiB device copy")
+    print(f"copy: FETCH_SIZE {fetch_copy:.1f} KiB -> scale {f_scale:.4f}; WRITE_SIZE {write_copy:.1f} KiB "
+          f"-> scale {w_scale:.4f}")
+    fetch, write = _counter_avgs(a.fetch), _counter_avgs(a.write)
+    print(f"{'kernel':<48} {'grid threads':>12} {'dispatches':>10} {'FETCH KiB':>11} {'WRITE KiB':>10} "
+          f"{'traffic MB':>11}")
+    for key in sorted(fetch):
+        name, grid = key
+        if "bp::" not in name and not a.all:
+            continue
+        _, k, fv = fetch[key]
+        wv = write.get(key, ("", 0, 0.0))[2]
+        traffic = (fv * f_scale + wv * w_scale) * 1024 / 1e6
+        print(f"{_short(name)[:48]:<48} {grid:>12} {k:>10} {fv:>11.1f} {wv:>10.1f} {traffic:>11.3f}")
+    if a.set_kind:
+        print()
+        print(f"## traffic per launch of the {a.set_kind} decode-step set shapes (bytes; read by bench.py)")
+        for (kernel, shape), grid in _set_launches(a.set_kind).items():
+            for key in fetch:
+                if key[1] == grid and _short(key[0]).replace("bp::", "") == kernel:
+                    nbytes = (fetch[key][2] * f_scale + write.get(key, ("", 0, 0.0))[2] * w_scale) * 1024
+                    print(f"traffic: {kernel} {shape} {nbytes:.0f}")
+    return 0
+
+
+def _set_launches(kind: str) -> dict[tuple[str, str], int]:
+    """(kernel instantiation, 'NxK') -> grid threads of the decode-step set's launches at M = 1."""
+    from . import decode_set as D
+    from .optim import skinny as S
+
+    out = {}
+    for _, n, k in D.shapes():
+        rows, waves, split = S._resolve(kind, n, k, 1, None)
+        grid = -(-n // rows) * waves * 64 * split
+        out[(D.kernel_key(kind, n, k, 1), f"{n}x{k}")] = grid
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("what", choices=("set", "copy", "summarize"))
+    ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
+    ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
+    ap.add_argument("--write", help="summarize: WRITE_SIZE database of the workload")
+    ap.add_argument("--fetch-copy", help="summarize: FETCH_SIZE database of the calibration copy")
+    ap.add_argument("--write-copy", help="summarize: WRITE_SIZE database of the calibration copy")
+    ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--all", action="store_true", help="summarize: include kernels outside this library")
+    ap.add_argument("--set-kind", choices=("bf16", "int8"), help="summarize: emit traffic lines for the set shapes")
+    ap.add_argument("--kind", default="bf16", choices=("bf16", "int8"))
+    ap.add_argument("--replays", type=int, default=5)
+    ap.add_argument("--mib", type=int, default=256)
+    ap.add_argument("--reps", type=int, default=5)
+    a = ap.parse_args(argv)
+    if a.what == "summarize":
+        return summarize(a)
+    device = torch.device("cuda:0")
+    if a.what == "copy":
+        src = torch.empty(a.mib << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(a.reps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copied {a.mib} MiB x {a.reps}", flush=True)
+        return 0
+    from . import _lib
+    from . import decode_set as D
+
+    _lib.lib()
+    ops = D.build(a.kind, 1, device)
+    g = D.capture(ops)
+    for _ in range(a.replays):
+        g.replay()
+    torch.cuda.synchronize()
+    print(f"replayed the {a.kind} decode-step set {a.replays} times ({len(ops)} launches each)", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,149 @@
+"""Tile-configuration tuner of the skinny kernels on the GPU; writes byteprof_amd/optim/skinny_cfg.json.
+
+The measurement follows the reference's method (byteprof tools/skinny_bench.py:45-71, tools/skinny_tune.py:30-93):
+a ring of distinct weight sets applied to one activation block inside a HIP graph, so the weights are streamed from
+HBM and not served from cache, the median of several trials per configuration. The ring here is sized against
+MI355X's 256 MB Infinity Cache (at least 1 GiB of weights per cell) instead of a 3 MB L2.
+
+Per (kind, N, K) the tuner keeps ONE K order (waves, split) for every activation-row bucket, so an output row stays
+bitwise independent of M: it picks (waves, split) by the M = 1 time (the decode metric), then the rows per
+workgroup separately for each bucket. Like the reference, a split > 1 is kept only if it wins by more than 3%.
+
+Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8] [--out path] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+import sys
+from pathlib import Path
+
+import torch
+
+from . import _lib
+from .optim import skinny as S
+from .quant.hip_int8 import quantize_rowwise_int8
+
+RING_BYTES = 1 << 30
+DEFAULT_SHAPES = [(2048, 2048), (8192, 2048), (2048, 8192), (100352, 2048), (6144, 2048), (16384, 2048),
+                  (100352, 8192), (8192, 8192)]
+ROWS = (2, 4, 8, 16, 32)
+WAVES = (1, 2, 4, 8, 16)
+SPLITS = (1, 2, 4)
+
+
+def _ring(kind: str, n: int, k: int, device) -> list[tuple]:
+    per = n * k * (2 if kind == "bf16" else 1)
+    count = max(2, min(64, RING_BYTES // per))
+    g = torch.Generator(device=device).manual_seed(n * 31 + k)
+    ring = []
+    for _ in range(count):
+        w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+        ring.append((w,) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16))
+    return ring
+
+
+def _time_cfg(ring, x, y, cfg, trials: int = 5) -> float:
+    """us per call: one graph holding one call per ring member."""
+    calls = [lambda a=a: S.skinny_mm(x, *a, out=y, cfg=cfg) for a in ring]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls[:2]:
+            c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    g.replay()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(trials):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b) * 1000.0 / len(calls))
+    del g
+    return statistics.median(out)
+
+
+def _supported(kind: str, bm: int, rows: int, waves: int) -> bool:
+    return bool(_lib.lib().bp_skinny_config_supported(S._KIND_CODE[kind], bm, rows, waves))
+
+
+def tune_shape(kind: str, n: int, k: int, device, quick: bool = False, log=print) -> dict:
+    ring = _ring(kind, n, k, device)
+    x16 = torch.randn(16, k, device=device).to(torch.bfloat16)
+    nch = -(-k // S._CHUNK[kind])
+    # 1. K order (waves, split) and rows at M = 1
+    x1 = x16[:1].contiguous()
+    y1 = torch.empty(1, n, dtype=torch.bfloat16, device=device)
+    best = None
+    results = {}
+    for waves in WAVES:
+        if waves > nch:
+            continue
+        for split in SPLITS:
+            if split > 1 and (split > nch // waves or quick):
+                continue
+            for rows in ROWS:
+                if not _supported(kind, 1, rows, waves):
+                    continue
+                us = _time_cfg(ring, x1, y1, (rows, waves, split))
+                results[(rows, waves, split)] = us
+                if best is None or us < best[0]:
+                    best = (us, rows, waves, split)
+    us1, rows1, waves, split = best
+    # keep split > 1 only if it wins by more than 3% over the best split-1 configuration
+    if split > 1:
+        no_split = min((v, r, w) for (r, w, s), v in results.items() if s == 1)
+        if no_split[0] <= us1 * 1.03:
+            us1, rows1, waves, split = no_split[0], no_split[1], no_split[2], 1
+    entry = {"waves": waves, "split": split, "rows": {"1": rows1}, "us": {"1": round(us1, 3)}}
+    log(f"  {kind} {n}x{k}: M=1 best rows={rows1} waves={waves} split={split}: {us1:.2f} us "
+        f"({(n * k * (2 if kind == 'bf16' else 1)) / us1 / 1e3:.0f} GB/s)")
+    # 2. rows for the other buckets at that K order
+    for bm in (2, 4, 8, 16):
+        xb = x16[:bm].contiguous()
+        yb = torch.empty(bm, n, dtype=torch.bfloat16, device=device)
+        cands = [(_time_cfg(ring, xb, yb, (r, waves, split)), r) for r in ROWS if _supported(kind, bm, r, waves)]
+        us_b, rows_b = min(cands)
+        entry["rows"][str(bm)] = rows_b
+        entry["us"][str(bm)] = round(us_b, 3)
+    log(f"    rows per bucket {entry['rows']} us {entry['us']}")
+    del ring
+    torch.cuda.empty_cache()
+    return entry
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--shapes", default=None, help="N:K,N:K,... (default: the decode-step set shapes)")
+    ap.add_argument("--kinds", default="bf16,int8")
+    ap.add_argument("--out", default=str(S._CFG_FILE))
+    ap.add_argument("--quick", action="store_true", help="no split-K candidates")
+    a = ap.parse_args(argv)
+    shapes = DEFAULT_SHAPES if a.shapes is None else [tuple(int(v) for v in s.split(":")) for s in a.shapes.split(",")]
+    device = torch.device("cuda:0")
+    out = Path(a.out)
+    table = json.loads(out.read_text()) if out.exists() else {}
+    table["_about"] = ("skinny kernel tile configurations for gfx950, tuned by python -m byteprof_amd.tune: "
+                       "key kind|N|K; waves and split fix the K order for every row bucket; rows per bucket; "
+                       "us = measured time per call (ring of distinct weights, HIP graph)")
+    for kind in a.kinds.split(","):
+        for n, k in shapes:
+            print(f"[tune] {kind} {n}x{k}", flush=True)
+            table[f"{kind}|{n}|{k}"] = tune_shape(kind, n, k, device, a.quick, log=lambda m: print(m, flush=True))
+            out.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")  # after every cell (resumable)
+    print(f"[tune] wrote {out}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
