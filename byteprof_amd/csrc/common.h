@@ -76,4 +76,23 @@ __device__ __forceinline__ void wave_transpose_reduce(float* v, int lane) {
   reduce_stage<(P > 32 ? P / 32 : 1), 1>(v, lane);
 }
 
+// Sum of v over the 64 lanes with DPP moves only (no LDS traffic): pairs within quads, quads within half-rows,
+// half-rows within rows of 16 (after which every lane of a row holds the row's sum), then rows 0..3 accumulated
+// into row 3 through row broadcasts. The order is fixed, so the result is deterministic; it is returned to every
+// lane (the value of lane 63).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f32<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp_f32<0x140, 0xF>(v);  // row_mirror
+  v += dpp_f32<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f32<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 }  // namespace bp

@@ -6,6 +6,12 @@ Infinity Cache, so nothing is served from cache across replays). Weights ~ N(0, 
 ~ N(0, 1) renormalised to unit RMS. The reference measures the same linears one call each inside a CUDA graph
 (byteprof tools/skinny_bench.py:45-71; FINDINGS "OLMo-2 16-block linear set").
 
+The same linears also run as one persistent launch (`build_chain`, optim/linear_set.py): stages q|k|v, o,
+gate|up, down per layer and the head, each stage's input the unit-RMS renormalisation of the output it depends on
+in a decode step (o <- v: attention over one cached position returns v; gate|up <- o; down <- up; the next
+layer's q|k|v and the head <- down), or, in the independent variant, a fresh unit-RMS vector per stage with no
+waits.
+
 Used by bench.py and by `python -m byteprof_amd.profiling`.
 """
 
@@ -17,6 +23,7 @@ from dataclasses import dataclass
 import torch
 
 from .optim import skinny as S
+from .optim.linear_set import LinearSet, Stage
 from .quant.accounting import Linear, call_bytes
 from .quant.hip_int8 import quantize_rowwise_int8
 
@@ -112,3 +119,86 @@ def kernel_key(kind: str, n: int, k: int, m: int) -> str:
     """Name of the kernel instantiation a launch uses, as the profiler reports it (template arguments)."""
     rows, waves, _ = S._resolve(kind, n, k, S._bm(m), None)
     return f"skinny_dot_kernel<{0 if kind == 'bf16' else 1}, {S._bm(m)}, {rows}, {waves}, true>"
+
+
+# stages of one layer: (stage name, linears sharing its input)
+LAYER_STAGES = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gateup", ("gate", "up")), ("down", ("down",)))
+
+
+@dataclass
+class Chain:
+    """The decode-step set as stages of one persistent launch."""
+
+    kind: str
+    stages: list
+    lset: LinearSet
+    weights: dict  # linear name -> (w,) or (q, scale)
+
+
+def make_weights(kind: str = "bf16", device="cuda:0", seed: int = 0, scale_dtype=torch.float16) -> dict:
+    """Seeded weights of the 113 linears, keyed by name (l{layer}.{q,k,v,o,gate,up,down}, lm_head)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = {}
+    for name, n, k in shapes():
+        w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+        out[name] = (w,) if kind == "bf16" else quantize_rowwise_int8(w, scale_dtype)
+        del w
+    return out
+
+
+def chain_stages(weights: dict, dependent: bool = True, device="cuda:0", seed: int = 1,
+                 record_inputs: bool = False) -> list:
+    """Stages of the set in decode order over `weights` (make_weights). dependent: each stage reads (renormalised)
+    the output it depends on in a decode step; otherwise each stage has its own unit-RMS input and no wait."""
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def fresh(k):
+        return unit_rms(torch.randn(1, k, generator=g, device=device))[0].contiguous()
+
+    kind = "bf16" if len(next(iter(weights.values()))) == 1 else "int8"
+    stages: list = []
+    prev = None  # (stage index, slice of its out) feeding the next qkv / head
+
+    def add(names, src, wait, renorm):
+        args = [weights[nm] for nm in names]
+        ws = [a[0] for a in args]
+        scales = [a[1] for a in args] if kind == "int8" else None
+        n = sum(int(w.shape[0]) for w in ws)
+        k = int(ws[0].shape[1])
+        out = torch.empty(n, dtype=torch.bfloat16, device=device)
+        xu = torch.empty(k, dtype=torch.bfloat16, device=device) if record_inputs else None
+        stages.append(Stage(ws, src, out, scales=scales, wait=wait, renorm=renorm, x_used=xu))
+        return len(stages) - 1
+
+    for layer in range(LAYERS):
+        pre = f"l{layer}."
+        if not dependent:
+            for _, names in LAYER_STAGES:
+                k = int(weights[pre + names[0]][0].shape[1])
+                add([pre + nm for nm in names], fresh(k), -1, False)
+            continue
+        src, wait = (fresh(HIDDEN), -1) if prev is None else (stages[prev].out, prev)
+        i_qkv = add([pre + "q", pre + "k", pre + "v"], src, wait, True)
+        i_o = add([pre + "o"], stages[i_qkv].out[2 * HIDDEN:3 * HIDDEN], i_qkv, True)
+        i_gu = add([pre + "gate", pre + "up"], stages[i_o].out, i_o, True)
+        prev = add([pre + "down"], stages[i_gu].out[FFN:2 * FFN], i_gu, True)
+    if dependent:
+        add(["lm_head"], stages[prev].out, prev, True)
+    else:
+        add(["lm_head"], fresh(HIDDEN), -1, False)
+    return stages
+
+
+def build_chain(kind: str = "bf16", device="cuda:0", seed: int = 0, scale_dtype=torch.float16,
+                dependent: bool = True, record_inputs: bool = False, weights: dict | None = None) -> Chain:
+    """The set as one persistent launch (weights from make_weights unless given)."""
+    weights = weights if weights is not None else make_weights(kind, device, seed, scale_dtype)
+    stages = chain_stages(weights, dependent, device, seed + 1, record_inputs)
+    return Chain(kind, stages, LinearSet(stages), weights)
+
+
+def chain_bytes(kind: str) -> int:
+    """Algorithmic bytes of one pass of the set at M = 1 (every linear's weights, scales, input and output once;
+    the same total as the per-launch set)."""
+    scheme = None if kind == "bf16" else "int8_wo"
+    return int(sum(call_bytes(Linear(n, k), scheme, 1) for _, n, k in shapes()))

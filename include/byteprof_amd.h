@@ -114,6 +114,60 @@ int bp_mlstm_multistep(const void* c, const void* n, const void* m,
                        int64_t str_t_qk, int64_t str_t_v, int64_t str_t_if, int64_t str_t_h,
                        int io_dtype, int gate_dtype, float qk_scale, float eps, int bv, void* stream);
 
+/*
+ * Decode-step linear set: a chain of skinny linears at one activation row run by one persistent launch.
+ *
+ * A stage is one or more linears sharing one input vector (q|k|v, gate|up, or a single linear). Its rows are the
+ * concatenation of its weight segments; its output y is the concatenation of their outputs. A stage may read its
+ * input from an earlier stage's output (wait_stage >= 0: it reads each of those rows once the workgroup that
+ * computes it has published it), optionally renormalised to unit RMS: x = bf16(src * (1 / sqrt(mean(src^2)))), with fp32
+ * arithmetic (an all-zero src is used unscaled). Each row is computed as the skinny kernels compute it (fp32
+ * accumulation of bf16 or exact int8 -> bf16 pairs, int8 scale on the fp32 sum, bf16 round to nearest even).
+ *
+ * Layout (128 bytes, 8-byte aligned pointers): the array lives in device memory for the kernel, and a host copy
+ * with the same contents is passed for validation.
+ */
+typedef struct BpSetStage {
+  const void* src;      /* bf16 [K], 16-byte aligned: the input (external, or a slice of an earlier stage's y) */
+  void* y;              /* bf16 [N], 16-byte aligned: the stage's outputs */
+  void* x_used;         /* bf16 [K] or NULL: receives the input vector the stage used (after renormalisation) */
+  int32_t K;            /* input length: a multiple of 512 (bf16 weights) or 1024 (int8), at most 8192 */
+  int32_t N;            /* rows: at most (2048 - 1) * workgroups */
+  int32_t wait_stage;   /* -1, or the index (< this stage's) of the stage whose outputs src reads (src must then
+                           lie inside that stage's y) */
+  int32_t renorm;       /* 1: renormalise the input to unit RMS; 0: use it as is */
+  int32_t nseg;         /* weight segments, 1..4 */
+  int32_t seg_end[4];   /* cumulative row ends of the segments; seg_end[nseg - 1] == N */
+  int32_t reserved;
+  const void* w[4];     /* segment weights [rows, K] row-major, 16-byte aligned (bf16 or int8) */
+  const void* scale[4]; /* int8: per-row scales of each segment (dtype given to bp_linear_set_run) */
+} BpSetStage;
+
+/* Bytes of scratch a launch of these stages needs: a launch counter, an error flag and every stage's outputs
+ * tagged with the launch (4 bytes per row, rows rounded up to 8). num_workgroups is accepted for future layouts.
+ * The scratch must be zero before its first launch and is then reused as is by every later launch (no reset
+ * between launches or graph replays). The 32-bit word at index 32 becomes non-zero if a launch gave up waiting
+ * for another workgroup (that launch's later results are invalid); the host clears it. */
+size_t bp_linear_set_scratch_bytes(const BpSetStage* stages, int num_stages, int num_workgroups);
+
+/* Workgroups the set kernel is launched with on `device`: one per compute unit (0 on error). */
+int bp_linear_set_workgroups(int device);
+
+/* Checks a host array of stages against the kernel's limits; BP_OK or a BP_E_* code. */
+int bp_linear_set_validate(const BpSetStage* stages, int num_stages, int wkind, int num_workgroups);
+
+/*
+ * Runs the set: one launch of num_workgroups workgroups (use bp_linear_set_workgroups) on `stream`.
+ * wkind: BP_DT_BF16 (0) bf16 weights or 1 int8 weights (scale_dtype BP_DT_BF16 / BP_DT_F16 / BP_DT_F32).
+ * host_stages is validated; dev_stages must hold the same array in device memory. Calls on one scratch must not
+ * overlap (they are ordered on one stream or a captured graph).
+ * Replaces: per-token replays of the decode-step linears, each a skinny_mm / SkinnyLinear.forward call
+ *           (byteprof/optim/skinny_linear.py:56-69 -> byteprof/optim/skinny.py:136-166) captured in the decode
+ *           graph (byteprof/optim/olmo.py:164-174); the per-row arithmetic is skinny.py:36-90's.
+ */
+int bp_linear_set_run(int wkind, int scale_dtype, const BpSetStage* host_stages, const void* dev_stages,
+                      int num_stages, void* scratch, size_t scratch_bytes, int num_workgroups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

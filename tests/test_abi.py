@@ -28,7 +28,9 @@ def L():
 def test_header_declares_the_expected_entry_points():
     names = declared_functions()
     for required in ("bp_skinny_bf16", "bp_skinny_int8", "bp_gemv_int8", "bp_splitk_reduce", "bp_mlstm_multistep",
-                     "bp_skinny_workspace_bytes", "bp_skinny_config_supported", "bp_version", "bp_status_string"):
+                     "bp_skinny_workspace_bytes", "bp_skinny_config_supported", "bp_version", "bp_status_string",
+                     "bp_linear_set_run", "bp_linear_set_validate", "bp_linear_set_scratch_bytes",
+                     "bp_linear_set_workgroups"):
         assert required in names
 
 
@@ -91,3 +93,65 @@ def test_invalid_arguments_are_rejected_before_any_launch(L):
     assert L.bp_mlstm_multistep(*args, 4, 2, 64, 16, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 5, None) == -2
     assert L.bp_mlstm_multistep(*args, 4, 2, 64, 12, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 8, None) == -2
     assert L.bp_mlstm_multistep(*args, 4, 0, 64, 16, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 8, None) == 0  # NH = 0: no-op
+
+
+def _set_stages(n_stages=2, k=2048, n=4096, kind=0):
+    from byteprof_amd.optim.linear_set import BpSetStage
+
+    arr = (BpSetStage * n_stages)()
+    for i, h in enumerate(arr):
+        h.src, h.y, h.x_used = (0x1000 if i == 0 else 0x2000), 0x2000, None
+        h.K, h.N, h.wait_stage, h.renorm, h.nseg = k, n, i - 1, 1, 1
+        h.seg_end[0] = n
+        h.w[0] = 0x3000
+        h.scale[0] = 0x4000 if kind == 1 else None
+    return arr
+
+
+def test_linear_set_descriptor_layout_matches_the_header():
+    from byteprof_amd.optim.linear_set import BpSetStage
+
+    text = HEADER.read_text()
+    body = text[text.index("typedef struct BpSetStage"):text.index("} BpSetStage;")]
+    fields = re.findall(r"^\s+[a-z_0-9 ]+?\*?\s*([a-z_A-Z]+)(?:\[\d\])?;", body, flags=re.M)
+    assert fields == [f[0] for f in BpSetStage._fields_]
+    assert ctypes.sizeof(BpSetStage) == 128
+
+
+def test_linear_set_validation_rejects_bad_descriptors(L):
+    """bp_linear_set_validate reads only the host descriptors: no GPU needed (the pointers are never used)."""
+    def rc(arr, kind=0, groups=256, n=None):
+        return L.bp_linear_set_validate(ctypes.addressof(arr), len(arr) if n is None else n, kind, groups)
+
+    assert rc(_set_stages()) == 0
+    assert rc(_set_stages(kind=1), kind=1) == 0
+    assert rc(_set_stages(), n=0) == -1                      # no stages
+    assert rc(_set_stages(), kind=2) == -2                   # unknown weight kind
+    assert rc(_set_stages(k=1000)) == -2                     # K not a multiple of the 512-element chunk
+    assert rc(_set_stages(k=1536), kind=1) == -2             # int8: K a multiple of 1024
+    assert rc(_set_stages(k=16384)) == -2                    # input longer than the LDS buffer
+    assert rc(_set_stages(n=2048 * 256)) == -2               # more rows per workgroup than LDS holds
+    assert rc(_set_stages(kind=0), kind=1) == -1             # int8 without scales
+    bad = _set_stages()
+    bad[1].wait_stage = 1                                    # a stage cannot wait for itself
+    assert rc(bad) == -1
+    bad = _set_stages()
+    bad[0].seg_end[0] = 100                                  # segments must cover N
+    assert rc(bad) == -1
+    bad = _set_stages()
+    bad[0].src = 0x1008                                      # inputs must be 16-byte aligned
+    assert rc(bad) == -1
+    bad = _set_stages()
+    bad[0].nseg = 5
+    assert rc(bad) == -1
+    assert rc(_set_stages(n_stages=300)) == -2               # more stages than the LDS row table holds
+    bad = _set_stages()
+    bad[1].src = 0x2000 + 2 * 4096 - 16                      # a dependent input must lie inside its source's y
+    assert rc(bad) == -1
+    bad = _set_stages()
+    bad[0].y = 0x2008                                        # outputs must be 16-byte aligned
+    assert rc(bad) == -1
+    arr = _set_stages(n_stages=3, n=4093)
+    # launch counter + error flag lines, 3 x (4093 rounded up to 8) tagged words
+    assert L.bp_linear_set_scratch_bytes(ctypes.addressof(arr), 3, 256) == 4 * (64 + 3 * 4096)
+    assert L.bp_linear_set_scratch_bytes(None, 0, 256) == 0

@@ -240,3 +240,55 @@ def test_bf16_of_torch_matches_the_oracle_rounding():
     """torch's .to(bfloat16) (what every drop-in output is compared in) rounds like the oracle."""
     x = torch.randn(5000) * 10
     assert np.array_equal(x.to(torch.bfloat16).float().numpy(), ON.bf16_round(x.numpy()))
+
+
+def test_linear_set_host_validation():
+    """LinearSet checks shapes, dtypes and dependencies before touching the GPU (CPU tensors here)."""
+    from byteprof_amd.optim.linear_set import LinearSet, Stage
+
+    w = torch.zeros(8, 512, dtype=torch.bfloat16)
+    x = torch.zeros(512, dtype=torch.bfloat16)
+    out = torch.zeros(8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="at least one stage"):
+        LinearSet([])
+    with pytest.raises(ValueError, match="unsupported weight dtype"):
+        LinearSet([Stage([w.float()], x, out)])
+    with pytest.raises(ValueError, match="multiple of 512"):
+        LinearSet([Stage([torch.zeros(8, 100, dtype=torch.bfloat16)], torch.zeros(100, dtype=torch.bfloat16), out)])
+    with pytest.raises(ValueError, match="multiple of 1024"):
+        LinearSet([Stage([torch.zeros(8, 512, dtype=torch.int8)], x, out, scales=[torch.ones(8)])])
+    with pytest.raises(ValueError, match="need one scale"):
+        LinearSet([Stage([torch.zeros(8, 1024, dtype=torch.int8)], torch.zeros(1024, dtype=torch.bfloat16), out)])
+    with pytest.raises(ValueError, match="src must be"):
+        LinearSet([Stage([w], x[:100], out)])
+    with pytest.raises(ValueError, match="out must be"):
+        LinearSet([Stage([w], x, out[:4])])
+    with pytest.raises(ValueError, match="earlier stage"):
+        LinearSet([Stage([w], x, out, wait=0)])
+    with pytest.raises(ValueError, match="inside stage 0"):
+        LinearSet([Stage([w], x, out), Stage([torch.zeros(4, 512, dtype=torch.bfloat16)], x, out[:4], wait=0)])
+    with pytest.raises(ValueError, match="1..4 weights"):
+        LinearSet([Stage([w] * 5, x, torch.zeros(40, dtype=torch.bfloat16))])
+    with pytest.raises(ValueError, match="runs on a GPU"):
+        LinearSet([Stage([w], x, out)])
+
+
+def test_decode_chain_structure():
+    """The decode-step chain on CPU tensors (structure only): 65 stages, each dependent stage reading the output
+    a decode step feeds it, and the same byte total as the per-launch set."""
+    from byteprof_amd import decode_set as D
+
+    weights = {name: (torch.zeros(n, k, dtype=torch.bfloat16),) for name, n, k in D.shapes()}
+    stages = D.chain_stages(weights, dependent=True, device="cpu")
+    assert len(stages) == 65
+    assert stages[0].wait == -1
+    for i, st in enumerate(stages[1:], start=1):
+        assert st.wait == i - 1 and st.renorm
+    o = stages[1]  # o reads v: rows 4096..6143 of q|k|v
+    assert o.src.data_ptr() == stages[0].out.data_ptr() + 2 * 2 * 2048
+    down = stages[3]  # down reads up: rows 8192..16383 of gate|up
+    assert down.src.data_ptr() == stages[2].out.data_ptr() + 2 * 8192 and down.k == 8192
+    assert stages[-1].n == 100352 and stages[-1].src.data_ptr() == stages[-2].out.data_ptr()
+    ind = D.chain_stages(weights, dependent=False, device="cpu")
+    assert len(ind) == 65 and all(st.wait == -1 for st in ind)
+    assert D.chain_bytes("bf16") == 2_560_237_568 and D.chain_bytes("int8") == 1_282_027_520

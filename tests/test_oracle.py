@@ -12,6 +12,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+from oracle import linear_set as OL
 from oracle import mlstm as OM
 from oracle import numerics as ON
 from oracle import skinny as OS
@@ -227,3 +228,45 @@ def test_error_metrics():
     x = np.array([[1.0, -1.0]])
     w = np.array([[1.0, 1.0]])  # exact output 0 (cancelling): componentwise error normalises by |x||w| = 2
     assert ON.componentwise_error(np.array([[0.01]]), x, w) == pytest.approx(0.005)
+
+
+# ---- decode-step set oracle -------------------------------------------------------------------------------------
+
+
+def test_unit_rms_of_a_constant_vector_is_all_ones():
+    # mean(c^2) = c^2 exactly, sqrt = |c|: a dropped mean or square root would give sqrt(K) or c instead of 1
+    for c in (0.375, -3.0, 17.0):
+        out = OL.unit_rms(np.full(2048, c, np.float32))
+        assert np.all(out == np.sign(c))
+
+
+def test_unit_rms_is_invariant_to_power_of_two_scaling():
+    rng = np.random.default_rng(7)
+    x = ON.bf16_round(rng.standard_normal(4096).astype(np.float32))
+    base = OL.unit_rms(x)
+    for e in (-20, -3, 5, 30):
+        assert np.array_equal(OL.unit_rms(x * np.float32(2.0 ** e)), base)
+
+
+def test_unit_rms_output_has_unit_mean_square_and_zero_stays_zero():
+    rng = np.random.default_rng(8)
+    x = ON.bf16_round((rng.standard_normal(8192) * 40).astype(np.float32))
+    out = OL.unit_rms(x)
+    assert abs(float(np.mean(out.astype(np.float64) ** 2)) - 1.0) < 2.0 ** -7
+    assert np.array_equal(ON.bf16_round(out), out)  # bf16 values
+    assert np.all(OL.unit_rms(np.zeros(512, np.float32)) == 0)
+
+
+def test_chain_second_stage_reads_the_first_stage_output():
+    """Two stages by hand: stage 1 reads stage 0's outputs 2..5 renormalised; K = 4, exact small integers."""
+    w0 = np.array([[1, 0, 0, 0], [0, 1, 0, 0], [1, 1, 0, 0], [0, 0, 1, 1], [2, 0, 0, 2], [0, 0, 0, 1]], np.float32)
+    w1 = np.array([[1, 1, 1, 1]], np.float32)
+    x0 = np.array([1, 2, 3, 4], np.float32)
+    st0 = OL.OracleStage([w0], ("ext", x0), renorm=False)
+    st1 = OL.OracleStage([w1], ("stage", 0, 2), renorm=True)
+    xs, ys = OL.chain([st0, st1])
+    assert np.array_equal(ys[0], [1, 2, 3, 7, 10, 4])
+    # stage 1 input: unit_rms([3, 7, 10, 4]) = [3, 7, 10, 4] / sqrt(174 / 4)
+    expect = ON.bf16_round(np.array([3, 7, 10, 4], np.float32) * np.float32(1.0 / np.sqrt(43.5)))
+    assert np.array_equal(xs[1], expect)
+    assert np.array_equal(ys[1], ON.bf16_round(np.array([expect.astype(np.float64).sum()], np.float32)))
