@@ -6,23 +6,22 @@
 // a launch's fixed cost and HBM idles while a small launch ramps up and drains. This kernel runs the whole chain
 // in one launch on one workgroup per CU and keeps the weight stream going across stage boundaries:
 //
-//   - compute waves (kSetCW per workgroup) own whole weight rows of every stage and stream them in 1 KiB
-//     wave-wide chunks (16-byte non-temporal loads per lane) through a register ring of kSetRing chunks, so
-//     kSetRing chunks per wave are in flight. Loads do not depend on activations, so a wave keeps
-//     loading the next stage's rows while the stage's input is still being produced elsewhere on the chip;
+//   - consumer waves (kSetCW per workgroup) own whole weight rows of every stage; each has a producer wave that
+//     streams its rows in 1 KiB wave-wide chunks into an LDS ring (LDS-DMA loads, non-temporal). Loads do not
+//     depend on activations, so the producers keep loading the next stage's rows while the stage's input is still
+//     being produced elsewhere on the chip, and only they stall when the CU's outstanding loads are at capacity:
+//     once a stage's input arrives, the consumers work through the landed ring at LDS speed;
 //   - one sync wave per workgroup does all the cross-workgroup work, so the compute waves never wait for their
 //     own outstanding loads: it gathers the stage's input vector into LDS (optionally renormalised to unit RMS)
-//     and publishes the workgroup's results of the stage. Results travel as 32-bit words holding the bf16 value
-//     and a per-launch tag, written and read with device-coherent (sc1) accesses: a reader that sees the current
-//     tag in a word has its value, so publishing needs no release fence (an L2 writeback per workgroup and stage
-//     costs more than the stage) and reading no acquire; a reader gathers its slice with LDS-DMA loads and waits
-//     only for the rows it reads;
+//     and publishes the workgroup's results of the stage with device-coherent (sc1) stores and a per-workgroup
+//     flag; readers poll the flags of the workgroups whose rows they read, then copy the rows into LDS with
+//     device-scope LDS-DMA loads;
 //   - inside the workgroup, LDS flags hand the input (xready) to the compute waves and the results (ydone)
 //     back to the sync wave. Every wait is bounded: past a cap of polls the wave records an error flag in the
 //     scratch words and stops waiting, so a launch always finishes.
 //
 // Nothing is reset between launches: launch g (counted by a launch counter every workgroup increments at the end)
-// tags its words g % 65535 + 1, so the kernel can be replayed in a HIP graph with no memset. Per-row arithmetic matches the skinny kernels: bf16 (or
+// sets its flags to g + 1, so the kernel can be replayed in a HIP graph with no memset. Per-row arithmetic matches the skinny kernels: bf16 (or
 // exact int8 -> bf16) pairs through v_dot2_f32_bf16 into fp32, a fixed wave butterfly, the int8 scale on the fp32
 // sum, round-to-nearest-even to bf16.
 //
@@ -45,30 +44,45 @@ namespace {
 typedef const BP_CONST BpSetStage* StageTable;
 typedef const BP_GLOBAL u32x4* GlobalVec;
 
-constexpr int kSetCW = 8;                           // compute waves per workgroup
-constexpr int kSetThreads = (kSetCW + 1) * kWave;   // + one sync wave
+constexpr int kSetCW = 4;                           // consumer waves per workgroup
+constexpr int kSetPW = kSetCW;                      // producer waves: one per consumer
+constexpr int kSetSyncWave = kSetCW + kSetPW;       // index of the sync wave
+constexpr int kSetThreads = (kSetSyncWave + 1) * kWave;
 constexpr int kSetKMax = 8192;                      // longest input vector (two bf16 buffers in LDS)
-constexpr int kSetRowsMax = 2048;                   // rows of one stage per workgroup (fp32 results in LDS)
-constexpr int kSetStagesMax = 256;                  // stages per set (row table in LDS)
-constexpr int kSetRing = 32;                        // 1 KiB weight chunks in flight per compute wave
+constexpr int kSetRowsMax = 1024;                   // rows of one stage per workgroup (fp32 results in LDS)
+constexpr int kSetStagesMax = 128;                  // stages per set (row table in LDS)
+constexpr int kSetSlots = 26;                       // 1 KiB LDS ring slots per consumer
+constexpr int kSetLag = 12;                         // loads a producer keeps in flight before publishing them
+constexpr int kSetPublish = 8;                      // chunks between two publications of the landed count
+#ifndef BP_PUBMODE
+#define BP_PUBMODE 16
+#endif
 constexpr int kCtrWords = 32;                       // one 128-byte line per counter
-constexpr uint32_t kSpinCapGlobal = 1u << 20;       // polls of a global counter before a wait gives up (~1 s)
-constexpr uint32_t kSpinCapLds = 1u << 24;          // polls of an LDS flag before a wait gives up (~1 s)
+constexpr uint32_t kSpinCapGlobal = 1u << 20;       // polls of a global word before a wait gives up (~1 s)
+constexpr uint32_t kSpinCapLds = 1u << 24;          // polls of an LDS word before a wait gives up (~1 s)
 
 struct SetLds {
+  alignas(16) uint8_t ring[kSetCW][kSetSlots][1024];  // weight chunks: producer i fills ring[i], consumer i drains it
   uint16_t x[2][kSetKMax];                // the stage's input vector, by stage parity
-  uint32_t tin[kSetKMax];                 // tagged input words as gathered from the producing stage
   float y[2][kSetRowsMax];                // the workgroup's fp32 row sums, by stage parity
   float scale[2][kSetRowsMax];            // int8: the workgroup's row scales, by stage parity
-  int32_t rows[kSetStagesMax][kSetCW + 1];  // stage s: wave i of this workgroup owns rows [rows[s][i], rows[s][i+1])
-  int32_t tag_off[kSetStagesMax];         // word offset of stage s's tagged outputs in the scratch
+  int32_t rows[kSetStagesMax][kSetCW + 1];  // stage s: consumer i of this workgroup owns rows [rows[s][i], rows[s][i+1])
+  int landed[kSetCW];                     // chunks of consumer i's stream in its ring (producer -> consumer)
+  int consumed[kSetCW];                   // chunks consumer i has read out of its ring (consumer -> producer)
   int xready;                             // stage s's input is in x[s & 1] once xready > s
-  int ydone[2];                           // compute waves done with the stage of that parity
+  int ydone[2];                           // consumer waves done with the stage of that parity
 };
 // More than half of the CU's 160 KiB of LDS: exactly one workgroup per CU, so the grid of one workgroup per CU is
 // resident at once (the cross-workgroup waits rely on it).
 static_assert(sizeof(SetLds) > 80 * 1024, "the set kernel must own its CU's LDS");
 static_assert(sizeof(SetLds) <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
+
+// s_waitcnt immediate that waits for at most N vector memory operations in flight (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+constexpr int waitcnt_vm() {
+  return (N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
 
 __device__ __forceinline__ int lds_load_relaxed(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -76,29 +90,23 @@ __device__ __forceinline__ int lds_load_relaxed(const int* p) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// Weight-chunk stream of one compute wave: its rows of every stage in stage order, each row in 1 KiB chunks.
-// Every issue slot loads: once the stream has ended, slots re-read a valid chunk (`idle`) that nobody consumes,
-// so the number of loads in flight is the same on every path and the compiler's wait counts stay exact.
+// Weight-chunk stream of one consumer: its rows of every stage in stage order, each row in 1 KiB chunks.
 template <int KIND>
-struct Producer {
+struct Cursor {
   int s;              // current stage (S: stream ended)
-  int r, r1;          // current row, end of this wave's rows
+  int r, r1;          // current row, end of the consumer's rows
   int c, C;           // chunk of the row, chunks per row
   int seg, seg_end;
-  const BP_GLOBAL uint8_t* p;      // next chunk
-  const BP_GLOBAL uint8_t* idle;   // a readable chunk for slots past the end
+  const BP_GLOBAL uint8_t* p;  // next chunk
   int row_bytes;
 
-  __device__ __forceinline__ void enter(StageTable st, const SetLds& L, int S, int wave, int from) {
+  __device__ __forceinline__ void enter(StageTable st, const SetLds& L, int S, int who, int from) {
     for (s = from; s < S; ++s) {
-      r = uniform(L.rows[s][wave]);
-      r1 = uniform(L.rows[s][wave + 1]);
+      r = uniform(L.rows[s][who]);
+      r1 = uniform(L.rows[s][who + 1]);
       if (r < r1) break;
     }
-    if (s >= S) {
-      p = idle;
-      return;
-    }
+    if (s >= S) return;
     row_bytes = st[s].K * Layout<KIND>::kElemBytes;
     C = row_bytes >> 10;
     c = 0;
@@ -109,57 +117,89 @@ struct Producer {
     p = (const BP_GLOBAL uint8_t*)(st[s].w[seg]) + static_cast<int64_t>(r - seg_begin) * row_bytes;
   }
 
-  __device__ __forceinline__ void advance(StageTable st, const SetLds& L, int S, int wave) {
-    if (s >= S) return;
+  __device__ __forceinline__ void advance(StageTable st, const SetLds& L, int S, int who) {
     p += 1024;
     if (++c < C) return;
     c = 0;
     if (++r == r1) {
-      enter(st, L, S, wave, s + 1);
+      enter(st, L, S, who, s + 1);
     } else if (r == seg_end) {
       ++seg;
       seg_end = st[s].seg_end[seg];
       p = (const BP_GLOBAL uint8_t*)(st[s].w[seg]);
     }
   }
-
-  __device__ __forceinline__ u32x4 issue(StageTable st, const SetLds& L, int S, int wave, int lane) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<GlobalVec>(p + lane * 16));
-    advance(st, L, S, wave);
-    return v;
-  }
 };
 
-// Same chunks, same order, consumed: dot products against the stage input in LDS, one wave sum per row. The LDS
-// chunk of the next item is read one item ahead. A wave visits only the stages where it owns rows; the sync wave
-// counts those waves per stage.
+// Cache policy of the weight stream: nt (streamed once, not kept in the caches).
+constexpr int kStreamPolicy = 2;
+
+// Producer wave i: copies consumer i's chunks into its LDS ring with LDS-DMA loads (global_load_lds_dwordx4,
+// 1 KiB per wave instruction, no registers). A load instruction stalls its wave while the CU's outstanding requests
+// are at capacity; only this wave stalls, so the consumer keeps reading landed chunks at LDS speed. Loads complete
+// in order: after each load the producer waits until at most kSetLag are in flight and publishes the count that
+// has landed. When the ring is full (its consumer is waiting for a stage's input) it publishes everything and
+// waits for a free slot, so a consumer that resumes finds the whole ring landed.
+template <int KIND>
+__device__ __forceinline__ void producer_wave(StageTable st, SetLds& L, int S, int who, int lane) {
+  Cursor<KIND> cur;
+  cur.enter(st, L, S, who, 0);
+  int n = 0, limit = kSetSlots;  // chunks issued; chunks that fit the ring as last seen
+  bool failed = false;
+  while (cur.s < S) {
+    if (n >= limit) {  // ring full as last seen: publish everything, then wait for the consumer
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
+      if (lane == 0) __hip_atomic_store(&L.landed[who], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      uint32_t it = 0;
+      while (!failed && n >= (limit = lds_load_relaxed(&L.consumed[who]) + kSetSlots)) {
+        if (++it > kSpinCapLds) failed = true;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (failed) break;
+    }
+    __builtin_amdgcn_global_load_lds((const BP_GLOBAL void*)(cur.p + lane * 16),
+                                     (BP_LDS void*)&L.ring[who][n % kSetSlots][0], 16, 0, kStreamPolicy);
+    cur.advance(st, L, S, who);
+    ++n;
+#if BP_PUBMODE == 0
+    if (n > kSetLag) __builtin_amdgcn_s_waitcnt(waitcnt_vm<kSetLag>());
+    // An LDS access of this wave waits for the LDS writes of its loads in flight, so the producer touches LDS
+    // every kSetPublish chunks only: it publishes what has landed and refreshes its view of the consumer.
+    if (n % kSetPublish == 0) {
+      if (lane == 0 && n > kSetLag)
+        __hip_atomic_store(&L.landed[who], n - kSetLag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      limit = lds_load_relaxed(&L.consumed[who]) + kSetSlots;
+    }
+#else
+    if (n % BP_PUBMODE == 0) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
+      if (lane == 0) __hip_atomic_store(&L.landed[who], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      limit = lds_load_relaxed(&L.consumed[who]) + kSetSlots;
+    }
+#endif
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
+  if (lane == 0) __hip_atomic_store(&L.landed[who], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Consumer wave i: the same chunks in the same order, read from its LDS ring once landed: dot products against
+// the stage input in LDS, one wave sum per row. Chunks are taken in groups of GS of one row (GS divides the
+// chunks per row): one poll of the landed count, all of the group's LDS reads in flight together, one release of
+// its ring slots. A consumer visits only the stages where it owns rows; the sync wave counts those per stage.
 template <int KIND>
 struct Consumer {
   int s;
-  int r, r1, row0;    // current row, end of this wave's rows, the workgroup's first row of the stage
+  int r, r1, row0;    // current row, end of this consumer's rows, the workgroup's first row of the stage
   int c, C;
+  int n, seen;        // chunks consumed; chunks known to have landed
   float acc;
   bool failed;
-  uint32_t xn[Layout<KIND>::kXDwords];  // input chunk of the current item
 
-  __device__ __forceinline__ void load_x(const SetLds& L, int lane) {
-    using Lay = Layout<KIND>;
-    const u32x4* xs = reinterpret_cast<const u32x4*>(&L.x[s & 1][c * Lay::kChunk + lane * Lay::kEpl]);
-#pragma unroll
-    for (int q = 0; q < Lay::kXDwords / 4; ++q) {
-      const u32x4 t = xs[q];
-      xn[4 * q + 0] = t.x;
-      xn[4 * q + 1] = t.y;
-      xn[4 * q + 2] = t.z;
-      xn[4 * q + 3] = t.w;
-    }
-  }
-
-  // Moves to stage `from` or the next one with rows for this wave and waits (bounded) for its input in LDS.
-  __device__ __forceinline__ void enter(StageTable st, SetLds& L, int S, int wave, int lane, int from) {
+  // Moves to stage `from` or the next one with rows for this consumer and waits (bounded) for its input in LDS.
+  __device__ __forceinline__ void enter(StageTable st, SetLds& L, int S, int who, int from) {
     for (s = from; s < S; ++s) {
-      r = uniform(L.rows[s][wave]);
-      r1 = uniform(L.rows[s][wave + 1]);
+      r = uniform(L.rows[s][who]);
+      r1 = uniform(L.rows[s][who + 1]);
       if (r < r1) break;
     }
     if (s >= S) return;
@@ -173,14 +213,48 @@ struct Consumer {
       __builtin_amdgcn_s_sleep(1);
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    load_x(L, lane);
   }
 
-  // Consumes one chunk (the stream's next item); false once every stage is done.
-  __device__ __forceinline__ bool consume(const u32x4& wv, StageTable st, SetLds& L, int S, int wave, int lane) {
-    if (s >= S) return false;
-    acc = chunk_dot<KIND>(wv, xn, acc);
-    if (++c == C) {
+  // GS chunks of the current row. RESIDENT: the row is exactly these GS chunks and xr already holds the stage's
+  // input chunks (loaded once per stage), so only the weights are read from LDS.
+  template <int GS, bool RESIDENT>
+  __device__ __forceinline__ void group(StageTable st, SetLds& L, int S, int who, int lane,
+                                        uint32_t (&xr)[4][Layout<KIND>::kXDwords]) {
+    using Lay = Layout<KIND>;
+    uint32_t it = 0;
+    while (seen < n + GS && !failed) {
+      seen = lds_load_relaxed(&L.landed[who]);
+      if (seen >= n + GS) break;
+      if (++it > kSpinCapLds) failed = true;
+      __builtin_amdgcn_s_sleep(0);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    u32x4 w[GS];
+    uint32_t xv[GS][Lay::kXDwords];
+    int slot = n % kSetSlots;
+#pragma unroll
+    for (int j = 0; j < GS; ++j) {
+      w[j] = *reinterpret_cast<const u32x4*>(&L.ring[who][slot][lane * 16]);
+      slot = slot + 1 == kSetSlots ? 0 : slot + 1;
+      if constexpr (!RESIDENT) {
+        const u32x4* xs = reinterpret_cast<const u32x4*>(&L.x[s & 1][(c + j) * Lay::kChunk + lane * Lay::kEpl]);
+#pragma unroll
+        for (int q = 0; q < Lay::kXDwords / 4; ++q) {
+          const u32x4 t = xs[q];
+          xv[j][4 * q + 0] = t.x;
+          xv[j][4 * q + 1] = t.y;
+          xv[j][4 * q + 2] = t.z;
+          xv[j][4 * q + 3] = t.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < GS; ++j) acc = chunk_dot<KIND>(w[j], RESIDENT ? xr[j] : xv[j], acc);
+    n += GS;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane == 0) __hip_atomic_store(&L.consumed[who], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    c += GS;
+    if (c == C) {
       const float tot = wave_sum_dpp(acc);
       if (lane == 0) L.y[s & 1][r - row0] = tot;
       acc = 0.f;
@@ -188,27 +262,63 @@ struct Consumer {
       if (++r == r1) {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if (lane == 0) __hip_atomic_fetch_add(&L.ydone[s & 1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        enter(st, L, S, wave, lane, s + 1);
-        return true;
+        enter(st, L, S, who, s + 1);
       }
     }
-    load_x(L, lane);
-    return true;
+  }
+
+  __device__ __forceinline__ void run(StageTable st, SetLds& L, int S, int who, int lane) {
+    using Lay = Layout<KIND>;
+    uint32_t xr[4][Lay::kXDwords];
+    enter(st, L, S, who, 0);
+    while (s < S) {
+      if (C == 4 || C == 2) {  // whole rows per group: the stage's input chunks stay in registers
+        const int stage = s;
+        for (int j = 0; j < C; ++j) {
+          const u32x4* xs = reinterpret_cast<const u32x4*>(&L.x[s & 1][j * Lay::kChunk + lane * Lay::kEpl]);
+#pragma unroll
+          for (int q = 0; q < Lay::kXDwords / 4; ++q) {
+            const u32x4 t = xs[q];
+            // static register index: j is 0..3 (unrolled by the select below)
+            if (j == 0) { xr[0][4 * q + 0] = t.x; xr[0][4 * q + 1] = t.y; xr[0][4 * q + 2] = t.z; xr[0][4 * q + 3] = t.w; }
+            if (j == 1) { xr[1][4 * q + 0] = t.x; xr[1][4 * q + 1] = t.y; xr[1][4 * q + 2] = t.z; xr[1][4 * q + 3] = t.w; }
+            if (j == 2) { xr[2][4 * q + 0] = t.x; xr[2][4 * q + 1] = t.y; xr[2][4 * q + 2] = t.z; xr[2][4 * q + 3] = t.w; }
+            if (j == 3) { xr[3][4 * q + 0] = t.x; xr[3][4 * q + 1] = t.y; xr[3][4 * q + 2] = t.z; xr[3][4 * q + 3] = t.w; }
+          }
+        }
+        if (C == 4) {
+          while (s == stage) group<4, true>(st, L, S, who, lane, xr);
+        } else {
+          while (s == stage) group<2, true>(st, L, S, who, lane, xr);
+        }
+      } else if ((C & 3) == 0) {
+        group<4, false>(st, L, S, who, lane, xr);
+      } else if ((C & 1) == 0) {
+        group<2, false>(st, L, S, who, lane, xr);
+      } else {
+        group<1, false>(st, L, S, who, lane, xr);
+      }
+    }
   }
 };
 
 // Scratch words: [0] launch counter (every workgroup adds 1 at the end of a launch), [kErrWord] error flag, then
-// the tagged outputs of every stage (stage s at kTagWord + tag_off[s], N rounded up to 8 words): the bf16 bits in
-// the low half, the launch's tag in the high half. A 32-bit store is seen whole or not at all, so a reader that
-// finds the current launch's tag in a word has that launch's value: no fence, counter or flag is needed, and a
-// reader waits only for the rows it reads.
+// S x G publish flags from kFlagWord: flag[s][g] = the launch's tag once workgroup g's rows of stage s are visible
+// device-wide. A producer stores its rows with device-scope (sc1, write-through) stores, waits until they are
+// acknowledged, then stores its flag; a reader polls the flags of the workgroups that produce the rows it reads
+// (one word each, all of a poll's loads in flight together) and then reads the rows with device-scope loads. Both
+// sides use device-coherent accesses for the rows, so no L2 writeback or invalidate is needed (a release fence
+// per workgroup and stage costs more than a stage), and a reader waits only for the rows it reads.
 constexpr int kErrWord = kCtrWords;
-constexpr int kTagWord = 2 * kCtrWords;
+constexpr int kFlagWord = 2 * kCtrWords;
 
 __device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent16(uint16_t* p, uint16_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -217,45 +327,41 @@ __device__ __forceinline__ void record_error(uint32_t* scratch) { st_agent(&scra
 // Cache policy of the gather loads: sc1 (device scope), so they are served coherently across the XCDs' L2s.
 constexpr int kDeviceScope = 16;
 
-// Waits (bounded) until rows [e0, e0 + K) of an earlier stage carry this launch's tag and copies their bf16 values
-// into xl. The tagged words come straight into LDS (global_load_lds_dwordx4, 1 KiB per wave instruction, no
-// registers); chunks of 512 words with a word of an older tag are fetched again.
-__device__ __forceinline__ void gather_input(const uint32_t* __restrict__ rows_t, int K, uint32_t tag, SetLds& L,
-                                             uint16_t* xl, int lane, bool& failed, uint32_t* scratch) {
-  const int nch = K / 512;
-  uint32_t pending = (1u << nch) - 1u;  // wave-uniform; nch <= 16
+// The workgroup that computes row r of a stage of N rows (workgroup g owns rows [g N / G, (g + 1) N / G)).
+__device__ __forceinline__ int owner_of(int64_t r, int64_t N, int G) {
+  return static_cast<int>(((r + 1) * G + N - 1) / N) - 1;
+}
+
+// Waits (bounded) until every workgroup in [g_lo, g_hi] has set its flag to `tag`: one load per workgroup per
+// poll, all of a poll's loads in flight together.
+__device__ __forceinline__ void wait_flags(const uint32_t* __restrict__ flags, int g_lo, int g_hi, uint32_t tag,
+                                           int lane, bool& failed, uint32_t* scratch) {
   uint32_t it = 0;
-  while (true) {
-    for (int c = 0; c < nch; ++c) {
-      if (!((pending >> c) & 1u)) continue;
+  while (!failed) {
+    bool ok = true;
+    for (int g0 = g_lo; g0 <= g_hi; g0 += 4 * kWave) {
+      uint32_t f[4];
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        __builtin_amdgcn_global_load_lds((const BP_GLOBAL void*)(rows_t + c * 512 + h * 256 + lane * 4),
-                                         (BP_LDS void*)&L.tin[c * 512 + h * 256], 16, 0, kDeviceScope);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    for (int c = 0; c < nch; ++c) {
-      if (!((pending >> c) & 1u)) continue;
-      const u32x4* tp = reinterpret_cast<const u32x4*>(&L.tin[c * 512 + lane * 8]);
-      const u32x4 a = tp[0], b = tp[1];
-      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      bool ok = true;
+      for (int i = 0; i < 4; ++i) f[i] = ld_agent(&flags[min(g0 + i * kWave + lane, g_hi)]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ok = ok && (w[e] >> 16) == tag;
-      if (__all(ok) || failed) {
-        *reinterpret_cast<u32x4*>(xl + c * 512 + lane * 8) =
-            u32x4{(w[0] & 0xffffu) | (w[1] << 16), (w[2] & 0xffffu) | (w[3] << 16), (w[4] & 0xffffu) | (w[5] << 16),
-                  (w[6] & 0xffffu) | (w[7] << 16)};
-        pending &= ~(1u << c);
-      }
+      for (int i = 0; i < 4; ++i) ok = ok && f[i] == tag;
     }
-    if (pending == 0u) break;
-    if (++it > kSpinCapGlobal && !failed) {
+    if (__all(ok)) return;
+    if (++it > kSpinCapGlobal) {
       failed = true;
       record_error(scratch);
     }
     __builtin_amdgcn_s_sleep(1);
   }
+}
+
+// Copies K published bf16 values into xl with device-scope LDS-DMA loads (global_load_lds_dwordx4: 1 KiB, one
+// 512-element chunk of the LDS layout, per wave instruction, no registers).
+__device__ __forceinline__ void gather_rows(const uint16_t* __restrict__ src, int K, uint16_t* xl, int lane) {
+  for (int c = 0; c < K / 512; ++c)
+    __builtin_amdgcn_global_load_lds((const BP_GLOBAL void*)(src + c * 512 + lane * 8), (BP_LDS void*)(xl + c * 512),
+                                     16, 0, kDeviceScope);
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 // The workgroup's sync wave: inputs in, results out.
@@ -265,8 +371,8 @@ __device__ __forceinline__ void sync_wave(StageTable st, int S, uint32_t* __rest
   const int g = blockIdx.x, G = gridDim.x;
   // launch generation: every workgroup of the previous launches added 1 to the launch counter
   const uint32_t gen = ld_agent(&scratch[0]) / static_cast<uint32_t>(G);
-  const uint32_t tag = gen % 65535u + 1u;  // 1..65535: a zeroed scratch holds no valid output
-  uint32_t* tagged = scratch + kTagWord;
+  const uint32_t tag = gen + 1u;  // never 0, the value of a zeroed scratch (wraps after 2^32 - 1 launches)
+  uint32_t* flags = scratch + kFlagWord;
   bool failed = false;
 
   for (int s = 0; s < S; ++s) {
@@ -283,7 +389,10 @@ __device__ __forceinline__ void sync_wave(StageTable st, int S, uint32_t* __rest
     const int ws = st[s].wait_stage;
     if (ws >= 0) {
       const int64_t e0 = (static_cast<const char*>(st[s].src) - static_cast<const char*>(st[ws].y)) / 2;
-      gather_input(tagged + L.tag_off[ws] + e0, K, tag, L, xl, lane, failed, scratch);
+      const int64_t Nw = st[ws].N;
+      wait_flags(flags + static_cast<int64_t>(ws) * G, owner_of(e0, Nw, G), owner_of(e0 + K - 1, Nw, G), tag, lane,
+                 failed, scratch);
+      gather_rows(static_cast<const uint16_t*>(st[s].src), K, xl, lane);
     } else {
       const BP_GLOBAL uint16_t* src = (const BP_GLOBAL uint16_t*)(st[s].src);
       for (int c0 = 0; c0 < nch; c0 += 8) {
@@ -296,34 +405,47 @@ __device__ __forceinline__ void sync_wave(StageTable st, int S, uint32_t* __rest
           if (c0 + j < nch) *reinterpret_cast<u32x4*>(xl + (c0 + j) * 512 + lane * 8) = t[j];
       }
     }
-    // 2. optional unit-RMS scaling: mean square in a fixed order (per lane over its chunks, then a wave butterfly)
+    // 2. optional unit-RMS scaling: mean square in a fixed order (per lane over its chunks, then a wave butterfly).
+    //    Chunks are taken four at a time so that their LDS reads are in flight together.
     if (st[s].renorm) {
       float ss = 0.f;
-      for (int c0 = 0; c0 < nch; ++c0) {
-        const u32x4 t = *reinterpret_cast<const u32x4*>(xl + c0 * 512 + lane * 8);
-        const uint32_t d[4] = {t.x, t.y, t.z, t.w};
+      for (int c0 = 0; c0 < nch; c0 += 4) {
+        u32x4 t[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float lo = bf16_bits_to_float(d[e] & 0xffffu), hi = bf16_bits_to_float(d[e] >> 16);
-          ss += lo * lo;
-          ss += hi * hi;
+        for (int j = 0; j < 4; ++j)
+          t[j] = c0 + j < nch ? *reinterpret_cast<const u32x4*>(xl + (c0 + j) * 512 + lane * 8) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t d[4] = {t[j].x, t[j].y, t[j].z, t[j].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = bf16_bits_to_float(d[e] & 0xffffu), hi = bf16_bits_to_float(d[e] >> 16);
+            ss += lo * lo;
+            ss += hi * hi;
+          }
         }
       }
       float tot[1] = {ss};
       wave_transpose_reduce<1>(tot, lane);  // every lane holds the total
       const float ms = tot[0] / static_cast<float>(K);
       const float inv = ms > 0.f ? 1.f / sqrtf(ms) : 1.f;
-      for (int c0 = 0; c0 < nch; ++c0) {
-        u32x4* p = reinterpret_cast<u32x4*>(xl + c0 * 512 + lane * 8);
-        const u32x4 t = *p;
-        uint32_t d[4] = {t.x, t.y, t.z, t.w};
+      for (int c0 = 0; c0 < nch; c0 += 4) {
+        u32x4 t[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = float_to_bf16_bits(bf16_bits_to_float(d[e] & 0xffffu) * inv);
-          const uint32_t hi = float_to_bf16_bits(bf16_bits_to_float(d[e] >> 16) * inv);
-          d[e] = lo | (hi << 16);
+        for (int j = 0; j < 4; ++j)
+          if (c0 + j < nch) t[j] = *reinterpret_cast<const u32x4*>(xl + (c0 + j) * 512 + lane * 8);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (c0 + j >= nch) continue;
+          uint32_t d[4] = {t[j].x, t[j].y, t[j].z, t[j].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = float_to_bf16_bits(bf16_bits_to_float(d[e] & 0xffffu) * inv);
+            const uint32_t hi = float_to_bf16_bits(bf16_bits_to_float(d[e] >> 16) * inv);
+            d[e] = lo | (hi << 16);
+          }
+          *reinterpret_cast<u32x4*>(xl + (c0 + j) * 512 + lane * 8) = u32x4{d[0], d[1], d[2], d[3]};
         }
-        *p = u32x4{d[0], d[1], d[2], d[3]};
       }
     }
     if (g == 0 && st[s].x_used != nullptr) {
@@ -345,7 +467,7 @@ __device__ __forceinline__ void sync_wave(StageTable st, int S, uint32_t* __rest
       }
     }
 
-    // 4. wait for the compute waves, publish the stage's rows (plain bf16 and tagged)
+    // 4. wait for the compute waves, publish the stage's rows
     {
       uint32_t it = 0;
       while (!failed && lds_load_relaxed(&L.ydone[s & 1]) < active) {
@@ -357,16 +479,18 @@ __device__ __forceinline__ void sync_wave(StageTable st, int S, uint32_t* __rest
       }
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
-    BP_GLOBAL uint16_t* y = (BP_GLOBAL uint16_t*)(st[s].y);
-    uint32_t* ty = tagged + L.tag_off[s];
+    // rows with device-scope stores; once they are acknowledged, the flag
+    uint16_t* y = static_cast<uint16_t*>(st[s].y);
     for (int i = lane; i < rows; i += kWave) {
       float v = L.y[s & 1][i];
       if constexpr (KIND == kInt8) v *= L.scale[s & 1][i];
-      const uint32_t bits = float_to_bf16_bits(v);
-      y[row0 + i] = static_cast<uint16_t>(bits);
-      st_agent(&ty[row0 + i], (tag << 16) | bits);
+      st_agent16(&y[row0 + i], float_to_bf16_bits(v));
     }
-    if (lane == 0) __hip_atomic_store(&L.ydone[s & 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_s_waitcnt(0);
+    if (lane == 0) {
+      st_agent(&flags[static_cast<int64_t>(s) * G + g], tag);
+      __hip_atomic_store(&L.ydone[s & 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
   }
   if (lane == 0) __hip_atomic_fetch_add(&scratch[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -378,49 +502,34 @@ __global__ __launch_bounds__(kSetThreads) void linear_set_kernel(const BpSetStag
   StageTable st = (StageTable)(stages);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = uniform(threadIdx.x / kWave);
-  // row table: wave i of workgroup g owns rows [u N / T, (u + 1) N / T) of every stage, u = g * CW + i
+  // row table: consumer i of workgroup g owns rows [u N / T, (u + 1) N / T) of every stage, u = g * CW + i
   const int64_t T = static_cast<int64_t>(gridDim.x) * kSetCW;
   for (int e = threadIdx.x; e < S * (kSetCW + 1); e += kSetThreads) {
     const int s = e / (kSetCW + 1), i = e % (kSetCW + 1);
     const int64_t u = static_cast<int64_t>(blockIdx.x) * kSetCW + i;
     lds.rows[s][i] = static_cast<int32_t>(u * st[s].N / T);
   }
+  if (threadIdx.x < kSetCW) {
+    lds.landed[threadIdx.x] = 0;
+    lds.consumed[threadIdx.x] = 0;
+  }
   if (threadIdx.x == 0) {
-    int32_t off = 0;
-    for (int s = 0; s < S; ++s) {
-      lds.tag_off[s] = off;
-      off += (st[s].N + 7) & ~7;
-    }
     lds.xready = 0;
     lds.ydone[0] = 0;
     lds.ydone[1] = 0;
   }
   __syncthreads();
-  if (wave == kSetCW) {
+  if (wave == kSetSyncWave) {
     sync_wave<KIND>(st, S, scratch, lds, scale_dt, lane);
-    return;
+  } else if (wave >= kSetCW) {
+    producer_wave<KIND>(st, lds, S, wave - kSetCW, lane);
+  } else {
+    Consumer<KIND> cons;
+    cons.failed = false;
+    cons.n = 0;
+    cons.seen = 0;
+    cons.run(st, lds, S, wave, lane);
   }
-  Producer<KIND> prod;
-  prod.idle = (const BP_GLOBAL uint8_t*)(st[0].w[0]);
-  prod.enter(st, lds, S, wave, 0);
-  Consumer<KIND> cons;
-  cons.failed = false;
-
-  // Ring of kSetRing chunks: slot j is consumed, then reloaded with the chunk kSetRing items ahead, so every
-  // consume finds exactly kSetRing - 1 younger loads in flight.
-  u32x4 ring[kSetRing];
-#pragma unroll
-  for (int j = 0; j < kSetRing; ++j) ring[j] = prod.issue(st, lds, S, wave, lane);
-  cons.enter(st, lds, S, wave, lane, 0);
-  bool more = true;
-  while (more) {
-#pragma unroll
-    for (int j = 0; j < kSetRing; ++j) {
-      if (more) more = cons.consume(ring[j], st, lds, S, wave, lane);
-      ring[j] = prod.issue(st, lds, S, wave, lane);  // unconditional: past the end it reloads the idle chunk
-    }
-  }
-  __builtin_amdgcn_s_waitcnt(0);
 }
 
 int set_validate(const BpSetStage* st, int S, int wkind, int G) {
@@ -429,7 +538,6 @@ int set_validate(const BpSetStage* st, int S, int wkind, int G) {
   if (wkind != kBf16 && wkind != kInt8) return BP_E_UNSUPPORTED;
   if (G > 65536) return BP_E_UNSUPPORTED;
   const int64_t chunk = wkind == kBf16 ? 512 : 1024;
-  int64_t words = 0;  // tagged outputs
   for (int s = 0; s < S; ++s) {
     const BpSetStage& a = st[s];
     if (a.src == nullptr || a.y == nullptr) return BP_E_INVALID_ARG;
@@ -454,17 +562,11 @@ int set_validate(const BpSetStage* st, int S, int wkind, int G) {
       const uintptr_t b = reinterpret_cast<uintptr_t>(a.src), e = b + 2 * static_cast<uintptr_t>(a.K);
       if (b < lo || e > hi) return BP_E_INVALID_ARG;
     }
-    words += (a.N + 7) & ~7;
   }
-  if (words > (int64_t{1} << 30)) return BP_E_UNSUPPORTED;
   return BP_OK;
 }
 
-int64_t scratch_words(const BpSetStage* st, int S, int G) {
-  int64_t words = kTagWord;
-  for (int s = 0; s < S; ++s) words += (st[s].N + 7) & ~7;
-  return words;
-}
+int64_t scratch_words(int S, int G) { return kFlagWord + static_cast<int64_t>(S) * G; }
 
 }  // namespace
 }  // namespace bp
@@ -473,7 +575,7 @@ extern "C" {
 
 size_t bp_linear_set_scratch_bytes(const BpSetStage* stages, int num_stages, int num_workgroups) {
   if (stages == nullptr || num_stages <= 0 || num_workgroups <= 0) return 0;
-  return static_cast<size_t>(bp::scratch_words(stages, num_stages, num_workgroups)) * sizeof(uint32_t);
+  return static_cast<size_t>(bp::scratch_words(num_stages, num_workgroups)) * sizeof(uint32_t);
 }
 
 int bp_linear_set_workgroups(int device) {

@@ -143,11 +143,11 @@ typedef struct BpSetStage {
   const void* scale[4]; /* int8: per-row scales of each segment (dtype given to bp_linear_set_run) */
 } BpSetStage;
 
-/* Bytes of scratch a launch of these stages needs: a launch counter, an error flag and every stage's outputs
- * tagged with the launch (4 bytes per row, rows rounded up to 8). num_workgroups is accepted for future layouts.
- * The scratch must be zero before its first launch and is then reused as is by every later launch (no reset
- * between launches or graph replays). The 32-bit word at index 32 becomes non-zero if a launch gave up waiting
- * for another workgroup (that launch's later results are invalid); the host clears it. */
+/* Bytes of scratch a launch of these stages on num_workgroups workgroups needs: a launch counter, an error flag
+ * and one publish flag per stage and workgroup. The scratch must be zero before its first launch and is then reused
+ * as is by every later launch (no reset between launches or graph replays). The 32-bit word at index 32 becomes
+ * non-zero if a launch gave up waiting for another workgroup (that launch's later results are invalid); the host
+ * clears it. */
 size_t bp_linear_set_scratch_bytes(const BpSetStage* stages, int num_stages, int num_workgroups);
 
 /* Workgroups the set kernel is launched with on `device`: one per compute unit (0 on error). */

@@ -152,6 +152,6 @@ def test_linear_set_validation_rejects_bad_descriptors(L):
     bad[0].y = 0x2008                                        # outputs must be 16-byte aligned
     assert rc(bad) == -1
     arr = _set_stages(n_stages=3, n=4093)
-    # launch counter + error flag lines, 3 x (4093 rounded up to 8) tagged words
-    assert L.bp_linear_set_scratch_bytes(ctypes.addressof(arr), 3, 256) == 4 * (64 + 3 * 4096)
+    # launch counter + error flag lines, 3 x 256 publish flags
+    assert L.bp_linear_set_scratch_bytes(ctypes.addressof(arr), 3, 256) == 4 * (64 + 3 * 256)
     assert L.bp_linear_set_scratch_bytes(None, 0, 256) == 0

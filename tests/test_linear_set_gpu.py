@@ -170,12 +170,30 @@ def test_input_change_between_launches_is_seen():
     _check_stages(stages, ostages)
 
 
+def test_fresh_inputs_on_every_launch_reach_every_stage():
+    """A new external input before each launch: every dependent stage must see this launch's rows (a stage that
+    read a row before its producer published it would see the previous launch's value, which differs)."""
+    stages, ostages = _small_chain("bf16", seed=7)
+    ls = LinearSet(stages)
+    for it in range(6):
+        x = torch.randn(stages[0].k, generator=_gen(700 + it), device=DEV).to(torch.bfloat16)
+        stages[0].src.copy_(x)
+        ostages[0].src = ("ext", _np(x))
+        ls.run()
+        torch.cuda.synchronize()
+        _check_stages(stages, ostages)
+    assert not ls.timed_out()
+
+
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
 @pytest.mark.parametrize("dependent", [True, False])
 def test_full_decode_step_set(kind, dependent):
     """The OLMo-2-1B-shaped set (16 layers x q|k|v, o, gate|up, down + the 100352-row head) in one launch."""
     ch = D.build_chain(kind, DEV, seed=11, dependent=dependent, record_inputs=True)
     ch.lset.run()
+    if dependent:  # a second launch with a new first input: every stage must see this launch's values
+        ch.stages[0].src.copy_(torch.randn(ch.stages[0].k, generator=_gen(12), device=DEV).to(torch.bfloat16))
+        ch.lset.run()
     torch.cuda.synchronize()
     assert not ch.lset.timed_out()
     assert len(ch.stages) == 16 * 4 + 1
@@ -187,6 +205,8 @@ def test_full_decode_step_set(kind, dependent):
             start = (st.src.data_ptr() - base.data_ptr()) // 2
             src = ys_host[st.wait][start:start + st.k]
             assert _bf16_step_close(_np(st.x_used), OL.unit_rms(src)), i
+        elif st.renorm:
+            assert _bf16_step_close(_np(st.x_used), OL.unit_rms(_np(st.src))), i
         else:
             assert torch.equal(st.x_used, st.src)
         if kind == "bf16":
