@@ -4,26 +4,34 @@
 // of v, gate|up read the attention block's output, down reads the MLP activation, the next layer's q|k|v read
 // down's output, and the LM head reads the last layer's output. Launched one linear at a time, every stage pays
 // a launch's fixed cost and HBM idles while a small launch ramps up and drains. This kernel runs the whole chain
-// in one launch on one workgroup per CU and keeps the weight stream going across stage boundaries:
+// in one launch on one workgroup per CU and keeps the weight stream going across stage boundaries. A workgroup
+// has three kinds of waves:
 //
-//   - consumer waves (kSetCW per workgroup) own whole weight rows of every stage; each has a producer wave that
-//     streams its rows in 1 KiB wave-wide chunks into an LDS ring (LDS-DMA loads, non-temporal). Loads do not
-//     depend on activations, so the producers keep loading the next stage's rows while the stage's input is still
-//     being produced elsewhere on the chip, and only they stall when the CU's outstanding loads are at capacity:
-//     once a stage's input arrives, the consumers work through the landed ring at LDS speed;
-//   - one sync wave per workgroup does all the cross-workgroup work, so the compute waves never wait for their
-//     own outstanding loads: it gathers the stage's input vector into LDS (optionally renormalised to unit RMS)
-//     and publishes the workgroup's results of the stage with device-coherent (sc1) stores and a per-workgroup
-//     flag; readers poll the flags of the workgroups whose rows they read, then copy the rows into LDS with
-//     device-scope LDS-DMA loads;
-//   - inside the workgroup, LDS flags hand the input (xready) to the compute waves and the results (ydone)
-//     back to the sync wave. Every wait is bounded: past a cap of polls the wave records an error flag in the
-//     scratch words and stops waiting, so a launch always finishes.
+//   - consumer waves (kSetCW) own whole weight rows of every stage: they take their rows' 1 KiB weight chunks
+//     from an LDS ring, dot them with the stage input in LDS (v_dot2_f32_bf16, fp32), sum each row over the wave
+//     and publish it;
+//   - producer waves (one per consumer) stream the consumer's chunks with non-temporal 16-byte loads through a
+//     small register ring into its LDS ring, publishing each chunk as it lands. Loads do not depend on
+//     activations, so producers keep loading the next stages' rows while a stage's input is still being computed
+//     elsewhere on the chip; a load instruction stalls its wave while the CU's outstanding requests are at
+//     capacity, and only producers stall, so when a stage's input arrives the consumers work through the landed
+//     ring at LDS speed;
+//   - one sync wave gathers each stage's input vector into LDS (optionally renormalised to unit RMS) and hands it
+//     to the consumers.
+//
+// Rows travel between workgroups as 32-bit words: the bf16 value in the low half, a per-launch tag in the high
+// half, written by the consumer that computed the row with a device-scope (sc1, write-through) store. A 32-bit
+// store is seen whole or not at all, so a reader that finds the current tag in a word has that launch's value: no
+// fence, counter or flag is needed (a release fence per workgroup and stage costs more than a stage), and a reader
+// waits only for the rows it reads. The sync wave starts reading a stage's input once its own consumers have
+// finished the producing stage, with device-scope LDS-DMA loads, and reads again the chunks still carrying an
+// older tag. Every wait is bounded: past a cap of polls the wave records an error flag in the scratch and stops
+// waiting, so a launch always finishes.
 //
 // Nothing is reset between launches: launch g (counted by a launch counter every workgroup increments at the end)
-// sets its flags to g + 1, so the kernel can be replayed in a HIP graph with no memset. Per-row arithmetic matches the skinny kernels: bf16 (or
-// exact int8 -> bf16) pairs through v_dot2_f32_bf16 into fp32, a fixed wave butterfly, the int8 scale on the fp32
-// sum, round-to-nearest-even to bf16.
+// tags its words g % 65535 + 1, so the kernel can be replayed in a HIP graph with no memset. Per-row arithmetic
+// matches the skinny kernels: bf16 (or exact int8 -> bf16) pairs through v_dot2_f32_bf16 into fp32, a fixed wave
+// reduction order, the int8 scale on the fp32 sum, round-to-nearest-even to bf16.
 //
 // Reference semantics per linear: byteprof/optim/skinny.py:36-90 (one-row product, bf16 / int8 modes); the set
 // and its shapes: the decode-step linears that byteprof's OLMo-2 graph loop replays per token
@@ -49,28 +57,28 @@ constexpr int kSetPW = kSetCW;                      // producer waves: one per c
 constexpr int kSetSyncWave = kSetCW + kSetPW;       // index of the sync wave
 constexpr int kSetThreads = (kSetSyncWave + 1) * kWave;
 constexpr int kSetKMax = 8192;                      // longest input vector (two bf16 buffers in LDS)
-constexpr int kSetRowsMax = 1024;                   // rows of one stage per workgroup (fp32 results in LDS)
-constexpr int kSetStagesMax = 128;                  // stages per set (row table in LDS)
+constexpr int kSetTin = 4096;                       // tagged input words gathered per round (16 KiB)
+constexpr int kSetRowsMax = 512;                    // rows of one stage per workgroup (int8 scales in LDS)
+constexpr int kSetStagesMax = 96;                   // stages per set (tables in LDS)
 constexpr int kSetSlots = 26;                       // 1 KiB LDS ring slots per consumer
-constexpr int kSetLag = 12;                         // loads a producer keeps in flight before publishing them
-constexpr int kSetPublish = 8;                      // chunks between two publications of the landed count
-#ifndef BP_PUBMODE
-#define BP_PUBMODE 16
-#endif
-constexpr int kCtrWords = 32;                       // one 128-byte line per counter
-constexpr uint32_t kSpinCapGlobal = 1u << 20;       // polls of a global word before a wait gives up (~1 s)
+constexpr int kSetInflight = 12;                    // weight chunks a producer keeps in flight (registers)
+constexpr int kWordsHeader = 64;                    // scratch: launch counter (word 0), error flag (word 32)
+constexpr int kErrWord = 32;
+constexpr uint32_t kSpinCapGlobal = 1u << 20;       // polls of global memory before a wait gives up (~1 s)
 constexpr uint32_t kSpinCapLds = 1u << 24;          // polls of an LDS word before a wait gives up (~1 s)
 
 struct SetLds {
   alignas(16) uint8_t ring[kSetCW][kSetSlots][1024];  // weight chunks: producer i fills ring[i], consumer i drains it
-  uint16_t x[2][kSetKMax];                // the stage's input vector, by stage parity
-  float y[2][kSetRowsMax];                // the workgroup's fp32 row sums, by stage parity
+  alignas(16) uint16_t x[2][kSetKMax];    // the stage's input vector, by stage parity
+  alignas(16) uint32_t tin[kSetTin];      // tagged input words as gathered
   float scale[2][kSetRowsMax];            // int8: the workgroup's row scales, by stage parity
-  int32_t rows[kSetStagesMax][kSetCW + 1];  // stage s: consumer i of this workgroup owns rows [rows[s][i], rows[s][i+1])
+  int32_t rows[kSetStagesMax][kSetCW + 1];  // stage s: consumer i owns rows [rows[s][i], rows[s][i+1])
+  int32_t tag_off[kSetStagesMax];         // word offset of stage s's tagged rows after the scratch header
+  int done[kSetStagesMax];                // consumers of this workgroup done with stage s
   int landed[kSetCW];                     // chunks of consumer i's stream in its ring (producer -> consumer)
   int consumed[kSetCW];                   // chunks consumer i has read out of its ring (consumer -> producer)
   int xready;                             // stage s's input is in x[s & 1] once xready > s
-  int ydone[2];                           // consumer waves done with the stage of that parity
+  uint32_t tag;                           // this launch's tag
 };
 // More than half of the CU's 160 KiB of LDS: exactly one workgroup per CU, so the grid of one workgroup per CU is
 // resident at once (the cross-workgroup waits rely on it).
@@ -87,8 +95,23 @@ constexpr int waitcnt_vm() {
 __device__ __forceinline__ int lds_load_relaxed(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
+__device__ __forceinline__ void lds_store_relaxed(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void record_error(uint32_t* scratch) { st_agent(&scratch[kErrWord], 1u); }
+
+// Cache policy of the gathers of published rows: device scope (sc1), served coherently across the XCDs' L2s.
+constexpr int kDeviceScope = 16;
 
 // Weight-chunk stream of one consumer: its rows of every stage in stage order, each row in 1 KiB chunks.
 template <int KIND>
@@ -131,61 +154,69 @@ struct Cursor {
   }
 };
 
-// Cache policy of the weight stream: nt (streamed once, not kept in the caches).
-constexpr int kStreamPolicy = 2;
-
-// Producer wave i: copies consumer i's chunks into its LDS ring with LDS-DMA loads (global_load_lds_dwordx4,
-// 1 KiB per wave instruction, no registers). A load instruction stalls its wave while the CU's outstanding requests
-// are at capacity; only this wave stalls, so the consumer keeps reading landed chunks at LDS speed. Loads complete
-// in order: after each load the producer waits until at most kSetLag are in flight and publishes the count that
-// has landed. When the ring is full (its consumer is waiting for a stage's input) it publishes everything and
-// waits for a free slot, so a consumer that resumes finds the whole ring landed.
+// Producer wave `who`: copies its consumer's chunks into the consumer's LDS ring. Chunks travel through a ring of
+// kSetInflight registers: the producer waits for its oldest load, writes that chunk into the LDS ring, publishes
+// it at once (one LDS word), and loads the next chunk into the freed registers. Exactly kSetInflight loads are
+// always in flight (past the end of its stream the producer re-reads its first chunk), so each wait is for the
+// oldest load only. Four producers keep 4 * kSetInflight KiB in flight per CU, below the CU's capacity, so the
+// sync wave's loads are not queued behind the weight stream. When the LDS ring is full (its consumer is waiting
+// for a stage's input) the producer waits for a free slot with its loads still in flight.
 template <int KIND>
-__device__ __forceinline__ void producer_wave(StageTable st, SetLds& L, int S, int who, int lane) {
+__device__ __forceinline__ void producer_wave(StageTable st, SetLds& L, int S, int who, int lane,
+                                              uint32_t* scratch) {
   Cursor<KIND> cur;
   cur.enter(st, L, S, who, 0);
-  int n = 0, limit = kSetSlots;  // chunks issued; chunks that fit the ring as last seen
+  if (cur.s >= S) return;  // no rows in any stage: the consumer has none either
+  const BP_GLOBAL uint8_t* const idle = cur.p;
+  u32x4 buf[kSetInflight];
+  int issued = 0;
+#pragma unroll
+  for (int j = 0; j < kSetInflight; ++j) {
+    const bool real = cur.s < S;
+    buf[j] = __builtin_nontemporal_load((const BP_GLOBAL u32x4*)((real ? cur.p : idle) + lane * 16));
+    if (real) {
+      cur.advance(st, L, S, who);
+      ++issued;
+    }
+  }
+  int n = 0, slot = 0, limit = kSetSlots;  // chunks written to the ring; ring slot of chunk n; chunks that fit
   bool failed = false;
-  while (cur.s < S) {
-    if (n >= limit) {  // ring full as last seen: publish everything, then wait for the consumer
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
-      if (lane == 0) __hip_atomic_store(&L.landed[who], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      uint32_t it = 0;
-      while (!failed && n >= (limit = lds_load_relaxed(&L.consumed[who]) + kSetSlots)) {
-        if (++it > kSpinCapLds) failed = true;
-        __builtin_amdgcn_s_sleep(1);
+  while (n < issued) {
+#pragma unroll
+    for (int j = 0; j < kSetInflight; ++j) {
+      if (n < issued) {
+        if (n >= limit) {
+          uint32_t it = 0;
+          while (!failed && n >= (limit = lds_load_relaxed(&L.consumed[who]) + kSetSlots)) {
+            if (++it > kSpinCapLds) {
+              failed = true;
+              record_error(scratch);
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          if (failed) limit = n + kSetSlots;  // stop waiting; the launch's results are flagged invalid
+        }
+        *reinterpret_cast<u32x4*>(&L.ring[who][slot][lane * 16]) = buf[j];
+        ++n;
+        slot = slot + 1 == kSetSlots ? 0 : slot + 1;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (lane == 0) lds_store_relaxed(&L.landed[who], n);
       }
-      if (failed) break;
+      const bool real = cur.s < S;
+      buf[j] = __builtin_nontemporal_load((const BP_GLOBAL u32x4*)((real ? cur.p : idle) + lane * 16));
+      if (real) {
+        cur.advance(st, L, S, who);
+        ++issued;
+      }
     }
-    __builtin_amdgcn_global_load_lds((const BP_GLOBAL void*)(cur.p + lane * 16),
-                                     (BP_LDS void*)&L.ring[who][n % kSetSlots][0], 16, 0, kStreamPolicy);
-    cur.advance(st, L, S, who);
-    ++n;
-#if BP_PUBMODE == 0
-    if (n > kSetLag) __builtin_amdgcn_s_waitcnt(waitcnt_vm<kSetLag>());
-    // An LDS access of this wave waits for the LDS writes of its loads in flight, so the producer touches LDS
-    // every kSetPublish chunks only: it publishes what has landed and refreshes its view of the consumer.
-    if (n % kSetPublish == 0) {
-      if (lane == 0 && n > kSetLag)
-        __hip_atomic_store(&L.landed[who], n - kSetLag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      limit = lds_load_relaxed(&L.consumed[who]) + kSetSlots;
-    }
-#else
-    if (n % BP_PUBMODE == 0) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
-      if (lane == 0) __hip_atomic_store(&L.landed[who], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      limit = lds_load_relaxed(&L.consumed[who]) + kSetSlots;
-    }
-#endif
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
-  if (lane == 0) __hip_atomic_store(&L.landed[who], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Consumer wave i: the same chunks in the same order, read from its LDS ring once landed: dot products against
-// the stage input in LDS, one wave sum per row. Chunks are taken in groups of GS of one row (GS divides the
-// chunks per row): one poll of the landed count, all of the group's LDS reads in flight together, one release of
-// its ring slots. A consumer visits only the stages where it owns rows; the sync wave counts those per stage.
+// Consumer wave `who`: the same chunks in the same order, read from its ring once landed, in groups of GS chunks
+// of one row (GS divides the chunks per row): one poll of the landed count, all of the group's LDS reads in flight
+// together, one release of the group's ring slots. At the end of a row the consumer stores the row's bf16 value
+// for the caller and, tagged, for the stages that read it. A consumer visits only the stages where it owns rows.
 template <int KIND>
 struct Consumer {
   int s;
@@ -194,9 +225,12 @@ struct Consumer {
   int n, seen;        // chunks consumed; chunks known to have landed
   float acc;
   bool failed;
+  uint32_t tag;
+  BP_GLOBAL uint16_t* y;   // the stage's outputs
+  uint32_t* ty;            // the stage's tagged outputs
 
   // Moves to stage `from` or the next one with rows for this consumer and waits (bounded) for its input in LDS.
-  __device__ __forceinline__ void enter(StageTable st, SetLds& L, int S, int who, int from) {
+  __device__ __forceinline__ void enter(StageTable st, SetLds& L, int S, int who, int from, uint32_t* tagged) {
     for (s = from; s < S; ++s) {
       r = uniform(L.rows[s][who]);
       r1 = uniform(L.rows[s][who + 1]);
@@ -207,25 +241,33 @@ struct Consumer {
     C = (st[s].K * Layout<KIND>::kElemBytes) >> 10;
     c = 0;
     acc = 0.f;
+    y = (BP_GLOBAL uint16_t*)(st[s].y);
+    ty = tagged + L.tag_off[s];
     uint32_t it = 0;
     while (!failed && lds_load_relaxed(&L.xready) <= s) {
-      if (++it > kSpinCapLds) failed = true;
+      if (++it > kSpinCapLds) {
+        failed = true;
+        record_error(tagged - kWordsHeader);
+      }
       __builtin_amdgcn_s_sleep(1);
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   }
 
-  // GS chunks of the current row. RESIDENT: the row is exactly these GS chunks and xr already holds the stage's
-  // input chunks (loaded once per stage), so only the weights are read from LDS.
+  // GS chunks of the current row. RESIDENT: the row is exactly these GS chunks and xr holds the stage's input
+  // chunks (loaded once per stage), so only the weights are read from LDS.
   template <int GS, bool RESIDENT>
-  __device__ __forceinline__ void group(StageTable st, SetLds& L, int S, int who, int lane,
+  __device__ __forceinline__ void group(StageTable st, SetLds& L, int S, int who, int lane, uint32_t* tagged,
                                         uint32_t (&xr)[4][Layout<KIND>::kXDwords]) {
     using Lay = Layout<KIND>;
     uint32_t it = 0;
     while (seen < n + GS && !failed) {
       seen = lds_load_relaxed(&L.landed[who]);
       if (seen >= n + GS) break;
-      if (++it > kSpinCapLds) failed = true;
+      if (++it > kSpinCapLds) {
+        failed = true;
+        record_error(tagged - kWordsHeader);
+      }
       __builtin_amdgcn_s_sleep(0);
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -252,102 +294,69 @@ struct Consumer {
     for (int j = 0; j < GS; ++j) acc = chunk_dot<KIND>(w[j], RESIDENT ? xr[j] : xv[j], acc);
     n += GS;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (lane == 0) __hip_atomic_store(&L.consumed[who], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (lane == 0) lds_store_relaxed(&L.consumed[who], n);
     c += GS;
     if (c == C) {
       const float tot = wave_sum_dpp(acc);
-      if (lane == 0) L.y[s & 1][r - row0] = tot;
+      if (lane == 0) {
+        float v = tot;
+        if constexpr (KIND == kInt8) v *= L.scale[s & 1][r - row0];
+        const uint32_t bits = float_to_bf16_bits(v);
+        y[r] = static_cast<uint16_t>(bits);
+        st_agent(&ty[r], (tag << 16) | bits);
+      }
       acc = 0.f;
       c = 0;
       if (++r == r1) {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        if (lane == 0) __hip_atomic_fetch_add(&L.ydone[s & 1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        enter(st, L, S, who, s + 1);
+        if (lane == 0) __hip_atomic_fetch_add(&L.done[s], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        enter(st, L, S, who, s + 1, tagged);
       }
     }
   }
 
-  __device__ __forceinline__ void run(StageTable st, SetLds& L, int S, int who, int lane) {
+  __device__ __forceinline__ void run(StageTable st, SetLds& L, int S, int who, int lane, uint32_t* tagged) {
     using Lay = Layout<KIND>;
     uint32_t xr[4][Lay::kXDwords];
-    enter(st, L, S, who, 0);
+    enter(st, L, S, who, 0, tagged);
     while (s < S) {
-      if (C == 4 || C == 2) {  // whole rows per group: the stage's input chunks stay in registers
+      if (C == 4 || C == 2) {  // one group per row: the stage's input chunks stay in registers
         const int stage = s;
-        for (int j = 0; j < C; ++j) {
-          const u32x4* xs = reinterpret_cast<const u32x4*>(&L.x[s & 1][j * Lay::kChunk + lane * Lay::kEpl]);
 #pragma unroll
-          for (int q = 0; q < Lay::kXDwords / 4; ++q) {
-            const u32x4 t = xs[q];
-            // static register index: j is 0..3 (unrolled by the select below)
-            if (j == 0) { xr[0][4 * q + 0] = t.x; xr[0][4 * q + 1] = t.y; xr[0][4 * q + 2] = t.z; xr[0][4 * q + 3] = t.w; }
-            if (j == 1) { xr[1][4 * q + 0] = t.x; xr[1][4 * q + 1] = t.y; xr[1][4 * q + 2] = t.z; xr[1][4 * q + 3] = t.w; }
-            if (j == 2) { xr[2][4 * q + 0] = t.x; xr[2][4 * q + 1] = t.y; xr[2][4 * q + 2] = t.z; xr[2][4 * q + 3] = t.w; }
-            if (j == 3) { xr[3][4 * q + 0] = t.x; xr[3][4 * q + 1] = t.y; xr[3][4 * q + 2] = t.z; xr[3][4 * q + 3] = t.w; }
+        for (int j = 0; j < 4; ++j) {
+          if (j < C) {
+            const u32x4* xs = reinterpret_cast<const u32x4*>(&L.x[s & 1][j * Lay::kChunk + lane * Lay::kEpl]);
+#pragma unroll
+            for (int q = 0; q < Lay::kXDwords / 4; ++q) {
+              const u32x4 t = xs[q];
+              xr[j][4 * q + 0] = t.x;
+              xr[j][4 * q + 1] = t.y;
+              xr[j][4 * q + 2] = t.z;
+              xr[j][4 * q + 3] = t.w;
+            }
           }
         }
         if (C == 4) {
-          while (s == stage) group<4, true>(st, L, S, who, lane, xr);
+          while (s == stage) group<4, true>(st, L, S, who, lane, tagged, xr);
         } else {
-          while (s == stage) group<2, true>(st, L, S, who, lane, xr);
+          while (s == stage) group<2, true>(st, L, S, who, lane, tagged, xr);
         }
       } else if ((C & 3) == 0) {
-        group<4, false>(st, L, S, who, lane, xr);
+        group<4, false>(st, L, S, who, lane, tagged, xr);
       } else if ((C & 1) == 0) {
-        group<2, false>(st, L, S, who, lane, xr);
+        group<2, false>(st, L, S, who, lane, tagged, xr);
       } else {
-        group<1, false>(st, L, S, who, lane, xr);
+        group<1, false>(st, L, S, who, lane, tagged, xr);
       }
     }
   }
 };
 
-// Scratch words: [0] launch counter (every workgroup adds 1 at the end of a launch), [kErrWord] error flag, then
-// S x G publish flags from kFlagWord: flag[s][g] = the launch's tag once workgroup g's rows of stage s are visible
-// device-wide. A producer stores its rows with device-scope (sc1, write-through) stores, waits until they are
-// acknowledged, then stores its flag; a reader polls the flags of the workgroups that produce the rows it reads
-// (one word each, all of a poll's loads in flight together) and then reads the rows with device-scope loads. Both
-// sides use device-coherent accesses for the rows, so no L2 writeback or invalidate is needed (a release fence
-// per workgroup and stage costs more than a stage), and a reader waits only for the rows it reads.
-constexpr int kErrWord = kCtrWords;
-constexpr int kFlagWord = 2 * kCtrWords;
-
-__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent16(uint16_t* p, uint16_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void record_error(uint32_t* scratch) { st_agent(&scratch[kErrWord], 1u); }
-
-// Cache policy of the gather loads: sc1 (device scope), so they are served coherently across the XCDs' L2s.
-constexpr int kDeviceScope = 16;
-
-// The workgroup that computes row r of a stage of N rows (workgroup g owns rows [g N / G, (g + 1) N / G)).
-__device__ __forceinline__ int owner_of(int64_t r, int64_t N, int G) {
-  return static_cast<int>(((r + 1) * G + N - 1) / N) - 1;
-}
-
-// Waits (bounded) until every workgroup in [g_lo, g_hi] has set its flag to `tag`: one load per workgroup per
-// poll, all of a poll's loads in flight together.
-__device__ __forceinline__ void wait_flags(const uint32_t* __restrict__ flags, int g_lo, int g_hi, uint32_t tag,
-                                           int lane, bool& failed, uint32_t* scratch) {
+// Waits (bounded) until `active` consumers of this workgroup are done with stage `stage`.
+__device__ __forceinline__ void wait_done(SetLds& L, int stage, int active, bool& failed, uint32_t* scratch) {
   uint32_t it = 0;
-  while (!failed) {
-    bool ok = true;
-    for (int g0 = g_lo; g0 <= g_hi; g0 += 4 * kWave) {
-      uint32_t f[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) f[i] = ld_agent(&flags[min(g0 + i * kWave + lane, g_hi)]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ok = ok && f[i] == tag;
-    }
-    if (__all(ok)) return;
-    if (++it > kSpinCapGlobal) {
+  while (!failed && lds_load_relaxed(&L.done[stage]) < active) {
+    if (++it > kSpinCapLds) {
       failed = true;
       record_error(scratch);
     }
@@ -355,110 +364,146 @@ __device__ __forceinline__ void wait_flags(const uint32_t* __restrict__ flags, i
   }
 }
 
-// Copies K published bf16 values into xl with device-scope LDS-DMA loads (global_load_lds_dwordx4: 1 KiB, one
-// 512-element chunk of the LDS layout, per wave instruction, no registers).
-__device__ __forceinline__ void gather_rows(const uint16_t* __restrict__ src, int K, uint16_t* xl, int lane) {
-  for (int c = 0; c < K / 512; ++c)
-    __builtin_amdgcn_global_load_lds((const BP_GLOBAL void*)(src + c * 512 + lane * 8), (BP_LDS void*)(xl + c * 512),
-                                     16, 0, kDeviceScope);
-  __builtin_amdgcn_s_waitcnt(0);
+__device__ __forceinline__ int active_consumers(const SetLds& L, int s) {
+  int a = 0;
+#pragma unroll
+  for (int i = 0; i < kSetCW; ++i) a += L.rows[s][i] < L.rows[s][i + 1] ? 1 : 0;
+  return a;
 }
 
-// The workgroup's sync wave: inputs in, results out.
+constexpr int kSetChMax = kSetKMax / 512;  // 512-element chunks of the longest input
+constexpr int kSetRound = kSetTin / 512;   // chunks of tagged words gathered per round
+
+// This lane's 8 values of chunk c of the input (4 packed bf16 pairs) and their sum of squares (in element order).
+__device__ __forceinline__ float chunk_ss(const uint32_t (&d)[4]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = bf16_bits_to_float(d[e] & 0xffffu), hi = bf16_bits_to_float(d[e] >> 16);
+    ss += lo * lo;
+    ss += hi * hi;
+  }
+  return ss;
+}
+
+// Writes the input held in registers (v: each lane's 8 values of every chunk) to xl, renormalised to unit RMS when
+// `norm`: mean square = (sum over lanes of the lane's chunk sums of squares, in chunk order) / K,
+// x = bf16(x * (1 / sqrt(mean square))); an all-zero vector is left as it is.
+__device__ __forceinline__ void write_input(uint32_t (&v)[kSetChMax][4], int K, bool norm, uint16_t* xl,
+                                            int lane) {
+  const int nch = K / 512;
+  float inv = 1.f;
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < kSetChMax; ++c)
+      if (c < nch) ss += chunk_ss(v[c]);
+    const float ms = wave_sum_dpp(ss) / static_cast<float>(K);
+    if (ms > 0.f) inv = 1.f / sqrtf(ms);
+  }
+#pragma unroll
+  for (int c = 0; c < kSetChMax; ++c) {
+    if (c < nch) {
+      uint32_t d[4] = {v[c][0], v[c][1], v[c][2], v[c][3]};
+      if (norm) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = float_to_bf16_bits(bf16_bits_to_float(d[e] & 0xffffu) * inv);
+          const uint32_t hi = float_to_bf16_bits(bf16_bits_to_float(d[e] >> 16) * inv);
+          d[e] = lo | (hi << 16);
+        }
+      }
+      *reinterpret_cast<u32x4*>(xl + c * 512 + lane * 8) = u32x4{d[0], d[1], d[2], d[3]};
+    }
+  }
+}
+
+// Reads round H of the K published rows at rows_t (tagged words) into registers: chunks H * kSetRound ..
+// (up to kSetRound chunks of 512 words, LDS-DMA into the staging buffer, device scope). A chunk is read again until
+// all of its words carry `tag` (bounded), then unpacked two words at a time (their tags into one dword, their
+// values into another).
+template <int H>
+__device__ __forceinline__ void gather_round(const uint32_t* __restrict__ rows_t, int K, uint32_t tag, SetLds& L,
+                                             uint32_t (&v)[kSetChMax][4], int lane,
+                                             bool& failed, uint32_t* scratch) {
+  const int hn = min(kSetRound, K / 512 - H * kSetRound);
+  const uint32_t tag2 = tag | (tag << 16);
+  uint32_t pending = (1u << hn) - 1u;  // wave-uniform
+  uint32_t it = 0;
+  while (true) {
+#pragma unroll
+    for (int c = 0; c < kSetRound; ++c) {
+      if (!((pending >> c) & 1u)) continue;
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        __builtin_amdgcn_global_load_lds((const BP_GLOBAL void*)(rows_t + (H * kSetRound + c) * 512 + q * 256 + lane * 4),
+                                         (BP_LDS void*)&L.tin[c * 512 + q * 256], 16, 0, kDeviceScope);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
+#pragma unroll
+    for (int c = 0; c < kSetRound; ++c) {
+      if (!((pending >> c) & 1u)) continue;
+      const u32x4* tp = reinterpret_cast<const u32x4*>(&L.tin[c * 512 + lane * 8]);
+      const u32x4 a = tp[0], b = tp[1];
+      const uint32_t t0 = (a.y & 0xffff0000u) | (a.x >> 16), t1 = (a.w & 0xffff0000u) | (a.z >> 16);
+      const uint32_t t2 = (b.y & 0xffff0000u) | (b.x >> 16), t3 = (b.w & 0xffff0000u) | (b.z >> 16);
+      const bool ok = t0 == tag2 && t1 == tag2 && t2 == tag2 && t3 == tag2;
+      if (__all(ok) || failed) {
+        uint32_t(&d)[4] = v[H * kSetRound + c];
+        d[0] = (a.y << 16) | (a.x & 0xffffu);
+        d[1] = (a.w << 16) | (a.z & 0xffffu);
+        d[2] = (b.y << 16) | (b.x & 0xffffu);
+        d[3] = (b.w << 16) | (b.z & 0xffffu);
+        pending &= ~(1u << c);
+      }
+    }
+    if (pending == 0u) break;
+    if (++it > kSpinCapGlobal && !failed) {
+      failed = true;
+      record_error(scratch);
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+static_assert(kSetChMax == 2 * kSetRound, "the input is gathered in two rounds");
+
+// Reads an external input vector (K bf16 at src) into registers.
+__device__ __forceinline__ void load_input(const BP_GLOBAL uint16_t* src, int K, uint32_t (&v)[kSetChMax][4],
+                                           int lane) {
+  const int nch = K / 512;
+#pragma unroll
+  for (int c = 0; c < kSetChMax; ++c) {
+    if (c < nch) {
+      const u32x4 t = *reinterpret_cast<GlobalVec>(src + c * 512 + lane * 8);
+      v[c][0] = t.x;
+      v[c][1] = t.y;
+      v[c][2] = t.z;
+      v[c][3] = t.w;
+    }
+  }
+}
+
+// The workgroup's sync wave: the input of every stage into LDS, in stage order.
 template <int KIND>
 __device__ __forceinline__ void sync_wave(StageTable st, int S, uint32_t* __restrict__ scratch, SetLds& L,
                                           int scale_dt, int lane) {
-  const int g = blockIdx.x, G = gridDim.x;
-  // launch generation: every workgroup of the previous launches added 1 to the launch counter
-  const uint32_t gen = ld_agent(&scratch[0]) / static_cast<uint32_t>(G);
-  const uint32_t tag = gen + 1u;  // never 0, the value of a zeroed scratch (wraps after 2^32 - 1 launches)
-  uint32_t* flags = scratch + kFlagWord;
+  const int g = blockIdx.x;
+  uint32_t* tagged = scratch + kWordsHeader;
+  const uint32_t tag = L.tag;
   bool failed = false;
 
   for (int s = 0; s < S; ++s) {
     const int K = st[s].K;
-    const int row0 = L.rows[s][0];
-    const int rows = L.rows[s][kSetCW] - row0;
-    int active = 0;  // compute waves of this workgroup with rows in the stage
-#pragma unroll
-    for (int i = 0; i < kSetCW; ++i) active += L.rows[s][i] < L.rows[s][i + 1] ? 1 : 0;
-    uint16_t* xl = L.x[s & 1];
     const int nch = K / 512;
+    uint16_t* xl = L.x[s & 1];
+    // x[s & 1] and scale[s & 1] were last used by stage s - 2
+    if (s >= 2) wait_done(L, s - 2, active_consumers(L, s - 2), failed, scratch);
 
-    // 1. the input vector into LDS: published rows of an earlier stage, or an external vector
-    const int ws = st[s].wait_stage;
-    if (ws >= 0) {
-      const int64_t e0 = (static_cast<const char*>(st[s].src) - static_cast<const char*>(st[ws].y)) / 2;
-      const int64_t Nw = st[ws].N;
-      wait_flags(flags + static_cast<int64_t>(ws) * G, owner_of(e0, Nw, G), owner_of(e0 + K - 1, Nw, G), tag, lane,
-                 failed, scratch);
-      gather_rows(static_cast<const uint16_t*>(st[s].src), K, xl, lane);
-    } else {
-      const BP_GLOBAL uint16_t* src = (const BP_GLOBAL uint16_t*)(st[s].src);
-      for (int c0 = 0; c0 < nch; c0 += 8) {
-        u32x4 t[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (c0 + j < nch) t[j] = *reinterpret_cast<GlobalVec>(src + (c0 + j) * 512 + lane * 8);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (c0 + j < nch) *reinterpret_cast<u32x4*>(xl + (c0 + j) * 512 + lane * 8) = t[j];
-      }
-    }
-    // 2. optional unit-RMS scaling: mean square in a fixed order (per lane over its chunks, then a wave butterfly).
-    //    Chunks are taken four at a time so that their LDS reads are in flight together.
-    if (st[s].renorm) {
-      float ss = 0.f;
-      for (int c0 = 0; c0 < nch; c0 += 4) {
-        u32x4 t[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          t[j] = c0 + j < nch ? *reinterpret_cast<const u32x4*>(xl + (c0 + j) * 512 + lane * 8) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t d[4] = {t[j].x, t[j].y, t[j].z, t[j].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float lo = bf16_bits_to_float(d[e] & 0xffffu), hi = bf16_bits_to_float(d[e] >> 16);
-            ss += lo * lo;
-            ss += hi * hi;
-          }
-        }
-      }
-      float tot[1] = {ss};
-      wave_transpose_reduce<1>(tot, lane);  // every lane holds the total
-      const float ms = tot[0] / static_cast<float>(K);
-      const float inv = ms > 0.f ? 1.f / sqrtf(ms) : 1.f;
-      for (int c0 = 0; c0 < nch; c0 += 4) {
-        u32x4 t[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (c0 + j < nch) t[j] = *reinterpret_cast<const u32x4*>(xl + (c0 + j) * 512 + lane * 8);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (c0 + j >= nch) continue;
-          uint32_t d[4] = {t[j].x, t[j].y, t[j].z, t[j].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = float_to_bf16_bits(bf16_bits_to_float(d[e] & 0xffffu) * inv);
-            const uint32_t hi = float_to_bf16_bits(bf16_bits_to_float(d[e] >> 16) * inv);
-            d[e] = lo | (hi << 16);
-          }
-          *reinterpret_cast<u32x4*>(xl + (c0 + j) * 512 + lane * 8) = u32x4{d[0], d[1], d[2], d[3]};
-        }
-      }
-    }
-    if (g == 0 && st[s].x_used != nullptr) {
-      BP_GLOBAL uint16_t* xu = (BP_GLOBAL uint16_t*)(st[s].x_used);
-      for (int c0 = 0; c0 < nch; ++c0)
-        *reinterpret_cast<BP_GLOBAL u32x4*>(xu + c0 * 512 + lane * 8) =
-            *reinterpret_cast<const u32x4*>(xl + c0 * 512 + lane * 8);
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (lane == 0) __hip_atomic_store(&L.xready, s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-
-    // 3. while the compute waves work: int8 row scales of the stage into LDS
+    // int8 row scales of the stage into LDS (the consumers apply them at the ends of their rows)
     if constexpr (KIND == kInt8) {
+      const int row0 = L.rows[s][0];
+      const int rows = L.rows[s][kSetCW] - row0;
       for (int i = lane; i < rows; i += kWave) {
         const int row = row0 + i;
         int seg = 0, seg_begin = 0;
@@ -467,29 +512,27 @@ __device__ __forceinline__ void sync_wave(StageTable st, int S, uint32_t* __rest
       }
     }
 
-    // 4. wait for the compute waves, publish the stage's rows
-    {
-      uint32_t it = 0;
-      while (!failed && lds_load_relaxed(&L.ydone[s & 1]) < active) {
-        if (++it > kSpinCapLds) {
-          failed = true;
-          record_error(scratch);
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // the input vector: published rows of an earlier stage (read once this workgroup's own consumers are done
+    // with that stage: the other workgroups finish it at about the same time), or an external vector
+    const int ws = st[s].wait_stage;
+    uint32_t v[kSetChMax][4];
+    if (ws >= 0) {
+      wait_done(L, ws, active_consumers(L, ws), failed, scratch);
+      const int64_t e0 = (static_cast<const char*>(st[s].src) - static_cast<const char*>(st[ws].y)) / 2;
+      gather_round<0>(tagged + L.tag_off[ws] + e0, K, tag, L, v, lane, failed, scratch);
+      if (K > kSetRound * 512) gather_round<1>(tagged + L.tag_off[ws] + e0, K, tag, L, v, lane, failed, scratch);
+    } else {
+      load_input((const BP_GLOBAL uint16_t*)(st[s].src), K, v, lane);
     }
-    // rows with device-scope stores; once they are acknowledged, the flag
-    uint16_t* y = static_cast<uint16_t*>(st[s].y);
-    for (int i = lane; i < rows; i += kWave) {
-      float v = L.y[s & 1][i];
-      if constexpr (KIND == kInt8) v *= L.scale[s & 1][i];
-      st_agent16(&y[row0 + i], float_to_bf16_bits(v));
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    if (lane == 0) {
-      st_agent(&flags[static_cast<int64_t>(s) * G + g], tag);
-      __hip_atomic_store(&L.ydone[s & 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    write_input(v, K, st[s].renorm != 0, xl, lane);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane == 0) lds_store_relaxed(&L.xready, s + 1);
+    // the input as used, for the caller (x[s & 1] stays unchanged until stage s + 2)
+    if (g == 0 && st[s].x_used != nullptr) {
+      BP_GLOBAL uint16_t* xu = (BP_GLOBAL uint16_t*)(st[s].x_used);
+      for (int c0 = 0; c0 < nch; ++c0)
+        *reinterpret_cast<BP_GLOBAL u32x4*>(xu + c0 * 512 + lane * 8) =
+            *reinterpret_cast<const u32x4*>(xl + c0 * 512 + lane * 8);
     }
   }
   if (lane == 0) __hip_atomic_fetch_add(&scratch[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -509,26 +552,34 @@ __global__ __launch_bounds__(kSetThreads) void linear_set_kernel(const BpSetStag
     const int64_t u = static_cast<int64_t>(blockIdx.x) * kSetCW + i;
     lds.rows[s][i] = static_cast<int32_t>(u * st[s].N / T);
   }
+  for (int s = threadIdx.x; s < S; s += kSetThreads) lds.done[s] = 0;
   if (threadIdx.x < kSetCW) {
     lds.landed[threadIdx.x] = 0;
     lds.consumed[threadIdx.x] = 0;
   }
   if (threadIdx.x == 0) {
+    int32_t off = 0;
+    for (int s = 0; s < S; ++s) {
+      lds.tag_off[s] = off;
+      off += (st[s].N + 7) & ~7;
+    }
     lds.xready = 0;
-    lds.ydone[0] = 0;
-    lds.ydone[1] = 0;
+    // launch generation: every workgroup of the previous launches added 1 to the launch counter
+    const uint32_t gen = ld_agent(&scratch[0]) / gridDim.x;
+    lds.tag = gen % 65535u + 1u;  // 1..65535: a zeroed scratch holds no valid row
   }
   __syncthreads();
   if (wave == kSetSyncWave) {
     sync_wave<KIND>(st, S, scratch, lds, scale_dt, lane);
   } else if (wave >= kSetCW) {
-    producer_wave<KIND>(st, lds, S, wave - kSetCW, lane);
+    producer_wave<KIND>(st, lds, S, wave - kSetCW, lane, scratch);
   } else {
     Consumer<KIND> cons;
     cons.failed = false;
     cons.n = 0;
     cons.seen = 0;
-    cons.run(st, lds, S, wave, lane);
+    cons.tag = lds.tag;
+    cons.run(st, lds, S, wave, lane, scratch + kWordsHeader);
   }
 }
 
@@ -538,6 +589,7 @@ int set_validate(const BpSetStage* st, int S, int wkind, int G) {
   if (wkind != kBf16 && wkind != kInt8) return BP_E_UNSUPPORTED;
   if (G > 65536) return BP_E_UNSUPPORTED;
   const int64_t chunk = wkind == kBf16 ? 512 : 1024;
+  int64_t words = 0;
   for (int s = 0; s < S; ++s) {
     const BpSetStage& a = st[s];
     if (a.src == nullptr || a.y == nullptr) return BP_E_INVALID_ARG;
@@ -562,11 +614,17 @@ int set_validate(const BpSetStage* st, int S, int wkind, int G) {
       const uintptr_t b = reinterpret_cast<uintptr_t>(a.src), e = b + 2 * static_cast<uintptr_t>(a.K);
       if (b < lo || e > hi) return BP_E_INVALID_ARG;
     }
+    words += (a.N + 7) & ~7;
   }
+  if (words > (int64_t{1} << 30)) return BP_E_UNSUPPORTED;
   return BP_OK;
 }
 
-int64_t scratch_words(int S, int G) { return kFlagWord + static_cast<int64_t>(S) * G; }
+int64_t scratch_words(const BpSetStage* st, int S) {
+  int64_t words = kWordsHeader;
+  for (int s = 0; s < S; ++s) words += (st[s].N + 7) & ~7;
+  return words;
+}
 
 }  // namespace
 }  // namespace bp
@@ -575,7 +633,7 @@ extern "C" {
 
 size_t bp_linear_set_scratch_bytes(const BpSetStage* stages, int num_stages, int num_workgroups) {
   if (stages == nullptr || num_stages <= 0 || num_workgroups <= 0) return 0;
-  return static_cast<size_t>(bp::scratch_words(num_stages, num_workgroups)) * sizeof(uint32_t);
+  return static_cast<size_t>(bp::scratch_words(stages, num_stages)) * sizeof(uint32_t);
 }
 
 int bp_linear_set_workgroups(int device) {

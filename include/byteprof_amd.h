@@ -132,7 +132,7 @@ typedef struct BpSetStage {
   void* y;              /* bf16 [N], 16-byte aligned: the stage's outputs */
   void* x_used;         /* bf16 [K] or NULL: receives the input vector the stage used (after renormalisation) */
   int32_t K;            /* input length: a multiple of 512 (bf16 weights) or 1024 (int8), at most 8192 */
-  int32_t N;            /* rows: at most (2048 - 1) * workgroups */
+  int32_t N;            /* rows: at most (512 - 1) * workgroups */
   int32_t wait_stage;   /* -1, or the index (< this stage's) of the stage whose outputs src reads (src must then
                            lie inside that stage's y) */
   int32_t renorm;       /* 1: renormalise the input to unit RMS; 0: use it as is */
@@ -143,11 +143,11 @@ typedef struct BpSetStage {
   const void* scale[4]; /* int8: per-row scales of each segment (dtype given to bp_linear_set_run) */
 } BpSetStage;
 
-/* Bytes of scratch a launch of these stages on num_workgroups workgroups needs: a launch counter, an error flag
- * and one publish flag per stage and workgroup. The scratch must be zero before its first launch and is then reused
- * as is by every later launch (no reset between launches or graph replays). The 32-bit word at index 32 becomes
- * non-zero if a launch gave up waiting for another workgroup (that launch's later results are invalid); the host
- * clears it. */
+/* Bytes of scratch a launch of these stages needs: a launch counter, an error flag and every stage's rows tagged
+ * with the launch (4 bytes per row, rows rounded up to 8); num_workgroups is the grid the launches use. The scratch
+ * must be zero before its first launch and is then reused as is by every later launch (no reset between launches
+ * or graph replays). The 32-bit word at index 32 becomes non-zero if a launch gave up waiting for another
+ * workgroup (that launch's later results are invalid); the host clears it. */
 size_t bp_linear_set_scratch_bytes(const BpSetStage* stages, int num_stages, int num_workgroups);
 
 /* Workgroups the set kernel is launched with on `device`: one per compute unit (0 on error). */

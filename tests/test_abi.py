@@ -130,7 +130,7 @@ def test_linear_set_validation_rejects_bad_descriptors(L):
     assert rc(_set_stages(k=1000)) == -2                     # K not a multiple of the 512-element chunk
     assert rc(_set_stages(k=1536), kind=1) == -2             # int8: K a multiple of 1024
     assert rc(_set_stages(k=16384)) == -2                    # input longer than the LDS buffer
-    assert rc(_set_stages(n=2048 * 256)) == -2               # more rows per workgroup than LDS holds
+    assert rc(_set_stages(n=512 * 256)) == -2                # more rows per workgroup than LDS holds
     assert rc(_set_stages(kind=0), kind=1) == -1             # int8 without scales
     bad = _set_stages()
     bad[1].wait_stage = 1                                    # a stage cannot wait for itself
@@ -144,7 +144,7 @@ def test_linear_set_validation_rejects_bad_descriptors(L):
     bad = _set_stages()
     bad[0].nseg = 5
     assert rc(bad) == -1
-    assert rc(_set_stages(n_stages=300)) == -2               # more stages than the LDS row table holds
+    assert rc(_set_stages(n_stages=100)) == -2               # more stages than the LDS tables hold
     bad = _set_stages()
     bad[1].src = 0x2000 + 2 * 4096 - 16                      # a dependent input must lie inside its source's y
     assert rc(bad) == -1
@@ -152,6 +152,6 @@ def test_linear_set_validation_rejects_bad_descriptors(L):
     bad[0].y = 0x2008                                        # outputs must be 16-byte aligned
     assert rc(bad) == -1
     arr = _set_stages(n_stages=3, n=4093)
-    # launch counter + error flag lines, 3 x 256 publish flags
-    assert L.bp_linear_set_scratch_bytes(ctypes.addressof(arr), 3, 256) == 4 * (64 + 3 * 256)
+    # launch counter + error flag lines, 3 x (4093 rounded up to 8) tagged rows
+    assert L.bp_linear_set_scratch_bytes(ctypes.addressof(arr), 3, 256) == 4 * (64 + 3 * 4096)
     assert L.bp_linear_set_scratch_bytes(None, 0, 256) == 0
