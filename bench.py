@@ -1,19 +1,21 @@
 #!/usr/bin/env python3
 """Benchmark of the batch-1 decode hot path on one MI355X.
 
-One step = one replay of a HIP graph holding the OLMo-2-1B-shaped decode-step linear set at M = 1 in bf16
-(byteprof_amd/decode_set.py): 16 layers x (q, k, v, o 2048 -> 2048; gate, up 2048 -> 8192; down 8192 -> 2048) +
-the LM head 2048 -> 100352, 113 skinny launches in decode order, every weight distinct (2.56 GB), all operands
-resident in HBM before the timed region.
+One step = one pass over the OLMo-2-1B-shaped decode-step linear set at M = 1 in bf16 (byteprof_amd/decode_set.py):
+16 layers x (q, k, v, o 2048 -> 2048; gate, up 2048 -> 8192; down 8192 -> 2048) + the LM head 2048 -> 100352,
+113 linears, every weight distinct (2.56 GB, ten times the 256 MB Infinity Cache), all operands resident in HBM
+before the timed region. The step runs as one launch of the persistent set kernel (csrc/linear_set.hip) with the
+reference's set semantics: every linear reads its own seeded unit-RMS input (q|k|v and gate|up share theirs), as
+in byteprof's set benchmark, where each linear is an independent skinny call (tools/skinny_bench.py:45-71).
 
-Printed (one JSON line): the set's aggregate HBM throughput (algorithmic bytes = weights + activations + outputs,
-each once: 2,560,237,568 B per step) in GB/s, us per set and % of the 8 TB/s peak; the roofline of the dominant
-kernel instantiation (the one with the largest share of the step's kernel time): its launches' algorithmic bytes
-over their average launch duration, measured with HIP events on the launch stream over a graph of those launches
-(rocprofv3 attributes the dispatch cost to the kernel too, so the two agree), and the HBM traffic per launch read
-from the committed rocprofv3 counter summary (profiles/skinny_dot_kernel_decode_set.md) when it covers the same
-kernel and shapes; the CPU baseline (torch F.linear, the reference's CPU path for these linears, on the host cores);
-and secondary figures (per-shape launch times, the int8 set with fp16 scales, the fused mLSTM block).
+Printed (one JSON line): the step's aggregate HBM throughput (algorithmic bytes = weights + activations + outputs,
+each once: 2,560,237,568 B per step) in GB/s, us per set and % of the 8 TB/s peak; the roofline of the set kernel
+(the only kernel of the step): algorithmic bytes per launch over the average launch duration, from HIP events on
+the launch stream over the timed steps, and the HBM traffic per launch from the committed rocprofv3 counter
+summary (profiles/linear_set_kernel_decode_set.md); the CPU baseline (torch F.linear, the reference's CPU path for
+these linears, on the host cores); and secondary figures: the same set as a dependent decode chain in one launch
+(each stage reads the renormalised output it depends on), the 113-launch HIP graph of skinny kernels, the int8
+set (fp16 scales) both ways, and the fused mLSTM block.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
 """
@@ -41,6 +43,7 @@ def log(msg: str) -> None:
 
 
 PROFILE = ROOT / "profiles" / "skinny_dot_kernel_decode_set.md"
+SET_PROFILE = ROOT / "profiles" / "linear_set_kernel_decode_set.md"
 
 
 def per_shape(ops, kind: str, m: int) -> dict:
@@ -66,11 +69,12 @@ def per_shape(ops, kind: str, m: int) -> dict:
     return res
 
 
-def profiled_traffic() -> dict[tuple[str, str], float]:
-    """(kernel, 'NxK') -> HBM bytes per launch from the committed counter summary ('traffic:' lines)."""
+def profiled_traffic(path: Path = PROFILE) -> dict[tuple[str, str], float]:
+    """(kernel, 'NxK' or workload tag) -> HBM bytes per launch from a committed counter summary ('traffic:'
+    lines)."""
     out = {}
-    if PROFILE.exists():
-        for line in PROFILE.read_text().splitlines():
+    if path.exists():
+        for line in path.read_text().splitlines():
             if line.startswith("traffic: "):
                 kernel, shape, nbytes = line[len("traffic: "):].rsplit(" ", 2)
                 out[(kernel, shape)] = float(nbytes)
@@ -161,13 +165,59 @@ def mlstm_block(device) -> dict:
             "us_per_step": us / t, "bytes": nbytes, "gbs": nbytes / us / 1e3}
 
 
+def time_set(lset, steps: int, warmup: int) -> tuple[float, float]:
+    """(ms per launch from HIP events on the launch stream, ms per launch by the host clock) over `steps`
+    back-to-back launches after `warmup` untimed ones, synchronised on both sides."""
+    import torch
+
+    for _ in range(warmup):
+        lset.run()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        lset.run()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    if lset.timed_out():
+        raise RuntimeError("a set launch gave up waiting for another workgroup: its results are invalid")
+    return ev0.elapsed_time(ev1) / steps, wall_ms
+
+
+def set_figures(lset, nbytes: int, steps: int) -> dict:
+    ev_ms, wall_ms = time_set(lset, steps, max(2, steps // 10))
+    ms = max(ev_ms, wall_ms)
+    return {"us_per_set": ms * 1e3, "gbs": nbytes / ms / 1e6, "pct_of_hbm_peak": nbytes / ms / 1e6 / HBM_PEAK_GBS
+            * 100, "stages": len(lset.stages)}
+
+
+def per_launch_graph(ops, kind: str, nbytes: int) -> dict:
+    """The same linears as a HIP graph of one skinny launch each (the reference's execution model)."""
+    from byteprof_amd import decode_set as D
+
+    g = D.capture(ops)
+    D.time_replays(g, 5, 1)
+    ms = statistics.median(D.time_replays(g, 20, 5))
+    del g
+    out = {"launches": len(ops), "us_per_set": ms * 1e3, "gbs": nbytes / ms / 1e6,
+           "pct_of_hbm_peak": nbytes / ms / 1e6 / HBM_PEAK_GBS * 100}
+    if kind == "bf16":
+        shapes = per_shape(ops, kind, 1)
+        out["kernels"] = shapes
+        out["roofline"] = roofline(shapes)
+        out["empty_launch_us"] = D.dispatch_gap_us()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-extras", action="store_true", help="skip the per-shape, int8 and mLSTM figures")
+    ap.add_argument("--no-extras", action="store_true", help="skip the secondary figures")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -187,57 +237,64 @@ def main() -> int:
 
     _lib.lib()
     log("[bench] building the bf16 decode-step set (2.56 GB of weights)")
-    ops = D.build("bf16", 1, device, seed=0)
-    nbytes = D.algorithmic_bytes(ops, "bf16", 1)
-    g = D.capture(ops)
-    log("[bench] warm-up")
-    for _ in range(a.warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    log(f"[bench] timing {a.steps} steps")
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(a.steps):
-        g.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / a.steps
-    ev_ms = ev0.elapsed_time(ev1) / a.steps
-    ms = max(wall_ms, ev_ms)
+    weights = D.make_weights("bf16", device, seed=0)
+    chain = D.build_chain("bf16", device, dependent=False, weights=weights)
+    nbytes = D.chain_bytes("bf16")
+    log(f"[bench] warm-up {a.warmup}, timing {a.steps} steps")
+    ev_ms, wall_ms = time_set(chain.lset, a.steps, a.warmup)
+    ms = max(ev_ms, wall_ms)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] {ms * 1e3:.1f} us per set, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
-    del g
 
+    achieved = nbytes / (ev_ms * 1e-3) / 1e9
+    traffic = profiled_traffic(SET_PROFILE).get(("linear_set_kernel<0>", "set-independent"))
     result = {
         "metric": METRIC, "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0, 0.02^2) bf16 weights, unit-RMS N(0,1) activations)",
         "config": {"workload": ("OLMo-2-1B-shaped decode-step linear set at M=1, bf16: 16 x (q,k,v,o 2048->2048; "
-                                "gate,up 2048->8192; down 8192->2048) + LM head 2048->100352, 113 skinny launches "
-                                "in one HIP graph"),
-                   "M": 1, "linears": len(ops), "bytes_per_step": nbytes, "us_per_set": ms * 1e3,
+                                "gate,up 2048->8192; down 8192->2048) + LM head 2048->100352, 113 linears with "
+                                "their own inputs, one persistent launch of 65 stages"),
+                   "M": 1, "linears": len(D.shapes()), "bytes_per_step": nbytes, "us_per_set": ms * 1e3,
                    "pct_of_hbm_peak": gbs / HBM_PEAK_GBS * 100, "event_ms": ev_ms, "wall_ms": wall_ms},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "linear_set_kernel<0>",
+                     "launches_per_step": 1, "avg_us_per_launch": ev_ms * 1e3, "bytes_per_launch": nbytes},
     }
-    shapes = per_shape(ops, "bf16", 1)
-    result["roofline"] = roofline(shapes)
-    result["roofline"]["empty_launch_us"] = D.dispatch_gap_us()
+    ops = None
     if not a.no_extras:
-        result["kernels"] = shapes
+        log("[bench] dependent bf16 chain")
+        dep = D.build_chain("bf16", device, dependent=True, weights=weights)
+        result["dependent_chain"] = set_figures(dep.lset, nbytes, 50)
+        del dep
+        log("[bench] 113-launch graph")
+        ops = D.build("bf16", 1, device, seed=0, weights=weights)
+        result["per_launch_graph"] = per_launch_graph(ops, "bf16", nbytes)
         log("[bench] int8 set")
-        ops8 = D.build("int8", 1, device, seed=0)
-        nb8 = D.algorithmic_bytes(ops8, "int8", 1)
-        g8 = D.capture(ops8)
-        D.time_replays(g8, 5, 1)
-        ms8 = statistics.median(D.time_replays(g8, 20, 5))
-        result["int8_set"] = {"us_per_set": ms8 * 1e3, "bytes_per_step": nb8, "gbs": nb8 / (ms8 * 1e-3) / 1e9,
-                              "bf16_over_int8_time": ms / ms8, "scales": "fp16 per output row"}
-        del g8, ops8
+        w8 = D.make_weights("int8", device, seed=0)
+        nb8 = D.chain_bytes("int8")
+        ind8 = D.build_chain("int8", device, dependent=False, weights=w8)
+        i8 = set_figures(ind8.lset, nb8, 100)
+        del ind8
+        dep8 = D.build_chain("int8", device, dependent=True, weights=w8)
+        d8 = set_figures(dep8.lset, nb8, 50)
+        del dep8
+        ops8 = D.build("int8", 1, device, seed=0, weights=w8)
+        g8 = per_launch_graph(ops8, "int8", nb8)
+        del ops8
+        result["int8_set"] = {"bytes_per_step": nb8, "scales": "fp16 per output row", "independent": i8,
+                              "dependent_chain": d8, "per_launch_graph": g8,
+                              "bf16_over_int8_time": ms * 1e3 / i8["us_per_set"],
+                              "bf16_over_int8_time_dependent": result["dependent_chain"]["us_per_set"]
+                              / d8["us_per_set"]}
+        del w8
+        torch.cuda.empty_cache()
         log("[bench] mLSTM block")
         result["mlstm"] = mlstm_block(device)
     if not a.no_cpu:
         log("[bench] CPU baseline")
+        if ops is None:
+            ops = D.build("bf16", 1, device, seed=0, weights=weights)
         result["cpu_baseline"] = cpu_baseline(ops)
     print(json.dumps(result), flush=True)
     return 0

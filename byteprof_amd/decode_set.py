@@ -58,16 +58,21 @@ class Op:
         S.skinny_mm(self.x, *self.args, out=self.y)
 
 
-def build(kind: str = "bf16", m: int = 1, device="cuda:0", seed: int = 0, scale_dtype=torch.float16) -> list[Op]:
-    """Seeded operands of the set; kind 'bf16' or 'int8' (per-row scales in `scale_dtype`)."""
+def build(kind: str = "bf16", m: int = 1, device="cuda:0", seed: int = 0, scale_dtype=torch.float16,
+          weights: dict | None = None) -> list[Op]:
+    """Seeded operands of the set; kind 'bf16' or 'int8' (per-row scales in `scale_dtype`). With `weights`
+    (make_weights of the same kind) the launches use those tensors and only the inputs are drawn here."""
     g = torch.Generator(device=device).manual_seed(seed)
     ops = []
     for name, n, k in shapes():
-        w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
-        args = (w,) if kind == "bf16" else quantize_rowwise_int8(w, scale_dtype)
+        if weights is not None:
+            args = weights[name]
+        else:
+            w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+            args = (w,) if kind == "bf16" else quantize_rowwise_int8(w, scale_dtype)
+            del w
         x = unit_rms(torch.randn(m, k, generator=g, device=device))
         ops.append(Op(name, n, k, args, x, torch.empty(m, n, dtype=torch.bfloat16, device=device)))
-        del w
     return ops
 
 

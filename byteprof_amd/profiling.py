@@ -1,6 +1,8 @@
 """Short GPU programs to run under rocprofv3 (kernel trace, HBM counters).
 
   python -m byteprof_amd.profiling set  [--kind bf16|int8] [--replays R]   the decode-step set graph, R replays
+  python -m byteprof_amd.profiling chain [--kind bf16|int8] [--dependent] [--replays R]
+                                                                         the set as one persistent launch, R launches
   python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
   python -m byteprof_amd.profiling summarize TRACE_DB [--fetch DB --write DB --fetch-copy DB --write-copy DB
                                              --copy-mib 256]               text summary of rocprofv3 databases
@@ -18,15 +20,18 @@ import sys
 import torch
 
 
-def _kernel_stats(db_path: str) -> list[tuple[str, int, int, float, float]]:
-    """(kernel name, grid threads, calls, total us, average us) from a kernel-trace database, longest total first;
-    the grid size tells the launches of one kernel instantiation on different shapes apart."""
+def _kernel_stats(db_path: str) -> list[tuple[str, int, int, float, float, float]]:
+    """(kernel name, grid threads, calls, total us, average us, median us) from a kernel-trace database, longest
+    total first; the grid size tells the launches of one kernel instantiation on different shapes apart."""
     import sqlite3
+    import statistics
 
     cur = sqlite3.connect(db_path).cursor()
-    rows = cur.execute("select name, grid_x * grid_y * grid_z, count(*), sum(duration), avg(duration) from kernels "
-                       "group by name, grid_x, grid_y, grid_z order by sum(duration) desc").fetchall()
-    return [(n, int(gs), int(c), tot / 1e3, avg / 1e3) for n, gs, c, tot, avg in rows]
+    groups: dict[tuple[str, int], list[float]] = {}
+    for name, grid, dur in cur.execute("select name, grid_x * grid_y * grid_z, duration from kernels"):
+        groups.setdefault((name, int(grid)), []).append(dur / 1e3)
+    out = [(n, gs, len(d), sum(d), sum(d) / len(d), statistics.median(d)) for (n, gs), d in groups.items()]
+    return sorted(out, key=lambda r: -r[3])
 
 
 def _counter_avgs(db_path: str) -> dict[tuple[str, int], tuple[str, int, float]]:
@@ -41,15 +46,15 @@ def _counter_avgs(db_path: str) -> dict[tuple[str, int], tuple[str, int, float]]
 
 
 def _short(name: str) -> str:
-    return name.split("(")[0].replace("void ", "")
+    return name.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
 
 
 def summarize(a) -> int:
     print("## kernel trace (rocprofv3 --kernel-trace --stats)")
-    print(f"{'kernel':<48} {'grid threads':>12} {'calls':>7} {'total us':>11} {'avg us':>9}")
-    for name, grid, calls, tot, avg in _kernel_stats(a.db):
+    print(f"{'kernel':<48} {'grid threads':>12} {'calls':>7} {'total us':>11} {'avg us':>9} {'median us':>10}")
+    for name, grid, calls, tot, avg, med in _kernel_stats(a.db):
         if a.all or "bp::" in name:
-            print(f"{_short(name)[:48]:<48} {grid:>12} {calls:>7} {tot:>11.1f} {avg:>9.3f}")
+            print(f"{_short(name)[:48]:<48} {grid:>12} {calls:>7} {tot:>11.1f} {avg:>9.3f} {med:>10.3f}")
     if not a.fetch:
         return 0
     expected_kib = a.copy_mib * 1024
@@ -71,6 +76,13 @@ def summarize(a) -> int:
         wv = write.get(key, ("", 0, 0.0))[2]
         traffic = (fv * f_scale + wv * w_scale) * 1024 / 1e6
         print(f"{_short(name)[:48]:<48} {grid:>12} {k:>10} {fv:>11.1f} {wv:>10.1f} {traffic:>11.3f}")
+    if a.chain_tag:
+        print()
+        print(f"## traffic per launch of the persistent set kernel, {a.chain_tag} (bytes; read by bench.py)")
+        for key in sorted(fetch):
+            if "linear_set_kernel" in key[0]:
+                nbytes = (fetch[key][2] * f_scale + write.get(key, ("", 0, 0.0))[2] * w_scale) * 1024
+                print(f"traffic: {_short(key[0]).replace('bp::', '')} {a.chain_tag} {nbytes:.0f}")
     if a.set_kind:
         print()
         print(f"## traffic per launch of the {a.set_kind} decode-step set shapes (bytes; read by bench.py)")
@@ -97,7 +109,7 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=("set", "copy", "summarize"))
+    ap.add_argument("what", choices=("set", "chain", "copy", "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
     ap.add_argument("--write", help="summarize: WRITE_SIZE database of the workload")
@@ -106,7 +118,9 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--all", action="store_true", help="summarize: include kernels outside this library")
     ap.add_argument("--set-kind", choices=("bf16", "int8"), help="summarize: emit traffic lines for the set shapes")
+    ap.add_argument("--chain-tag", help="summarize: emit traffic lines for the set kernel under this tag")
     ap.add_argument("--kind", default="bf16", choices=("bf16", "int8"))
+    ap.add_argument("--dependent", action="store_true", help="chain: stages read the outputs they depend on")
     ap.add_argument("--replays", type=int, default=5)
     ap.add_argument("--mib", type=int, default=256)
     ap.add_argument("--reps", type=int, default=5)
@@ -126,6 +140,17 @@ def main(argv=None) -> int:
     from . import decode_set as D
 
     _lib.lib()
+    if a.what == "chain":
+        ch = D.build_chain(a.kind, device, dependent=a.dependent)
+        for _ in range(a.replays):
+            ch.lset.run()
+        torch.cuda.synchronize()
+        if ch.lset.timed_out():
+            print("a launch gave up waiting for another workgroup", file=sys.stderr)
+            return 1
+        print(f"ran the {a.kind} decode-step set as one persistent launch {a.replays} times "
+              f"({len(ch.stages)} stages, {'dependent' if a.dependent else 'independent'})", flush=True)
+        return 0
     ops = D.build(a.kind, 1, device)
     g = D.capture(ops)
     for _ in range(a.replays):
