@@ -36,6 +36,12 @@ SIGNATURES: dict[str, tuple] = {
                                 _c_vp]),
     "bp_skinny_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
                                 _c_vp, _c_size, _c_vp]),
+    "bp_skinny_mfma_config_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
+    "bp_skinny_mfma_k_step": (_c_int, [_c_int]),
+    "bp_skinny_mfma_bf16": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                     _c_vp, _c_size, _c_vp]),
+    "bp_skinny_mfma_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                     _c_int, _c_int, _c_vp, _c_size, _c_vp]),
     "bp_gemv_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
     "bp_splitk_reduce": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_int, _c_vp]),
     "bp_mlstm_multistep": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,

@@ -21,6 +21,11 @@ extern template SkinnyFn skinny_pick<kInt8, 4>(int, int, bool);
 extern template SkinnyFn skinny_pick<kInt8, 8>(int, int, bool);
 extern template SkinnyFn skinny_pick<kInt8, 16>(int, int, bool);
 
+// Matrix-core variant (skinny_mfma.hip): kernel for (kind, 16-row blocks per workgroup, waves, steps in flight
+// per wave), K per step.
+SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth);
+int mfma_k_step(int wkind);
+
 namespace {
 
 __global__ void splitk_reduce_kernel(const float* __restrict__ ws, uint16_t* __restrict__ y,
@@ -117,10 +122,68 @@ int skinny_launch(int wkind, const void* x, const void* w, const void* scale, in
   return launch_status();
 }
 
+int skinny_mfma_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y,
+                       int64_t M, int64_t N, int64_t K, int rb, int waves, int depth, int split, void* ws,
+                       size_t ws_bytes, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || M > 16) return BP_E_INVALID_ARG;
+  if (M == 0 || N == 0) return BP_OK;
+  if (x == nullptr || w == nullptr || y == nullptr) return BP_E_INVALID_ARG;
+  if (wkind == kInt8 && (scale == nullptr || scale_dt < BP_DT_BF16 || scale_dt > BP_DT_F32)) return BP_E_INVALID_ARG;
+  if (split < 1 || split > 1024) return BP_E_UNSUPPORTED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K == 0) {
+    fill_zero_bf16_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<uint16_t*>(y), M * N);
+    return launch_status();
+  }
+  const int step = mfma_k_step(wkind);
+  if (K % step != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
+    return BP_E_UNSUPPORTED;
+  SkinnyFn fn = mfma_pick(wkind, rb, waves, depth);
+  if (fn == nullptr) return BP_E_UNSUPPORTED;
+  const int64_t nst = K / step;
+  if (split > nst) split = static_cast<int>(nst);
+  if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
+    return BP_E_WORKSPACE;
+  const int64_t tiles = (N + 16 * rb - 1) / (16 * rb);
+  if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
+  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(split));
+  fn<<<grid, waves * kWave, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale,
+                                     scale_dt, static_cast<uint16_t*>(y), static_cast<float*>(ws),
+                                     static_cast<int>(M), N, K, split);
+  const int rc = launch_status();
+  if (rc != BP_OK || split == 1) return rc;
+  splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
+                                                       wkind == kInt8 ? scale : nullptr, scale_dt, M, N, split);
+  return launch_status();
+}
+
 }  // namespace
 }  // namespace bp
 
 extern "C" {
+
+int bp_skinny_mfma_config_supported(int wkind, int block_rows, int waves, int depth) {
+  return block_rows % 16 == 0 && bp::mfma_pick(wkind, block_rows / 16, waves, depth) != nullptr ? 1 : 0;
+}
+
+int bp_skinny_mfma_k_step(int wkind) {
+  return wkind == bp::kBf16 || wkind == bp::kInt8 ? bp::mfma_k_step(wkind) : 0;
+}
+
+int bp_skinny_mfma_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int block_rows,
+                        int waves, int depth, int split, void* workspace, size_t workspace_bytes, void* stream) {
+  if (block_rows <= 0 || block_rows % 16 != 0) return BP_E_UNSUPPORTED;
+  return bp::skinny_mfma_launch(bp::kBf16, x, w, nullptr, 0, y, M, N, K, block_rows / 16, waves, depth, split,
+                                workspace, workspace_bytes, stream);
+}
+
+int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y, int64_t M,
+                        int64_t N, int64_t K, int block_rows, int waves, int depth, int split, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (block_rows <= 0 || block_rows % 16 != 0) return BP_E_UNSUPPORTED;
+  return bp::skinny_mfma_launch(bp::kInt8, x, q, scale, scale_dtype, y, M, N, K, block_rows / 16, waves, depth,
+                                split, workspace, workspace_bytes, stream);
+}
 
 int bp_version(void) { return 100; }
 

