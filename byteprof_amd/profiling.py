@@ -3,6 +3,8 @@
   python -m byteprof_amd.profiling set  [--kind bf16|int8] [--replays R]   the decode-step set graph, R replays
   python -m byteprof_amd.profiling chain [--kind bf16|int8] [--dependent] [--replays R]
                                                                          the set as one persistent launch, R launches
+  python -m byteprof_amd.profiling skinny [--kind bf16|int8] [--n N] [--k K] [--m M] [--replays R]
+                                                                         skinny_mm over a ring of distinct weights
   python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
   python -m byteprof_amd.profiling summarize TRACE_DB [--fetch DB --write DB --fetch-copy DB --write-copy DB
                                              --copy-mib 256]               text summary of rocprofv3 databases
@@ -45,6 +47,20 @@ def _counter_avgs(db_path: str) -> dict[tuple[str, int], tuple[str, int, float]]
     return {(n, int(gs)): (c, int(k), v) for n, gs, c, k, v in rows}
 
 
+def _counter_table(db_path: str) -> dict[tuple[str, int], dict[str, tuple[int, float]]]:
+    """(kernel name, grid size) -> {counter: (dispatches, average value per dispatch)} for every counter of a
+    --pmc database (derived metrics such as MfmaUtil included)."""
+    import sqlite3
+
+    cur = sqlite3.connect(db_path).cursor()
+    rows = cur.execute("select kernel_name, grid_size, counter_name, count(*), avg(value) from counters_collection "
+                       "group by kernel_name, grid_size, counter_name").fetchall()
+    out: dict[tuple[str, int], dict[str, tuple[int, float]]] = {}
+    for n, gs, c, k, v in rows:
+        out.setdefault((n, int(gs)), {})[c] = (int(k), float(v))
+    return out
+
+
 def _short(name: str) -> str:
     return name.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
 
@@ -55,6 +71,14 @@ def summarize(a) -> int:
     for name, grid, calls, tot, avg, med in _kernel_stats(a.db):
         if a.all or "bp::" in name:
             print(f"{_short(name)[:48]:<48} {grid:>12} {calls:>7} {tot:>11.1f} {avg:>9.3f} {med:>10.3f}")
+    for db in a.pmc or []:
+        print()
+        print(f"## counters per dispatch ({db.split('/')[-2] if '/' in db else db})")
+        for (name, grid), counters in sorted(_counter_table(db).items()):
+            if "bp::" not in name and not a.all:
+                continue
+            vals = ", ".join(f"{c} {v:.4g}" for c, (_, v) in sorted(counters.items()))
+            print(f"{_short(name)[:64]:<64} grid {grid:>9}: {vals}")
     if not a.fetch:
         return 0
     expected_kib = a.copy_mib * 1024
@@ -109,19 +133,24 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=("set", "chain", "copy", "summarize"))
+    ap.add_argument("what", choices=("set", "chain", "skinny", "copy", "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
     ap.add_argument("--write", help="summarize: WRITE_SIZE database of the workload")
     ap.add_argument("--fetch-copy", help="summarize: FETCH_SIZE database of the calibration copy")
     ap.add_argument("--write-copy", help="summarize: WRITE_SIZE database of the calibration copy")
     ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--pmc", action="append", help="summarize: any --pmc database, counters per dispatch")
+    ap.add_argument("--valu", action="store_true", help="skinny: force the VALU kernels (the tuned VALU tiles)")
     ap.add_argument("--all", action="store_true", help="summarize: include kernels outside this library")
     ap.add_argument("--set-kind", choices=("bf16", "int8"), help="summarize: emit traffic lines for the set shapes")
     ap.add_argument("--chain-tag", help="summarize: emit traffic lines for the set kernel under this tag")
     ap.add_argument("--kind", default="bf16", choices=("bf16", "int8"))
     ap.add_argument("--dependent", action="store_true", help="chain: stages read the outputs they depend on")
     ap.add_argument("--replays", type=int, default=5)
+    ap.add_argument("--n", type=int, default=100352, help="skinny: output rows")
+    ap.add_argument("--k", type=int, default=2048, help="skinny: input length")
+    ap.add_argument("--m", type=int, default=16, help="skinny: activation rows")
     ap.add_argument("--mib", type=int, default=256)
     ap.add_argument("--reps", type=int, default=5)
     a = ap.parse_args(argv)
@@ -140,6 +169,26 @@ def main(argv=None) -> int:
     from . import decode_set as D
 
     _lib.lib()
+    if a.what == "skinny":
+        from .optim import skinny as S
+        from .quant.hip_int8 import quantize_rowwise_int8
+
+        per = a.n * a.k * (2 if a.kind == "bf16" else 1)
+        ring = []
+        for r in range(max(2, (1 << 30) // per)):  # >= 1 GiB of distinct weights: streamed from HBM every call
+            w = (torch.randn(a.n, a.k, device=device) * 0.02).to(torch.bfloat16)
+            ring.append((w,) if a.kind == "bf16" else quantize_rowwise_int8(w, torch.float16))
+            del w
+        x = torch.randn(a.m, a.k, device=device).to(torch.bfloat16)
+        y = torch.empty(a.m, a.n, dtype=torch.bfloat16, device=device)
+        cfg = S.get_cfg(a.kind, a.n, a.k, S._bm(a.m)) if a.valu else None
+        for _ in range(a.replays):
+            for args in ring:
+                S.skinny_mm(x, *args, out=y, cfg=cfg)
+        torch.cuda.synchronize()
+        print(f"skinny_mm {a.kind} {a.n}x{a.k} at M={a.m} ({'VALU' if a.valu else 'routed'}): {a.replays} passes "
+              f"over {len(ring)} weights", flush=True)
+        return 0
     if a.what == "chain":
         ch = D.build_chain(a.kind, device, dependent=a.dependent)
         for _ in range(a.replays):
