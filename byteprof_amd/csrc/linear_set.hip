@@ -497,32 +497,45 @@ __device__ __forceinline__ void sync_wave(StageTable st, int S, uint32_t* __rest
     const int K = st[s].K;
     const int nch = K / 512;
     uint16_t* xl = L.x[s & 1];
-    // x[s & 1] and scale[s & 1] were last used by stage s - 2
-    if (s >= 2) wait_done(L, s - 2, active_consumers(L, s - 2), failed, scratch);
+    const int ws = st[s].wait_stage;
 
-    // int8 row scales of the stage into LDS (the consumers apply them at the ends of their rows)
+    // Loads that depend on no other stage go out first, so that their latency (a few us behind the weight stream)
+    // overlaps the wait for this stage's LDS buffers: an external input vector, and the int8 row scales of the
+    // stage (the consumers apply them at the ends of their rows).
+    uint32_t v[kSetChMax][4];
+    if (ws < 0) load_input((const BP_GLOBAL uint16_t*)(st[s].src), K, v, lane);
+    float sc[kSetRowsMax / kWave];
+    int rows = 0;
     if constexpr (KIND == kInt8) {
       const int row0 = L.rows[s][0];
-      const int rows = L.rows[s][kSetCW] - row0;
-      for (int i = lane; i < rows; i += kWave) {
-        const int row = row0 + i;
-        int seg = 0, seg_begin = 0;
-        while (st[s].seg_end[seg] <= row) seg_begin = st[s].seg_end[seg++];
-        L.scale[s & 1][i] = load_scale(st[s].scale[seg], row - seg_begin, scale_dt);
+      rows = L.rows[s][kSetCW] - row0;
+#pragma unroll
+      for (int j = 0; j < kSetRowsMax / kWave; ++j) {
+        const int i = lane + j * kWave;
+        if (i < rows) {
+          const int row = row0 + i;
+          int seg = 0, seg_begin = 0;
+          while (st[s].seg_end[seg] <= row) seg_begin = st[s].seg_end[seg++];
+          sc[j] = load_scale(st[s].scale[seg], row - seg_begin, scale_dt);
+        }
       }
     }
 
+    // x[s & 1] and scale[s & 1] were last used by stage s - 2
+    if (s >= 2) wait_done(L, s - 2, active_consumers(L, s - 2), failed, scratch);
+    if constexpr (KIND == kInt8) {
+#pragma unroll
+      for (int j = 0; j < kSetRowsMax / kWave; ++j)
+        if (lane + j * kWave < rows) L.scale[s & 1][lane + j * kWave] = sc[j];
+    }
+
     // the input vector: published rows of an earlier stage (read once this workgroup's own consumers are done
-    // with that stage: the other workgroups finish it at about the same time), or an external vector
-    const int ws = st[s].wait_stage;
-    uint32_t v[kSetChMax][4];
+    // with that stage: the other workgroups finish it at about the same time), or the external vector loaded above
     if (ws >= 0) {
       wait_done(L, ws, active_consumers(L, ws), failed, scratch);
       const int64_t e0 = (static_cast<const char*>(st[s].src) - static_cast<const char*>(st[ws].y)) / 2;
       gather_round<0>(tagged + L.tag_off[ws] + e0, K, tag, L, v, lane, failed, scratch);
       if (K > kSetRound * 512) gather_round<1>(tagged + L.tag_off[ws] + e0, K, tag, L, v, lane, failed, scratch);
-    } else {
-      load_input((const BP_GLOBAL uint16_t*)(st[s].src), K, v, lane);
     }
     write_input(v, K, st[s].renorm != 0, xl, lane);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
