@@ -15,7 +15,8 @@ the launch stream over the timed steps, and the HBM traffic per launch from the 
 summary (profiles/linear_set_kernel_decode_set.md); the CPU baseline (torch F.linear, the reference's CPU path for
 these linears, on the host cores); and secondary figures: the same set as a dependent decode chain in one launch
 (each stage reads the renormalised output it depends on), the 113-launch HIP graph of skinny kernels, the int8
-set (fp16 scales) both ways, and the fused mLSTM block.
+set (fp16 scales) both ways, the fused mLSTM block, and the bf16 verify-width sweep (M = 1..16, VALU / matrix-core
+kernels).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
 """
@@ -211,6 +212,35 @@ def per_launch_graph(ops, kind: str, nbytes: int) -> dict:
     return out
 
 
+def sweep(device) -> dict:
+    """The verify-width sweep: us per skinny_mm call for M in {1, 2, 4, 8, 16} x K in {2048, 8192} x N in {2048,
+    8192, 100352} (bf16), each cell over a ring of >= 1 GiB of distinct weights in one HIP graph (weights streamed
+    from HBM), with the kernel family skinny_mm routes the row count to."""
+    import torch
+
+    from byteprof_amd import decode_set as D
+    from byteprof_amd.optim import skinny as S
+
+    out = {}
+    for n in (2048, 8192, 100352):
+        for k in (2048, 8192):
+            per = 2 * n * k
+            ring = [(torch.randn(n, k, device=device) * 0.02).to(torch.bfloat16) for _ in range(max(2, (1 << 30) // per))]
+            cell = {}
+            for m in (1, 2, 4, 8, 16):
+                x = torch.randn(m, k, device=device).to(torch.bfloat16)
+                y = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+                g = D.capture([lambda w=w: S.skinny_mm(x, w, out=y) for w in ring])
+                us = statistics.median(D.time_replays(g, 2, 5)) * 1000.0 / len(ring)
+                del g
+                fam = "mfma" if S._bm(m) in S.MFMA_BUCKETS and S.mfma_cfg("bf16", n, k) is not None else "valu"
+                cell[str(m)] = {"us": round(us, 2), "gbs": round((per + 2 * m * (n + k)) / us / 1e3), "kernel": fam}
+            out[f"{n}x{k}"] = cell
+            del ring
+            torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -291,6 +321,8 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("[bench] mLSTM block")
         result["mlstm"] = mlstm_block(device)
+        log("[bench] verify-width sweep")
+        result["sweep_bf16"] = sweep(device)
     if not a.no_cpu:
         log("[bench] CPU baseline")
         if ops is None:
