@@ -26,6 +26,11 @@ extern template SkinnyFn skinny_pick<kInt8, 16>(int, int, bool);
 SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth);
 int mfma_k_step(int wkind);
 
+// int4 group-128 kernels (skinny_int4.hip).
+using Int4Fn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
+                        int64_t, int64_t, int);
+Int4Fn int4_pick(int mt, int tile_rows, int waves);
+
 namespace {
 
 __global__ void splitk_reduce_kernel(const float* __restrict__ ws, uint16_t* __restrict__ y,
@@ -157,10 +162,57 @@ int skinny_mfma_launch(int wkind, const void* x, const void* w, const void* scal
   return launch_status();
 }
 
+int skinny_int4_launch(const void* x, const void* packed, const void* scale, int scale_dt, const void* zero, void* y,
+                       int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int split, void* ws,
+                       size_t ws_bytes, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || M > 16 || K % 128 != 0) return BP_E_INVALID_ARG;
+  if (M == 0 || N == 0) return BP_OK;
+  if (x == nullptr || packed == nullptr || y == nullptr || scale == nullptr || zero == nullptr)
+    return BP_E_INVALID_ARG;
+  if (scale_dt < BP_DT_BF16 || scale_dt > BP_DT_F32) return BP_E_INVALID_ARG;
+  if (split < 1 || split > 1024) return BP_E_UNSUPPORTED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K == 0) {
+    fill_zero_bf16_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<uint16_t*>(y), M * N);
+    return launch_status();
+  }
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(packed) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(zero) % 2 != 0)
+    return BP_E_UNSUPPORTED;
+  Int4Fn fn = int4_pick(row_bucket(M), tile_rows, waves);
+  if (fn == nullptr) return BP_E_UNSUPPORTED;
+  const int64_t groups = K / 128;
+  if (split > groups) split = static_cast<int>(groups);
+  if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
+    return BP_E_WORKSPACE;
+  const int64_t tiles = (N + tile_rows - 1) / tile_rows;
+  if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
+  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(split));
+  fn<<<grid, waves * kWave, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(packed), scale,
+                                     scale_dt, static_cast<const uint16_t*>(zero), static_cast<uint16_t*>(y),
+                                     static_cast<float*>(ws), static_cast<int>(M), N, K, split);
+  const int rc = launch_status();
+  if (rc != BP_OK || split == 1) return rc;
+  splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
+                                                       nullptr, 0, M, N, split);
+  return launch_status();
+}
+
 }  // namespace
 }  // namespace bp
 
 extern "C" {
+
+int bp_skinny_int4_config_supported(int mt, int tile_rows, int waves) {
+  return bp::int4_pick(mt, tile_rows, waves) != nullptr ? 1 : 0;
+}
+
+int bp_skinny_int4(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero, void* y,
+                   int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int split, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  return bp::skinny_int4_launch(x, packed, scale, scale_dtype, zero, y, M, N, K, tile_rows, waves, split, workspace,
+                                workspace_bytes, stream);
+}
 
 int bp_skinny_mfma_config_supported(int wkind, int block_rows, int waves, int depth) {
   return block_rows % 16 == 0 && bp::mfma_pick(wkind, block_rows / 16, waves, depth) != nullptr ? 1 : 0;

@@ -16,7 +16,9 @@ Differences from the reference, each forced by the hardware mapping or by raw-po
     kernels; bitwise row independence (test_skinny.py:114-121) holds within each family, i.e. for M = 1..4 and for
     M = 5..16 (the reference's single M <= 16 bucket is split at the change of arithmetic unit). An explicit `cfg`
     selects the VALU kernel;
-  - int4 group-128 weights (uint8 tile-major) are not implemented yet: they raise NotImplementedError.
+  - int4 group-128 weights (uint8 tile-major, `quantize_int4` / `pack_int4`, the reference's format byte for byte)
+    run on skinny_int4.hip, whose products use the codes, zeros and activations exactly (the reference rounds
+    code - zero to bf16 before its tensor-core product): closer to the dequantize-then-matmul result.
 """
 
 from __future__ import annotations
@@ -223,14 +225,20 @@ def skinny_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None = Non
         if scale is None or zero is None or w.dim() != 4 or k % GROUP or w.shape[1] * GROUP != k or \
                 scale.shape[0] != w.shape[1]:
             raise ValueError("int4 needs packed [N/R, K/128, R, 64], scale/zero [K/128, N] and K % 128 == 0")
-        raise NotImplementedError("int4 group-128 weights are not implemented by the gfx950 kernels yet")
+        kind, n = "int4", scale.shape[1]
+        if scale.dim() != 2 or zero.shape != scale.shape or zero.dtype != torch.float16 or w.shape[3] != 64 or \
+                w.shape[0] * w.shape[2] < n or scale.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise ValueError("int4 needs scale [K/128, N] (bf16 / fp16 / fp32) and zero [K/128, N] fp16 matching the "
+                             "packed weights")
     else:
         raise ValueError(f"unsupported weight dtype {w.dtype}")
-    if w.dim() != 2 or not w.is_contiguous():
+    if kind != "int4" and (w.dim() != 2 or not w.is_contiguous()):
         raise ValueError("w must be a contiguous [N, K] tensor")
+    if kind == "int4" and not (w.is_contiguous() and scale.is_contiguous() and zero.is_contiguous()):
+        raise ValueError("int4 packed weights, scale and zero must be contiguous")
     if x.dtype != torch.bfloat16:
         raise ValueError("x must be bfloat16")
-    _check_device(x, w, scale, out)
+    _check_device(x, w, scale, zero, out)
     if out is not None:
         if out.shape != (m, n) or out.dtype != x.dtype or not out.is_contiguous():
             raise ValueError(f"out must be a contiguous [{m}, {n}] {x.dtype} tensor")
@@ -242,8 +250,93 @@ def skinny_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None = Non
             y.zero_()
         return y
     for r0 in range(0, m, ROWS_PER_LAUNCH):
-        _launch(kind, x[r0:r0 + ROWS_PER_LAUNCH], w, scale, y[r0:r0 + ROWS_PER_LAUNCH], cfg)
+        if kind == "int4":
+            _launch_int4(x[r0:r0 + ROWS_PER_LAUNCH], w, scale, zero, y[r0:r0 + ROWS_PER_LAUNCH], cfg)
+        else:
+            _launch(kind, x[r0:r0 + ROWS_PER_LAUNCH], w, scale, y[r0:r0 + ROWS_PER_LAUNCH], cfg)
     return y
+
+
+def int4_cfg(n: int, k: int, tile_rows: int, cfg=None) -> tuple[int, int]:
+    """(waves, split) of an int4 launch: the tuned table entry 'int4|N|K', else a heuristic; a user cfg is
+    (waves, split) or the reference's (BN, BK, warps, stages[, split])."""
+    if cfg is not None:
+        if len(cfg) == 2:
+            waves, split = int(cfg[0]), int(cfg[1])
+        elif len(cfg) in (4, 5):
+            waves, split = int(cfg[2]), int(cfg[4]) if len(cfg) == 5 else 1
+        else:
+            raise ValueError(f"int4 cfg must be (waves, split) or (BN, BK, warps, stages[, split]), got {cfg!r}")
+    else:
+        entry = _TABLE.get(("int4", n, k))
+        if entry is not None:
+            waves, split = int(entry["waves"]), int(entry.get("split", 1))
+        else:
+            groups = k // GROUP
+            waves = 1
+            while waves * 2 <= min(groups, 4):
+                waves *= 2
+            split = 1
+    waves = max(w for w in (1, 2, 4, 8) if w <= max(waves, 1))
+    return waves, max(1, split)
+
+
+def _launch_int4(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor, y: torch.Tensor,
+                 cfg=None) -> None:
+    m, k = x.shape
+    n = scale.shape[1]
+    tile_rows = int(w.shape[2])
+    if tile_rows not in (16, 32, 64):
+        raise ValueError(f"int4 tile rows must be 16, 32 or 64 on gfx950, got {tile_rows}")
+    waves, split = int4_cfg(n, k, tile_rows, cfg)
+    split = min(split, k // GROUP)
+    if x.data_ptr() % 16:
+        x = x.clone()
+    L = _lib.lib()
+    ws = None
+    ws_bytes = 0
+    if split > 1:
+        ws_bytes = L.bp_skinny_workspace_bytes(m, n, split)
+        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=x.device)
+    rc = L.bp_skinny_int4(x.data_ptr(), w.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype], zero.data_ptr(),
+                          y.data_ptr(), m, n, k, tile_rows, waves, split, _lib.ptr(ws), ws_bytes,
+                          _lib.stream_ptr(x.device))
+    _lib.check(rc, "bp_skinny_int4")
+
+
+def quantize_int4(w: torch.Tensor, tile_rows: int = 32) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Asymmetric group-128 int4 of w [N, K] (byteprof/optim/skinny.py:172-185): per row and group of 128 inputs,
+    scale = max((max - min) / 15, 1e-6) stored in w.dtype, zero = -min / scale stored in fp16, code =
+    round_half_even(w / scale + zero) clamped to 0..15 (fp32 arithmetic). Returns (packed [ceil(N/R), K/128, R, 64]
+    uint8, scale [K/128, N] w.dtype, zero [K/128, N] fp16)."""
+    n, k = w.shape
+    if k % GROUP:
+        raise ValueError("int4 needs K % 128 == 0")
+    groups = w.float().reshape(n, k // GROUP, GROUP)
+    lo, hi = groups.amin(dim=-1), groups.amax(dim=-1)
+    scale = ((hi - lo) / 15.0).clamp_min(1e-6).to(w.dtype)
+    zero = (-lo / scale.float()).to(torch.float16)
+    codes = torch.round(groups / scale.float().unsqueeze(-1) + zero.float().unsqueeze(-1)).clamp_(0, 15)
+    return pack_int4(codes.to(torch.uint8).reshape(n, k), tile_rows), scale.t().contiguous(), zero.t().contiguous()
+
+
+def pack_int4(codes: torch.Tensor, tile_rows: int = 32) -> torch.Tensor:
+    """Codes 0..15 [N, K] -> the tile-major layout [ceil(N/R), K/128, R, 64] (byteprof/optim/skinny.py:188-198):
+    within a row's group of 128, byte j = code j | code (j + 64) << 4; the R rows of a tile and group are one
+    contiguous R x 64-byte block; padding rows are zero."""
+    n, k = codes.shape
+    tiles = -(-n // tile_rows)
+    full = codes.new_zeros(tiles * tile_rows, k)
+    full[:n] = codes
+    g = full.reshape(tiles, tile_rows, k // GROUP, 2, GROUP // 2)
+    return (g[:, :, :, 0] | (g[:, :, :, 1] << 4)).permute(0, 2, 1, 3).contiguous()
+
+
+def unpack_int4(packed: torch.Tensor, n: int) -> torch.Tensor:
+    """Inverse of pack_int4: codes [N, K] (byteprof/optim/skinny.py:201-206)."""
+    tiles, groups, rows, _ = packed.shape
+    p = packed.permute(0, 2, 1, 3)
+    return torch.stack([p & 0xF, p >> 4], dim=3).reshape(tiles * rows, groups * GROUP)[:n]
 
 
 def dequantize(kind: str, w: torch.Tensor, scale=None, zero=None) -> torch.Tensor:
@@ -252,4 +345,6 @@ def dequantize(kind: str, w: torch.Tensor, scale=None, zero=None) -> torch.Tenso
         return w.float()
     if kind == "int8":
         return w.float() * scale.float()[:, None]
-    raise NotImplementedError("int4 group-128 weights are not implemented by the gfx950 kernels yet")
+    groups, n = scale.shape
+    codes = unpack_int4(w, n).float().reshape(n, groups, GROUP) - zero.float().t().unsqueeze(-1)
+    return (codes * scale.float().t().unsqueeze(-1)).reshape(n, groups * GROUP)

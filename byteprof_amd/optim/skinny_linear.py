@@ -3,7 +3,8 @@
 Mirrors byteprof/optim/skinny_linear.py:20-71: schemes bf16_wo (the original bf16 weights) and int8_wo (per-row
 symmetric int8, the same quantization as `Int8Linear`); inputs with 1..MAX_M rows on the GPU in bf16 use the
 kernel; empty inputs return an empty tensor; larger inputs and non-bf16 activations use the weights dequantized to
-the activation dtype with `F.linear`, as the reference does. int4_wo raises NotImplementedError (not built yet).
+the activation dtype with `F.linear`, as the reference does. int4_wo: the skinny group-128 format
+(`skinny.quantize_int4`), buffers q (packed), scale and zero, as the reference (skinny_linear.py:39-44).
 """
 
 from __future__ import annotations
@@ -30,10 +31,14 @@ class SkinnyLinear(nn.Module):
             self.weight = lin.weight  # kept as is: callers read weight.dtype
             self.scale = self.zero = None
             return
-        if scheme == "int4_wo":
-            raise NotImplementedError("int4_wo is not implemented by the gfx950 skinny kernels yet")
         # An empty parameter keeps `weight.dtype` readable without holding the bf16 weights.
         self.weight = nn.Parameter(torch.empty(0, dtype=w.dtype, device=w.device), requires_grad=False)
+        if scheme == "int4_wo":
+            packed, scale, zero = skinny.quantize_int4(w)
+            self.register_buffer("q", packed)
+            self.register_buffer("scale", scale)
+            self.register_buffer("zero", zero)
+            return
         from ..quant.hip_int8 import quantize_rowwise_int8
 
         q, scale = quantize_rowwise_int8(w)

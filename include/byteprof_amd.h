@@ -99,6 +99,23 @@ int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int sca
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * int4 group-128 weights in the tile-major format of byteprof's skinny kernels:
+ *   packed uint8 [ceil(N / R), K / 128, R, 64]: the R rows (tile_rows: 16, 32 or 64) of one row tile and one group of
+ *   128 inputs form a contiguous R x 64-byte block; byte j of a row's group holds code j (low nibble) and code
+ *   j + 64 (high nibble), codes 0..15; padding rows of the last tile are ignored;
+ *   scale [K / 128, N] (scale_dtype BP_DT_BF16 / BP_DT_F16 / BP_DT_F32), zero [K / 128, N] fp16.
+ * y[M, N] (bf16) = sum over groups g of scale[g, n] * sum_j (code - zero[g, n]) * x[m, 128 g + j], fp32; the codes,
+ * zeros and activations enter the products exactly. 1 <= M <= 16; K a multiple of 128; x and packed 16-byte aligned.
+ * waves: 1, 2, 4 or 8 (groups dealt to the waves); split: as for the other skinny kernels (the scale is applied per
+ * group, so the reduce adds the partial sums as they are). The K order depends only on (K, waves, split).
+ * Replaces: byteprof/optim/skinny.py:46-63 (_skinny_kernel MODE 3) via skinny_mm (skinny.py:136-166).
+ */
+int bp_skinny_int4_config_supported(int mt, int tile_rows, int waves);
+int bp_skinny_int4(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero, void* y,
+                   int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int split, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/*
  * One-row int8 product: y[1, N] (bf16) = scale[n] * sum_k float(q[n, k]) * float(x[k]).
  * Replaces: byteprof/quant/triton_int8.py:40-47 (gemv_int8) and :16-28 (_gemv_int8).
  */

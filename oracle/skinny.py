@@ -12,6 +12,16 @@ quantize_rowwise_int8: byteprof/quant/triton_int8.py:50-55 — scale = max|row| 
             Pinned by known answers derived with exact rational arithmetic plus float32 rounding of each step
             (tests/golden/make_golden.py), by the reference's own bound (|q * s - w| <= 0.51 s + 1e-3,
             tests/test_quant_int8.py:10-16), and by the invariants |q| <= 127 and q = +-127 at the row maximum.
+int4 (group-128, asymmetric; the tile-major format of byteprof/optim/skinny.py:172-217):
+quantize_int4: per row and group of 128 inputs, in float32: scale = max((max - min) / 15, 1e-6) rounded to bf16,
+            zero = fp16(-min / scale), code = round_half_even(w / scale + zero) clamped to 0..15
+            (skinny.py:172-185). Pinned by a hand-derived group (scale and zero exact, codes with ties to even), by the
+            reference's half-step bound (test_skinny.py:56-62) and by codes within 0..15 at the group extremes.
+pack_int4 / unpack_int4: codes [N, K] <-> [ceil(N/R), K/128, R, 64], byte j of a row's group = code j | code (j + 64)
+            << 4, padding rows zero (skinny.py:188-206). Pinned by the round trip and the reference's layout
+            known answer (test_skinny.py:47-53).
+skinny_int4: y = x @ ((code - zero) * scale)^T in float64 (exact operands: the kernel's products use the codes,
+            zeros and activations exactly), rounded to bf16. Pinned by exact rational arithmetic on a small case.
 """
 
 from __future__ import annotations
@@ -61,3 +71,65 @@ def quantize_rowwise_int8(w, scale_dtype: str = "bf16") -> tuple[np.ndarray, np.
     ratio = (w / s[:, None]).astype(np.float32)
     q = np.clip(np.rint(ratio), -127, 127).astype(np.int8)
     return q, s.astype(np.float32)
+
+
+GROUP = 128
+
+
+def pack_int4(codes, tile_rows: int = 32) -> np.ndarray:
+    """uint8 [ceil(N/R), K/128, R, 64] of codes [N, K] (0..15)."""
+    q = np.asarray(codes, dtype=np.uint8)
+    n, k = q.shape
+    tiles = -(-n // tile_rows)
+    full = np.zeros((tiles * tile_rows, k), dtype=np.uint8)
+    full[:n] = q
+    out = np.zeros((tiles, k // GROUP, tile_rows, 64), dtype=np.uint8)
+    for t in range(tiles):
+        for g in range(k // GROUP):
+            for r in range(tile_rows):
+                row = full[t * tile_rows + r, g * GROUP:(g + 1) * GROUP]
+                out[t, g, r] = row[:64] | (row[64:] << 4)
+    return out
+
+
+def unpack_int4(packed, n: int) -> np.ndarray:
+    """codes [N, K] of a packed [T, G, R, 64] array."""
+    p = np.asarray(packed, dtype=np.uint8)
+    tiles, groups, rows, _ = p.shape
+    out = np.zeros((tiles * rows, groups * GROUP), dtype=np.uint8)
+    for t in range(tiles):
+        for g in range(groups):
+            blk = p[t, g]  # [R, 64]
+            out[t * rows:(t + 1) * rows, g * GROUP:g * GROUP + 64] = blk & 0xF
+            out[t * rows:(t + 1) * rows, g * GROUP + 64:(g + 1) * GROUP] = blk >> 4
+    return out[:n]
+
+
+def quantize_int4(w, tile_rows: int = 32):
+    """(packed, scale [K/128, N] as float32 values of bf16, zero [K/128, N] as float32 values of fp16) of float
+    weights w [N, K] (values of bf16 data); float32 arithmetic in the order of the reference."""
+    w = np.asarray(w, dtype=np.float32)
+    n, k = w.shape
+    if k % GROUP:
+        raise ValueError("int4 needs K % 128 == 0")
+    grp = w.reshape(n, k // GROUP, GROUP)
+    lo, hi = grp.min(axis=-1), grp.max(axis=-1)
+    scale = bf16_round(np.maximum(((hi - lo) / np.float32(15.0)).astype(np.float32), np.float32(1e-6)))
+    zero = f16_round((-lo / scale).astype(np.float32))
+    t = (grp / scale[..., None]).astype(np.float32) + zero[..., None]
+    codes = np.clip(np.rint(t.astype(np.float32)), 0, 15).astype(np.uint8).reshape(n, k)
+    return pack_int4(codes, tile_rows), scale.T.copy(), zero.T.copy()
+
+
+def dequantize_int4(packed, scale, zero) -> np.ndarray:
+    """float64 weights [N, K] = (code - zero) * scale, exactly."""
+    scale = np.asarray(scale, dtype=np.float64)
+    zero = np.asarray(zero, dtype=np.float64)
+    groups, n = scale.shape
+    codes = unpack_int4(packed, n).astype(np.float64).reshape(n, groups, GROUP)
+    return ((codes - zero.T[..., None]) * scale.T[..., None]).reshape(n, groups * GROUP)
+
+
+def skinny_int4(x, packed, scale, zero) -> np.ndarray:
+    """bf16-rounded output (as float32) of an int4 skinny call."""
+    return bf16_round(matmul(x, dequantize_int4(packed, scale, zero)).astype(np.float32))

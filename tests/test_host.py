@@ -124,9 +124,15 @@ def test_skinny_mm_validation_errors():
         S.skinny_mm(torch.zeros(2, 128, dtype=torch.bfloat16), torch.zeros(8, 128, dtype=torch.float64))
     with pytest.raises(ValueError):
         S.skinny_mm(torch.zeros(2, 128, dtype=torch.bfloat16), w)  # on the CPU: no CPU path
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):  # int4 on the CPU: no CPU path
         S.skinny_mm(torch.zeros(2, 256, dtype=torch.bfloat16), torch.zeros(1, 2, 32, 64, dtype=torch.uint8),
                     torch.zeros(2, 32, dtype=torch.bfloat16), torch.zeros(2, 32, dtype=torch.float16))
+    with pytest.raises(ValueError):  # int4 with K not a multiple of the group
+        S.skinny_mm(torch.zeros(2, 200, dtype=torch.bfloat16), torch.zeros(1, 2, 32, 64, dtype=torch.uint8),
+                    torch.zeros(2, 32, dtype=torch.bfloat16), torch.zeros(2, 32, dtype=torch.float16))
+    with pytest.raises(ValueError):  # int4 without zero
+        S.skinny_mm(torch.zeros(2, 256, dtype=torch.bfloat16), torch.zeros(1, 2, 32, 64, dtype=torch.uint8),
+                    torch.zeros(2, 32, dtype=torch.bfloat16))
 
 
 def test_configuration_keeps_one_k_order_per_shape():
@@ -162,8 +168,9 @@ def test_skinny_linear_cpu_inputs_use_the_dequantized_weights():
     assert m(x.new_empty(0, 256)).shape == (0, 64)
     with pytest.raises(ValueError):
         SkinnyLinear(lin, "int3_wo")
-    with pytest.raises(NotImplementedError):
-        SkinnyLinear(lin, "int4_wo")
+    m4 = SkinnyLinear(lin, "int4_wo")  # fp32 weights: scale in fp32, zero in fp16
+    y4 = m4(x)
+    assert torch.allclose(y4, x @ m4.dequantized(torch.float32).T + lin.bias, atol=1e-5, rtol=1e-5)
 
 
 class _Block(nn.Module):
@@ -292,3 +299,32 @@ def test_decode_chain_structure():
     ind = D.chain_stages(weights, dependent=False, device="cpu")
     assert len(ind) == 65 and all(st.wait == -1 for st in ind)
     assert D.chain_bytes("bf16") == 2_560_237_568 and D.chain_bytes("int8") == 1_282_027_520
+
+
+def test_int4_quantizer_and_packing_match_the_oracle():
+    """The host-side int4 format (torch, CPU) equals the oracle's restatement byte for byte."""
+    from oracle import skinny as OS
+
+    g = torch.Generator().manual_seed(7)
+    for n, k, rows in ((37, 256, 32), (16, 384, 16), (70, 128, 64)):
+        w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16)
+        packed, scale, zero = S.quantize_int4(w, rows)
+        assert packed.dtype == torch.uint8 and scale.dtype == torch.bfloat16 and zero.dtype == torch.float16
+        p_o, s_o, z_o = OS.quantize_int4(w.float().numpy(), rows)
+        assert np.array_equal(packed.numpy(), p_o)
+        assert np.array_equal(scale.float().numpy(), s_o) and np.array_equal(zero.float().numpy(), z_o)
+        assert torch.equal(S.unpack_int4(packed, n), torch.from_numpy(OS.unpack_int4(p_o, n)))
+        deq = S.dequantize("int4", packed, scale, zero).numpy()
+        assert np.allclose(deq, OS.dequantize_int4(p_o, s_o, z_o), rtol=0, atol=1e-7)
+
+
+def test_int4_skinny_linear_holds_the_packed_format():
+    from byteprof_amd.optim.skinny_linear import SkinnyLinear
+
+    lin = torch.nn.Linear(256, 40, bias=False, dtype=torch.bfloat16)
+    m = SkinnyLinear(lin, "int4_wo")
+    assert m.q.shape == (2, 2, 32, 64) and m.scale.shape == (2, 40) and m.zero.shape == (2, 40)
+    assert m.weight.numel() == 0 and m.weight.dtype == torch.bfloat16
+    x = torch.randn(3, 256, dtype=torch.bfloat16)
+    y = m(x)  # CPU input: dequantized F.linear, as the reference
+    assert torch.equal(y, torch.nn.functional.linear(x, m.dequantized(torch.bfloat16)))

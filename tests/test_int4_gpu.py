@@ -1,0 +1,135 @@
+"""int4 group-128 skinny kernel (skinny_int4.hip) on the GPU against the CPU oracle: every M = 1..33 on the
+reference's real and odd shapes, tile heights, configurations, bitwise row independence, the sentinel out-of-bounds
+check, scale dtypes, graph capture and SkinnyLinear int4_wo. Mirrors byteprof tests/test_skinny.py:71-149 for the
+int4 kind."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from byteprof_amd.optim import skinny as S
+from oracle import skinny as OS
+from tests.helpers import check_against_oracle, randn_x
+
+pytestmark = pytest.mark.gpu
+
+REAL = [(2048, 2048), (8192, 2048), (2048, 8192), (1024, 2048), (2816, 2048), (2048, 2816)]
+ODD = [(37, 256), (1, 128), (50, 384), (129, 640)]
+
+
+def make_int4(n: int, k: int, seed: int = 0, tile_rows: int = 32, scale_dtype=None):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    packed, scale, zero = S.quantize_int4(w, tile_rows)
+    if scale_dtype is not None:
+        scale = scale.to(scale_dtype)
+    w_np = OS.dequantize_int4(packed.cpu().numpy(), scale.float().cpu().numpy(), zero.float().cpu().numpy())
+    return (packed, scale, zero), w_np
+
+
+@pytest.mark.parametrize("n,k", REAL + ODD)
+def test_matches_the_oracle_for_every_m(n, k):
+    print(f"\n[int4] n={n} k={k}", flush=True)
+    args, w_np = make_int4(n, k, seed=n + k)
+    x = randn_x(33, k, seed=7)
+    worst = (0.0, 0.0)
+    for m in range(1, 34):
+        y = S.skinny_mm(x[:m].contiguous(), *args)
+        assert y.shape == (m, n) and y.dtype == torch.bfloat16
+        worst = max(worst, check_against_oracle(y, x[:m], w_np))
+    print("worst componentwise / normwise", worst)
+
+
+@pytest.mark.parametrize("tile_rows", [16, 64])
+@pytest.mark.parametrize("n,k", [(37, 256), (2048, 2048), (129, 640)])
+def test_tile_heights(tile_rows, n, k):
+    args, w_np = make_int4(n, k, seed=3, tile_rows=tile_rows)
+    assert args[0].shape[2] == tile_rows
+    x = randn_x(16, k, seed=1)
+    for m in (1, 7, 16):
+        check_against_oracle(S.skinny_mm(x[:m].contiguous(), *args), x[:m], w_np)
+
+
+@pytest.mark.parametrize("cfg", [(1, 1), (2, 1), (4, 1), (8, 1), (2, 3), (8, 2), (32, 128, 4, 3, 5)])
+def test_configurations_match(cfg):
+    args, w_np = make_int4(192, 2048, seed=5)
+    for m in (1, 5, 16, 17):
+        x = randn_x(m, 2048, seed=m)
+        check_against_oracle(S.skinny_mm(x, *args, cfg=cfg), x, w_np)
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_scale_dtypes(scale_dtype):
+    args, w_np = make_int4(300, 1024, seed=8, scale_dtype=scale_dtype)
+    x = randn_x(4, 1024, seed=2)
+    check_against_oracle(S.skinny_mm(x, *args), x, w_np)
+
+
+@pytest.mark.parametrize("n,k", [(2048, 2048), (129, 640)])
+def test_rows_do_not_depend_on_the_other_rows(n, k):
+    """One int4 kernel serves 1..16 rows with one K order: row i is bitwise the same for every M."""
+    args, _ = make_int4(n, k, seed=4)
+    x = randn_x(33, k, seed=3)
+    full16 = S.skinny_mm(x[:16].contiguous(), *args)
+    for m in (1, 2, 3, 5, 9, 15):
+        assert torch.equal(S.skinny_mm(x[:m].contiguous(), *args), full16[:m]), m
+    full33 = S.skinny_mm(x, *args)
+    assert torch.equal(full33[:16], full16)
+    assert torch.equal(S.skinny_mm(x[16:19].contiguous(), *args), full33[16:19])
+
+
+@pytest.mark.parametrize("m", [1, 3, 17])
+def test_kernel_writes_only_the_output_block(m):
+    n, k = 70, 384
+    args, w_np = make_int4(n, k, seed=1)
+    x = randn_x(m, k, seed=8)
+    flat = torch.full((m * n + 4096,), 777.0, device="cuda", dtype=torch.bfloat16)
+    out = flat[:m * n].view(m, n)
+    S.skinny_mm(x, *args, out=out)
+    assert torch.equal(flat[m * n:], torch.full_like(flat[m * n:], 777.0))
+    assert not (out == 777.0).any()
+    check_against_oracle(out, x, w_np)
+
+
+def test_unaligned_activations_and_empty_inputs():
+    args, w_np = make_int4(64, 256, seed=2)
+    buf = randn_x(3 * 256 + 1, 1, seed=5).reshape(-1)
+    x = buf[1:].view(3, 256)  # 2-byte offset: the host copies it to an aligned buffer
+    check_against_oracle(S.skinny_mm(x, *args), x, w_np)
+    assert S.skinny_mm(torch.empty(0, 256, device="cuda", dtype=torch.bfloat16), *args).shape == (0, 64)
+
+
+def test_graph_replays_match_eager():
+    args, _ = make_int4(2048, 2048, seed=6)
+    x = randn_x(5, 2048, seed=3)
+    eager = S.skinny_mm(x, *args)
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        S.skinny_mm(x, *args, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        S.skinny_mm(x, *args, out=out)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+def test_skinny_linear_int4_scheme():
+    from byteprof_amd.optim.skinny_linear import SkinnyLinear
+
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(512, 300, bias=True, dtype=torch.bfloat16, device="cuda")
+    m = SkinnyLinear(lin, "int4_wo")
+    x = torch.randn(2, 3, 512, device="cuda", dtype=torch.bfloat16)
+    y = m(x)
+    ref = x.float() @ m.dequantized(torch.float32).T + lin.bias.float()
+    assert y.shape == (2, 3, 300)
+    assert float((y.float() - ref).abs().max() / ref.abs().max()) < 1e-2

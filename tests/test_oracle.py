@@ -270,3 +270,71 @@ def test_chain_second_stage_reads_the_first_stage_output():
     expect = ON.bf16_round(np.array([3, 7, 10, 4], np.float32) * np.float32(1.0 / np.sqrt(43.5)))
     assert np.array_equal(xs[1], expect)
     assert np.array_equal(ys[1], ON.bf16_round(np.array([expect.astype(np.float64).sum()], np.float32)))
+
+
+# ---- int4 group-128 format ---------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("n,rows", [(32, 32), (37, 32), (5, 16), (64, 16)])
+def test_int4_pack_round_trip_and_documented_layout(n, rows):
+    """byteprof tests/test_skinny.py:47-53: byte j of a row's group holds code j (low nibble), code j + 64 (high)."""
+    rng = np.random.default_rng(n + rows)
+    q = rng.integers(0, 16, (n, 384), dtype=np.uint8)
+    packed = OS.pack_int4(q, rows)
+    assert packed.shape == (-(-n // rows), 3, rows, 64) and packed.dtype == np.uint8
+    assert np.array_equal(OS.unpack_int4(packed, n), q)
+    assert int(packed[0, 1, 0, 5]) == int(q[0, 128 + 5]) | (int(q[0, 128 + 64 + 5]) << 4)
+    if n % rows:
+        assert not packed[-1, :, n % rows:].any()  # padding rows are zero
+
+
+def test_int4_quantizer_known_answer_by_hand():
+    """A group from -1.5 to 6: scale = 7.5 / 15 = 0.5 and zero = 3 are exact; code = rint(w / 0.5 + 3) with ties to
+    even: 0.25 -> 3.5 -> 4, 0.75 -> 4.5 -> 4, 1.25 -> 5.5 -> 6; the extremes map to 0 and 15."""
+    w = np.zeros((1, 128), np.float32)
+    w[0, :6] = [-1.5, 6.0, 0.25, 0.75, 1.25, -0.5]
+    packed, scale, zero = OS.quantize_int4(w, 16)
+    assert scale.shape == zero.shape == (1, 1) and scale[0, 0] == 0.5 and zero[0, 0] == 3.0
+    codes = OS.unpack_int4(packed, 1)[0]
+    assert list(codes[:6]) == [0, 15, 4, 4, 6, 2]
+    assert (codes[6:] == 3).all()  # w = 0 -> zero
+
+
+def test_int4_quantizer_rounds_scale_and_zero_to_their_stored_types():
+    """scale is stored in bf16 and zero in fp16 before the codes are computed (the codes use the stored values)."""
+    rng = np.random.default_rng(3)
+    w = ON.bf16_round((rng.standard_normal((8, 256)) * 0.05).astype(np.float32))
+    packed, scale, zero = OS.quantize_int4(w)
+    assert np.array_equal(scale, ON.bf16_round(scale)) and np.array_equal(zero, ON.f16_round(zero))
+    codes = OS.unpack_int4(packed, 8).astype(np.float32).reshape(8, 2, 128)
+    want = np.clip(np.rint((w.reshape(8, 2, 128) / scale.T[..., None]).astype(np.float32) + zero.T[..., None]), 0, 15)
+    assert np.array_equal(codes, want)
+
+
+def test_int4_quantization_error_is_at_most_half_a_step():
+    """byteprof tests/test_skinny.py:56-62."""
+    rng = np.random.default_rng(4)
+    w = ON.bf16_round((rng.standard_normal((24, 256)) * 0.05).astype(np.float32))
+    packed, scale, zero = OS.quantize_int4(w)
+    deq = OS.dequantize_int4(packed, scale, zero)
+    step = np.repeat(scale.T, 128, axis=1)
+    assert (np.abs(deq - w) <= 0.55 * step + 1e-3).all()
+    assert OS.unpack_int4(packed, 24).max() <= 15
+    with pytest.raises(ValueError):
+        OS.quantize_int4(np.zeros((4, 100), np.float32))
+
+
+def test_int4_skinny_oracle_against_exact_rational_sum():
+    rng = np.random.default_rng(5)
+    n, k, m = 5, 256, 3
+    codes = rng.integers(0, 16, (n, k), dtype=np.uint8)
+    packed = OS.pack_int4(codes, 16)
+    scale = ON.bf16_round(rng.uniform(0.01, 0.1, (2, n)).astype(np.float32))
+    zero = ON.f16_round(rng.uniform(0, 15, (2, n)).astype(np.float32))
+    x = ON.bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    y = OS.skinny_int4(x, packed, scale, zero)
+    for i in range(m):
+        for j in range(n):
+            exact = sum(Fraction(float(x[i, kk])) * (int(codes[j, kk]) - Fraction(float(zero[kk // 128, j])))
+                        * Fraction(float(scale[kk // 128, j])) for kk in range(k))
+            assert y[i, j] == np.float32(exact_round(exact, BF16)), (i, j)
