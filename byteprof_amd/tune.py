@@ -11,7 +11,7 @@ the rows per workgroup separately for each bucket. Like the reference, a split >
 than 3%. The matrix-core kernels get one configuration per shape for the 8- and 16-row buckets together ('mfma',
 chosen at M = 16, used when it beats the VALU kernels over both buckets).
 
-Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8] [--out path] [--quick] [--mfma-only]
+Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8,int4] [--out path] [--quick] [--mfma-only]
 """
 
 from __future__ import annotations
@@ -199,6 +199,49 @@ def tune_mfma(kind: str, n: int, k: int, device, entry: dict, log=print) -> dict
     return {"block_rows": br, "waves": w, "depth": d, "split": sp, "us": us, "use": use}
 
 
+INT4_WAVES = (1, 2, 4, 8)
+
+
+def tune_int4(n: int, k: int, device, log=print) -> dict | None:
+    """int4 (tile rows 32, the quantizer's default): (waves, split) by the M = 1 time (split > 1 kept only if it
+    wins by more than 3%), then the time of every row bucket at that K order."""
+    if k % S.GROUP:
+        return None
+    groups = k // S.GROUP
+    per = n * k // 2
+    count = max(2, min(64, RING_BYTES // per))
+    g = torch.Generator(device=device).manual_seed(n * 17 + k)
+    ring = []
+    for _ in range(count):
+        w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+        ring.append(S.quantize_int4(w))
+        del w
+    x16 = torch.randn(16, k, device=device).to(torch.bfloat16)
+    y = torch.empty(16, n, dtype=torch.bfloat16, device=device)
+    results = {}
+    x1, y1 = x16[:1].contiguous(), y[:1]
+    for w in INT4_WAVES:
+        if w > groups:
+            continue
+        for sp in SPLITS:
+            if sp > 1 and sp * w > groups:
+                continue
+            results[(w, sp)] = _time_calls([lambda a=a: S.skinny_mm(x1, *a, out=y1, cfg=(w, sp)) for a in ring])
+    best = min(results, key=results.get)
+    if best[1] > 1:
+        no_split = min((c for c in results if c[1] == 1), key=results.get)
+        if results[no_split] <= results[best] * 1.03:
+            best = no_split
+    us = {}
+    for bm in (1, 2, 4, 8, 16):
+        xb, yb = x16[:bm].contiguous(), y[:bm]
+        us[str(bm)] = round(_time_calls([lambda a=a: S.skinny_mm(xb, *a, out=yb, cfg=best) for a in ring]), 3)
+    log(f"  int4 {n}x{k}: waves={best[0]} split={best[1]}: us {us} (M=1: {per / us['1'] / 1e3:.0f} GB/s of codes)")
+    del ring
+    torch.cuda.empty_cache()
+    return {"waves": best[0], "split": best[1], "us": us}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--shapes", default=None, help="N:K,N:K,... (default: the decode-step set shapes)")
@@ -216,6 +259,14 @@ def main(argv=None) -> int:
                        "key kind|N|K; waves and split fix the K order for every row bucket; rows per bucket; "
                        "us = measured time per call (ring of distinct weights, HIP graph)")
     for kind in a.kinds.split(","):
+        if kind == "int4":
+            for n, k in shapes:
+                print(f"[tune] int4 {n}x{k}", flush=True)
+                e = tune_int4(n, k, device, log=lambda m: print(m, flush=True))
+                if e is not None:
+                    table[f"int4|{n}|{k}"] = e
+                    out.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
+            continue
         for n, k in shapes:
             print(f"[tune] {kind} {n}x{k}", flush=True)
             key = f"{kind}|{n}|{k}"
