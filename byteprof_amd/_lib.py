@@ -50,6 +50,12 @@ SIGNATURES: dict[str, tuple] = {
     "bp_mlstm_multistep": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                     _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                     _c_float, _c_float, _c_int, _c_vp]),
+    "bp_mlstm_lazy_commit": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                      _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                      _c_int, _c_vp]),
+    "bp_draft_accept": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
+    "bp_draft_commit": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                                 _c_vp]),
     "bp_linear_set_scratch_bytes": (_c_size, [_c_vp, _c_int, _c_int]),
     "bp_linear_set_workgroups": (_c_int, [_c_int]),
     "bp_linear_set_validate": (_c_int, [_c_vp, _c_int, _c_int, _c_int]),

@@ -172,6 +172,96 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
   }
 }
 
+// Lazy commit of a verify round: the state after positions 0 .. L (L read from device memory, so a captured graph
+// serves every accepted length), recomputed from the start state with the round's saved k, v and gates: C is the
+// start C on entry (multistep left it untouched) and is updated in place; n and m start from nstart / mstart (the
+// copies multistep made) and are written to n and m. Positions are clamped to the T that k, v, i, f hold. The
+// recurrence is elementwise, so a thread carries its DPT x BV block of C (and its n rows) through all positions with
+// no reduction; the gate chain is computed by every thread the same way as in mlstm_multistep_kernel.
+// Reference semantics: byteprof/optim/mlstm_multistep.py:89-134 (lazy_commit_kernel), draft_fused.py:43-56.
+template <int IO, int BV, int DPT>
+__global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_lazy_commit_kernel(
+    float* __restrict__ c, float* __restrict__ n, float* __restrict__ m, const float* __restrict__ nstart,
+    const float* __restrict__ mstart, const void* __restrict__ k, const void* __restrict__ v,
+    const void* __restrict__ ig, const void* __restrict__ fg, const int64_t* __restrict__ length, int T, int DQ,
+    int DV, int64_t str_qk, int64_t str_v, int64_t str_if, int gate_dt) {
+  const int hd = blockIdx.y;
+  const int v0 = blockIdx.x * BV;
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int64_t L = *length;
+  const int npos = L < 0 ? 0 : (L + 1 > T ? T : static_cast<int>(L + 1));
+
+  float C[DPT][BV];
+  float nn[DPT];
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int dq = tid + j * nthreads;
+    const float* crow = c + (static_cast<int64_t>(hd) * DQ + dq) * DV + v0;
+#pragma unroll
+    for (int b = 0; b < BV; ++b) C[j][b] = crow[b];
+    nn[j] = nstart[static_cast<int64_t>(hd) * DQ + dq];
+  }
+  float m_prev = mstart[hd];
+  for (int t = 0; t < npos; ++t) {
+    const int64_t off = static_cast<int64_t>(t) * str_if + hd;
+    const float fv = load_gate(fg, off, gate_dt);
+    const float iv = load_gate(ig, off, gate_dt);
+    const float fl = logf(1.f / (1.f + expf(-fv)));
+    const float mn = fmaxf(fl + m_prev, iv);
+    const float fa = round_io<IO>(expf(fl + m_prev - mn));
+    const float ia = round_io<IO>(expf(iv - mn));
+    m_prev = mn;
+    float vv[BV];
+#pragma unroll
+    for (int b = 0; b < BV; ++b) vv[b] = load_io<IO>(v, static_cast<int64_t>(t) * str_v + static_cast<int64_t>(hd) * DV + v0 + b);
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) {
+      const int dq = tid + j * nthreads;
+      const float ik = ia * load_io<IO>(k, static_cast<int64_t>(t) * str_qk + static_cast<int64_t>(hd) * DQ + dq);
+#pragma unroll
+      for (int b = 0; b < BV; ++b) C[j][b] = fmaf(ik, vv[b], fa * C[j][b]);
+      nn[j] = fmaf(fa, nn[j], ik);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int dq = tid + j * nthreads;
+    float* crow = c + (static_cast<int64_t>(hd) * DQ + dq) * DV + v0;
+#pragma unroll
+    for (int b = 0; b < BV; ++b) crow[b] = C[j][b];
+    if (blockIdx.x == 0) n[static_cast<int64_t>(hd) * DQ + dq] = nn[j];
+  }
+  if (blockIdx.x == 0 && tid == 0) m[hd] = m_prev;
+}
+
+using CommitFn = void (*)(float*, float*, float*, const float*, const float*, const void*, const void*, const void*,
+                          const void*, const int64_t*, int, int, int, int64_t, int64_t, int64_t, int);
+
+template <int IO, int BV>
+CommitFn commit_dpt(int dpt) {
+  return dpt == 1 ? &mlstm_lazy_commit_kernel<IO, BV, 1> : &mlstm_lazy_commit_kernel<IO, BV, 2>;
+}
+
+template <int IO>
+CommitFn commit_bv(int bv, int dpt) {
+  switch (bv) {
+    case 4: return commit_dpt<IO, 4>(dpt);
+    case 8: return commit_dpt<IO, 8>(dpt);
+    case 16: return commit_dpt<IO, 16>(dpt);
+    default: return nullptr;
+  }
+}
+
+CommitFn pick_commit(int io, int bv, int dpt) {
+  switch (io) {
+    case BP_DT_BF16: return commit_bv<BP_DT_BF16>(bv, dpt);
+    case BP_DT_F16: return commit_bv<BP_DT_F16>(bv, dpt);
+    case BP_DT_F32: return commit_bv<BP_DT_F32>(bv, dpt);
+    default: return nullptr;
+  }
+}
+
 using MlstmFn = void (*)(const float*, const float*, const float*, const void*, const void*, const void*,
                          const void*, const void*, void*, float*, float*, int, int, int, int64_t, int64_t, int64_t,
                          int64_t, int, float, float);
@@ -225,6 +315,31 @@ extern "C" int bp_mlstm_multistep(const void* c, const void* n, const void* m, c
       static_cast<const float*>(c), static_cast<const float*>(n), static_cast<const float*>(m), q, k, v, i, f, h,
       static_cast<float*>(nstart), static_cast<float*>(mstart), T, DQ, DV, str_t_qk, str_t_v, str_t_if, str_t_h,
       gate_dtype, qk_scale, eps);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? BP_OK : static_cast<int>(e);
+}
+
+extern "C" int bp_mlstm_lazy_commit(void* c, void* n, void* m, const void* nstart, const void* mstart, const void* k,
+                                    const void* v, const void* i, const void* f, const void* length, int T, int NH,
+                                    int DQ, int DV, int64_t str_t_qk, int64_t str_t_v, int64_t str_t_if,
+                                    int io_dtype, int gate_dtype, int bv, void* stream) {
+  if (T < 0 || NH < 0 || DQ <= 0 || DV <= 0) return BP_E_INVALID_ARG;
+  if (NH == 0) return BP_OK;
+  if (c == nullptr || n == nullptr || m == nullptr || nstart == nullptr || mstart == nullptr || length == nullptr)
+    return BP_E_INVALID_ARG;
+  if (T > 0 && (k == nullptr || v == nullptr || i == nullptr || f == nullptr)) return BP_E_INVALID_ARG;
+  if (DQ % bp::kWave != 0 || DQ > 2 * bp::kMaxWaves * bp::kWave) return BP_E_UNSUPPORTED;
+  if (gate_dtype < BP_DT_BF16 || gate_dtype > BP_DT_F32) return BP_E_UNSUPPORTED;
+  if (bv != 4 && bv != 8 && bv != 16) return BP_E_UNSUPPORTED;
+  if (DV % bv != 0) return BP_E_UNSUPPORTED;
+  const int dpt = DQ <= bp::kMaxWaves * bp::kWave ? 1 : 2;
+  bp::CommitFn fn = bp::pick_commit(io_dtype, bv, dpt);
+  if (fn == nullptr) return BP_E_UNSUPPORTED;
+  dim3 grid(static_cast<unsigned>(DV / bv), static_cast<unsigned>(NH));
+  fn<<<grid, DQ / dpt, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<float*>(c), static_cast<float*>(n), static_cast<float*>(m), static_cast<const float*>(nstart),
+      static_cast<const float*>(mstart), k, v, i, f, static_cast<const int64_t*>(length), T, DQ, DV, str_t_qk,
+      str_t_v, str_t_if, gate_dtype);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? BP_OK : static_cast<int>(e);
 }

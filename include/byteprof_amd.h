@@ -154,6 +154,36 @@ int bp_mlstm_multistep(const void* c, const void* n, const void* m,
                        int io_dtype, int gate_dtype, float qk_scale, float eps, int bv, void* stream);
 
 /*
+ * Lazy commit of a verify round: the state after positions 0 .. L, with L = *length (an int64 in device memory, so
+ * one captured graph serves every accepted length; clamped to the T positions that k, v, i, f hold), recomputed
+ * from the start state with the same per-position update as bp_mlstm_multistep:
+ *   c [NH, DQ, DV] fp32 holds the start C on entry and the committed C on return (in place);
+ *   nstart [NH, DQ], mstart [NH] (the copies bp_mlstm_multistep made) -> n [NH, DQ], m [NH] (written).
+ * k [T, NH, DQ], v [T, NH, DV]: io_dtype; i, f [T, NH]: gate_dtype; str_t_*: element strides along T.
+ * Replaces: byteprof/optim/mlstm_multistep.py:89-134 (lazy_commit_kernel), draft_fused.py:43-56 (lazy_commit).
+ */
+int bp_mlstm_lazy_commit(void* c, void* n, void* m, const void* nstart, const void* mstart, const void* k,
+                         const void* v, const void* i, const void* f, const void* length, int T, int NH, int DQ,
+                         int DV, int64_t str_t_qk, int64_t str_t_v, int64_t str_t_if, int io_dtype, int gate_dtype,
+                         int bv, void* stream);
+
+/*
+ * Accepted length of a verify pass, on the device: out[:S] <- tok[:S]; out[SMAX] <- the number of leading drafts
+ * ids[1 + j] equal to tok[j] (j < S - 1). ids, tok, out: int64.
+ * Replaces: byteprof/optim/mlstm_multistep.py:136-146 (accept_kernel), draft_fused.py:57-62 (accept).
+ */
+int bp_draft_accept(const void* ids, const void* tok, void* out, int S, int SMAX, void* stream);
+
+/*
+ * cur <- hist[slot] for one layer's state, slot = *length (int64 in device memory, clamped to [0, slots)):
+ * c_cur[i] = c_hist[slot * c_n + i] (i < c_n), likewise n (n_n <= c_n) and m (m_n <= c_n); fp32.
+ * Replaces: byteprof/optim/draft_kernels.py (commit_kernel) via draft_core.py:92-111 (commit_state).
+ */
+int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n_cur, const void* m_hist,
+                    void* m_cur, const void* length, int64_t slots, int64_t c_n, int64_t n_n, int64_t m_n,
+                    void* stream);
+
+/*
  * Decode-step linear set: a chain of skinny linears at one activation row run by one persistent launch.
  *
  * A stage is one or more linears sharing one input vector (q|k|v, gate|up, or a single linear). Its rows are the

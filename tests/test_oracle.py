@@ -338,3 +338,35 @@ def test_int4_skinny_oracle_against_exact_rational_sum():
             exact = sum(Fraction(float(x[i, kk])) * (int(codes[j, kk]) - Fraction(float(zero[kk // 128, j])))
                         * Fraction(float(scale[kk // 128, j])) for kk in range(k))
             assert y[i, j] == np.float32(exact_round(exact, BF16)), (i, j)
+
+
+# ---- drafting bookkeeping ----------------------------------------------------------------------------------------
+
+
+def test_accepted_length_known_answers_of_the_reference():
+    """byteprof tests/test_fused_kernels_gpu.py:116-126 (drafts ids[1:] against the verifier's tokens)."""
+    from oracle import draft as OD
+
+    ids = [10, 5, 6, 7, 8, 9]
+    for tok, want in (([5, 6, 99, 8, 9, 3], 2), ([5, 6, 7, 8, 9 + 260, 3], 4), ([1, 6, 7, 8, 9, 3], 0),
+                      ([5, 6, 7, 8, 9, 3], 5)):
+        assert OD.accepted_length(ids, tok, 6) == want
+    assert OD.accepted_length(ids, [5], 1) == 0  # a single position has no draft to accept
+
+
+def test_committed_state_is_the_multistep_state_of_the_prefix():
+    from oracle import draft as OD
+
+    rng = np.random.default_rng(6)
+    t, nh, dq, dv = 5, 2, 4, 3
+    c, n, m = rng.standard_normal((nh, dq, dv)), rng.standard_normal((nh, dq)), rng.standard_normal(nh)
+    k, v = rng.standard_normal((t, nh, dq)), rng.standard_normal((t, nh, dv))
+    i, f = rng.standard_normal((t, nh)), rng.standard_normal((t, nh)) + 2
+    for length in (0, 2, 4, 9):
+        st = OD.committed_state(c, n, m, k, v, i, f, length, "f64")
+        steps = min(length + 1, t)
+        _, want = OM.multistep(c, n, m, k[:steps], k[:steps], v[:steps], i[:steps], f[:steps], eps=1e-6, io="f64")
+        for a, b in zip(st, want):
+            assert np.array_equal(a, b)
+    c0, n0, m0 = OD.committed_state(c, n, m, k, v, i, f, -1, "f64")
+    assert np.array_equal(c0, c) and np.array_equal(n0, n) and np.array_equal(m0, m)
