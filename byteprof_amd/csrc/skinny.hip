@@ -25,6 +25,10 @@ extern template SkinnyFn skinny_pick<kInt8, 16>(int, int, bool);
 // per wave), K per step.
 SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth);
 int mfma_k_step(int wkind);
+// LDS-staged matrix-core variant (depth 3: each wave owns whole blocks; 4: the waves share each block's steps):
+// kernel for (kind, waves, share), largest K slice per workgroup.
+SkinnyFn mfma_staged_pick(int wkind, int waves, bool share);
+int mfma_staged_k_max();
 
 // int4 group-128 kernels (skinny_int4.hip).
 using Int4Fn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
@@ -127,6 +131,48 @@ int skinny_launch(int wkind, const void* x, const void* w, const void* scale, in
   return launch_status();
 }
 
+// Compute units of the current device (cached per device; 0 when the query fails).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cache[dev] > 0) return cache[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cache[dev] = cus;
+  return cus;
+}
+
+// The staged variant: 16-row blocks only; each workgroup stages K / split activations (at most mfma_staged_k_max(),
+// K / split a multiple of the 1 KiB step, and the steps of a slice a multiple or a divisor of the waves) and loops
+// over rounds of row blocks; one workgroup per CU (LDS).
+int skinny_mfma_staged_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y,
+                              int64_t M, int64_t N, int64_t K, int rb, int waves, bool share, int split, void* ws,
+                              size_t ws_bytes, hipStream_t st) {
+  SkinnyFn fn = mfma_staged_pick(wkind, waves, share);
+  if (fn == nullptr || rb != 1) return BP_E_UNSUPPORTED;
+  const int64_t step = wkind == kBf16 ? 512 : 1024;
+  if (K % (static_cast<int64_t>(split) * step) != 0 || K / split > mfma_staged_k_max()) return BP_E_UNSUPPORTED;
+  const int64_t nsteps = K / split / step;
+  if (share && nsteps % waves != 0 && waves % nsteps != 0) return BP_E_UNSUPPORTED;
+  const int64_t per_round = share ? waves / std::min<int64_t>(waves, nsteps) : waves;  // blocks per round
+  if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
+    return BP_E_WORKSPACE;
+  const int cus = device_cus();
+  if (cus <= 0) return static_cast<int>(hipErrorInvalidDevice);
+  const int64_t blocks = (N + 15) / 16;
+  const int64_t gx = std::min<int64_t>((blocks + per_round - 1) / per_round, std::max(1, cus / split));
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(split));
+  fn<<<grid, waves * kWave, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale,
+                                     scale_dt, static_cast<uint16_t*>(y), static_cast<float*>(ws),
+                                     static_cast<int>(M), N, K, split);
+  const int rc = launch_status();
+  if (rc != BP_OK || split == 1) return rc;
+  splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
+                                                       wkind == kInt8 ? scale : nullptr, scale_dt, M, N, split);
+  return launch_status();
+}
+
 int skinny_mfma_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y,
                        int64_t M, int64_t N, int64_t K, int rb, int waves, int depth, int split, void* ws,
                        size_t ws_bytes, void* stream) {
@@ -140,9 +186,12 @@ int skinny_mfma_launch(int wkind, const void* x, const void* w, const void* scal
     fill_zero_bf16_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<uint16_t*>(y), M * N);
     return launch_status();
   }
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0) return BP_E_UNSUPPORTED;
+  if (depth == 3 || depth == 4)
+    return skinny_mfma_staged_launch(wkind, x, w, scale, scale_dt, y, M, N, K, rb, waves, depth == 4, split, ws,
+                                     ws_bytes, st);
   const int step = mfma_k_step(wkind);
-  if (K % step != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
-    return BP_E_UNSUPPORTED;
+  if (K % step != 0) return BP_E_UNSUPPORTED;
   SkinnyFn fn = mfma_pick(wkind, rb, waves, depth);
   if (fn == nullptr) return BP_E_UNSUPPORTED;
   const int64_t nst = K / step;
@@ -215,6 +264,8 @@ int bp_skinny_int4(const void* x, const void* packed, const void* scale, int sca
 }
 
 int bp_skinny_mfma_config_supported(int wkind, int block_rows, int waves, int depth) {
+  if (depth == 3 || depth == 4)
+    return block_rows == 16 && bp::mfma_staged_pick(wkind, waves, depth == 4) != nullptr ? 1 : 0;
   return block_rows % 16 == 0 && bp::mfma_pick(wkind, block_rows / 16, waves, depth) != nullptr ? 1 : 0;
 }
 

@@ -115,6 +115,27 @@ def _resolve(kind: str, n: int, k: int, bm: int, cfg) -> tuple[int, int, int]:
 MFMA_BUCKETS = (8, 16)  # row buckets (M = 5..16) served by the matrix-core kernels when the shape allows
 
 
+# The LDS-staged matrix-core kernel (depth 3: each wave owns whole 16-row blocks; depth 4: the waves of a workgroup
+# share each block's steps): K per 1 KiB step, activation elements a workgroup stages in LDS.
+STAGED_DEPTHS = (3, 4)
+STAGED_STEP = {"bf16": 512, "int8": 1024}
+STAGED_K_MAX = 2048
+
+
+def staged_split(kind: str, k: int, split: int = 1, waves: int = 1, depth: int = 3) -> int | None:
+    """The smallest split >= `split` that the LDS-staged kernel takes for K (K / split a multiple of the step and
+    at most STAGED_K_MAX; at depth 4 its steps a multiple or a divisor of the waves), or None."""
+    step = STAGED_STEP[kind]
+    if k <= 0 or k % step:
+        return None
+    for s in range(max(1, split), k // step + 1):
+        if k % (s * step) == 0 and k // s <= STAGED_K_MAX:
+            steps = k // s // step
+            if depth != 4 or steps % waves == 0 or waves % steps == 0:
+                return s
+    return None
+
+
 def mfma_cfg(kind: str, n: int, k: int) -> tuple[int, int, int, int] | None:
     """(block_rows, waves, depth, split) of the matrix-core kernel for a shape's 8- and 16-row buckets, or None
     when those buckets stay on the VALU kernel (table entry 'mfma', else a heuristic)."""
@@ -124,7 +145,11 @@ def mfma_cfg(kind: str, n: int, k: int) -> tuple[int, int, int, int] | None:
     if entry is not None:
         if not entry.get("use", True):
             return None
-        return int(entry["block_rows"]), int(entry["waves"]), int(entry["depth"]), int(entry.get("split", 1))
+        depth = int(entry["depth"])
+        if depth in STAGED_DEPTHS and staged_split(kind, k, int(entry.get("split", 1)), int(entry["waves"]),
+                                                  depth) is None:
+            return None
+        return int(entry["block_rows"]), int(entry["waves"]), depth, int(entry.get("split", 1))
     steps = k // mfma_k_step(kind)
     waves = 1
     while waves * 2 <= min(steps, 4):
@@ -175,7 +200,12 @@ def launch_mfma(kind: str, x: torch.Tensor, w: torch.Tensor, scale, y: torch.Ten
     """One launch of the matrix-core kernel on 1..16 activation rows (operands validated by the caller)."""
     m, k = x.shape
     n = w.shape[0]
-    split = max(1, min(split, k // mfma_k_step(kind)))
+    if depth in STAGED_DEPTHS:
+        split = staged_split(kind, k, split, waves, depth)
+        if split is None:
+            raise ValueError(f"K = {k} does not fit the LDS-staged matrix-core kernel")
+    else:
+        split = max(1, min(split, k // mfma_k_step(kind)))
     L = _lib.lib()
     ws = None
     ws_bytes = 0

@@ -179,11 +179,23 @@ def tune_mfma(kind: str, n: int, k: int, device, entry: dict, log=print) -> dict
                     calls = [lambda a=a: S.launch_mfma(kind, x16, a[0], a[1] if kind == "int8" else None, y16, br, w,
                                                        d, sp) for a in ring]
                     results[(br, w, d, sp)] = _time_calls(calls)
+    # the LDS-staged variants: 16-row blocks, the smallest valid split and twice it
+    for d in S.STAGED_DEPTHS:
+        for w in (1, 2, 4):
+            s0 = S.staged_split(kind, k, 1, w, d)
+            if s0 is None:
+                continue
+            for sp in sorted({s0, S.staged_split(kind, k, 2 * s0, w, d)} - {None}):
+                calls = [lambda a=a: S.launch_mfma(kind, x16, a[0], a[1] if kind == "int8" else None, y16, 16, w, d,
+                                                   sp) for a in ring]
+                results[(16, w, d, sp)] = _time_calls(calls)
     best = min(results, key=results.get)
     if best[3] > 1:
-        no_split = min((c for c in results if c[3] == 1), key=results.get)
-        if results[no_split] <= results[best] * 1.03:
-            best = no_split
+        no_split = [c for c in results if c[3] == 1]
+        if no_split:
+            no_split = min(no_split, key=results.get)
+            if results[no_split] <= results[best] * 1.03:
+                best = no_split
     br, w, d, sp = best
     us = {"16": round(results[best], 3)}
     x8 = x16[:8].contiguous()
@@ -255,9 +267,13 @@ def main(argv=None) -> int:
     device = torch.device("cuda:0")
     out = Path(a.out)
     table = json.loads(out.read_text()) if out.exists() else {}
-    table["_about"] = ("skinny kernel tile configurations for gfx950, tuned by python -m byteprof_amd.tune: "
-                       "key kind|N|K; waves and split fix the K order for every row bucket; rows per bucket; "
-                       "us = measured time per call (ring of distinct weights, HIP graph)")
+    table["_about"] = ("skinny kernel tile configurations for gfx950, tuned by python -m byteprof_amd.tune: key "
+                       "kind|N|K; VALU kernels: waves and split fix the K order for every row bucket, rows per "
+                       "bucket; 'mfma': the matrix-core configuration (block_rows, waves, depth, split) of the 8- and "
+                       "16-row buckets and whether it is used (depth 1, 2: register-fed, steps in flight; 3, 4: "
+                       "LDS-staged, each wave owns whole blocks / the waves share each block); int4|N|K: waves and "
+                       "split of the int4 kernel (tile rows 32); us = measured time per call (ring of distinct "
+                       "weights, HIP graph)")
     for kind in a.kinds.split(","):
         if kind == "int4":
             for n, k in shapes:

@@ -80,12 +80,17 @@ int bp_skinny_int8(const void* x, const void* q, const void* scale, int scale_dt
  * Matrix-core variants of bp_skinny_bf16 / bp_skinny_int8 (v_mfma_f32_16x16x32_bf16 with the weights as the A
  * operand: 16 output channels x 16 activation rows x 32 K per instruction), same arguments and results, for the
  * speculative-verify widths where the VALU kernels run out of instruction throughput. 1 <= M <= 16.
- *   block_rows: weight rows per workgroup, 16, 32 or 64; waves: 1, 2, 4 or 8; depth: K steps in flight per wave,
- *   1 or 2; split: as above.
- *   K must be a multiple of bp_skinny_mfma_k_step(wkind) (128 for bf16, 256 for int8) and x, w 16-byte aligned
- *   (BP_E_UNSUPPORTED otherwise: the VALU kernels take any K).
- * The K order of every sum depends only on (K, waves, split), so output row i does not change with M (bitwise);
- * it differs from the VALU kernels' order (both fp32; the results agree within rounding).
+ *   depth 1 or 2 (register-fed kernel: each lane loads its MFMA operands straight from memory, depth = K steps in
+ *   flight per wave): block_rows 16, 32 or 64 weight rows per workgroup; waves 1, 2, 4 or 8; split as above;
+ *   K a multiple of bp_skinny_mfma_k_step(wkind) (128 for bf16, 256 for int8).
+ *   depth 3 or 4 (LDS-staged kernel: each weight row is streamed in 1 KiB contiguous loads and re-read from LDS in
+ *   MFMA layout; the activations of the workgroup's K slice are staged in LDS once): block_rows 16; waves 1, 2 or
+ *   4; K / split a multiple of 1 KiB of weight row (512 bf16 / 1024 int8 elements) and at most 2048; depth 3: each
+ *   wave owns whole 16-row blocks; depth 4: the waves of a workgroup share each block's K steps (the steps of the
+ *   slice a multiple or a divisor of waves), adding their partial tiles in wave order.
+ *   x, w 16-byte aligned. BP_E_UNSUPPORTED when a condition fails (the VALU kernels take any K).
+ * The K order of every sum depends only on (K, waves, depth family, split), so output row i does not change with M
+ * (bitwise); it differs from the VALU kernels' order (both fp32; the results agree within rounding).
  * Replaces: byteprof/optim/skinny.py:36-90 (_skinny_kernel MODE 0 / 1, whose tl.dot maps onto the tensor cores
  *           at every BM) via skinny_mm (skinny.py:136-166).
  */

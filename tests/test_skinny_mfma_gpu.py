@@ -45,6 +45,40 @@ def test_every_configuration_matches_the_oracle(kind, depth):
 
 
 @pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("depth", S.STAGED_DEPTHS)
+def test_staged_configurations_match_the_oracle(kind, depth):
+    """The LDS-staged variants (16-row blocks; depth 3 each wave owns whole blocks, depth 4 the waves share them):
+    every wave count, K of one to six 1 KiB steps, K slices of one workgroup up to 2048 (larger K needs split),
+    ragged N, 1..16 rows."""
+    for n, k in ((70, 1024), (33, 3072), (1000, 6144)):
+        print(f"\n[mfma-staged] kind={kind} depth={depth} n={n} k={k}", flush=True)
+        _, args = make_weights(kind, n, k, seed=n + k)
+        w_np = oracle_weights(kind, args)
+        x = randn_x(16, k, seed=13)
+        for waves in (1, 2, 4):
+            splits = {S.staged_split(kind, k, 1, waves, depth), S.staged_split(kind, k, 3, waves, depth)} - {None}
+            assert splits
+            for split in sorted(splits):
+                for m in (1, 5, 16):
+                    y = _mfma(kind, x[:m].contiguous(), args, 16, waves, depth, split, n)
+                    check_against_oracle(y, x[:m], w_np)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("depth", S.STAGED_DEPTHS)
+def test_staged_rows_do_not_depend_on_the_other_rows(kind, depth):
+    n, k = 300, 4096
+    _, args = make_weights(kind, n, k, seed=19)
+    x = randn_x(16, k, seed=7)
+    split = S.staged_split(kind, k, 1, 4, depth)
+    full = _mfma(kind, x, args, 16, 4, depth, split, n)
+    for m in (1, 3, 8, 15):
+        assert torch.equal(_mfma(kind, x[:m].contiguous(), args, 16, 4, depth, split, n), full[:m]), m
+    if depth == 3:  # each wave adds a block's steps in K order, whatever the number of waves
+        assert torch.equal(_mfma(kind, x, args, 16, 1, depth, split, n), full)
+
+
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("n,k", [(2048, 2048), (8192, 2048), (2048, 8192), (6144, 2048), (16384, 2048),
                                  (100352, 2048)])
 def test_verify_widths_match_the_oracle(kind, n, k):
@@ -141,7 +175,14 @@ def test_argument_checks():
     assert call(2, 128, br=24) == -2   # block rows not a multiple of 16
     assert call(2, 128, br=128) == -2  # not compiled
     assert call(2, 128, waves=3) == -2
-    assert call(2, 128, depth=3) == -2
+    assert call(2, 128, depth=3) == -2           # the staged variants need K a multiple of 512 (bf16)
+    assert call(2, 512, br=32, depth=4) == -2    # and 16-row blocks
+    assert call(2, 512, waves=8, depth=3) == -2  # at most 4 waves
+    assert call(2, 1536, waves=2, depth=4) == -2  # 3 steps: not a multiple or divisor of 2 sharing waves
+    assert call(2, 128, depth=5) == -2
+    assert L.bp_skinny_mfma_config_supported(0, 16, 4, 4) == 1
+    assert L.bp_skinny_mfma_config_supported(1, 16, 2, 3) == 1
+    assert L.bp_skinny_mfma_config_supported(0, 32, 4, 3) == 0
     assert L.bp_skinny_mfma_config_supported(0, 64, 8, 2) == 1
     assert L.bp_skinny_mfma_config_supported(1, 48, 8, 2) == 0
     torch.cuda.synchronize()
