@@ -95,4 +95,23 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Totals of four rows' per-lane partial sums a0..a3: every row is added in the same order, ((x[j] + x[j + 32]) +
+// (x[j + 16] + x[j + 48])) for j < 16 (v_permlane32_swap, then v_permlane16_swap), then a butterfly over 16 lanes;
+// returns with a0's total in lanes 0..15, a2's in 16..31, a1's in 32..47 and a3's in 48..63.
+__device__ __forceinline__ float wave_sum4_rows(float a0, float a1, float a2, float a3) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a0), __float_as_uint(a1), false, false);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(a2), __float_as_uint(a3), false, false);
+  // p: {[a0 lanes 0-31 | a1 lanes 0-31], [a0 lanes 32-63 | a1 lanes 32-63]}, q likewise for a2, a3
+  const float b01 = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const float b23 = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+  // odd 16-lane rows of b01 <-> even rows of b23: {[b01 r0, b23 r0, b01 r2, b23 r2], [b01 r1, b23 r1, b01 r3, b23 r3]}
+  const auto u = __builtin_amdgcn_permlane16_swap(__float_as_uint(b01), __float_as_uint(b23), false, false);
+  float c = __uint_as_float(u[0]) + __uint_as_float(u[1]);
+  c += dpp_f32<0xB1, 0xF>(c);   // quad_perm [1,0,3,2]
+  c += dpp_f32<0x4E, 0xF>(c);   // quad_perm [2,3,0,1]
+  c += dpp_f32<0x141, 0xF>(c);  // row_half_mirror
+  c += dpp_f32<0x140, 0xF>(c);  // row_mirror
+  return c;
+}
+
 }  // namespace bp

@@ -315,6 +315,60 @@ struct Consumer {
     }
   }
 
+  // R <= 4 rows of two chunks each (C == 2, the input chunks resident in xr): one wait and one round of ring reads
+  // for all R rows, their dot chains interleaved, one wave reduction for the four (wave_sum4_rows) and one store
+  // instruction per output array (lanes 0, 16, 32, 48 hold the four totals). Short rows (an int8 row of 2048 is
+  // 2 KiB) make the per-row wait, reduction and stores the consumer's bound; this divides them by R. Every row of
+  // such a stage goes through here (R = 4, then 2 and 1 for the last rows), so its sum order does not depend on
+  // where the row falls in a group.
+  template <int R>
+  __device__ __forceinline__ void rows(StageTable st, SetLds& L, int S, int who, int lane, uint32_t* tagged,
+                                       uint32_t (&xr)[4][Layout<KIND>::kXDwords]) {
+    constexpr int G = 2 * R;  // chunks
+    static_assert(G <= kSetSlots, "the ring holds a consumer's largest group");
+    uint32_t it = 0;
+    while (seen < n + G && !failed) {
+      seen = lds_load_relaxed(&L.landed[who]);
+      if (seen >= n + G) break;
+      if (++it > kSpinCapLds) {
+        failed = true;
+        record_error(tagged - kWordsHeader);
+      }
+      __builtin_amdgcn_s_sleep(0);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    u32x4 w[G];
+    int slot = n % kSetSlots;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      w[j] = *reinterpret_cast<const u32x4*>(&L.ring[who][slot][lane * 16]);
+      slot = slot + 1 == kSetSlots ? 0 : slot + 1;
+    }
+    float a[R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q], xr[0], 0.f);
+#pragma unroll
+    for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q + 1], xr[1], a[q]);
+    n += G;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane == 0) lds_store_relaxed(&L.consumed[who], n);
+    const float tot = wave_sum4_rows(a[0], a[R > 1 ? 1 : 0], a[R > 2 ? 2 : 0], a[R > 3 ? 3 : 0]);
+    const int q = ((lane >> 5) & 1) | ((lane >> 3) & 2);  // row of the total in lanes 0, 16, 32, 48
+    if ((lane & 15) == 0 && q < R) {
+      float v = tot;
+      if constexpr (KIND == kInt8) v *= L.scale[s & 1][r + q - row0];
+      const uint32_t bits = float_to_bf16_bits(v);
+      y[r + q] = static_cast<uint16_t>(bits);
+      st_agent(&ty[r + q], (tag << 16) | bits);
+    }
+    r += R;
+    if (r == r1) {
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (lane == 0) __hip_atomic_fetch_add(&L.done[s], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      enter(st, L, S, who, s + 1, tagged);
+    }
+  }
+
   __device__ __forceinline__ void run(StageTable st, SetLds& L, int S, int who, int lane, uint32_t* tagged) {
     using Lay = Layout<KIND>;
     uint32_t xr[4][Lay::kXDwords];
@@ -339,7 +393,14 @@ struct Consumer {
         if (C == 4) {
           while (s == stage) group<4, true>(st, L, S, who, lane, tagged, xr);
         } else {
-          while (s == stage) group<2, true>(st, L, S, who, lane, tagged, xr);
+          while (s == stage) {
+            if (r1 - r >= 4)
+              rows<4>(st, L, S, who, lane, tagged, xr);
+            else if (r1 - r >= 2)
+              rows<2>(st, L, S, who, lane, tagged, xr);
+            else
+              rows<1>(st, L, S, who, lane, tagged, xr);
+          }
         }
       } else if ((C & 3) == 0) {
         group<4, false>(st, L, S, who, lane, tagged, xr);
