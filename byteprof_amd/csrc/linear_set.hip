@@ -92,6 +92,12 @@ constexpr int waitcnt_vm() {
   return (N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8);
 }
 
+// s_waitcnt lgkmcnt(0), vector memory and export counts left at their maxima. Ends a path that issued scalar loads,
+// so that no scalar load is pending where it joins the common path (lgkmcnt also counts LDS operations, and the
+// only wait the compiler can place for an out-of-order scalar load at a join is lgkmcnt(0), which would make every
+// chunk of the common path wait for its own LDS writes).
+constexpr int kWaitLgkm0 = 0xF | (0x3 << 14) | (0x7 << 4);
+
 __device__ __forceinline__ int lds_load_relaxed(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -113,15 +119,29 @@ __device__ __forceinline__ void record_error(uint32_t* scratch) { st_agent(&scra
 // Cache policy of the gathers of published rows: device scope (sc1), served coherently across the XCDs' L2s.
 constexpr int kDeviceScope = 16;
 
-// Weight-chunk stream of one consumer: its rows of every stage in stage order, each row in 1 KiB chunks.
+// Weight-chunk stream of one consumer: its rows of every stage in stage order, each row in 1 KiB chunks. The rows
+// of one weight segment are contiguous in memory, so the stream is a sequence of contiguous runs (the consumer's
+// rows of a stage within one segment): the common step is one 64-bit add and one count, and the stage table is read
+// only where a run ends.
 template <int KIND>
 struct Cursor {
   int s;              // current stage (S: stream ended)
-  int r, r1;          // current row, end of the consumer's rows
-  int c, C;           // chunk of the row, chunks per row
-  int seg, seg_end;
-  const BP_GLOBAL uint8_t* p;  // next chunk
-  int row_bytes;
+  int r, r1;          // first row after the current run, end of the consumer's rows in stage s
+  int seg;            // segment of the current run
+  int left;           // chunks left in the current run
+  const BP_GLOBAL uint8_t* p;  // the next chunk; once the stream has ended, its first chunk (loads stay in bounds)
+  const BP_GLOBAL uint8_t* first;
+
+  // The run of rows r .. min(r1, end of segment seg) - 1.
+  __device__ __forceinline__ void start_run(StageTable st, int seg_begin) {
+    const int row_bytes = st[s].K * Layout<KIND>::kElemBytes;
+    const int run_end = min(r1, st[s].seg_end[seg]);
+    left = (run_end - r) * (row_bytes >> 10);
+    p = (const BP_GLOBAL uint8_t*)(st[s].w[seg]) + static_cast<int64_t>(r - seg_begin) * row_bytes;
+    r = run_end;
+    // the stage-table values in registers here, so that no scalar load is pending where the common path resumes
+    asm volatile("" ::"s"(p), "s"(left));
+  }
 
   __device__ __forceinline__ void enter(StageTable st, const SetLds& L, int S, int who, int from) {
     for (s = from; s < S; ++s) {
@@ -129,30 +149,42 @@ struct Cursor {
       r1 = uniform(L.rows[s][who + 1]);
       if (r < r1) break;
     }
-    if (s >= S) return;
-    row_bytes = st[s].K * Layout<KIND>::kElemBytes;
-    C = row_bytes >> 10;
-    c = 0;
+    if (s >= S) {
+      p = first;
+      return;
+    }
     seg = 0;
     int seg_begin = 0;
     while (st[s].seg_end[seg] <= r) seg_begin = st[s].seg_end[seg++];
-    seg_end = st[s].seg_end[seg];
-    p = (const BP_GLOBAL uint8_t*)(st[s].w[seg]) + static_cast<int64_t>(r - seg_begin) * row_bytes;
+    start_run(st, seg_begin);
   }
 
   __device__ __forceinline__ void advance(StageTable st, const SetLds& L, int S, int who) {
     p += 1024;
-    if (++c < C) return;
-    c = 0;
-    if (++r == r1) {
+    if (__builtin_expect(--left > 0, 1)) return;
+    if (r == r1) {
       enter(st, L, S, who, s + 1);
-    } else if (r == seg_end) {
+    } else {  // r is the first row of segment seg + 1
       ++seg;
-      seg_end = st[s].seg_end[seg];
-      p = (const BP_GLOBAL uint8_t*)(st[s].w[seg]);
+      start_run(st, r);
     }
   }
 };
+
+// int8 rows against activations held as fp16 pairs (x * 2^e, see Consumer::run): each weight byte q becomes the fp16
+// value 1024 + (q ^ 0x80) = 1152 + q with one v_perm_b32 per pair (0x64 is the fp16 exponent byte of 1024 and the
+// byte fills the low 8 of its 10 mantissa bits, so the value is exact), so the chunk costs 5 instructions per 4
+// weights where the exact bf16 conversion costs 8; the caller removes 1152 * sum(x) once per row. Products are
+// exact in fp32 (11 x 11 significant bits); only the fp32 accumulation rounds.
+__device__ __forceinline__ float chunk_dot_i8_f16(const u32x4& wv, const uint32_t (&xh)[8], float acc) {
+  const uint32_t wd[4] = {wv.x ^ 0x80808080u, wv.y ^ 0x80808080u, wv.z ^ 0x80808080u, wv.w ^ 0x80808080u};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc = dot2_f16(__builtin_amdgcn_perm(wd[j], 0x64646464u, 0x00050004u), xh[2 * j], acc);
+    acc = dot2_f16(__builtin_amdgcn_perm(wd[j], 0x64646464u, 0x00070006u), xh[2 * j + 1], acc);
+  }
+  return acc;
+}
 
 // Producer wave `who`: copies its consumer's chunks into the consumer's LDS ring. Chunks travel through a ring of
 // kSetInflight registers: the producer waits for its oldest load, writes that chunk into the LDS ring, publishes
@@ -165,15 +197,19 @@ template <int KIND>
 __device__ __forceinline__ void producer_wave(StageTable st, SetLds& L, int S, int who, int lane,
                                               uint32_t* scratch) {
   Cursor<KIND> cur;
+  cur.first = nullptr;
   cur.enter(st, L, S, who, 0);
   if (cur.s >= S) return;  // no rows in any stage: the consumer has none either
-  const BP_GLOBAL uint8_t* const idle = cur.p;
+  cur.first = cur.p;
+  // a 32-bit lane offset on a wave-uniform base: the loads take the scalar-base form (saddr + voffset), with no
+  // per-chunk vector address arithmetic on the SIMD the producer shares with its consumer
+  const uint32_t lane_off = static_cast<uint32_t>(lane) * 16u;
   u32x4 buf[kSetInflight];
   int issued = 0;
 #pragma unroll
   for (int j = 0; j < kSetInflight; ++j) {
     const bool real = cur.s < S;
-    buf[j] = __builtin_nontemporal_load((const BP_GLOBAL u32x4*)((real ? cur.p : idle) + lane * 16));
+    buf[j] = __builtin_nontemporal_load((const BP_GLOBAL u32x4*)(cur.p + lane_off));
     if (real) {
       cur.advance(st, L, S, who);
       ++issued;
@@ -187,7 +223,7 @@ __device__ __forceinline__ void producer_wave(StageTable st, SetLds& L, int S, i
       if (n < issued) {
         if (n >= limit) {
           uint32_t it = 0;
-          while (!failed && n >= (limit = lds_load_relaxed(&L.consumed[who]) + kSetSlots)) {
+          while (!failed && n >= (limit = uniform(lds_load_relaxed(&L.consumed[who])) + kSetSlots)) {
             if (++it > kSpinCapLds) {
               failed = true;
               record_error(scratch);
@@ -203,7 +239,7 @@ __device__ __forceinline__ void producer_wave(StageTable st, SetLds& L, int S, i
         if (lane == 0) lds_store_relaxed(&L.landed[who], n);
       }
       const bool real = cur.s < S;
-      buf[j] = __builtin_nontemporal_load((const BP_GLOBAL u32x4*)((real ? cur.p : idle) + lane * 16));
+      buf[j] = __builtin_nontemporal_load((const BP_GLOBAL u32x4*)(cur.p + lane_off));
       if (real) {
         cur.advance(st, L, S, who);
         ++issued;
@@ -226,6 +262,7 @@ struct Consumer {
   float acc;
   bool failed;
   uint32_t tag;
+  float xsum, xinv;        // int8 rows of two chunks: sum of the lane's fp16 input values, 2^-e of their scaling
   BP_GLOBAL uint16_t* y;   // the stage's outputs
   uint32_t* ty;            // the stage's tagged outputs
 
@@ -262,7 +299,7 @@ struct Consumer {
     using Lay = Layout<KIND>;
     uint32_t it = 0;
     while (seen < n + GS && !failed) {
-      seen = lds_load_relaxed(&L.landed[who]);
+      seen = uniform(lds_load_relaxed(&L.landed[who]));
       if (seen >= n + GS) break;
       if (++it > kSpinCapLds) {
         failed = true;
@@ -328,7 +365,7 @@ struct Consumer {
     static_assert(G <= kSetSlots, "the ring holds a consumer's largest group");
     uint32_t it = 0;
     while (seen < n + G && !failed) {
-      seen = lds_load_relaxed(&L.landed[who]);
+      seen = uniform(lds_load_relaxed(&L.landed[who]));
       if (seen >= n + G) break;
       if (++it > kSpinCapLds) {
         failed = true;
@@ -338,17 +375,33 @@ struct Consumer {
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     u32x4 w[G];
-    int slot = n % kSetSlots;
+    const int slot0 = n % kSetSlots;
+    if (slot0 + G <= kSetSlots) {  // the group's slots are contiguous: one address, immediate offsets
+      const uint8_t* base = &L.ring[who][slot0][lane * 16];
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-      w[j] = *reinterpret_cast<const u32x4*>(&L.ring[who][slot][lane * 16]);
-      slot = slot + 1 == kSetSlots ? 0 : slot + 1;
+      for (int j = 0; j < G; ++j) w[j] = *reinterpret_cast<const u32x4*>(base + j * 1024);
+    } else {
+      int slot = slot0;
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        w[j] = *reinterpret_cast<const u32x4*>(&L.ring[who][slot][lane * 16]);
+        slot = slot + 1 == kSetSlots ? 0 : slot + 1;
+      }
     }
     float a[R];
+    if constexpr (KIND == kInt8) {  // xr holds fp16 pairs of x * 2^e (run)
 #pragma unroll
-    for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q], xr[0], 0.f);
+      for (int q = 0; q < R; ++q) a[q] = chunk_dot_i8_f16(w[2 * q], xr[0], 0.f);
 #pragma unroll
-    for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q + 1], xr[1], a[q]);
+      for (int q = 0; q < R; ++q) a[q] = chunk_dot_i8_f16(w[2 * q + 1], xr[1], a[q]);
+#pragma unroll
+      for (int q = 0; q < R; ++q) a[q] = (a[q] - 1152.f * xsum) * xinv;
+    } else {
+#pragma unroll
+      for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q], xr[0], 0.f);
+#pragma unroll
+      for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q + 1], xr[1], a[q]);
+    }
     n += G;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (lane == 0) lds_store_relaxed(&L.consumed[who], n);
@@ -393,6 +446,31 @@ struct Consumer {
         if (C == 4) {
           while (s == stage) group<4, true>(st, L, S, who, lane, tagged, xr);
         } else {
+          if constexpr (KIND == kInt8) {
+            // the lane's 32 input values as fp16 pairs of x * 2^e, e chosen so that the largest lies in
+            // [2^14, 2^15): exact for every value down to 2^-28 of the largest (fp16 normals), then rounded
+            float m = 0.f;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int d = 0; d < 8; ++d)
+                m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_float(xr[j][d] & 0xffffu)),
+                                   fabsf(bf16_bits_to_float(xr[j][d] >> 16))));
+            const int e = min(141 - ((__float_as_int(m) >> 23) & 0xff), 126);  // 2^e and 2^-e are fp32 normals
+            const float sc = __int_as_float((e + 127) << 23);
+            xinv = __int_as_float((127 - e) << 23);
+            xsum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int d = 0; d < 8; ++d) {
+                const _Float16 lo = static_cast<_Float16>(bf16_bits_to_float(xr[j][d] & 0xffffu) * sc);
+                const _Float16 hi = static_cast<_Float16>(bf16_bits_to_float(xr[j][d] >> 16) * sc);
+                xsum += static_cast<float>(lo) + static_cast<float>(hi);
+                xr[j][d] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+              }
+          }
           while (s == stage) {
             if (r1 - r >= 4)
               rows<4>(st, L, S, who, lane, tagged, xr);
