@@ -15,8 +15,8 @@ the launch stream over the timed steps, and the HBM traffic per launch from the 
 summary (profiles/linear_set_kernel_decode_set.md); the CPU baseline (torch F.linear, the reference's CPU path for
 these linears, on the host cores); and secondary figures: the same set as a dependent decode chain in one launch
 (each stage reads the renormalised output it depends on), the 113-launch HIP graph of skinny kernels, the int8
-set (fp16 scales) both ways, the fused mLSTM block, and the bf16 verify-width sweep (M = 1..16, VALU / matrix-core
-kernels).
+set (fp16 scales) both ways, the fused mLSTM block, the bf16 verify-width sweep (M = 1..16, VALU / matrix-core
+kernels), and the graph-captured greedy decode loop of the OLMo-2-1B-shaped model (us per token, bf16 and int8).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
 """
@@ -241,6 +241,67 @@ def sweep(device) -> dict:
     return out
 
 
+def decode_loop(device, new_tokens: int = 128) -> dict:
+    """The graph-captured greedy decode loop (byteprof_amd/optim/olmo.py) on the OLMo-2-1B shape with synthetic
+    weights: per kind, the GPU time of one captured decode step (replays timed with events), the loop's time per
+    token (one replay + one pinned read + one sync; a generate of 1 + N tokens minus one of 1, over N) and the
+    eager loop's, with the weight bytes a step streams."""
+    import torch
+
+    from byteprof_amd.optim import olmo as OG
+
+    cfg = OG.OLMO2_1B
+    prompt = torch.tensor([[11, 2027, 5, 99999, 42, 3, 3, 1000]])
+    out = {"model": "OLMo-2-1B shape (16 x 2048, FFN 8192, 16 heads, vocab 100352), synthetic weights",
+           "prompt_tokens": prompt.shape[1], "new_tokens": new_tokens, "launches_per_step": 4 + 9 * cfg.layers}
+    for kind in ("bf16", "int8"):
+        dec = OG.OlmoDecoder(cfg, OG.random_weights(cfg, device, seed=4), kind)
+        graph = OG.make_generate_graph(dec)
+        graph(prompt, max_new_tokens=4)  # captures the step
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graph(prompt, max_new_tokens=1)
+        t1 = time.perf_counter()
+        graph(prompt, max_new_tokens=1 + new_tokens)
+        t2 = time.perf_counter()
+        loop_us = ((t2 - t1) - (t1 - t0)) / new_tokens * 1e6
+        eager = OG.make_generate(dec)
+        e0 = time.perf_counter()
+        eager(prompt, max_new_tokens=1)
+        e1 = time.perf_counter()
+        eager(prompt, max_new_tokens=1 + 32)
+        e2 = time.perf_counter()
+        eager_us = ((e2 - e1) - (e1 - e0)) / 32 * 1e6
+        # the captured step alone: replays back to back, timed on the GPU
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        reps = 50
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            dec.step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            dec.step()
+        dec.pos.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(reps):
+            g.replay()
+        ev[1].record()
+        ev[1].synchronize()
+        step_us = ev[0].elapsed_time(ev[1]) / reps * 1e3
+        nb = dec.weight_bytes()
+        out[kind] = {"us_per_token_loop": loop_us, "us_per_step_graph": step_us, "us_per_token_eager": eager_us,
+                     "weight_bytes_per_step": nb, "weight_gbs_graph_step": nb / step_us / 1e3,
+                     "tokens_per_s_loop": 1e6 / loop_us}
+        del dec, graph, eager, g
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -323,6 +384,8 @@ def main() -> int:
         result["mlstm"] = mlstm_block(device)
         log("[bench] verify-width sweep")
         result["sweep_bf16"] = sweep(device)
+        log("[bench] decode loop")
+        result["decode_loop"] = decode_loop(device)
     if not a.no_cpu:
         log("[bench] CPU baseline")
         if ops is None:

@@ -56,6 +56,13 @@ SIGNATURES: dict[str, tuple] = {
     "bp_draft_accept": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
     "bp_draft_commit": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
                                  _c_vp]),
+    "bp_decode_embed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_vp]),
+    "bp_decode_qk_rope_cache": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int,
+                                         _c_int, _c_float, _c_vp]),
+    "bp_decode_attention": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_float, _c_vp]),
+    "bp_decode_norm_residual": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_float, _c_vp]),
+    "bp_decode_silu_mul": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp]),
+    "bp_decode_argmax_next": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_vp]),
     "bp_linear_set_scratch_bytes": (_c_size, [_c_vp, _c_int, _c_int]),
     "bp_linear_set_workgroups": (_c_int, [_c_int]),
     "bp_linear_set_validate": (_c_int, [_c_vp, _c_int, _c_int, _c_int]),

@@ -1,0 +1,251 @@
+"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 148
+launches for the 16-layer model) captured in one HIP graph, greedy generation with one replay, one pinned
+device-to-host read and one event synchronize per token.
+
+Drop-in for the loops of byteprof/optim/olmo.py: `make_generate_graph` (olmo.py:122-219, the manually captured
+graph of the eager forward incl. argmax and next-step inputs) and `make_generate` (olmo.py:51-119, the minimal
+loop: the same step run eagerly, one read per token). Both return `generate(inputs, max_new_tokens=...)` with the
+reference's contract: batch 1 and greedy only (OptimizeError otherwise), the prompt plus the new tokens within the
+static cache (MAX_CACHE_LEN), generation stops after an EOS id or max_new_tokens, and the result is the prompt
+followed by the new tokens, [1, L + n].
+
+The model is the OLMo-2 architecture with synthetic weights (the checkpoint is not available here): an
+`OlmoDecoder` holds the weights of transformers' Olmo2ForCausalLM layout with q|k|v and gate|up fused into one
+linear each (one launch instead of three or two; the outputs are the same rows), bf16 or int8 (per-row scales).
+The prompt is fed one position at a time through the same step (the reference prefills with one batched
+forward; the cache contents and the first new token are the same up to rounding).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable
+
+import torch
+
+from .. import _lib
+from ..quant.hip_int8 import quantize_rowwise_int8
+from . import skinny as S
+
+MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
+
+
+class OptimizeError(RuntimeError):
+    """A generate() call outside what the loop supports (the reference's byteprof.optim.OptimizeError)."""
+
+
+@dataclass(frozen=True)
+class OlmoConfig:
+    hidden: int
+    ffn: int
+    layers: int
+    heads: int
+    vocab: int
+    rope_theta: float = 500000.0
+    eps: float = 1e-6
+    max_len: int = MAX_CACHE_LEN
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+
+# allenai/OLMo-2-0425-1B: 16 layers, hidden 2048, FFN 8192, 16 heads of 128, vocabulary 100352
+OLMO2_1B = OlmoConfig(hidden=2048, ffn=8192, layers=16, heads=16, vocab=100352)
+
+LAYER_WEIGHTS = ("q", "k", "v", "o", "q_norm", "k_norm", "post_attn", "gate", "up", "down", "post_ff")
+
+
+def random_weights(cfg: OlmoConfig, device, seed: int = 0, std: float | None = None) -> dict[str, torch.Tensor]:
+    """Seeded synthetic bf16 weights on `device`, keyed like oracle/olmo.py (embed, l{i}.{q,k,v,o,q_norm,k_norm,
+    post_attn,gate,up,down,post_ff}, norm, lm_head): linears ~ N(0, std^2) with std = 2 / sqrt(hidden) by default,
+    norm weights ~ 1 + N(0, 0.1^2), embeddings ~ N(0, 1)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    std = 2.0 / cfg.hidden ** 0.5 if std is None else std
+    H, F, V = cfg.hidden, cfg.ffn, cfg.vocab
+
+    def lin(n, k):
+        return (torch.randn(n, k, generator=g, device=device) * std).to(torch.bfloat16)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
+
+    W = {"embed": torch.randn(V, H, generator=g, device=device).to(torch.bfloat16)}
+    for layer in range(cfg.layers):
+        p = f"l{layer}."
+        for name in ("q", "k", "v", "o"):
+            W[p + name] = lin(H, H)
+        for name in ("q_norm", "k_norm", "post_attn", "post_ff"):
+            W[p + name] = norm(H)
+        W[p + "gate"], W[p + "up"], W[p + "down"] = lin(F, H), lin(F, H), lin(H, F)
+    W["norm"] = norm(H)
+    W["lm_head"] = lin(V, H)
+    return W
+
+
+class OlmoDecoder:
+    """One OLMo-2 decode step on the GPU, reading the token id and the position from device memory (tok, pos) and
+    leaving the next token in tok and pos + 1 in pos. kind: 'bf16' or 'int8' (every linear quantized per row,
+    fp16 scales; embeddings and norm weights stay bf16)."""
+
+    def __init__(self, cfg: OlmoConfig, weights: dict[str, torch.Tensor], kind: str = "bf16"):
+        if kind not in ("bf16", "int8"):
+            raise ValueError("kind must be 'bf16' or 'int8'")
+        if cfg.hidden % cfg.heads or cfg.head_dim % 8 or 256 % cfg.head_dim or cfg.max_len > 4096:
+            raise ValueError("head_dim must be a multiple of 8 dividing 256 and max_len at most 4096")
+        self.cfg, self.kind = cfg, kind
+        dev = weights["embed"].device
+        if dev.type != "cuda":
+            raise ValueError("the decoder runs on the GPU only")
+        self.device = dev
+        H, F, V, D = cfg.hidden, cfg.ffn, cfg.vocab, cfg.head_dim
+
+        def lin(w: torch.Tensor) -> tuple:
+            w = w.contiguous()
+            return (w,) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
+
+        bf = torch.bfloat16
+        self.embed = weights["embed"].to(bf).contiguous()
+        self.norm = weights["norm"].to(bf).contiguous()
+        self.lm_head = lin(weights["lm_head"])
+        self.layers = []
+        for layer in range(cfg.layers):
+            p = f"l{layer}."
+            self.layers.append({
+                "qkv": lin(torch.cat([weights[p + "q"], weights[p + "k"], weights[p + "v"]])),
+                "o": lin(weights[p + "o"]),
+                "gate_up": lin(torch.cat([weights[p + "gate"], weights[p + "up"]])),
+                "down": lin(weights[p + "down"]),
+                **{n: weights[p + n].to(bf).contiguous() for n in ("q_norm", "k_norm", "post_attn", "post_ff")},
+            })
+        # Olmo2RotaryEmbedding.compute_default_rope_parameters, in float32 on the host
+        self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float) / D))).to(dev)
+        self.scale = float(D) ** -0.5
+        z = lambda *shape, dtype=bf: torch.zeros(*shape, dtype=dtype, device=dev)  # noqa: E731
+        self.tok, self.pos = z(1, dtype=torch.int64), z(1, dtype=torch.int64)
+        self.x, self.xn, self.attn, self.o, self.dn = z(1, H), z(1, H), z(1, H), z(1, H), z(1, H)
+        self.q = z(H)
+        self.qkv, self.gu, self.act, self.logits = z(1, 3 * H), z(1, 2 * F), z(1, F), z(1, V)
+        self.k_cache = z(cfg.layers, cfg.heads, cfg.max_len, D)
+        self.v_cache = z(cfg.layers, cfg.heads, cfg.max_len, D)
+
+    @staticmethod
+    def _mm(x: torch.Tensor, args: tuple, out: torch.Tensor) -> None:
+        S.skinny_mm(x, *args, out=out)
+
+    def step(self) -> None:
+        """Logits of token tok at position pos; then tok <- argmax, pos <- pos + 1 (all on the device)."""
+        cfg, L = self.cfg, _lib.lib()
+        H, D = cfg.hidden, cfg.head_dim
+        st = _lib.stream_ptr(self.device)
+        c = _lib.check
+        c(L.bp_decode_embed(self.tok.data_ptr(), self.embed.data_ptr(), self.x.data_ptr(), H, cfg.vocab, st),
+          "bp_decode_embed")
+        for i, w in enumerate(self.layers):
+            kc, vc = self.k_cache[i], self.v_cache[i]
+            self._mm(self.x, w["qkv"], self.qkv)
+            c(L.bp_decode_qk_rope_cache(self.qkv.data_ptr(), w["q_norm"].data_ptr(), w["k_norm"].data_ptr(),
+                                        self.inv_freq.data_ptr(), self.pos.data_ptr(), self.q.data_ptr(),
+                                        kc.data_ptr(), vc.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, st),
+              "bp_decode_qk_rope_cache")
+            c(L.bp_decode_attention(self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.pos.data_ptr(),
+                                    self.attn.data_ptr(), cfg.heads, D, cfg.max_len, self.scale, st),
+              "bp_decode_attention")
+            self._mm(self.attn, w["o"], self.o)
+            c(L.bp_decode_norm_residual(self.o.data_ptr(), w["post_attn"].data_ptr(), self.x.data_ptr(),
+                                        self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")
+            self._mm(self.x, w["gate_up"], self.gu)
+            c(L.bp_decode_silu_mul(self.gu.data_ptr(), self.act.data_ptr(), cfg.ffn, st), "bp_decode_silu_mul")
+            self._mm(self.act, w["down"], self.dn)
+            c(L.bp_decode_norm_residual(self.dn.data_ptr(), w["post_ff"].data_ptr(), self.x.data_ptr(),
+                                        self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")
+        c(L.bp_decode_norm_residual(self.x.data_ptr(), self.norm.data_ptr(), None, self.xn.data_ptr(), H, cfg.eps,
+                                    st), "bp_decode_norm_residual")
+        self._mm(self.xn, self.lm_head, self.logits)
+        c(L.bp_decode_argmax_next(self.logits.data_ptr(), cfg.vocab, self.tok.data_ptr(), self.pos.data_ptr(), st),
+          "bp_decode_argmax_next")
+
+    def weight_bytes(self) -> int:
+        """Bytes of the linears' weights (and scales) a step streams."""
+        lins = [self.lm_head] + [w[n] for w in self.layers for n in ("qkv", "o", "gate_up", "down")]
+        return sum(t.numel() * t.element_size() for args in lins for t in args)
+
+
+def _loop(dec: OlmoDecoder, replay: Callable[[], None] | None, prepare: Callable[[], None] | None):
+    pinned = torch.zeros(1, dtype=torch.long).pin_memory()
+    pinned_np = pinned.numpy()
+    done = torch.cuda.Event()
+
+    @torch.no_grad()
+    def generate(inputs: torch.Tensor, generation_config=None, **kwargs) -> torch.Tensor:
+        if inputs.dim() != 2 or inputs.shape[0] != 1 or kwargs.get("do_sample"):
+            raise OptimizeError("minimal loop supports batch size 1 and greedy decoding only")
+        max_new = int(kwargs["max_new_tokens"])
+        eos = kwargs.get("eos_token_id")
+        eos_ids = set([eos] if isinstance(eos, int) else (eos or []))
+        L = inputs.shape[1]
+        if L < 1 or max_new < 1:
+            raise OptimizeError("need a prompt and at least one new token")
+        if L + max_new > dec.cfg.max_len:
+            raise OptimizeError(f"{L}+{max_new} tokens exceed the static cache ({dec.cfg.max_len})")
+        ids = inputs[0].tolist()
+        if min(ids) < 0 or max(ids) >= dec.cfg.vocab:
+            raise OptimizeError("token id outside the vocabulary")
+        dev = dec.device
+        dec.pos.zero_()
+        for t in ids:  # prefill one position at a time; the last step leaves the first new token in tok
+            dec.tok.fill_(t)
+            dec.step()
+        pinned.copy_(dec.tok, non_blocking=True)
+        done.record()
+        done.synchronize()
+        new = [int(pinned_np[0])]
+        if prepare is not None and new[0] not in eos_ids and len(new) < max_new:
+            prepare()
+        while new[-1] not in eos_ids and len(new) < max_new:
+            if replay is not None:
+                replay()
+            else:
+                dec.step()
+            pinned.copy_(dec.tok, non_blocking=True)
+            done.record()
+            done.synchronize()  # the single sync of this token
+            new.append(int(pinned_np[0]))
+        return torch.cat([inputs[0].to(dev), torch.tensor(new, dtype=torch.long, device=dev)]).unsqueeze(0)
+
+    return generate
+
+
+def make_generate(dec: OlmoDecoder):
+    """The minimal loop (olmo.py:51-119): the decode step run eagerly, one device-to-host read per token."""
+    return _loop(dec, None, None)
+
+
+def make_generate_graph(dec: OlmoDecoder):
+    """The graph loop (olmo.py:122-219): the first decode captures the step (after three warm-up steps on a side
+    stream, which run at positions L .. L + 2 and leave cache rows that the real steps overwrite before they are
+    read); each token is then one replay, one pinned read and one synchronize."""
+    state: dict = {}
+
+    def prepare() -> None:
+        if "graph" in state:
+            return
+        tok, pos = dec.tok.clone(), dec.pos.clone()
+        s = torch.cuda.Stream(dec.device)
+        s.wait_stream(torch.cuda.current_stream(dec.device))
+        with torch.cuda.stream(s):
+            for _ in range(3):  # initialise every kernel and allocation before the capture
+                dec.step()
+        torch.cuda.current_stream(dec.device).wait_stream(s)
+        torch.cuda.synchronize(dec.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            dec.step()
+        state["graph"] = g
+        dec.tok.copy_(tok)
+        dec.pos.copy_(pos)
+
+    def replay() -> None:
+        state["graph"].replay()
+
+    return _loop(dec, replay, prepare)

@@ -189,6 +189,37 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
                     void* stream);
 
 /*
+ * The non-linear steps of one OLMo-2 decode step (batch 1), for a decode loop captured whole in one HIP graph: the
+ * token id and the position are int64 values in device memory, read by the kernels, and the last step writes the
+ * next token and advances the position, so that a replay needs no host value. bf16 tensors throughout; the
+ * roundings are those of transformers' Olmo2ForCausalLM in bf16 with the eager attention (modeling_olmo2.py:
+ * Olmo2RMSNorm, apply_rotary_pos_emb, eager_attention_forward, Olmo2MLP, Olmo2DecoderLayer).
+ * Replaces: byteprof/optim/olmo.py:122-219 (make_generate_graph: the captured eager forward of the HF model, its
+ * argmax and the in-graph update of the next step's inputs), with the linears done by bp_skinny_* launches.
+ *
+ * embed:          x[hidden] <- table[tok] (table [vocab, hidden]; tok clamped into range).
+ * qk_rope_cache:  qkv = [q | k | v] (3 * heads * head_dim); q, k RMSNorm'd over their whole length with their
+ *                 weights, rotated by RoPE at *pos (inv_freq[head_dim / 2] fp32, cos / sin in fp32); q -> q_out;
+ *                 k, v -> k_cache, v_cache [heads, max_len, head_dim] at row *pos (no write if *pos >= max_len).
+ * attention:      per head, positions 0 .. *pos: out = bf16(softmax_fp32(bf16(bf16(q . k) * scale)) as bf16 . v);
+ *                 head_dim a multiple of 8 dividing 256, max_len <= 4096.
+ * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
+ *                 out may alias residual.
+ * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn).
+ * argmax_next:    *tok = first index of the largest logit (NaN counts as largest); *pos += 1.
+ */
+int bp_decode_embed(const int64_t* tok, const void* table, void* x, int hidden, int64_t vocab, void* stream);
+int bp_decode_qk_rope_cache(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                            const int64_t* pos, void* q_out, void* k_cache, void* v_cache, int heads, int head_dim,
+                            int max_len, float eps, void* stream);
+int bp_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos, void* out,
+                        int heads, int head_dim, int max_len, float scale, void* stream);
+int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
+                            void* stream);
+int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream);
+int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* stream);
+
+/*
  * Decode-step linear set: a chain of skinny linears at one activation row run by one persistent launch.
  *
  * A stage is one or more linears sharing one input vector (q|k|v, gate|up, or a single linear). Its rows are the

@@ -10,6 +10,8 @@ Modules:
   skinny    fp64 matmul oracle, dequantize, the per-row int8 quantizer
   mlstm     the stabilised multi-step mLSTM recurrence in fp64 with the reference's io-dtype roundings, and the
             unstabilised closed form that pins it
+  olmo      the OLMo-2 decode step (one token, static KV cache) with the roundings of transformers'
+            Olmo2ForCausalLM in bf16, pinned against that model on the CPU
 
 How each function is pinned (checked against something other than itself) is stated in its docstring; the tests
 that do it are tests/test_oracle.py. Every function here is pinned; none is "parity unpinned", except where a

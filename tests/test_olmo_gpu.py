@@ -1,0 +1,235 @@
+"""The OLMo-2 decode loop on the GPU (byteprof_amd/optim/olmo.py, csrc/decode.hip) against the CPU oracle
+(oracle/olmo.py, itself pinned against transformers' Olmo2ForCausalLM in tests/test_oracle_olmo.py).
+
+  - each decode kernel on random inputs against the oracle's function: RMSNorm (+ residual), q/k norm + RoPE +
+    cache write (and nothing else written), the attention, SwiGLU, the argmax (ties, NaN) and position update;
+  - whole decode steps on a small model, teacher-forced: logits within the decode gate of the oracle, bf16 and int8;
+  - the graph loop against the eager loop: the same tokens, bit for bit, over repeated generate calls (graph
+    replays with eager work between them), at the small shape and at the OLMo-2-1B shape;
+  - the generate() contract of the reference (batch 1 only, the static cache bound, EOS stops the loop).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from byteprof_amd import _lib
+from byteprof_amd.optim import olmo as OG
+from oracle import numerics as ON
+from oracle import olmo as OO
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SMALL = OG.OlmoConfig(hidden=256, ffn=512, layers=2, heads=4, vocab=512, max_len=64)
+GATE = 2e-2  # max |d| / max |logits|, the gate of tests/test_oracle_olmo.py
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+def _bf16(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(ON.bf16_round(a))).to(DEV).to(torch.bfloat16)
+
+
+def _ulps(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Distance in bf16 steps between two arrays of bf16 values."""
+    ia = ON.bf16_bits(a).astype(np.int32)
+    ib = ON.bf16_bits(b).astype(np.int32)
+    ia = np.where(ia & 0x8000, 0x8000 - ia, ia)
+    ib = np.where(ib & 0x8000, 0x8000 - ib, ib)
+    return np.abs(ia - ib)
+
+
+def _ocfg(cfg: OG.OlmoConfig) -> OO.Config:
+    return OO.Config(hidden=cfg.hidden, ffn=cfg.ffn, layers=cfg.layers, heads=cfg.heads, vocab=cfg.vocab,
+                     rope_theta=cfg.rope_theta, eps=cfg.eps, max_len=cfg.max_len)
+
+
+def test_norm_residual_matches_the_oracle():
+    rng = np.random.default_rng(0)
+    L = _lib.lib()
+    for n in (256, 2048, 3000):
+        print(f"\n[olmo] norm n={n}", flush=True)
+        x, w, r = (ON.bf16_round(rng.standard_normal(n).astype(np.float32) * s) for s in (3.0, 1.0, 2.0))
+        tx, tw, tr = _bf16(x), _bf16(w), _bf16(r)
+        out = torch.empty_like(tx)
+        st = _lib.stream_ptr(tx.device)
+        _lib.check(L.bp_decode_norm_residual(tx.data_ptr(), tw.data_ptr(), None, out.data_ptr(), n, 1e-6, st), "n")
+        assert _ulps(_np(out), OO.rmsnorm(x, w, 1e-6)).max() <= 1
+        _lib.check(L.bp_decode_norm_residual(tx.data_ptr(), tw.data_ptr(), tr.data_ptr(), tr.data_ptr(), n, 1e-6,
+                                             st), "n")  # in place on the residual
+        assert _ulps(_np(tr), ON.bf16_round(r + OO.rmsnorm(x, w, 1e-6))).max() <= 1
+
+
+@pytest.mark.parametrize("pos", [0, 5, 63])
+def test_qk_rope_cache_matches_the_oracle_and_writes_one_cache_row(pos):
+    cfg = SMALL
+    oc = _ocfg(cfg)
+    H, D = cfg.hidden, cfg.head_dim
+    rng = np.random.default_rng(pos)
+    qkv = ON.bf16_round(rng.standard_normal(3 * H).astype(np.float32))
+    qw, kw = (ON.bf16_round(1 + 0.1 * rng.standard_normal(H).astype(np.float32)) for _ in range(2))
+    dec_inv = (1.0 / (cfg.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float) / D))).to(DEV)
+    np.testing.assert_array_equal(dec_inv.cpu().numpy(), OO.inv_freq(oc))
+    kc = torch.full((cfg.heads, cfg.max_len, D), 7.0, dtype=torch.bfloat16, device=DEV)
+    vc = torch.full_like(kc, 7.0)
+    q_out = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    t_qkv, t_qw, t_kw = _bf16(qkv), _bf16(qw), _bf16(kw)
+    _lib.check(_lib.lib().bp_decode_qk_rope_cache(
+        t_qkv.data_ptr(), t_qw.data_ptr(), t_kw.data_ptr(), dec_inv.data_ptr(), p.data_ptr(), q_out.data_ptr(),
+        kc.data_ptr(), vc.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, _lib.stream_ptr(kc.device)), "rope")
+    want_q = OO.rope(OO.rmsnorm(qkv[:H], qw, cfg.eps).reshape(cfg.heads, D), pos, oc).reshape(-1)
+    want_k = OO.rope(OO.rmsnorm(qkv[H:2 * H], kw, cfg.eps).reshape(cfg.heads, D), pos, oc)
+    assert _ulps(_np(q_out), want_q).max() <= 1
+    kcn, vcn = _np(kc), _np(vc)
+    assert _ulps(kcn[:, pos], want_k).max() <= 1
+    np.testing.assert_array_equal(vcn[:, pos], qkv[2 * H:].reshape(cfg.heads, D))
+    others = np.ones(cfg.max_len, bool)
+    others[pos] = False
+    assert (kcn[:, others] == 7.0).all() and (vcn[:, others] == 7.0).all()
+
+
+@pytest.mark.parametrize("pos", [0, 1, 37, 63])
+def test_attention_matches_the_oracle(pos):
+    cfg = SMALL
+    oc = _ocfg(cfg)
+    D = cfg.head_dim
+    rng = np.random.default_rng(100 + pos)
+    kc = ON.bf16_round(rng.standard_normal((cfg.heads, cfg.max_len, D)).astype(np.float32))
+    vc = ON.bf16_round(rng.standard_normal((cfg.heads, cfg.max_len, D)).astype(np.float32))
+    q = ON.bf16_round(rng.standard_normal((cfg.heads, D)).astype(np.float32) * 2.0)
+    out = torch.empty(cfg.hidden, dtype=torch.bfloat16, device=DEV)
+    p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    tq, tk, tv = _bf16(q), _bf16(kc), _bf16(vc)
+    _lib.check(_lib.lib().bp_decode_attention(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), p.data_ptr(),
+                                              out.data_ptr(), cfg.heads, D, cfg.max_len, D ** -0.5,
+                                              _lib.stream_ptr(out.device)), "attention")
+    want = OO.attention(q, kc, vc, pos, oc)
+    got = _np(out)
+    assert ON.normwise_error(got, want) < 1e-2
+    if pos == 0:
+        np.testing.assert_array_equal(got, vc[:, 0].reshape(-1))  # one position: the softmax is exactly 1
+
+
+def test_silu_mul_matches_the_oracle():
+    rng = np.random.default_rng(3)
+    F = 5000
+    gu = ON.bf16_round(rng.standard_normal(2 * F).astype(np.float32) * 4.0)
+    out = torch.empty(F, dtype=torch.bfloat16, device=DEV)
+    t = _bf16(gu)
+    _lib.check(_lib.lib().bp_decode_silu_mul(t.data_ptr(), out.data_ptr(), F, _lib.stream_ptr(out.device)), "silu")
+    assert _ulps(_np(out), OO.silu_mul(gu[:F], gu[F:])).max() <= 1
+
+
+def test_argmax_next_takes_the_first_maximum_and_advances_the_position():
+    L = _lib.lib()
+    st = _lib.stream_ptr(torch.device(DEV))
+    for V, setup, want in ((100352, {5: 3.0, 70000: 3.0}, 5), (1000, {999: 1.0}, 999), (7, {}, 0),
+                           (4096, {10: 2.0, 3000: float("nan")}, 3000)):
+        lg = torch.zeros(V, dtype=torch.bfloat16, device=DEV) - 1.0
+        for i, v in setup.items():
+            lg[i] = v
+        tok = torch.tensor([-1], dtype=torch.int64, device=DEV)
+        pos = torch.tensor([41], dtype=torch.int64, device=DEV)
+        _lib.check(L.bp_decode_argmax_next(lg.data_ptr(), V, tok.data_ptr(), pos.data_ptr(), st), "argmax")
+        assert int(tok) == want and int(pos) == 42
+
+
+def _deq(args: tuple) -> np.ndarray:
+    """q * scale, exact in float32 (8-bit q times an fp16 scale)."""
+    q, scale = args
+    return q.float().cpu().numpy() * scale.float().cpu().numpy()[:, None]
+
+
+def _small_decoder(kind: str, seed: int = 1):
+    cfg = SMALL
+    oc = _ocfg(cfg)
+    W = OO.random_weights(oc, seed=seed, std=2.0 / np.sqrt(cfg.hidden))
+    dec = OG.OlmoDecoder(cfg, {k: _bf16(v) for k, v in W.items()}, kind)
+    if kind == "int8":  # the oracle runs on the weights the kernels see: q * scale
+        for i, lw in enumerate(dec.layers):
+            p = f"l{i}."
+            qkv = _deq(lw["qkv"])
+            H = cfg.hidden
+            W[p + "q"], W[p + "k"], W[p + "v"] = qkv[:H], qkv[H:2 * H], qkv[2 * H:]
+            gu = _deq(lw["gate_up"])
+            W[p + "gate"], W[p + "up"] = gu[:cfg.ffn], gu[cfg.ffn:]
+            W[p + "o"] = _deq(lw["o"])
+            W[p + "down"] = _deq(lw["down"])
+        W["lm_head"] = _deq(dec.lm_head)
+    return dec, W, oc
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_decode_steps_match_the_oracle(kind):
+    dec, W, oc = _small_decoder(kind)
+    prompt = [3, 17, 99, 250, 7]
+    toks, logits = OO.greedy(W, oc, prompt, 10)
+    feed = prompt + toks[:-1]
+    dec.pos.zero_()
+    errs = []
+    for i, t in enumerate(feed):
+        dec.tok.fill_(t)
+        dec.step()
+        if i >= len(prompt) - 1:
+            want = logits[i - len(prompt) + 1]
+            got = _np(dec.logits[0])
+            errs.append(ON.normwise_error(got, want))
+            top2 = np.sort(want)[-2:]
+            if top2[1] - top2[0] > 2 * errs[-1] * np.abs(want).max():
+                assert int(dec.tok) == int(np.argmax(want)), i
+    assert int(dec.pos) == len(feed)
+    assert max(errs) < GATE, errs
+
+
+def test_graph_loop_equals_the_eager_loop_small():
+    dec, W, oc = _small_decoder("bf16", seed=2)
+    eager = OG.make_generate(dec)
+    graph = OG.make_generate_graph(dec)
+    for prompt in ([1, 2, 3], [400, 9, 9, 9, 17, 250], [5]):
+        inp = torch.tensor([prompt])
+        a = eager(inp, max_new_tokens=20)
+        for _ in range(2):  # the captured graph is reused; eager work runs between the replays
+            b = graph(inp, max_new_tokens=20)
+            assert torch.equal(a.cpu(), b.cpu()), (prompt, a, b)
+        assert a.shape == (1, len(prompt) + 20)
+        toks, _ = OO.greedy(W, oc, prompt, 20)
+        assert a[0, len(prompt)].item() == toks[0]
+
+
+def test_generate_contract():
+    dec, _, _ = _small_decoder("bf16", seed=3)
+    gen = OG.make_generate_graph(dec)
+    with pytest.raises(OG.OptimizeError):
+        gen(torch.tensor([[1, 2], [3, 4]]), max_new_tokens=4)
+    with pytest.raises(OG.OptimizeError):
+        gen(torch.tensor([[1, 2]]), max_new_tokens=SMALL.max_len)
+    with pytest.raises(OG.OptimizeError):
+        gen(torch.tensor([[1, 2]]), max_new_tokens=4, do_sample=True)
+    with pytest.raises(OG.OptimizeError):
+        gen(torch.tensor([[1, SMALL.vocab]]), max_new_tokens=4)
+    full = gen(torch.tensor([[7, 8, 9]]), max_new_tokens=12)
+    eos = int(full[0, 3 + 4])  # the fifth new token as the end-of-sequence id
+    first = [int(t) for t in full[0, 3:]].index(eos)
+    out = gen(torch.tensor([[7, 8, 9]]), max_new_tokens=12, eos_token_id=eos)
+    assert torch.equal(out.cpu(), full[:, :3 + first + 1].cpu())
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_graph_loop_equals_the_eager_loop_olmo2_1b(kind):
+    cfg = OG.OLMO2_1B
+    print(f"\n[olmo] 1B {kind}", flush=True)
+    dec = OG.OlmoDecoder(cfg, OG.random_weights(cfg, DEV, seed=4), kind)
+    prompt = torch.tensor([[11, 2027, 5, 99999, 42, 3, 3, 1000]])
+    a = OG.make_generate(dec)(prompt, max_new_tokens=24)
+    graph = OG.make_generate_graph(dec)
+    for _ in range(2):
+        b = graph(prompt, max_new_tokens=24)
+        assert torch.equal(a.cpu(), b.cpu())
+    assert len(set(a[0, 8:].tolist())) > 1
+    del dec
+    torch.cuda.empty_cache()
