@@ -171,21 +171,6 @@ struct Cursor {
   }
 };
 
-// int8 rows against activations held as fp16 pairs (x * 2^e, see Consumer::run): each weight byte q becomes the fp16
-// value 1024 + (q ^ 0x80) = 1152 + q with one v_perm_b32 per pair (0x64 is the fp16 exponent byte of 1024 and the
-// byte fills the low 8 of its 10 mantissa bits, so the value is exact), so the chunk costs 5 instructions per 4
-// weights where the exact bf16 conversion costs 8; the caller removes 1152 * sum(x) once per row. Products are
-// exact in fp32 (11 x 11 significant bits); only the fp32 accumulation rounds.
-__device__ __forceinline__ float chunk_dot_i8_f16(const u32x4& wv, const uint32_t (&xh)[8], float acc) {
-  const uint32_t wd[4] = {wv.x ^ 0x80808080u, wv.y ^ 0x80808080u, wv.z ^ 0x80808080u, wv.w ^ 0x80808080u};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    acc = dot2_f16(__builtin_amdgcn_perm(wd[j], 0x64646464u, 0x00050004u), xh[2 * j], acc);
-    acc = dot2_f16(__builtin_amdgcn_perm(wd[j], 0x64646464u, 0x00070006u), xh[2 * j + 1], acc);
-  }
-  return acc;
-}
-
 // Producer wave `who`: copies its consumer's chunks into the consumer's LDS ring. Chunks travel through a ring of
 // kSetInflight registers: the producer waits for its oldest load, writes that chunk into the LDS ring, publishes
 // it at once (one LDS word), and loads the next chunk into the freed registers. Exactly kSetInflight loads are
@@ -262,7 +247,6 @@ struct Consumer {
   float acc;
   bool failed;
   uint32_t tag;
-  float xsum, xinv;        // int8 rows of two chunks: sum of the lane's fp16 input values, 2^-e of their scaling
   BP_GLOBAL uint16_t* y;   // the stage's outputs
   uint32_t* ty;            // the stage's tagged outputs
 
@@ -389,19 +373,10 @@ struct Consumer {
       }
     }
     float a[R];
-    if constexpr (KIND == kInt8) {  // xr holds fp16 pairs of x * 2^e (run)
 #pragma unroll
-      for (int q = 0; q < R; ++q) a[q] = chunk_dot_i8_f16(w[2 * q], xr[0], 0.f);
+    for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q], xr[0], 0.f);
 #pragma unroll
-      for (int q = 0; q < R; ++q) a[q] = chunk_dot_i8_f16(w[2 * q + 1], xr[1], a[q]);
-#pragma unroll
-      for (int q = 0; q < R; ++q) a[q] = (a[q] - 1152.f * xsum) * xinv;
-    } else {
-#pragma unroll
-      for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q], xr[0], 0.f);
-#pragma unroll
-      for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q + 1], xr[1], a[q]);
-    }
+    for (int q = 0; q < R; ++q) a[q] = chunk_dot<KIND>(w[2 * q + 1], xr[1], a[q]);
     n += G;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (lane == 0) lds_store_relaxed(&L.consumed[who], n);
@@ -446,31 +421,6 @@ struct Consumer {
         if (C == 4) {
           while (s == stage) group<4, true>(st, L, S, who, lane, tagged, xr);
         } else {
-          if constexpr (KIND == kInt8) {
-            // the lane's 32 input values as fp16 pairs of x * 2^e, e chosen so that the largest lies in
-            // [2^14, 2^15): exact for every value down to 2^-28 of the largest (fp16 normals), then rounded
-            float m = 0.f;
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-              for (int d = 0; d < 8; ++d)
-                m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_float(xr[j][d] & 0xffffu)),
-                                   fabsf(bf16_bits_to_float(xr[j][d] >> 16))));
-            const int e = min(141 - ((__float_as_int(m) >> 23) & 0xff), 126);  // 2^e and 2^-e are fp32 normals
-            const float sc = __int_as_float((e + 127) << 23);
-            xinv = __int_as_float((127 - e) << 23);
-            xsum = 0.f;
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-              for (int d = 0; d < 8; ++d) {
-                const _Float16 lo = static_cast<_Float16>(bf16_bits_to_float(xr[j][d] & 0xffffu) * sc);
-                const _Float16 hi = static_cast<_Float16>(bf16_bits_to_float(xr[j][d] >> 16) * sc);
-                xsum += static_cast<float>(lo) + static_cast<float>(hi);
-                xr[j][d] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
-                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
-              }
-          }
           while (s == stage) {
             if (r1 - r >= 4)
               rows<4>(st, L, S, who, lane, tagged, xr);

@@ -116,6 +116,31 @@ def test_small_chain_matches_the_oracle_stage_by_stage(kind, scale_dtype):
     _check_stages(stages, ostages)
 
 
+def test_int8_rows_of_two_chunks_at_extreme_input_scales():
+    """int8 rows of K = 2048 go through the fp16 form of the weights against x * 2^e (e per lane from its largest
+    |x|): inputs from 1e-30 to 3e4, a single large outlier among tiny values, and an all-zero input, each checked
+    against the oracle (the zero input must give exact zeros)."""
+    g = _gen(11)
+    k = 2048
+    base = torch.randn(k, generator=g, device=DEV)
+    outlier = torch.full((k,), 1e-3, device=DEV)
+    outlier[5] = 3.0e4
+    inputs = [base * 1e4, base * 1e-4, base * 1e-30, outlier, torch.zeros(k, device=DEV)]
+    stages, ostages = [], []
+    for x in inputs:
+        w, sc, ow = _weights("int8", 777, k, g, torch.float16)
+        xb = x.to(torch.bfloat16)
+        out = torch.empty(777, dtype=torch.bfloat16, device=DEV)
+        stages.append(Stage([w], xb, out, scales=[sc], x_used=torch.empty(k, dtype=torch.bfloat16, device=DEV)))
+        ostages.append(OL.OracleStage([ow], ("ext", _np(xb)), False, "int8"))
+    ls = LinearSet(stages)
+    ls.run()
+    torch.cuda.synchronize()
+    assert not ls.timed_out()
+    _check_stages(stages, ostages)
+    assert torch.count_nonzero(stages[-1].out) == 0
+
+
 def test_repeated_launches_are_deterministic_and_need_no_reset():
     stages, ostages = _small_chain("bf16", seed=4)
     ls = LinearSet(stages)
