@@ -674,6 +674,9 @@ __global__ __launch_bounds__(kSetThreads) void linear_set_kernel(const BpSetStag
   if (wave == kSetSyncWave) {
     sync_wave<KIND>(st, S, scratch, lds, scale_dt, lane);
   } else if (wave >= kSetCW) {
+    // Issue priority over the consumer sharing its SIMD: the producer issues a few instructions per chunk and must
+    // keep the weight loads flowing; at equal priority a VALU-heavy consumer (int8 conversion) delays them.
+    __builtin_amdgcn_s_setprio(3);
     producer_wave<KIND>(st, lds, S, wave - kSetCW, lane, scratch);
   } else {
     Consumer<KIND> cons;
