@@ -5,6 +5,7 @@
 //   embed           x <- table[tok]
 //   qk_rope_cache   q, k <- RMSNorm over the whole projection (fp32, weight applied in fp32, rounded to bf16),
 //                   rotated by RoPE at pos (cos / sin in fp32, one rounding), k and v written to the cache at pos
+//   rope_attention  qk_rope_cache and attention fused, one workgroup per head (the decode loop's path)
 //   attention       per head: s_t = bf16(bf16(q . k_t) * scale) for t <= pos, p = bf16(softmax_fp32(s)),
 //                   out = bf16(sum_t p_t v_t)
 //   norm_residual   out <- bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))) (no residual: the plain norm)
@@ -166,6 +167,99 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const uint16_t*
   }
 }
 
+// qk_rope_cache and attention in one launch: every workgroup h computes the q / k norms over the whole projections
+// (the same sums in every workgroup; their summation order differs from qk_rope_cache_kernel's, so a value may land
+// one bf16 step apart), rotates its own head, writes its k and v at pos, and attends over positions 0 .. pos.
+__global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint16_t* __restrict__ qkv,
+                                                                      const uint16_t* __restrict__ qw,
+                                                                      const uint16_t* __restrict__ kw,
+                                                                      const float* __restrict__ inv_freq,
+                                                                      const int64_t* __restrict__ pos_p,
+                                                                      uint16_t* __restrict__ kc,
+                                                                      uint16_t* __restrict__ vc,
+                                                                      uint16_t* __restrict__ out, int heads, int D,
+                                                                      int max_len, float eps, float scale) {
+  __shared__ float sc[kAttnMaxLen];
+  __shared__ float qs[512];
+  __shared__ float red[kAttnThreads / kWave];
+  __shared__ float part[kAttnThreads];
+  const int h = blockIdx.x;
+  const int H = heads * D, half = D / 2;
+  const int64_t pos_in = *pos_p;
+  const bool in_cache = pos_in >= 0 && pos_in < max_len;
+  const uint16_t* q = qkv;
+  const uint16_t* k = qkv + H;
+  const uint16_t* v = qkv + 2 * H;
+  float sq = 0.f, sk = 0.f;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) {
+    const float a = ld_bf16(q, i), b = ld_bf16(k, i);
+    sq += a * a;
+    sk += b * b;
+  }
+  const float rq = 1.f / sqrtf(block_sum(sq, red) / static_cast<float>(H) + eps);
+  const float rk = 1.f / sqrtf(block_sum(sk, red) / static_cast<float>(H) + eps);
+  uint16_t* K = kc + static_cast<int64_t>(h) * max_len * D;
+  uint16_t* V = vc + static_cast<int64_t>(h) * max_len * D;
+  for (int j = threadIdx.x; j < half; j += blockDim.x) {
+    const int a = h * D + j, b = a + half;
+    const float f = inv_freq[j] * static_cast<float>(pos_in);
+    const float c = cosf(f), s = sinf(f);
+    const float qa = round_to_bf16(ld_bf16(qw, a) * (ld_bf16(q, a) * rq));
+    const float qb = round_to_bf16(ld_bf16(qw, b) * (ld_bf16(q, b) * rq));
+    const float ka = round_to_bf16(ld_bf16(kw, a) * (ld_bf16(k, a) * rk));
+    const float kb = round_to_bf16(ld_bf16(kw, b) * (ld_bf16(k, b) * rk));
+    qs[j] = round_to_bf16(qa * c + (-qb) * s);
+    qs[j + half] = round_to_bf16(qb * c + qa * s);
+    if (in_cache) {
+      const int64_t row = pos_in * D;
+      K[row + j] = float_to_bf16_bits(ka * c + (-kb) * s);
+      K[row + j + half] = float_to_bf16_bits(kb * c + ka * s);
+      V[row + j] = v[a];
+      V[row + j + half] = v[b];
+    }
+  }
+  __syncthreads();  // qs and this position's cache row, written above, are read below
+  const int64_t pos = pos_in < 0 ? 0 : (pos_in >= max_len ? max_len - 1 : pos_in);
+  const int T = static_cast<int>(pos) + 1;
+  float m = -INFINITY;
+  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    const uint16_t* kr = K + static_cast<int64_t>(t) * D;
+    float dot = 0.f;
+    for (int d = 0; d < D; d += 8) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(kr + d);
+      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dot += bf16_bits_to_float(wd[e] & 0xffffu) * qs[d + 2 * e];
+        dot += bf16_bits_to_float(wd[e] >> 16) * qs[d + 2 * e + 1];
+      }
+    }
+    const float s = round_to_bf16(round_to_bf16(dot) * scale);
+    sc[t] = s;
+    m = fmaxf(m, s);
+  }
+  m = block_max(m, red);
+  float l = 0.f;
+  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    const float e = expf(sc[t] - m);
+    sc[t] = e;
+    l += e;
+  }
+  l = block_sum(l, red);
+  const float inv = 1.f / l;
+  const int R = blockDim.x / D;
+  const int d = threadIdx.x % D, r = threadIdx.x / D;
+  float acc = 0.f;
+  for (int t = r; t < T; t += R) acc += round_to_bf16(sc[t] * inv) * ld_bf16(V, static_cast<int64_t>(t) * D + d);
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float t = 0.f;
+    for (int i = 0; i < R; ++i) t += part[i * D + threadIdx.x];
+    out[static_cast<int64_t>(h) * D + threadIdx.x] = float_to_bf16_bits(t);
+  }
+}
+
 __global__ __launch_bounds__(kBlock) void norm_residual_kernel(const uint16_t* __restrict__ x,
                                                                const uint16_t* __restrict__ w,
                                                                const uint16_t* residual, uint16_t* out, int n,
@@ -270,6 +364,22 @@ int bp_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   bp::attention_kernel<<<heads, bp::kAttnThreads, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_cache), static_cast<const uint16_t*>(v_cache),
       pos, static_cast<uint16_t*>(out), head_dim, max_len, scale);
+  return bp::status();
+}
+
+int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                             const int64_t* pos, void* k_cache, void* v_cache, void* out, int heads, int head_dim,
+                             int max_len, float eps, float scale, void* stream) {
+  if (qkv == nullptr || q_norm_w == nullptr || k_norm_w == nullptr || inv_freq == nullptr || pos == nullptr ||
+      k_cache == nullptr || v_cache == nullptr || out == nullptr || heads <= 0 || max_len <= 0)
+    return BP_E_INVALID_ARG;
+  if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256 || bp::kAttnThreads % head_dim != 0 ||
+      max_len > bp::kAttnMaxLen)
+    return BP_E_UNSUPPORTED;
+  bp::rope_attention_kernel<<<heads, bp::kAttnThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(q_norm_w),
+      static_cast<const uint16_t*>(k_norm_w), inv_freq, pos, static_cast<uint16_t*>(k_cache),
+      static_cast<uint16_t*>(v_cache), static_cast<uint16_t*>(out), heads, head_dim, max_len, eps, scale);
   return bp::status();
 }
 

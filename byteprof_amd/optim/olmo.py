@@ -1,4 +1,4 @@
-"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 148
+"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 132
 launches for the 16-layer model) captured in one HIP graph, greedy generation with one replay, one pinned
 device-to-host read and one event synchronize per token.
 
@@ -124,7 +124,6 @@ class OlmoDecoder:
         z = lambda *shape, dtype=bf: torch.zeros(*shape, dtype=dtype, device=dev)  # noqa: E731
         self.tok, self.pos = z(1, dtype=torch.int64), z(1, dtype=torch.int64)
         self.x, self.xn, self.attn, self.o, self.dn = z(1, H), z(1, H), z(1, H), z(1, H), z(1, H)
-        self.q = z(H)
         self.qkv, self.gu, self.act, self.logits = z(1, 3 * H), z(1, 2 * F), z(1, F), z(1, V)
         self.k_cache = z(cfg.layers, cfg.heads, cfg.max_len, D)
         self.v_cache = z(cfg.layers, cfg.heads, cfg.max_len, D)
@@ -144,13 +143,10 @@ class OlmoDecoder:
         for i, w in enumerate(self.layers):
             kc, vc = self.k_cache[i], self.v_cache[i]
             self._mm(self.x, w["qkv"], self.qkv)
-            c(L.bp_decode_qk_rope_cache(self.qkv.data_ptr(), w["q_norm"].data_ptr(), w["k_norm"].data_ptr(),
-                                        self.inv_freq.data_ptr(), self.pos.data_ptr(), self.q.data_ptr(),
-                                        kc.data_ptr(), vc.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, st),
-              "bp_decode_qk_rope_cache")
-            c(L.bp_decode_attention(self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.pos.data_ptr(),
-                                    self.attn.data_ptr(), cfg.heads, D, cfg.max_len, self.scale, st),
-              "bp_decode_attention")
+            c(L.bp_decode_rope_attention(self.qkv.data_ptr(), w["q_norm"].data_ptr(), w["k_norm"].data_ptr(),
+                                         self.inv_freq.data_ptr(), self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                         self.attn.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, self.scale, st),
+              "bp_decode_rope_attention")
             self._mm(self.attn, w["o"], self.o)
             c(L.bp_decode_norm_residual(self.o.data_ptr(), w["post_attn"].data_ptr(), self.x.data_ptr(),
                                         self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")

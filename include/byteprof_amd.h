@@ -203,6 +203,8 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  *                 k, v -> k_cache, v_cache [heads, max_len, head_dim] at row *pos (no write if *pos >= max_len).
  * attention:      per head, positions 0 .. *pos: out = bf16(softmax_fp32(bf16(bf16(q . k) * scale)) as bf16 . v);
  *                 head_dim a multiple of 8 dividing 256, max_len <= 4096.
+ * rope_attention: qk_rope_cache and attention in one launch (one workgroup per head; the q / k norms summed in
+ *                 another order, so a value may differ by one bf16 step from the two-launch path).
  * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
  *                 out may alias residual.
  * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn).
@@ -214,6 +216,9 @@ int bp_decode_qk_rope_cache(const void* qkv, const void* q_norm_w, const void* k
                             int max_len, float eps, void* stream);
 int bp_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos, void* out,
                         int heads, int head_dim, int max_len, float scale, void* stream);
+int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                             const int64_t* pos, void* k_cache, void* v_cache, void* out, int heads, int head_dim,
+                             int max_len, float eps, float scale, void* stream);
 int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
                             void* stream);
 int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream);

@@ -115,6 +115,38 @@ def test_attention_matches_the_oracle(pos):
         np.testing.assert_array_equal(got, vc[:, 0].reshape(-1))  # one position: the softmax is exactly 1
 
 
+@pytest.mark.parametrize("pos", [0, 9, 63])
+def test_fused_rope_attention_matches_the_oracle(pos):
+    """The decode loop's launch: q / k norm + RoPE + cache write + attention for every head at once."""
+    cfg = SMALL
+    oc = _ocfg(cfg)
+    H, D = cfg.hidden, cfg.head_dim
+    rng = np.random.default_rng(200 + pos)
+    qkv = ON.bf16_round(rng.standard_normal(3 * H).astype(np.float32))
+    qw, kw = (ON.bf16_round(1 + 0.1 * rng.standard_normal(H).astype(np.float32)) for _ in range(2))
+    kc = ON.bf16_round(rng.standard_normal((cfg.heads, cfg.max_len, D)).astype(np.float32))
+    vc = ON.bf16_round(rng.standard_normal((cfg.heads, cfg.max_len, D)).astype(np.float32))
+    tkc, tvc = _bf16(kc), _bf16(vc)
+    out = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    inv = torch.from_numpy(OO.inv_freq(oc)).to(DEV)
+    p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    t_qkv, t_qw, t_kw = _bf16(qkv), _bf16(qw), _bf16(kw)
+    _lib.check(_lib.lib().bp_decode_rope_attention(
+        t_qkv.data_ptr(), t_qw.data_ptr(), t_kw.data_ptr(), inv.data_ptr(), p.data_ptr(), tkc.data_ptr(),
+        tvc.data_ptr(), out.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, D ** -0.5,
+        _lib.stream_ptr(out.device)), "rope_attention")
+    q = OO.rope(OO.rmsnorm(qkv[:H], qw, cfg.eps).reshape(cfg.heads, D), pos, oc)
+    k = OO.rope(OO.rmsnorm(qkv[H:2 * H], kw, cfg.eps).reshape(cfg.heads, D), pos, oc)
+    kc[:, pos], vc[:, pos] = k, qkv[2 * H:].reshape(cfg.heads, D)
+    kcn, vcn = _np(tkc), _np(tvc)
+    assert _ulps(kcn[:, pos], k).max() <= 1
+    np.testing.assert_array_equal(vcn[:, pos], vc[:, pos])
+    others = np.ones(cfg.max_len, bool)
+    others[pos] = False
+    np.testing.assert_array_equal(kcn[:, others], kc[:, others])
+    assert ON.normwise_error(_np(out), OO.attention(q, kc, vc, pos, oc)) < 1e-2
+
+
 def test_silu_mul_matches_the_oracle():
     rng = np.random.default_rng(3)
     F = 5000
