@@ -4,19 +4,22 @@
 One step = one pass over the OLMo-2-1B-shaped decode-step linear set at M = 1 in bf16 (byteprof_amd/decode_set.py):
 16 layers x (q, k, v, o 2048 -> 2048; gate, up 2048 -> 8192; down 8192 -> 2048) + the LM head 2048 -> 100352,
 113 linears, every weight distinct (2.56 GB, ten times the 256 MB Infinity Cache), all operands resident in HBM
-before the timed region. The step runs as one launch of the persistent set kernel (csrc/linear_set.hip) with the
-reference's set semantics: every linear reads its own seeded unit-RMS input (q|k|v and gate|up share theirs), as
-in byteprof's set benchmark, where each linear is an independent skinny call (tools/skinny_bench.py:45-71).
+before the timed region. The reference's set semantics: every linear reads its own seeded unit-RMS input, as in
+byteprof's set benchmark, where each linear is an independent skinny call (tools/skinny_bench.py:45-71). The step
+runs as one grouped launch (csrc/skinny_group.hip): one grid over the row blocks of all 113 linears, every output
+bitwise equal to its own skinny_mm call.
 
 Printed (one JSON line): the step's aggregate HBM throughput (algorithmic bytes = weights + activations + outputs,
-each once: 2,560,237,568 B per step) in GB/s, us per set and % of the 8 TB/s peak; the roofline of the set kernel
-(the only kernel of the step): algorithmic bytes per launch over the average launch duration, from HIP events on
-the launch stream over the timed steps, and the HBM traffic per launch from the committed rocprofv3 counter
-summary (profiles/linear_set_kernel_decode_set.md); the CPU baseline (torch F.linear, the reference's CPU path for
-these linears, on the host cores); and secondary figures: the same set as a dependent decode chain in one launch
-(each stage reads the renormalised output it depends on), the 113-launch HIP graph of skinny kernels, the int8
-set (fp16 scales) both ways, the fused mLSTM block, the bf16 verify-width sweep (M = 1..16, VALU / matrix-core
-kernels), and the graph-captured greedy decode loop of the OLMo-2-1B-shaped model (us per token, bf16 and int8).
+each once: 2,560,237,568 B per step) in GB/s, us per set and % of the 8 TB/s peak; the roofline of the grouped
+kernel (the only kernel of the step): algorithmic bytes per launch over the average launch duration, from HIP
+events on the launch stream over the timed steps, and the HBM traffic per launch from the committed rocprofv3
+counter summary (profiles/skinny_group_kernel_decode_set.md); the CPU baseline (torch F.linear, the reference's
+CPU path for these linears, on the host cores); and secondary figures: the same set in one launch of the
+persistent set kernel (csrc/linear_set.hip), independent and as a dependent decode chain (each stage reads the
+renormalised output it depends on), the 113-launch HIP graph of skinny kernels (the reference's execution model),
+the int8 set (fp16 scales) the same ways, the fused mLSTM block, the bf16 verify-width sweep (M = 1..16, VALU /
+matrix-core kernels), and the graph-captured greedy decode loop of the OLMo-2-1B-shaped model (us per token, bf16
+and int8).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
 """
@@ -44,7 +47,7 @@ def log(msg: str) -> None:
 
 
 PROFILE = ROOT / "profiles" / "skinny_dot_kernel_decode_set.md"
-SET_PROFILE = ROOT / "profiles" / "linear_set_kernel_decode_set.md"
+GROUP_PROFILE = ROOT / "profiles" / "skinny_group_kernel_decode_set.md"
 
 
 def per_shape(ops, kind: str, m: int) -> dict:
@@ -166,32 +169,52 @@ def mlstm_block(device) -> dict:
             "us_per_step": us / t, "bytes": nbytes, "gbs": nbytes / us / 1e3}
 
 
-def time_set(lset, steps: int, warmup: int) -> tuple[float, float]:
+def time_launches(run, steps: int, warmup: int) -> tuple[float, float]:
     """(ms per launch from HIP events on the launch stream, ms per launch by the host clock) over `steps`
-    back-to-back launches after `warmup` untimed ones, synchronised on both sides."""
+    back-to-back launches of `run` (one launch each, on torch's current stream) after `warmup` untimed ones,
+    synchronised on both sides."""
     import torch
 
     for _ in range(warmup):
-        lset.run()
+        run()
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record()
     for _ in range(steps):
-        lset.run()
+        run()
     ev1.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    if lset.timed_out():
-        raise RuntimeError("a set launch gave up waiting for another workgroup: its results are invalid")
     return ev0.elapsed_time(ev1) / steps, wall_ms
 
 
-def set_figures(lset, nbytes: int, steps: int) -> dict:
-    ev_ms, wall_ms = time_set(lset, steps, max(2, steps // 10))
+def time_set(lset, steps: int, warmup: int) -> tuple[float, float]:
+    """time_launches of the persistent set kernel, checking that no launch gave up waiting."""
+    out = time_launches(lset.run, steps, warmup)
+    if lset.timed_out():
+        raise RuntimeError("a set launch gave up waiting for another workgroup: its results are invalid")
+    return out
+
+
+def _figures(ev_ms: float, wall_ms: float, nbytes: int) -> dict:
     ms = max(ev_ms, wall_ms)
     return {"us_per_set": ms * 1e3, "gbs": nbytes / ms / 1e6, "pct_of_hbm_peak": nbytes / ms / 1e6 / HBM_PEAK_GBS
-            * 100, "stages": len(lset.stages)}
+            * 100}
+
+
+def set_figures(lset, nbytes: int, steps: int) -> dict:
+    return {**_figures(*time_set(lset, steps, max(2, steps // 10)), nbytes), "stages": len(lset.stages)}
+
+
+def group_roofline(group, ev_ms: float, nbytes: int, tag: str) -> dict:
+    """Roofline of the grouped kernel: algorithmic bytes per launch over the HIP-event launch time, traffic per
+    launch from the committed counter summary."""
+    kernel = f"skinny_group_kernel<{0 if group.kind == 'bf16' else 1}, {group.rows}, {group.waves}>"
+    achieved = nbytes / (ev_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+            "traffic": profiled_traffic(GROUP_PROFILE).get((kernel, tag)), "kernel": kernel, "launches_per_step": 1,
+            "avg_us_per_launch": ev_ms * 1e3, "bytes_per_launch": nbytes, "workgroups": group.blocks}
 
 
 def per_launch_graph(ops, kind: str, nbytes: int) -> dict:
@@ -329,55 +352,55 @@ def main() -> int:
     _lib.lib()
     log("[bench] building the bf16 decode-step set (2.56 GB of weights)")
     weights = D.make_weights("bf16", device, seed=0)
-    chain = D.build_chain("bf16", device, dependent=False, weights=weights)
+    ops = D.build("bf16", 1, device, seed=0, weights=weights)
+    group = D.group_of(ops)
     nbytes = D.chain_bytes("bf16")
     log(f"[bench] warm-up {a.warmup}, timing {a.steps} steps")
-    ev_ms, wall_ms = time_set(chain.lset, a.steps, a.warmup)
+    ev_ms, wall_ms = time_launches(group.run, a.steps, a.warmup)
     ms = max(ev_ms, wall_ms)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] {ms * 1e3:.1f} us per set, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
 
-    achieved = nbytes / (ev_ms * 1e-3) / 1e9
-    traffic = profiled_traffic(SET_PROFILE).get(("linear_set_kernel<0>", "set-independent"))
     result = {
         "metric": METRIC, "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0, 0.02^2) bf16 weights, unit-RMS N(0,1) activations)",
         "config": {"workload": ("OLMo-2-1B-shaped decode-step linear set at M=1, bf16: 16 x (q,k,v,o 2048->2048; "
                                 "gate,up 2048->8192; down 8192->2048) + LM head 2048->100352, 113 linears with "
-                                "their own inputs, one persistent launch of 65 stages"),
+                                "their own inputs, one grouped launch"),
                    "M": 1, "linears": len(D.shapes()), "bytes_per_step": nbytes, "us_per_set": ms * 1e3,
                    "pct_of_hbm_peak": gbs / HBM_PEAK_GBS * 100, "event_ms": ev_ms, "wall_ms": wall_ms},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "linear_set_kernel<0>",
-                     "launches_per_step": 1, "avg_us_per_launch": ev_ms * 1e3, "bytes_per_launch": nbytes},
+        "roofline": group_roofline(group, ev_ms, nbytes, "group-bf16"),
     }
-    ops = None
     if not a.no_extras:
-        log("[bench] dependent bf16 chain")
+        log("[bench] persistent set kernel, independent and dependent")
+        ind = D.build_chain("bf16", device, dependent=False, weights=weights)
         dep = D.build_chain("bf16", device, dependent=True, weights=weights)
-        result["dependent_chain"] = set_figures(dep.lset, nbytes, 50)
-        del dep
+        result["persistent_set"] = {"independent": set_figures(ind.lset, nbytes, 100),
+                                    "dependent_chain": set_figures(dep.lset, nbytes, 50)}
+        del ind, dep
         log("[bench] 113-launch graph")
-        ops = D.build("bf16", 1, device, seed=0, weights=weights)
         result["per_launch_graph"] = per_launch_graph(ops, "bf16", nbytes)
         log("[bench] int8 set")
         w8 = D.make_weights("int8", device, seed=0)
         nb8 = D.chain_bytes("int8")
+        ops8 = D.build("int8", 1, device, seed=0, weights=w8)
+        group8 = D.group_of(ops8)
+        ev8, wall8 = time_launches(group8.run, 100, 10)
+        grp8 = {**_figures(ev8, wall8, nb8), "roofline": group_roofline(group8, ev8, nb8, "group-int8")}
         ind8 = D.build_chain("int8", device, dependent=False, weights=w8)
         i8 = set_figures(ind8.lset, nb8, 100)
         del ind8
         dep8 = D.build_chain("int8", device, dependent=True, weights=w8)
         d8 = set_figures(dep8.lset, nb8, 50)
         del dep8
-        ops8 = D.build("int8", 1, device, seed=0, weights=w8)
         g8 = per_launch_graph(ops8, "int8", nb8)
-        del ops8
-        result["int8_set"] = {"bytes_per_step": nb8, "scales": "fp16 per output row", "independent": i8,
-                              "dependent_chain": d8, "per_launch_graph": g8,
-                              "bf16_over_int8_time": ms * 1e3 / i8["us_per_set"],
-                              "bf16_over_int8_time_dependent": result["dependent_chain"]["us_per_set"]
-                              / d8["us_per_set"]}
+        del ops8, group8
+        result["int8_set"] = {"bytes_per_step": nb8, "scales": "fp16 per output row", "grouped": grp8,
+                              "persistent_set": {"independent": i8, "dependent_chain": d8}, "per_launch_graph": g8,
+                              "bf16_over_int8_time": ms * 1e3 / grp8["us_per_set"],
+                              "bf16_over_int8_time_dependent": result["persistent_set"]["dependent_chain"]
+                              ["us_per_set"] / d8["us_per_set"]}
         del w8
         torch.cuda.empty_cache()
         log("[bench] mLSTM block")
@@ -388,8 +411,6 @@ def main() -> int:
         result["decode_loop"] = decode_loop(device)
     if not a.no_cpu:
         log("[bench] CPU baseline")
-        if ops is None:
-            ops = D.build("bf16", 1, device, seed=0, weights=weights)
         result["cpu_baseline"] = cpu_baseline(ops)
     print(json.dumps(result), flush=True)
     return 0

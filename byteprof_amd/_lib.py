@@ -69,6 +69,9 @@ SIGNATURES: dict[str, tuple] = {
     "bp_linear_set_workgroups": (_c_int, [_c_int]),
     "bp_linear_set_validate": (_c_int, [_c_vp, _c_int, _c_int, _c_int]),
     "bp_linear_set_run": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_size, _c_int, _c_vp]),
+    "bp_skinny_group_config_supported": (_c_int, [_c_int, _c_int, _c_int]),
+    "bp_skinny_group_plan": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_vp, _c_int]),
+    "bp_skinny_group_run": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

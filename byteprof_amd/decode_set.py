@@ -6,6 +6,9 @@ Infinity Cache, so nothing is served from cache across replays). Weights ~ N(0, 
 ~ N(0, 1) renormalised to unit RMS. The reference measures the same linears one call each inside a CUDA graph
 (byteprof tools/skinny_bench.py:45-71; FINDINGS "OLMo-2 16-block linear set").
 
+The same independent linears also run as one grouped launch (`group_of`, optim/skinny_group.py): one grid over the
+row blocks of all 113 linears, every output bitwise equal to its own skinny_mm call.
+
 The same linears also run as one persistent launch (`build_chain`, optim/linear_set.py): stages q|k|v, o,
 gate|up, down per layer and the head, each stage's input the unit-RMS renormalisation of the output it depends on
 in a decode step (o <- v: attention over one cached position returns v; gate|up <- o; down <- up; the next
@@ -24,6 +27,7 @@ import torch
 
 from .optim import skinny as S
 from .optim.linear_set import LinearSet, Stage
+from .optim.skinny_group import GroupItem, SkinnyGroup
 from .quant.accounting import Linear, call_bytes
 from .quant.hip_int8 import quantize_rowwise_int8
 
@@ -74,6 +78,12 @@ def build(kind: str = "bf16", m: int = 1, device="cuda:0", seed: int = 0, scale_
         x = unit_rms(torch.randn(m, k, generator=g, device=device))
         ops.append(Op(name, n, k, args, x, torch.empty(m, n, dtype=torch.bfloat16, device=device)))
     return ops
+
+
+def group_of(ops: list[Op], cfg: tuple[int, int] | None = None) -> SkinnyGroup:
+    """The ops (each on its own input, M = 1) as one grouped launch writing the ops' own outputs."""
+    return SkinnyGroup([GroupItem(o.x[0], o.args[0], o.y[0], o.args[1] if len(o.args) > 1 else None) for o in ops],
+                       cfg=cfg)
 
 
 def algorithmic_bytes(ops: list[Op], kind: str, m: int) -> int:

@@ -3,6 +3,8 @@
   python -m byteprof_amd.profiling set  [--kind bf16|int8] [--replays R]   the decode-step set graph, R replays
   python -m byteprof_amd.profiling chain [--kind bf16|int8] [--dependent] [--replays R]
                                                                          the set as one persistent launch, R launches
+  python -m byteprof_amd.profiling group [--kind bf16|int8] [--replays R]
+                                                                         the set as one grouped launch, R launches
   python -m byteprof_amd.profiling skinny [--kind bf16|int8] [--n N] [--k K] [--m M] [--replays R]
                                                                          skinny_mm over a ring of distinct weights
   python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
@@ -101,10 +103,11 @@ def summarize(a) -> int:
         traffic = (fv * f_scale + wv * w_scale) * 1024 / 1e6
         print(f"{_short(name)[:48]:<48} {grid:>12} {k:>10} {fv:>11.1f} {wv:>10.1f} {traffic:>11.3f}")
     if a.chain_tag:
+        kernel = "skinny_group_kernel" if a.chain_tag.startswith("group") else "linear_set_kernel"
         print()
-        print(f"## traffic per launch of the persistent set kernel, {a.chain_tag} (bytes; read by bench.py)")
+        print(f"## traffic per launch of the {kernel}, {a.chain_tag} (bytes; read by bench.py)")
         for key in sorted(fetch):
-            if "linear_set_kernel" in key[0]:
+            if kernel in key[0]:
                 nbytes = (fetch[key][2] * f_scale + write.get(key, ("", 0, 0.0))[2] * w_scale) * 1024
                 print(f"traffic: {_short(key[0]).replace('bp::', '')} {a.chain_tag} {nbytes:.0f}")
     if a.set_kind:
@@ -133,7 +136,7 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=("set", "chain", "skinny", "copy", "summarize"))
+    ap.add_argument("what", choices=("set", "chain", "group", "skinny", "copy", "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
     ap.add_argument("--write", help="summarize: WRITE_SIZE database of the workload")
@@ -144,7 +147,8 @@ def main(argv=None) -> int:
     ap.add_argument("--valu", action="store_true", help="skinny: force the VALU kernels (the tuned VALU tiles)")
     ap.add_argument("--all", action="store_true", help="summarize: include kernels outside this library")
     ap.add_argument("--set-kind", choices=("bf16", "int8"), help="summarize: emit traffic lines for the set shapes")
-    ap.add_argument("--chain-tag", help="summarize: emit traffic lines for the set kernel under this tag")
+    ap.add_argument("--chain-tag", help="summarize: emit traffic lines for the set kernel under this tag (a tag "
+                    "starting with 'group': for the grouped kernel)")
     ap.add_argument("--kind", default="bf16", choices=("bf16", "int8"))
     ap.add_argument("--dependent", action="store_true", help="chain: stages read the outputs they depend on")
     ap.add_argument("--replays", type=int, default=5)
@@ -199,6 +203,15 @@ def main(argv=None) -> int:
             return 1
         print(f"ran the {a.kind} decode-step set as one persistent launch {a.replays} times "
               f"({len(ch.stages)} stages, {'dependent' if a.dependent else 'independent'})", flush=True)
+        return 0
+    if a.what == "group":
+        ops = D.build(a.kind, 1, device)
+        grp = D.group_of(ops)
+        for _ in range(a.replays):
+            grp.run()
+        torch.cuda.synchronize()
+        print(f"ran the {a.kind} decode-step set as one grouped launch {a.replays} times ({len(ops)} linears, "
+              f"{grp.blocks} workgroups of {grp.rows} rows x {grp.waves} waves)", flush=True)
         return 0
     ops = D.build(a.kind, 1, device)
     g = D.capture(ops)

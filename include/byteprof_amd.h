@@ -278,6 +278,46 @@ int bp_linear_set_validate(const BpSetStage* stages, int num_stages, int wkind, 
 int bp_linear_set_run(int wkind, int scale_dtype, const BpSetStage* host_stages, const void* dev_stages,
                       int num_stages, void* scratch, size_t scratch_bytes, int num_workgroups, void* stream);
 
+/*
+ * Grouped skinny launch: G independent linears at one activation row, y_i = x_i . W_i^T, in one non-persistent
+ * launch. Workgroup b computes `rows` consecutive output rows of the item whose workgroup range holds b; every
+ * output is bitwise equal to bp_skinny_bf16 / bp_skinny_int8 at M = 1 with the same rows and waves and split 1.
+ *
+ * Layout (48 bytes, 8-byte aligned pointers): the array lives in device memory for the kernel, and a host copy with
+ * the same contents is passed for validation.
+ */
+typedef struct BpGroupItem {
+  const void* x;      /* bf16 [K], 16-byte aligned: the item's activation row */
+  const void* w;      /* [N, K] row-major, 16-byte aligned: bf16 or int8 weights (one kind for the whole group) */
+  const void* scale;  /* int8: [N] per-row scales (dtype given to bp_skinny_group_run); bf16: ignored */
+  void* y;            /* bf16 [N]: the outputs */
+  int64_t N;          /* rows, >= 0 (an item of 0 rows takes no workgroup) */
+  int32_t K;          /* a positive multiple of 512 (bf16 weights) or 1024 (int8) */
+  int32_t block0;     /* first workgroup of the item: written by bp_skinny_group_plan */
+} BpGroupItem;
+
+/* Workgroups per entry of the lookup table: lut[j] is the item that holds workgroup j * BP_GROUP_LUT_SPAN. */
+#define BP_GROUP_LUT_SPAN 256
+
+/* 1 if a grouped kernel with `rows` output rows and `waves` wavefronts per workgroup is compiled for wkind. */
+int bp_skinny_group_config_supported(int wkind, int rows, int waves);
+
+/* Host-side plan: checks every item, writes items[i].block0 (workgroups of `rows` rows, items in order) and, when
+ * lut is not NULL, fills lut[0 .. ceil(blocks / BP_GROUP_LUT_SPAN)) (lut_capacity entries available). Returns the
+ * number of workgroups (>= 0) or a BP_E_* code. No device access. */
+int bp_skinny_group_plan(BpGroupItem* items, int num_items, int wkind, int rows, int32_t* lut, int lut_capacity);
+
+/*
+ * Runs the group: one launch of `blocks` workgroups on `stream`. host_items must be the planned array (checked:
+ * operands and every block0), dev_items and dev_lut its device copies. wkind BP_DT_BF16 (0) or 1 (int8 weights, with
+ * scale_dtype BP_DT_BF16 / BP_DT_F16 / BP_DT_F32).
+ * Replaces: the set benchmark's independent skinny_mm calls, one per linear (tools/skinny_bench.py:45-71 ->
+ *           byteprof/optim/skinny.py:136-166), captured in one CUDA graph; the per-row arithmetic is
+ *           skinny.py:36-90's at split 1.
+ */
+int bp_skinny_group_run(int wkind, int scale_dtype, const BpGroupItem* host_items, const void* dev_items,
+                        const void* dev_lut, int num_items, int blocks, int rows, int waves, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

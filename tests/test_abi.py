@@ -155,3 +155,100 @@ def test_linear_set_validation_rejects_bad_descriptors(L):
     # launch counter + error flag lines, 3 x (4093 rounded up to 8) tagged rows
     assert L.bp_linear_set_scratch_bytes(ctypes.addressof(arr), 3, 256) == 4 * (64 + 3 * 4096)
     assert L.bp_linear_set_scratch_bytes(None, 0, 256) == 0
+
+
+def _group_items(shapes, kind=0):
+    from byteprof_amd.optim.skinny_group import BpGroupItem
+
+    arr = (BpGroupItem * len(shapes))()
+    for i, (h, (n, k)) in enumerate(zip(arr, shapes)):
+        h.x, h.w, h.y = 0x10000 * (i + 1), 0x100000 * (i + 1), 0x1000000 * (i + 1)
+        h.scale = 0x2000000 if kind == 1 else None
+        h.N, h.K, h.block0 = n, k, -7
+    return arr
+
+
+def test_group_descriptor_layout_matches_the_header():
+    from byteprof_amd.optim.skinny_group import LUT_SPAN, BpGroupItem
+
+    text = HEADER.read_text()
+    body = text[text.index("typedef struct BpGroupItem"):text.index("} BpGroupItem;")]
+    fields = re.findall(r"^\s+[a-z_0-9 ]+?\*?\s*([a-z_A-Z0-9]+);", body, flags=re.M)
+    assert fields == [f[0] for f in BpGroupItem._fields_]
+    assert ctypes.sizeof(BpGroupItem) == 48
+    assert f"#define BP_GROUP_LUT_SPAN {LUT_SPAN}" in text
+
+
+@pytest.mark.parametrize("rows", [1, 2, 4, 8])
+def test_group_plan_matches_a_brute_force_assignment(L, rows):
+    """block0 is the running sum of ceil(N / rows); lut[j] is the item holding workgroup 256 j, found here by
+    assigning every workgroup to its item one by one (items of 0 rows take none, tiny items share a span)."""
+    shapes = [(2048, 2048), (0, 512), (3, 512), (1, 1024), (8192, 2048), (0, 512), (700, 8192), (5, 512),
+              (100352, 2048), (0, 1024)]
+    arr = _group_items(shapes)
+    owner = [i for i, (n, _) in enumerate(shapes) for _ in range(-(-n // rows))]
+    lut = (ctypes.c_int32 * 4096)()
+    blocks = L.bp_skinny_group_plan(ctypes.addressof(arr), len(arr), 0, rows, ctypes.addressof(lut), len(lut))
+    assert blocks == len(owner)
+    starts = [sum(-(-n // rows) for n, _ in shapes[:i]) for i in range(len(shapes))]
+    assert [h.block0 for h in arr] == starts
+    spans = -(-blocks // 256)
+    assert list(lut[:spans]) == [owner[256 * j] for j in range(spans)]
+    # the kernel's walk from lut[b / 256] reaches the owner of every workgroup
+    for b in range(blocks):
+        g = lut[b // 256]
+        while g + 1 < len(arr) and arr[g + 1].block0 <= b:
+            g += 1
+        assert g == owner[b], b
+    # counting only (no lut)
+    assert L.bp_skinny_group_plan(ctypes.addressof(arr), len(arr), 0, rows, None, 0) == blocks
+
+
+def test_group_plan_and_run_reject_bad_items_before_any_launch(L):
+    def plan(arr, kind=0, rows=2, cap=64):
+        lut = (ctypes.c_int32 * cap)()
+        return L.bp_skinny_group_plan(ctypes.addressof(arr), len(arr), kind, rows, ctypes.addressof(lut), cap)
+
+    assert plan(_group_items([(64, 512)])) == 32
+    assert plan(_group_items([(64, 1024)], kind=1), kind=1) == 32
+    assert plan(_group_items([(64, 1000)])) == -1               # K not a multiple of the 512-element chunk
+    assert plan(_group_items([(64, 1536)], kind=1), kind=1) == -1  # int8: K a multiple of 1024
+    assert plan(_group_items([(64, 0)])) == -1                  # K = 0
+    assert plan(_group_items([(-1, 512)])) == -1                # negative N
+    assert plan(_group_items([(64, 512)]), kind=1) == -1        # int8 without scales
+    assert plan(_group_items([(64, 512)]), kind=2) == -2        # unknown weight kind
+    assert plan(_group_items([(64, 512)]), rows=0) == -1
+    assert plan(_group_items([(2 * 256 * 64 + 2, 512)]), cap=64) == -1  # lut too small (65 spans)
+    bad = _group_items([(64, 512)])
+    bad[0].x = 0x10008                                          # x must be 16-byte aligned
+    assert plan(bad) == -1
+    bad = _group_items([(64, 512)])
+    bad[0].w = None
+    assert plan(bad) == -1
+    assert L.bp_skinny_group_plan(None, 0, 0, 2, None, 0) == -1
+    assert L.bp_skinny_group_config_supported(0, 2, 4) == 1
+    assert L.bp_skinny_group_config_supported(1, 8, 8) == 1
+    assert L.bp_skinny_group_config_supported(0, 3, 4) == 0
+    assert L.bp_skinny_group_config_supported(0, 2, 16) == 0
+    assert L.bp_skinny_group_config_supported(2, 2, 4) == 0
+
+    arr = _group_items([(64, 512), (10, 512)])
+    blocks = plan(arr)
+    assert blocks == 37
+
+    def run(arr, kind=0, sdt=0, blocks=blocks, rows=2, waves=4):
+        return L.bp_skinny_group_run(kind, sdt, ctypes.addressof(arr), 0x5000, 0x6000, len(arr), blocks, rows, waves,
+                                     None)
+
+    assert run(arr, rows=3) == -2                                # no compiled kernel
+    assert run(arr, blocks=36) == -1                             # blocks must match the plan
+    arr[1].block0 = 31                                           # a stale plan
+    assert run(arr) == -1
+    arr[1].block0 = 32
+    assert run(arr, rows=4) == -1                                # planned for 2 rows per workgroup
+    int8 = _group_items([(64, 1024)], kind=1)
+    assert plan(int8, kind=1) == 32
+    assert run(int8, kind=1, sdt=3, blocks=32) == -1              # int8 scale dtype must be bf16 / fp16 / fp32
+    empty = _group_items([(0, 512)])
+    assert plan(empty) == 0
+    assert run(empty, blocks=0) == 0                             # nothing to launch
