@@ -23,7 +23,7 @@ namespace bp {
 namespace {
 
 constexpr int kBlock = 1024;       // threads of the one-workgroup kernels
-constexpr int kAttnThreads = 256;  // threads per head in the attention
+constexpr int kAttnThreads = 512;  // threads per head in the attention
 constexpr int kAttnMaxLen = 4096;  // positions a cache may hold (scores in LDS)
 
 // Sum of v over the workgroup (blockDim.x a multiple of 64, at most kBlock); every thread gets the total.
@@ -106,70 +106,218 @@ __global__ __launch_bounds__(kBlock) void qk_rope_cache_kernel(const uint16_t* _
   }
 }
 
-// grid = heads; positions 0 .. pos of the head's cache rows [max_len, D].
+constexpr int kAttnUnroll = 4;  // row batches whose loads are in flight together
+
+// q_row . w_row for 8 bf16 cache values packed in w and 8 q values: the products summed in order.
+__device__ __forceinline__ float dot8(const u32x4& w, const float (&qv)[8]) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+  float dot = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    dot += bf16_bits_to_float(wd[e] & 0xffffu) * qv[2 * e];
+    dot += bf16_bits_to_float(wd[e] >> 16) * qv[2 * e + 1];
+  }
+  return dot;
+}
+
+// Sum of v over each group of LPR consecutive lanes (LPR a power of two <= 32), returned to every lane of the
+// group: DPP pairs within quads, quads within half-rows, half-rows within rows of 16, then rows of 16 in pairs.
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (LPR >= 2) v += dpp_f32<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  if constexpr (LPR >= 4) v += dpp_f32<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  if constexpr (LPR >= 8) v += dpp_f32<0x141, 0xF>(v);  // row_half_mirror
+  if constexpr (LPR >= 16) v += dpp_f32<0x140, 0xF>(v); // row_mirror
+  if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
+  return v;
+}
+
+// Sum (or maximum) of v over the wave, returned to every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+constexpr int kAttnWaves = kAttnThreads / kWave;
+
+// One head's attention over its cache rows K, V ([max_len, D] bf16, 16-byte aligned, D = 8 * LPR) at positions
+// 0 .. T-1, run by the workgroup's kAttnThreads threads. Layout: LPR lanes per cache row (16 bytes each), 64 / LPR
+// rows per wave instruction, the waves on consecutive rows, and kAttnUnroll such row batches loaded before they
+// are used. The first batch of K and V rows can be loaded early (prefetch(), before the caller's own work), so that
+// its latency overlaps the caller's; a row can be taken from LDS instead of the cache (SUB: the row the caller
+// writes in this launch). Scores: a lane's 8 products in order, then the row's lanes summed (group_sum);
+// s_t = bf16(bf16(q . k_t) * scale), p = bf16(softmax_fp32(s)). Values: each lane accumulates its 8 dimensions
+// over its rows; the row groups of a wave are added by lane butterflies, the waves' sums in wave order through LDS.
+template <int LPR, bool SUB>
+struct HeadAttention {
+  static constexpr int D = 8 * LPR;
+  static constexpr int RPW = kWave / LPR;           // rows per wave instruction
+  static constexpr int STEP = kAttnWaves * RPW;     // rows per workgroup-wide batch
+  static constexpr int BATCH = kAttnUnroll * STEP;  // rows per round of loads
+  const uint16_t* K;
+  const uint16_t* V;
+  int T, s, slot;
+  u32x4 k0[kAttnUnroll], v0[kAttnUnroll];
+
+  __device__ __forceinline__ HeadAttention(const uint16_t* K_, const uint16_t* V_, int T_) : K(K_), V(V_), T(T_) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    s = lane % LPR;
+    slot = wave * RPW + lane / LPR;  // this lane's row within a batch
+  }
+
+  __device__ __forceinline__ void load_batch(const uint16_t* base, int t0, u32x4 (&out)[kAttnUnroll]) const {
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) {
+      const int t = t0 + u * STEP + slot;
+      out[u] = u32x4{0u, 0u, 0u, 0u};
+      if (t < T) out[u] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(t) * D + 8 * s);
+    }
+  }
+
+  // Issues the loads of the first batch of K and V rows.
+  __device__ __forceinline__ void prefetch() {
+    load_batch(K, 0, k0);
+    load_batch(V, 0, v0);
+  }
+
+  __device__ __forceinline__ void scores(const u32x4 (&kv)[kAttnUnroll], int t0, const float (&qv)[8],
+                                         const uint16_t* ksub, int sub_t, float scale, float* sc, float& m) const {
+    float dot[kAttnUnroll];
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) {
+      const int t = t0 + u * STEP + slot;
+      const u32x4 w = SUB && t == sub_t ? *reinterpret_cast<const u32x4*>(ksub + 8 * s) : kv[u];
+      dot[u] = dot8(w, qv);
+    }
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) dot[u] = group_sum<LPR>(dot[u]);
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) {
+      const int t = t0 + u * STEP + slot;
+      if (t < T) {
+        const float v = round_to_bf16(round_to_bf16(dot[u]) * scale);
+        if (s == 0) sc[t] = v;
+        m = fmaxf(m, v);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void values(const u32x4 (&vv)[kAttnUnroll], int t0, const uint16_t* vsub, int sub_t,
+                                         const float* sc, float inv, float (&acc)[8]) const {
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) {
+      const int t = t0 + u * STEP + slot;
+      if (t < T) {
+        const u32x4 w = SUB && t == sub_t ? *reinterpret_cast<const u32x4*>(vsub + 8 * s) : vv[u];
+        const float p = round_to_bf16(sc[t] * inv);
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[2 * e] += p * bf16_bits_to_float(wd[e] & 0xffffu);
+          acc[2 * e + 1] += p * bf16_bits_to_float(wd[e] >> 16);
+        }
+      }
+    }
+  }
+
+  // q: bf16 values in LDS qs[0 .. D). Row sub_t (-1: none) is read from ksub / vsub (bf16, LDS, 16-byte aligned)
+  // instead of the cache. Writes out[0 .. D). The caller has made qs, ksub and vsub visible (a barrier).
+  // LDS: sc[T] scores, red_m / red_l [kAttnWaves], part [kAttnWaves * D].
+  __device__ __forceinline__ void run(const float* qs, const uint16_t* ksub, const uint16_t* vsub, int sub_t,
+                                      float scale, float* sc, float* red_m, float* red_l, float* part,
+                                      uint16_t* __restrict__ out) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    float qv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = qs[8 * s + e];
+    float m = -INFINITY;
+    scores(k0, 0, qv, ksub, sub_t, scale, sc, m);
+    for (int t0 = BATCH; t0 < T; t0 += BATCH) {
+      u32x4 kv[kAttnUnroll];
+      load_batch(K, t0, kv);
+      scores(kv, t0, qv, ksub, sub_t, scale, sc, m);
+    }
+    m = wave_max(m);
+    if (lane == 0) red_m[wave] = m;
+    __syncthreads();  // also orders the sc writes before the reads below
+    m = red_m[0];
+    for (int w = 1; w < kAttnWaves; ++w) m = fmaxf(m, red_m[w]);
+    float l = 0.f;
+    for (int t = threadIdx.x; t < T; t += kAttnThreads) {
+      const float e = expf(sc[t] - m);
+      sc[t] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) red_l[wave] = l;
+    __syncthreads();  // also orders the sc writes before the reads below
+    l = red_l[0];
+    for (int w = 1; w < kAttnWaves; ++w) l += red_l[w];
+    const float inv = 1.f / l;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    values(v0, 0, vsub, sub_t, sc, inv, acc);
+    for (int t0 = BATCH; t0 < T; t0 += BATCH) {
+      u32x4 vv[kAttnUnroll];
+      load_batch(V, t0, vv);
+      values(vv, t0, vsub, sub_t, sc, inv, acc);
+    }
+    // the wave's row groups (lanes s, s + LPR, s + 2 LPR, ...) added by butterflies over the group bits
+#pragma unroll
+    for (int o = LPR; o < kWave; o <<= 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
+    }
+    if (lane < LPR) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[wave * D + 8 * s + e] = acc[e];
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < D; d += kAttnThreads) {
+      float t = part[d];
+      for (int w = 1; w < kAttnWaves; ++w) t += part[w * D + d];
+      out[d] = float_to_bf16_bits(t);
+    }
+  }
+};
+
+constexpr int kAttnPart = kAttnWaves * 256;  // floats of the value partials: waves x D (D <= 256)
+
+// grid = heads; positions 0 .. pos of the head's cache rows [max_len, D], D = 8 * LPR.
+template <int LPR>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ kc,
                                                                  const uint16_t* __restrict__ vc,
                                                                  const int64_t* __restrict__ pos_p,
-                                                                 uint16_t* __restrict__ out, int D, int max_len,
+                                                                 uint16_t* __restrict__ out, int max_len,
                                                                  float scale) {
+  constexpr int D = 8 * LPR;
   __shared__ float sc[kAttnMaxLen];
-  __shared__ float qs[512];
-  __shared__ float red[kAttnThreads / kWave];
-  __shared__ float part[kAttnThreads];
+  __shared__ float qs[D];
+  __shared__ float red_m[kAttnWaves], red_l[kAttnWaves];
+  __shared__ float part[kAttnPart];
   const int h = blockIdx.x;
   int64_t pos = *pos_p;
   pos = pos < 0 ? 0 : (pos >= max_len ? max_len - 1 : pos);
-  const int T = static_cast<int>(pos) + 1;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) qs[d] = ld_bf16(q, static_cast<int64_t>(h) * D + d);
+  HeadAttention<LPR, false> att(kc + static_cast<int64_t>(h) * max_len * D,
+                                vc + static_cast<int64_t>(h) * max_len * D, static_cast<int>(pos) + 1);
+  att.prefetch();
+  for (int d = threadIdx.x; d < D; d += kAttnThreads) qs[d] = ld_bf16(q, static_cast<int64_t>(h) * D + d);
   __syncthreads();
-  const uint16_t* K = kc + static_cast<int64_t>(h) * max_len * D;
-  const uint16_t* V = vc + static_cast<int64_t>(h) * max_len * D;
-  float m = -INFINITY;
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const uint16_t* kr = K + static_cast<int64_t>(t) * D;
-    float dot = 0.f;
-    for (int d = 0; d < D; d += 8) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(kr + d);
-      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        dot += bf16_bits_to_float(wd[e] & 0xffffu) * qs[d + 2 * e];
-        dot += bf16_bits_to_float(wd[e] >> 16) * qs[d + 2 * e + 1];
-      }
-    }
-    const float s = round_to_bf16(round_to_bf16(dot) * scale);
-    sc[t] = s;
-    m = fmaxf(m, s);
-  }
-  m = block_max(m, red);
-  float l = 0.f;
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const float e = expf(sc[t] - m);
-    sc[t] = e;
-    l += e;
-  }
-  l = block_sum(l, red);  // its barriers also order the sc writes before the reads below
-  const float inv = 1.f / l;
-  // thread (d, r): dimension d, positions t = r, r + R, ... (R = blockDim.x / D rows of threads)
-  const int R = blockDim.x / D;
-  const int d = threadIdx.x % D, r = threadIdx.x / D;
-  float acc = 0.f;
-  if (r < R) {
-    for (int t = r; t < T; t += R) acc += round_to_bf16(sc[t] * inv) * ld_bf16(V, static_cast<int64_t>(t) * D + d);
-  }
-  part[threadIdx.x] = acc;
-  __syncthreads();
-  if (threadIdx.x < D) {
-    float t = 0.f;
-    for (int i = 0; i < R; ++i) t += part[i * D + threadIdx.x];
-    out[static_cast<int64_t>(h) * D + threadIdx.x] = float_to_bf16_bits(t);
-  }
+  att.run(qs, nullptr, nullptr, -1, scale, sc, red_m, red_l, part, out + static_cast<int64_t>(h) * D);
 }
 
 // qk_rope_cache and attention in one launch: every workgroup h computes the q / k norms over the whole projections
 // (the same sums in every workgroup; their summation order differs from qk_rope_cache_kernel's, so a value may land
-// one bf16 step apart), rotates its own head, writes its k and v at pos, and attends over positions 0 .. pos.
+// one bf16 step apart), rotates its own head, writes its k and v at pos to the cache, and attends over positions
+// 0 .. pos with that row taken from LDS. Every load that does not depend on the norms (the projections, the RoPE
+// operands, the first batch of cache rows) is issued before the first reduction.
+template <int LPR>
 __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint16_t* __restrict__ qkv,
                                                                       const uint16_t* __restrict__ qw,
                                                                       const uint16_t* __restrict__ kw,
@@ -177,94 +325,164 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint
                                                                       const int64_t* __restrict__ pos_p,
                                                                       uint16_t* __restrict__ kc,
                                                                       uint16_t* __restrict__ vc,
-                                                                      uint16_t* __restrict__ out, int heads, int D,
+                                                                      uint16_t* __restrict__ out, int heads,
                                                                       int max_len, float eps, float scale) {
+  constexpr int D = 8 * LPR;
+  constexpr int half = D / 2;
   __shared__ float sc[kAttnMaxLen];
-  __shared__ float qs[512];
-  __shared__ float red[kAttnThreads / kWave];
-  __shared__ float part[kAttnThreads];
+  __shared__ float qs[D];
+  __shared__ __align__(16) uint16_t ks[D];
+  __shared__ __align__(16) uint16_t vs[D];
+  __shared__ float red_q[kAttnWaves], red_k[kAttnWaves], red_m[kAttnWaves], red_l[kAttnWaves];
+  __shared__ float part[kAttnPart];
   const int h = blockIdx.x;
-  const int H = heads * D, half = D / 2;
+  const int H = heads * D;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int64_t pos_in = *pos_p;
   const bool in_cache = pos_in >= 0 && pos_in < max_len;
+  const int64_t pos = pos_in < 0 ? 0 : (pos_in >= max_len ? max_len - 1 : pos_in);
   const uint16_t* q = qkv;
   const uint16_t* k = qkv + H;
   const uint16_t* v = qkv + 2 * H;
-  float sq = 0.f, sk = 0.f;
-  for (int i = threadIdx.x; i < H; i += blockDim.x) {
-    const float a = ld_bf16(q, i), b = ld_bf16(k, i);
-    sq += a * a;
-    sk += b * b;
-  }
-  const float rq = 1.f / sqrtf(block_sum(sq, red) / static_cast<float>(H) + eps);
-  const float rk = 1.f / sqrtf(block_sum(sk, red) / static_cast<float>(H) + eps);
   uint16_t* K = kc + static_cast<int64_t>(h) * max_len * D;
   uint16_t* V = vc + static_cast<int64_t>(h) * max_len * D;
-  for (int j = threadIdx.x; j < half; j += blockDim.x) {
-    const int a = h * D + j, b = a + half;
-    const float f = inv_freq[j] * static_cast<float>(pos_in);
-    const float c = cosf(f), s = sinf(f);
-    const float qa = round_to_bf16(ld_bf16(qw, a) * (ld_bf16(q, a) * rq));
-    const float qb = round_to_bf16(ld_bf16(qw, b) * (ld_bf16(q, b) * rq));
-    const float ka = round_to_bf16(ld_bf16(kw, a) * (ld_bf16(k, a) * rk));
-    const float kb = round_to_bf16(ld_bf16(kw, b) * (ld_bf16(k, b) * rk));
-    qs[j] = round_to_bf16(qa * c + (-qb) * s);
-    qs[j + half] = round_to_bf16(qb * c + qa * s);
-    if (in_cache) {
-      const int64_t row = pos_in * D;
-      K[row + j] = float_to_bf16_bits(ka * c + (-kb) * s);
-      K[row + j + half] = float_to_bf16_bits(kb * c + ka * s);
-      V[row + j] = v[a];
-      V[row + j + half] = v[b];
-    }
+
+  // RoPE operands of this thread's pair (j, j + D/2) of head h (threads j < D/2; D <= 256 <= threads)
+  const int j = threadIdx.x;
+  const bool roper = j < half;
+  const int a = h * D + j, b = a + half;
+  float f_qa = 0.f, f_qb = 0.f, f_ka = 0.f, f_kb = 0.f, w_qa = 0.f, w_qb = 0.f, w_ka = 0.f, w_kb = 0.f, fr = 0.f;
+  uint16_t v_a = 0, v_b = 0;
+  if (roper) {
+    f_qa = ld_bf16(q, a);
+    f_qb = ld_bf16(q, b);
+    f_ka = ld_bf16(k, a);
+    f_kb = ld_bf16(k, b);
+    w_qa = ld_bf16(qw, a);
+    w_qb = ld_bf16(qw, b);
+    w_ka = ld_bf16(kw, a);
+    w_kb = ld_bf16(kw, b);
+    v_a = v[a];
+    v_b = v[b];
+    fr = inv_freq[j];
   }
-  __syncthreads();  // qs and this position's cache row, written above, are read below
-  const int64_t pos = pos_in < 0 ? 0 : (pos_in >= max_len ? max_len - 1 : pos_in);
-  const int T = static_cast<int>(pos) + 1;
-  float m = -INFINITY;
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const uint16_t* kr = K + static_cast<int64_t>(t) * D;
-    float dot = 0.f;
-    for (int d = 0; d < D; d += 8) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(kr + d);
-      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+  HeadAttention<LPR, true> att(K, V, static_cast<int>(pos) + 1);
+  att.prefetch();
+
+  // the norms over the whole projections: 8 elements (one 16-byte load) of q and of k per thread and pass
+  float sq = 0.f, sk = 0.f;
+  for (int i = 8 * threadIdx.x; i < H; i += 8 * kAttnThreads) {
+    const u32x4 qa = *reinterpret_cast<const u32x4*>(q + i);
+    const u32x4 ka = *reinterpret_cast<const u32x4*>(k + i);
+    const uint32_t qd[4] = {qa.x, qa.y, qa.z, qa.w}, kd[4] = {ka.x, ka.y, ka.z, ka.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        dot += bf16_bits_to_float(wd[e] & 0xffffu) * qs[d + 2 * e];
-        dot += bf16_bits_to_float(wd[e] >> 16) * qs[d + 2 * e + 1];
-      }
+    for (int e = 0; e < 4; ++e) {
+      const float q0 = bf16_bits_to_float(qd[e] & 0xffffu), q1 = bf16_bits_to_float(qd[e] >> 16);
+      const float k0 = bf16_bits_to_float(kd[e] & 0xffffu), k1 = bf16_bits_to_float(kd[e] >> 16);
+      sq += q0 * q0;
+      sq += q1 * q1;
+      sk += k0 * k0;
+      sk += k1 * k1;
     }
-    const float s = round_to_bf16(round_to_bf16(dot) * scale);
-    sc[t] = s;
-    m = fmaxf(m, s);
   }
-  m = block_max(m, red);
-  float l = 0.f;
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const float e = expf(sc[t] - m);
-    sc[t] = e;
-    l += e;
+  sq = wave_sum(sq);
+  sk = wave_sum(sk);
+  if (lane == 0) {
+    red_q[wave] = sq;
+    red_k[wave] = sk;
   }
-  l = block_sum(l, red);
-  const float inv = 1.f / l;
-  const int R = blockDim.x / D;
-  const int d = threadIdx.x % D, r = threadIdx.x / D;
-  float acc = 0.f;
-  for (int t = r; t < T; t += R) acc += round_to_bf16(sc[t] * inv) * ld_bf16(V, static_cast<int64_t>(t) * D + d);
-  part[threadIdx.x] = acc;
   __syncthreads();
-  if (threadIdx.x < D) {
-    float t = 0.f;
-    for (int i = 0; i < R; ++i) t += part[i * D + threadIdx.x];
-    out[static_cast<int64_t>(h) * D + threadIdx.x] = float_to_bf16_bits(t);
+  sq = red_q[0];
+  sk = red_k[0];
+  for (int w = 1; w < kAttnWaves; ++w) {
+    sq += red_q[w];
+    sk += red_k[w];
   }
+  const float rq = 1.f / sqrtf(sq / static_cast<float>(H) + eps);
+  const float rk = 1.f / sqrtf(sk / static_cast<float>(H) + eps);
+  if (roper) {
+    const float f = fr * static_cast<float>(pos_in);
+    const float c = cosf(f), sn = sinf(f);
+    const float qa = round_to_bf16(w_qa * (f_qa * rq));
+    const float qb = round_to_bf16(w_qb * (f_qb * rq));
+    const float ka = round_to_bf16(w_ka * (f_ka * rk));
+    const float kb = round_to_bf16(w_kb * (f_kb * rk));
+    qs[j] = round_to_bf16(qa * c + (-qb) * sn);
+    qs[j + half] = round_to_bf16(qb * c + qa * sn);
+    const uint16_t k_lo = float_to_bf16_bits(ka * c + (-kb) * sn);
+    const uint16_t k_hi = float_to_bf16_bits(kb * c + ka * sn);
+    ks[j] = k_lo;
+    ks[j + half] = k_hi;
+    vs[j] = v_a;
+    vs[j + half] = v_b;
+    if (in_cache) {
+      const int64_t r = pos_in * D;
+      K[r + j] = k_lo;
+      K[r + j + half] = k_hi;
+      V[r + j] = v_a;
+      V[r + j + half] = v_b;
+    }
+  }
+  __syncthreads();  // qs, ks and vs, written above, are read below
+  att.run(qs, ks, vs, in_cache ? static_cast<int>(pos_in) : -1, scale, sc, red_m, red_l, part,
+          out + static_cast<int64_t>(h) * D);
 }
 
+// Launches of the attention kernels for head_dim = 8 * LPR (LPR = 1, 2, 4, 8, 16 or 32).
+template <int LPR>
+void launch_attention(const void* q, const void* kc, const void* vc, const int64_t* pos, void* out, int heads,
+                      int max_len, float scale, hipStream_t st) {
+  attention_kernel<LPR><<<heads, kAttnThreads, 0, st>>>(static_cast<const uint16_t*>(q),
+                                                        static_cast<const uint16_t*>(kc),
+                                                        static_cast<const uint16_t*>(vc), pos,
+                                                        static_cast<uint16_t*>(out), max_len, scale);
+}
+
+template <int LPR>
+void launch_rope_attention(const void* qkv, const void* qw, const void* kw, const float* inv_freq, const int64_t* pos,
+                           void* kc, void* vc, void* out, int heads, int max_len, float eps, float scale,
+                           hipStream_t st) {
+  rope_attention_kernel<LPR><<<heads, kAttnThreads, 0, st>>>(
+      static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(qw), static_cast<const uint16_t*>(kw),
+      inv_freq, pos, static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), static_cast<uint16_t*>(out), heads,
+      max_len, eps, scale);
+}
+
+constexpr int kNormPer = 8;  // elements per thread kept in registers by norm_residual (n <= kBlock * kNormPer)
+
+// One workgroup. For n <= kBlock * kNormPer, x, the weight and the residual are loaded once, together, before the
+// reduction (one round trip to memory); longer vectors take a second pass over memory.
 __global__ __launch_bounds__(kBlock) void norm_residual_kernel(const uint16_t* __restrict__ x,
                                                                const uint16_t* __restrict__ w,
                                                                const uint16_t* residual, uint16_t* out, int n,
                                                                float eps) {
   __shared__ float red[kBlock / kWave];
+  if (n <= static_cast<int>(blockDim.x) * kNormPer) {
+    float xv[kNormPer], wv[kNormPer], rv[kNormPer];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < kNormPer; ++e) {
+      const int i = threadIdx.x + e * blockDim.x;
+      xv[e] = wv[e] = rv[e] = 0.f;
+      if (i < n) {
+        xv[e] = ld_bf16(x, i);
+        wv[e] = ld_bf16(w, i);
+        if (residual != nullptr) rv[e] = ld_bf16(residual, i);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kNormPer; ++e) ss += xv[e] * xv[e];
+    const float r = 1.f / sqrtf(block_sum(ss, red) / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int e = 0; e < kNormPer; ++e) {
+      const int i = threadIdx.x + e * blockDim.x;
+      if (i < n) {
+        const float y = round_to_bf16(wv[e] * (xv[e] * r));
+        out[i] = float_to_bf16_bits(residual != nullptr ? rv[e] + y : y);
+      }
+    }
+    return;
+  }
   float ss = 0.f;
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const float v = ld_bf16(x, i);
@@ -293,34 +511,102 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
   return ia < ib;
 }
 
-__global__ __launch_bounds__(kBlock) void argmax_next_kernel(const uint16_t* __restrict__ logits, int V,
-                                                             int64_t* __restrict__ tok, int64_t* __restrict__ pos) {
-  __shared__ float bv[kBlock];
-  __shared__ int bi[kBlock];
-  float best = -INFINITY;
-  int idx = 0x7fffffff;
-  for (int i = threadIdx.x; i < V; i += blockDim.x) {
-    const float v = ld_bf16(logits, i);
-    if (better(v, i, best, idx)) {
-      best = v;
-      idx = i;
-    }
-  }
-  bv[threadIdx.x] = best;
-  bi[threadIdx.x] = idx;
-  __syncthreads();
-  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
-    if (threadIdx.x < o && better(bv[threadIdx.x + o], bi[threadIdx.x + o], bv[threadIdx.x], bi[threadIdx.x])) {
-      bv[threadIdx.x] = bv[threadIdx.x + o];
-      bi[threadIdx.x] = bi[threadIdx.x + o];
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    *tok = bi[0] == 0x7fffffff ? 0 : bi[0];
-    *pos += 1;
+constexpr int kArgmaxBlocks = 64;    // workgroups of argmax_next
+constexpr int kArgmaxThreads = 256;  // threads per workgroup
+
+// (best value, index) of this thread folded with (v, i).
+__device__ __forceinline__ void take(float& best, int& idx, float v, int i) {
+  if (better(v, i, best, idx)) {
+    best = v;
+    idx = i;
   }
 }
+
+// Wave-wide fold of (best, idx): every lane ends with the wave's result.
+__device__ __forceinline__ void wave_take(float& best, int& idx) {
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o);
+    const int oi = __shfl_xor(idx, o);
+    take(best, idx, ov, oi);
+  }
+}
+
+// kArgmaxBlocks workgroups, each over an even share of the logits (vec: 16-byte aligned logits, 8 per load; the
+// V % 8 tail and, when not vec, every element one at a time); each writes its (value, index) to the scratch, and
+// the last workgroup to finish (a ticket counter, reset by that workgroup) folds them, writes the token and
+// advances the position. better() is a total order, so the result does not depend on the split. Scratch: values
+// [kArgmaxBlocks] float, indices [kArgmaxBlocks] int, then the counter (zero before the first launch).
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint16_t* __restrict__ logits, int V,
+                                                                     int vec, int64_t* __restrict__ tok,
+                                                                     int64_t* __restrict__ pos,
+                                                                     uint32_t* __restrict__ scratch) {
+  __shared__ float bv[kArgmaxThreads / kWave];
+  __shared__ int bi[kArgmaxThreads / kWave];
+  __shared__ uint32_t ticket;
+  float* part_v = reinterpret_cast<float*>(scratch);
+  int* part_i = reinterpret_cast<int*>(scratch + kArgmaxBlocks);
+  uint32_t* counter = scratch + 2 * kArgmaxBlocks;
+  const int b = blockIdx.x, G = gridDim.x;
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  const int nvec = vec ? V / 8 : 0;
+  const int c_lo = static_cast<int>(static_cast<int64_t>(nvec) * b / G);
+  const int c_hi = static_cast<int>(static_cast<int64_t>(nvec) * (b + 1) / G);
+  for (int c0 = c_lo + static_cast<int>(threadIdx.x); c0 < c_hi; c0 += 4 * blockDim.x) {
+    u32x4 w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + u * static_cast<int>(blockDim.x);
+      w[u] = u32x4{0u, 0u, 0u, 0u};
+      if (c < c_hi) w[u] = *reinterpret_cast<const u32x4*>(logits + 8 * static_cast<int64_t>(c));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + u * static_cast<int>(blockDim.x);
+      if (c < c_hi) {
+        const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          take(best, idx, bf16_bits_to_float(wd[e] & 0xffffu), 8 * c + 2 * e);
+          take(best, idx, bf16_bits_to_float(wd[e] >> 16), 8 * c + 2 * e + 1);
+        }
+      }
+    }
+  }
+  // elements past the vectors: an even share per workgroup
+  const int rest = V - 8 * nvec;
+  const int e_lo = 8 * nvec + static_cast<int>(static_cast<int64_t>(rest) * b / G);
+  const int e_hi = 8 * nvec + static_cast<int>(static_cast<int64_t>(rest) * (b + 1) / G);
+  for (int i = e_lo + static_cast<int>(threadIdx.x); i < e_hi; i += blockDim.x) take(best, idx, ld_bf16(logits, i), i);
+  wave_take(best, idx);
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) {
+    bv[wave] = best;
+    bi[wave] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 0; w < static_cast<int>(blockDim.x / kWave); ++w) take(best, idx, bv[w], bi[w]);
+    part_v[b] = best;
+    part_i[b] = idx;
+    __threadfence();  // the partial is visible device-wide before the ticket is taken
+    ticket = atomicAdd(counter, 1u);
+  }
+  __syncthreads();
+  if (ticket != static_cast<uint32_t>(G - 1) || threadIdx.x >= kWave) return;
+  __threadfence();  // every other workgroup's partial is visible to the loads below
+  best = -INFINITY;
+  idx = 0x7fffffff;
+  for (int k = threadIdx.x; k < G; k += kWave) take(best, idx, part_v[k], part_i[k]);
+  wave_take(best, idx);
+  if (threadIdx.x == 0) {
+    *tok = idx == 0x7fffffff ? 0 : idx;
+    *pos += 1;
+    *counter = 0u;  // ready for the next launch
+  }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 int status() {
   const hipError_t e = hipGetLastError();
@@ -361,9 +647,17 @@ int bp_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256 || bp::kAttnThreads % head_dim != 0 ||
       max_len > bp::kAttnMaxLen)
     return BP_E_UNSUPPORTED;
-  bp::attention_kernel<<<heads, bp::kAttnThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_cache), static_cast<const uint16_t*>(v_cache),
-      pos, static_cast<uint16_t*>(out), head_dim, max_len, scale);
+  if (!bp::aligned16(k_cache) || !bp::aligned16(v_cache)) return BP_E_INVALID_ARG;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (head_dim / 8) {
+    case 1: bp::launch_attention<1>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
+    case 2: bp::launch_attention<2>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
+    case 4: bp::launch_attention<4>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
+    case 8: bp::launch_attention<8>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
+    case 16: bp::launch_attention<16>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
+    case 32: bp::launch_attention<32>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
+    default: return BP_E_UNSUPPORTED;
+  }
   return bp::status();
 }
 
@@ -376,10 +670,21 @@ int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* 
   if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256 || bp::kAttnThreads % head_dim != 0 ||
       max_len > bp::kAttnMaxLen)
     return BP_E_UNSUPPORTED;
-  bp::rope_attention_kernel<<<heads, bp::kAttnThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(q_norm_w),
-      static_cast<const uint16_t*>(k_norm_w), inv_freq, pos, static_cast<uint16_t*>(k_cache),
-      static_cast<uint16_t*>(v_cache), static_cast<uint16_t*>(out), heads, head_dim, max_len, eps, scale);
+  if (!bp::aligned16(qkv) || !bp::aligned16(k_cache) || !bp::aligned16(v_cache)) return BP_E_INVALID_ARG;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define BP_ROPE_ATT(L)                                                                                           \
+  bp::launch_rope_attention<L>(qkv, q_norm_w, k_norm_w, inv_freq, pos, k_cache, v_cache, out, heads, max_len, eps, \
+                               scale, st)
+  switch (head_dim / 8) {
+    case 1: BP_ROPE_ATT(1); break;
+    case 2: BP_ROPE_ATT(2); break;
+    case 4: BP_ROPE_ATT(4); break;
+    case 8: BP_ROPE_ATT(8); break;
+    case 16: BP_ROPE_ATT(16); break;
+    case 32: BP_ROPE_ATT(32); break;
+    default: return BP_E_UNSUPPORTED;
+  }
+#undef BP_ROPE_ATT
   return bp::status();
 }
 
@@ -400,10 +705,14 @@ int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream) {
   return bp::status();
 }
 
-int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* stream) {
-  if (logits == nullptr || tok == nullptr || pos == nullptr || vocab <= 0) return BP_E_INVALID_ARG;
-  bp::argmax_next_kernel<<<1, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(logits), vocab, tok, pos);
+size_t bp_decode_argmax_scratch_bytes(void) { return (2 * bp::kArgmaxBlocks + 1) * sizeof(uint32_t); }
+
+int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream) {
+  if (logits == nullptr || tok == nullptr || pos == nullptr || scratch == nullptr || vocab <= 0)
+    return BP_E_INVALID_ARG;
+  bp::argmax_next_kernel<<<bp::kArgmaxBlocks, bp::kArgmaxThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(logits), vocab, bp::aligned16(logits) ? 1 : 0, tok, pos,
+      static_cast<uint32_t*>(scratch));
   return bp::status();
 }
 

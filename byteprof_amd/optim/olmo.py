@@ -125,6 +125,8 @@ class OlmoDecoder:
         self.tok, self.pos = z(1, dtype=torch.int64), z(1, dtype=torch.int64)
         self.x, self.xn, self.attn, self.o, self.dn = z(1, H), z(1, H), z(1, H), z(1, H), z(1, H)
         self.qkv, self.gu, self.act, self.logits = z(1, 3 * H), z(1, 2 * F), z(1, F), z(1, V)
+        # the argmax's partials and counter: zeroed once, left at zero by every launch
+        self.argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_scratch_bytes() // 4), dtype=torch.int32)
         self.k_cache = z(cfg.layers, cfg.heads, cfg.max_len, D)
         self.v_cache = z(cfg.layers, cfg.heads, cfg.max_len, D)
 
@@ -158,8 +160,8 @@ class OlmoDecoder:
         c(L.bp_decode_norm_residual(self.x.data_ptr(), self.norm.data_ptr(), None, self.xn.data_ptr(), H, cfg.eps,
                                     st), "bp_decode_norm_residual")
         self._mm(self.xn, self.lm_head, self.logits)
-        c(L.bp_decode_argmax_next(self.logits.data_ptr(), cfg.vocab, self.tok.data_ptr(), self.pos.data_ptr(), st),
-          "bp_decode_argmax_next")
+        c(L.bp_decode_argmax_next(self.logits.data_ptr(), cfg.vocab, self.tok.data_ptr(), self.pos.data_ptr(),
+                                  self.argmax_scratch.data_ptr(), st), "bp_decode_argmax_next")
 
     def weight_bytes(self) -> int:
         """Bytes of the linears' weights (and scales) a step streams."""

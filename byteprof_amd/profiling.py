@@ -5,6 +5,8 @@
                                                                          the set as one persistent launch, R launches
   python -m byteprof_amd.profiling group [--kind bf16|int8] [--replays R]
                                                                          the set as one grouped launch, R launches
+  python -m byteprof_amd.profiling decode [--kind bf16|int8] [--tokens N]  the graph-captured greedy decode loop
+                                                                         of the OLMo-2-1B shape, 8 prompt + N tokens
   python -m byteprof_amd.profiling skinny [--kind bf16|int8] [--n N] [--k K] [--m M] [--replays R]
                                                                          skinny_mm over a ring of distinct weights
   python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
@@ -136,7 +138,7 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=("set", "chain", "group", "skinny", "copy", "summarize"))
+    ap.add_argument("what", choices=("set", "chain", "group", "decode", "skinny", "copy", "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
     ap.add_argument("--write", help="summarize: WRITE_SIZE database of the workload")
@@ -155,6 +157,7 @@ def main(argv=None) -> int:
     ap.add_argument("--n", type=int, default=100352, help="skinny: output rows")
     ap.add_argument("--k", type=int, default=2048, help="skinny: input length")
     ap.add_argument("--m", type=int, default=16, help="skinny: activation rows")
+    ap.add_argument("--tokens", type=int, default=128, help="decode: new tokens")
     ap.add_argument("--mib", type=int, default=256)
     ap.add_argument("--reps", type=int, default=5)
     a = ap.parse_args(argv)
@@ -203,6 +206,16 @@ def main(argv=None) -> int:
             return 1
         print(f"ran the {a.kind} decode-step set as one persistent launch {a.replays} times "
               f"({len(ch.stages)} stages, {'dependent' if a.dependent else 'independent'})", flush=True)
+        return 0
+    if a.what == "decode":
+        from .optim import olmo as OG
+
+        dec = OG.OlmoDecoder(OG.OLMO2_1B, OG.random_weights(OG.OLMO2_1B, device, seed=4), a.kind)
+        generate = OG.make_generate_graph(dec)
+        prompt = torch.tensor([[11, 2027, 5, 99999, 42, 3, 3, 1000]])
+        out = generate(prompt, max_new_tokens=a.tokens)
+        torch.cuda.synchronize()
+        print(f"decoded {out.shape[1] - prompt.shape[1]} tokens ({a.kind}, graph loop)", flush=True)
         return 0
     if a.what == "group":
         ops = D.build(a.kind, 1, device)

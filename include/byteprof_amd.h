@@ -202,13 +202,17 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  *                 weights, rotated by RoPE at *pos (inv_freq[head_dim / 2] fp32, cos / sin in fp32); q -> q_out;
  *                 k, v -> k_cache, v_cache [heads, max_len, head_dim] at row *pos (no write if *pos >= max_len).
  * attention:      per head, positions 0 .. *pos: out = bf16(softmax_fp32(bf16(bf16(q . k) * scale)) as bf16 . v);
- *                 head_dim a multiple of 8 dividing 256, max_len <= 4096.
+ *                 head_dim a multiple of 8 dividing 256, max_len <= 4096; caches 16-byte aligned.
  * rope_attention: qk_rope_cache and attention in one launch (one workgroup per head; the q / k norms summed in
- *                 another order, so a value may differ by one bf16 step from the two-launch path).
+ *                 another order, so a value may differ by one bf16 step from the two-launch path); qkv 16-byte
+ *                 aligned.
  * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
  *                 out may alias residual.
  * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn).
- * argmax_next:    *tok = first index of the largest logit (NaN counts as largest); *pos += 1.
+ * argmax_next:    *tok = first index of the largest logit (NaN counts as largest); *pos += 1. Several workgroups
+ *                 share the logits and the last to finish writes the result; `scratch` holds their partials and
+ *                 a counter: bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is
+ *                 (each call leaves the counter at zero); calls sharing one scratch must not overlap.
  */
 int bp_decode_embed(const int64_t* tok, const void* table, void* x, int hidden, int64_t vocab, void* stream);
 int bp_decode_qk_rope_cache(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
@@ -222,7 +226,8 @@ int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* 
 int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
                             void* stream);
 int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream);
-int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* stream);
+size_t bp_decode_argmax_scratch_bytes(void);
+int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream);
 
 /*
  * Decode-step linear set: a chain of skinny linears at one activation row run by one persistent launch.

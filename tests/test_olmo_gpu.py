@@ -51,7 +51,7 @@ def _ocfg(cfg: OG.OlmoConfig) -> OO.Config:
 def test_norm_residual_matches_the_oracle():
     rng = np.random.default_rng(0)
     L = _lib.lib()
-    for n in (256, 2048, 3000):
+    for n in (256, 2048, 3000, 8192, 10000):  # registers up to 8192, two passes above
         print(f"\n[olmo] norm n={n}", flush=True)
         x, w, r = (ON.bf16_round(rng.standard_normal(n).astype(np.float32) * s) for s in (3.0, 1.0, 2.0))
         tx, tw, tr = _bf16(x), _bf16(w), _bf16(r)
@@ -93,9 +93,18 @@ def test_qk_rope_cache_matches_the_oracle_and_writes_one_cache_row(pos):
     assert (kcn[:, others] == 7.0).all() and (vcn[:, others] == 7.0).all()
 
 
-@pytest.mark.parametrize("pos", [0, 1, 37, 63])
-def test_attention_matches_the_oracle(pos):
-    cfg = SMALL
+# Head dims at both ends of the kernels' range (one to 32 lanes per cache row), and positions that take several row
+# batches (up to the longest cache, 4096).
+ATTN_CFGS = {"d64": SMALL,
+             "d256": OG.OlmoConfig(hidden=512, ffn=512, layers=1, heads=2, vocab=512, max_len=300),
+             "d8": OG.OlmoConfig(hidden=64, ffn=512, layers=1, heads=8, vocab=512, max_len=600),
+             "d128": OG.OlmoConfig(hidden=512, ffn=512, layers=1, heads=4, vocab=512, max_len=4096)}
+
+
+@pytest.mark.parametrize("shape,pos", [("d64", 0), ("d64", 1), ("d64", 37), ("d64", 63), ("d256", 299),
+                                       ("d8", 599), ("d128", 130), ("d128", 4095)])
+def test_attention_matches_the_oracle(shape, pos):
+    cfg = ATTN_CFGS[shape]
     oc = _ocfg(cfg)
     D = cfg.head_dim
     rng = np.random.default_rng(100 + pos)
@@ -115,10 +124,11 @@ def test_attention_matches_the_oracle(pos):
         np.testing.assert_array_equal(got, vc[:, 0].reshape(-1))  # one position: the softmax is exactly 1
 
 
-@pytest.mark.parametrize("pos", [0, 9, 63])
-def test_fused_rope_attention_matches_the_oracle(pos):
+@pytest.mark.parametrize("shape,pos", [("d64", 0), ("d64", 9), ("d64", 63), ("d256", 299), ("d8", 599),
+                                       ("d128", 4095)])
+def test_fused_rope_attention_matches_the_oracle(shape, pos):
     """The decode loop's launch: q / k norm + RoPE + cache write + attention for every head at once."""
-    cfg = SMALL
+    cfg = ATTN_CFGS[shape]
     oc = _ocfg(cfg)
     H, D = cfg.hidden, cfg.head_dim
     rng = np.random.default_rng(200 + pos)
@@ -160,6 +170,7 @@ def test_silu_mul_matches_the_oracle():
 def test_argmax_next_takes_the_first_maximum_and_advances_the_position():
     L = _lib.lib()
     st = _lib.stream_ptr(torch.device(DEV))
+    scratch = torch.zeros(-(-L.bp_decode_argmax_scratch_bytes() // 4), dtype=torch.int32, device=DEV)
     for V, setup, want in ((100352, {5: 3.0, 70000: 3.0}, 5), (1000, {999: 1.0}, 999), (7, {}, 0),
                            (4096, {10: 2.0, 3000: float("nan")}, 3000)):
         lg = torch.zeros(V, dtype=torch.bfloat16, device=DEV) - 1.0
@@ -167,8 +178,45 @@ def test_argmax_next_takes_the_first_maximum_and_advances_the_position():
             lg[i] = v
         tok = torch.tensor([-1], dtype=torch.int64, device=DEV)
         pos = torch.tensor([41], dtype=torch.int64, device=DEV)
-        _lib.check(L.bp_decode_argmax_next(lg.data_ptr(), V, tok.data_ptr(), pos.data_ptr(), st), "argmax")
+        _lib.check(L.bp_decode_argmax_next(lg.data_ptr(), V, tok.data_ptr(), pos.data_ptr(), scratch.data_ptr(), st),
+                   "argmax")
         assert int(tok) == want and int(pos) == 42
+        assert int(scratch[-1]) == 0  # the ticket counter is back at zero for the next call
+
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+def test_argmax_next_matches_numpy_on_vector_and_tail_elements(offset):
+    """16-byte reads plus the one-at-a-time tail (V not a multiple of 8), and an unaligned buffer (offset 1: every
+    element one at a time): the first index of the maximum, NaN counted as largest, -inf everywhere -> 0."""
+    L = _lib.lib()
+    st = _lib.stream_ptr(torch.device(DEV))
+    scratch = torch.zeros(-(-L.bp_decode_argmax_scratch_bytes() // 4), dtype=torch.int32, device=DEV)
+    rng = np.random.default_rng(5)
+    V = 100351
+    cases = [rng.standard_normal(V).astype(np.float32)]
+    tie = np.full(V, -2.0, np.float32)
+    tie[[3, V - 1]] = 4.0  # a vector element and a tail element tie: the first wins
+    cases.append(tie)
+    tail = np.full(V, -2.0, np.float32)
+    tail[V - 2] = 1.0  # the maximum only in the tail
+    cases.append(tail)
+    nan = rng.standard_normal(V).astype(np.float32)
+    nan[[777, V - 3]] = np.nan
+    cases.append(nan)
+    cases.append(np.full(V, -np.inf, np.float32))
+    for c in cases:
+        c = ON.bf16_round(c)
+        buf = torch.zeros(V + 8, dtype=torch.bfloat16, device=DEV)
+        lg = buf[offset:offset + V]
+        lg.copy_(_bf16(c))
+        tok = torch.tensor([-1], dtype=torch.int64, device=DEV)
+        pos = torch.tensor([0], dtype=torch.int64, device=DEV)
+        _lib.check(L.bp_decode_argmax_next(lg.data_ptr(), V, tok.data_ptr(), pos.data_ptr(), scratch.data_ptr(), st),
+                   "argmax")
+        want = int(np.argmax(c)) if not np.isnan(c).any() else int(np.flatnonzero(np.isnan(c))[0])
+        assert int(tok) == want and int(pos) == 1
+        assert int(scratch[-1]) == 0
 
 
 def _deq(args: tuple) -> np.ndarray:
