@@ -276,9 +276,10 @@ def decode_loop(device, new_tokens: int = 128) -> dict:
     cfg = OG.OLMO2_1B
     prompt = torch.tensor([[11, 2027, 5, 99999, 42, 3, 3, 1000]])
     out = {"model": "OLMo-2-1B shape (16 x 2048, FFN 8192, 16 heads, vocab 100352), synthetic weights",
-           "prompt_tokens": prompt.shape[1], "new_tokens": new_tokens, "launches_per_step": 4 + 8 * cfg.layers}
+           "prompt_tokens": prompt.shape[1], "new_tokens": new_tokens}
     for kind in ("bf16", "int8"):
         dec = OG.OlmoDecoder(cfg, OG.random_weights(cfg, device, seed=4), kind)
+        out["launches_per_step"] = dec.launches_per_step
         graph = OG.make_generate_graph(dec)
         graph(prompt, max_new_tokens=4)  # captures the step
         torch.cuda.synchronize()

@@ -65,6 +65,7 @@ SIGNATURES: dict[str, tuple] = {
     "bp_decode_norm_residual": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_float, _c_vp]),
     "bp_decode_silu_mul": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp]),
     "bp_decode_argmax_scratch_bytes": (_c_size, []),
+    "bp_decode_gate_up_silu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
     "bp_decode_argmax_next": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp]),
     "bp_linear_set_scratch_bytes": (_c_size, [_c_vp, _c_int, _c_int]),
     "bp_linear_set_workgroups": (_c_int, [_c_int]),

@@ -1,4 +1,4 @@
-"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 132
+"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 116
 launches for the 16-layer model) captured in one HIP graph, greedy generation with one replay, one pinned
 device-to-host read and one event synchronize per token.
 
@@ -12,6 +12,9 @@ followed by the new tokens, [1, L + n].
 The model is the OLMo-2 architecture with synthetic weights (the checkpoint is not available here): an
 `OlmoDecoder` holds the weights of transformers' Olmo2ForCausalLM layout with q|k|v and gate|up fused into one
 linear each (one launch instead of three or two; the outputs are the same rows), bf16 or int8 (per-row scales).
+The gate and up rows are interleaved (row 2n gate n, row 2n + 1 up n) so that one launch computes the projection
+and the SiLU product (bp_decode_gate_up_silu), where the hidden size is a multiple of the kernels' 1 KiB chunk;
+otherwise gate|up is one skinny launch followed by silu_mul.
 The prompt is fed one position at a time through the same step (the reference prefills with one batched
 forward; the cache contents and the first new token are the same up to rounding).
 """
@@ -28,6 +31,8 @@ from ..quant.hip_int8 import quantize_rowwise_int8
 from . import skinny as S
 
 MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
+GATE_UP_WAVES = {"bf16": 4, "int8": 2}  # waves per workgroup of the fused gate|up + SiLU launch
+_CHUNK = {"bf16": 512, "int8": 1024}  # K granularity of the skinny kernels' 16-byte loads
 
 
 class OptimizeError(RuntimeError):
@@ -105,6 +110,12 @@ class OlmoDecoder:
             return (w,) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
 
         bf = torch.bfloat16
+        # one launch for gate|up and the SiLU product where the hidden size allows it (rows interleaved)
+        self.gate_up_interleaved = H % _CHUNK[kind] == 0
+
+        def gate_up(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+            return torch.stack([g, u], dim=1).reshape(2 * F, H) if self.gate_up_interleaved else torch.cat([g, u])
+
         self.embed = weights["embed"].to(bf).contiguous()
         self.norm = weights["norm"].to(bf).contiguous()
         self.lm_head = lin(weights["lm_head"])
@@ -114,7 +125,7 @@ class OlmoDecoder:
             self.layers.append({
                 "qkv": lin(torch.cat([weights[p + "q"], weights[p + "k"], weights[p + "v"]])),
                 "o": lin(weights[p + "o"]),
-                "gate_up": lin(torch.cat([weights[p + "gate"], weights[p + "up"]])),
+                "gate_up": lin(gate_up(weights[p + "gate"], weights[p + "up"])),
                 "down": lin(weights[p + "down"]),
                 **{n: weights[p + n].to(bf).contiguous() for n in ("q_norm", "k_norm", "post_attn", "post_ff")},
             })
@@ -152,8 +163,15 @@ class OlmoDecoder:
             self._mm(self.attn, w["o"], self.o)
             c(L.bp_decode_norm_residual(self.o.data_ptr(), w["post_attn"].data_ptr(), self.x.data_ptr(),
                                         self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")
-            self._mm(self.x, w["gate_up"], self.gu)
-            c(L.bp_decode_silu_mul(self.gu.data_ptr(), self.act.data_ptr(), cfg.ffn, st), "bp_decode_silu_mul")
+            if self.gate_up_interleaved:
+                gw = w["gate_up"]
+                sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
+                c(L.bp_decode_gate_up_silu(0 if self.kind == "bf16" else 1, self.x.data_ptr(), gw[0].data_ptr(), sc,
+                                           sdt, self.act.data_ptr(), cfg.ffn, H, GATE_UP_WAVES[self.kind], st),
+                  "bp_decode_gate_up_silu")
+            else:
+                self._mm(self.x, w["gate_up"], self.gu)
+                c(L.bp_decode_silu_mul(self.gu.data_ptr(), self.act.data_ptr(), cfg.ffn, st), "bp_decode_silu_mul")
             self._mm(self.act, w["down"], self.dn)
             c(L.bp_decode_norm_residual(self.dn.data_ptr(), w["post_ff"].data_ptr(), self.x.data_ptr(),
                                         self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")
@@ -162,6 +180,11 @@ class OlmoDecoder:
         self._mm(self.xn, self.lm_head, self.logits)
         c(L.bp_decode_argmax_next(self.logits.data_ptr(), cfg.vocab, self.tok.data_ptr(), self.pos.data_ptr(),
                                   self.argmax_scratch.data_ptr(), st), "bp_decode_argmax_next")
+
+    @property
+    def launches_per_step(self) -> int:
+        """Kernel launches of one step: embed, 7 or 8 per layer, final norm, LM head, argmax."""
+        return 4 + (7 if self.gate_up_interleaved else 8) * self.cfg.layers
 
     def weight_bytes(self) -> int:
         """Bytes of the linears' weights (and scales) a step streams."""

@@ -209,6 +209,11 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
  *                 out may alias residual.
  * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn).
+ * gate_up_silu:   the gate|up projection of x[hidden] and silu_mul in one launch: w [2 * ffn, hidden] (wkind
+ *                 BP_DT_BF16 (0) bf16 or 1 int8 with per-row scale [2 * ffn] of scale_dtype) with row 2n the gate
+ *                 row n and row 2n + 1 the up row n; out[ffn] equal bit for bit to bp_skinny_* on w with 2 rows and
+ *                 `waves` per workgroup (split 1) followed by silu_mul; hidden a multiple of 512 (bf16) / 1024
+ *                 (int8); x, w 16-byte aligned; waves 1, 2, 4 or 8.
  * argmax_next:    *tok = first index of the largest logit (NaN counts as largest); *pos += 1. Several workgroups
  *                 share the logits and the last to finish writes the result; `scratch` holds their partials and
  *                 a counter: bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is
@@ -226,6 +231,8 @@ int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* 
 int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
                             void* stream);
 int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream);
+int bp_decode_gate_up_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
+                           int ffn, int hidden, int waves, void* stream);
 size_t bp_decode_argmax_scratch_bytes(void);
 int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream);
 

@@ -17,6 +17,8 @@ import torch
 
 from byteprof_amd import _lib
 from byteprof_amd.optim import olmo as OG
+from byteprof_amd.optim.skinny import skinny_mm
+from byteprof_amd.quant.hip_int8 import quantize_rowwise_int8
 from oracle import numerics as ON
 from oracle import olmo as OO
 
@@ -157,6 +159,39 @@ def test_fused_rope_attention_matches_the_oracle(shape, pos):
     assert ON.normwise_error(_np(out), OO.attention(q, kc, vc, pos, oc)) < 1e-2
 
 
+@pytest.mark.parametrize("waves", [1, 2, 4, 8])
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_gate_up_silu_equals_the_two_launch_path(kind, waves):
+    """The fused gate|up + SiLU launch against skinny_mm on the same interleaved weight (2 rows, same waves, split 1)
+    followed by silu_mul on the de-interleaved halves: equal bit for bit; and within one bf16 step of the oracle."""
+    L = _lib.lib()
+    F, H = 3000, 2048
+    rng = np.random.default_rng(7 + waves)
+    x = _bf16(ON.bf16_round(rng.standard_normal(H).astype(np.float32)))
+    w = _bf16(ON.bf16_round(rng.standard_normal((2 * F, H)).astype(np.float32) * 0.05))
+    if kind == "bf16":
+        args, sc, sdt = (w,), None, 0
+    else:
+        args = quantize_rowwise_int8(w, torch.float16)
+        sc, sdt = args[1].data_ptr(), _lib.TORCH_DT[torch.float16]
+    out = torch.empty(F, dtype=torch.bfloat16, device=DEV)
+    st = _lib.stream_ptr(out.device)
+    _lib.check(L.bp_decode_gate_up_silu(0 if kind == "bf16" else 1, x.data_ptr(), args[0].data_ptr(), sc, sdt,
+                                        out.data_ptr(), F, H, waves, st), "gate_up_silu")
+    y = skinny_mm(x[None], *args, cfg=(2, waves, 1))[0]
+    gu = torch.cat([y[0::2], y[1::2]]).contiguous()
+    ref = torch.empty(F, dtype=torch.bfloat16, device=DEV)
+    _lib.check(L.bp_decode_silu_mul(gu.data_ptr(), ref.data_ptr(), F, st), "silu_mul")
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    g, u = _np(y[0::2]), _np(y[1::2])
+    assert _ulps(_np(out), OO.silu_mul(g, u)).max() <= 1
+    bad = torch.empty(F, dtype=torch.bfloat16, device=DEV)
+    assert L.bp_decode_gate_up_silu(0, x.data_ptr(), w.data_ptr(), None, 0, bad.data_ptr(), F, 1000, 4, st) == -2
+    assert L.bp_decode_gate_up_silu(0, x.data_ptr(), w.data_ptr(), None, 0, bad.data_ptr(), F, H, 3, st) == -2
+    assert L.bp_decode_gate_up_silu(1, x.data_ptr(), args[0].data_ptr(), None, 1, bad.data_ptr(), F, H, 2, st) == -1
+
+
 def test_silu_mul_matches_the_oracle():
     rng = np.random.default_rng(3)
     F = 5000
@@ -225,8 +260,11 @@ def _deq(args: tuple) -> np.ndarray:
     return q.float().cpu().numpy() * scale.float().cpu().numpy()[:, None]
 
 
-def _small_decoder(kind: str, seed: int = 1):
-    cfg = SMALL
+# hidden a multiple of 1024: the decoder takes the fused gate|up + SiLU launch (bf16 and int8)
+FUSED_SMALL = OG.OlmoConfig(hidden=1024, ffn=1024, layers=2, heads=8, vocab=512, max_len=64)
+
+
+def _small_decoder(kind: str, seed: int = 1, cfg: OG.OlmoConfig = SMALL):
     oc = _ocfg(cfg)
     W = OO.random_weights(oc, seed=seed, std=2.0 / np.sqrt(cfg.hidden))
     dec = OG.OlmoDecoder(cfg, {k: _bf16(v) for k, v in W.items()}, kind)
@@ -237,16 +275,21 @@ def _small_decoder(kind: str, seed: int = 1):
             H = cfg.hidden
             W[p + "q"], W[p + "k"], W[p + "v"] = qkv[:H], qkv[H:2 * H], qkv[2 * H:]
             gu = _deq(lw["gate_up"])
-            W[p + "gate"], W[p + "up"] = gu[:cfg.ffn], gu[cfg.ffn:]
+            if dec.gate_up_interleaved:
+                W[p + "gate"], W[p + "up"] = gu[0::2], gu[1::2]
+            else:
+                W[p + "gate"], W[p + "up"] = gu[:cfg.ffn], gu[cfg.ffn:]
             W[p + "o"] = _deq(lw["o"])
             W[p + "down"] = _deq(lw["down"])
         W["lm_head"] = _deq(dec.lm_head)
     return dec, W, oc
 
 
+@pytest.mark.parametrize("shape", ["small", "fused"])
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
-def test_decode_steps_match_the_oracle(kind):
-    dec, W, oc = _small_decoder(kind)
+def test_decode_steps_match_the_oracle(kind, shape):
+    dec, W, oc = _small_decoder(kind, cfg=SMALL if shape == "small" else FUSED_SMALL)
+    assert dec.gate_up_interleaved == (shape == "fused")
     prompt = [3, 17, 99, 250, 7]
     toks, logits = OO.greedy(W, oc, prompt, 10)
     feed = prompt + toks[:-1]
