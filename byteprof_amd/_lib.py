@@ -67,6 +67,16 @@ SIGNATURES: dict[str, tuple] = {
     "bp_decode_argmax_scratch_bytes": (_c_size, []),
     "bp_decode_gate_up_silu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
     "bp_decode_argmax_next": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp]),
+    "bp_decode_embed_rows": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_i64, _c_vp]),
+    "bp_decode_qk_rope_cache_rows": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int,
+                                              _c_int, _c_float, _c_int, _c_vp]),
+    "bp_decode_attention_rows": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_float, _c_int,
+                                          _c_vp]),
+    "bp_decode_norm_residual_rows": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_float, _c_int, _c_vp]),
+    "bp_decode_silu_mul_rows": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
+    "bp_decode_argmax_rows_scratch_bytes": (_c_size, [_c_int]),
+    "bp_decode_argmax_rows": (_c_int, [_c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "bp_draft_verify_next": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
     "bp_linear_set_scratch_bytes": (_c_size, [_c_vp, _c_int, _c_int]),
     "bp_linear_set_workgroups": (_c_int, [_c_int]),
     "bp_linear_set_validate": (_c_int, [_c_vp, _c_int, _c_int, _c_int]),

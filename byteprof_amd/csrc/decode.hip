@@ -54,60 +54,16 @@ __device__ float block_max(float v, float* red) {
 
 __device__ __forceinline__ float ld_bf16(const uint16_t* p, int64_t i) { return bf16_bits_to_float(p[i]); }
 
+// grid = rows: x[r] <- table[tok[r]].
 __global__ __launch_bounds__(kBlock) void embed_kernel(const int64_t* __restrict__ tok,
                                                        const uint16_t* __restrict__ table,
                                                        uint16_t* __restrict__ x, int H, int64_t V) {
-  int64_t t = *tok;
+  int64_t t = tok[blockIdx.x];
   t = t < 0 ? 0 : (t >= V ? V - 1 : t);  // ids are validated on the host; the clamp keeps the read in bounds
-  for (int i = threadIdx.x; i < H; i += blockDim.x) x[i] = table[t * H + i];
+  uint16_t* xr = x + static_cast<int64_t>(blockIdx.x) * H;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) xr[i] = table[t * H + i];
 }
 
-// One workgroup; thread t owns the RoPE pairs (h, j), (h, j + D/2) of q and of k for pair index i = t, t + block..
-__global__ __launch_bounds__(kBlock) void qk_rope_cache_kernel(const uint16_t* __restrict__ qkv,
-                                                               const uint16_t* __restrict__ qw,
-                                                               const uint16_t* __restrict__ kw,
-                                                               const float* __restrict__ inv_freq,
-                                                               const int64_t* __restrict__ pos_p,
-                                                               uint16_t* __restrict__ q_out,
-                                                               uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-                                                               int heads, int D, int max_len, float eps) {
-  __shared__ float red[kBlock / kWave];
-  const int H = heads * D, half = D / 2;
-  const int64_t pos = *pos_p;
-  const bool in_cache = pos >= 0 && pos < max_len;
-  const uint16_t* q = qkv;
-  const uint16_t* k = qkv + H;
-  const uint16_t* v = qkv + 2 * H;
-  float sq = 0.f, sk = 0.f;
-  for (int i = threadIdx.x; i < H / 2; i += blockDim.x) {
-    const int h = i / half, j = i % half;
-    const float qa = ld_bf16(q, h * D + j), qb = ld_bf16(q, h * D + j + half);
-    const float ka = ld_bf16(k, h * D + j), kb = ld_bf16(k, h * D + j + half);
-    sq += qa * qa + qb * qb;
-    sk += ka * ka + kb * kb;
-  }
-  const float rq = 1.f / sqrtf(block_sum(sq, red) / static_cast<float>(H) + eps);
-  const float rk = 1.f / sqrtf(block_sum(sk, red) / static_cast<float>(H) + eps);
-  for (int i = threadIdx.x; i < H / 2; i += blockDim.x) {
-    const int h = i / half, j = i % half;
-    const int a = h * D + j, b = a + half;
-    const float f = inv_freq[j] * static_cast<float>(pos);
-    const float c = cosf(f), s = sinf(f);
-    const float qa = round_to_bf16(ld_bf16(qw, a) * (ld_bf16(q, a) * rq));
-    const float qb = round_to_bf16(ld_bf16(qw, b) * (ld_bf16(q, b) * rq));
-    const float ka = round_to_bf16(ld_bf16(kw, a) * (ld_bf16(k, a) * rk));
-    const float kb = round_to_bf16(ld_bf16(kw, b) * (ld_bf16(k, b) * rk));
-    q_out[a] = float_to_bf16_bits(qa * c + (-qb) * s);
-    q_out[b] = float_to_bf16_bits(qb * c + qa * s);
-    if (in_cache) {
-      const int64_t row = (static_cast<int64_t>(h) * max_len + pos) * D;
-      kc[row + j] = float_to_bf16_bits(ka * c + (-kb) * s);
-      kc[row + j + half] = float_to_bf16_bits(kb * c + ka * s);
-      vc[row + j] = v[a];
-      vc[row + j + half] = v[b];
-    }
-  }
-}
 
 constexpr int kAttnUnroll = 4;  // row batches whose loads are in flight together
 
@@ -291,7 +247,107 @@ struct HeadAttention {
 
 constexpr int kAttnPart = kAttnWaves * 256;  // floats of the value partials: waves x D (D <= 256)
 
-// grid = heads; positions 0 .. pos of the head's cache rows [max_len, D], D = 8 * LPR.
+// 1 / rms of q[0 .. H) and of k[0 .. H) (+ eps inside the root), by a kAttnThreads-thread workgroup: thread t sums
+// the squares of elements 8t .. 8t + 7 (then + 8 * kAttnThreads ...) in order, each wave by a butterfly, the waves in
+// order. Both attention paths use it, so their q and k are equal bit for bit.
+__device__ __forceinline__ void qk_rms(const uint16_t* q, const uint16_t* k, int H, float eps, float* red_q,
+                                       float* red_k, float& rq, float& rk) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  float sq = 0.f, sk = 0.f;
+  for (int i = 8 * threadIdx.x; i < H; i += 8 * kAttnThreads) {
+    const u32x4 qa = *reinterpret_cast<const u32x4*>(q + i);
+    const u32x4 ka = *reinterpret_cast<const u32x4*>(k + i);
+    const uint32_t qd[4] = {qa.x, qa.y, qa.z, qa.w}, kd[4] = {ka.x, ka.y, ka.z, ka.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float q0 = bf16_bits_to_float(qd[e] & 0xffffu), q1 = bf16_bits_to_float(qd[e] >> 16);
+      const float k0 = bf16_bits_to_float(kd[e] & 0xffffu), k1 = bf16_bits_to_float(kd[e] >> 16);
+      sq += q0 * q0;
+      sq += q1 * q1;
+      sk += k0 * k0;
+      sk += k1 * k1;
+    }
+  }
+  sq = wave_sum(sq);
+  sk = wave_sum(sk);
+  if (lane == 0) {
+    red_q[wave] = sq;
+    red_k[wave] = sk;
+  }
+  __syncthreads();
+  sq = red_q[0];
+  sk = red_k[0];
+  for (int w = 1; w < kAttnWaves; ++w) {
+    sq += red_q[w];
+    sk += red_k[w];
+  }
+  rq = 1.f / sqrtf(sq / static_cast<float>(H) + eps);
+  rk = 1.f / sqrtf(sk / static_cast<float>(H) + eps);
+}
+
+// The RoPE pair (a, a + D/2) of head h at position pos: q and k normalised (weights in fp32, bf16 rounding), rotated
+// with fp32 cos / sin; returns the rotated q as bf16 values and k as bf16 bits.
+struct RopePair {
+  float qa, qb;
+  uint16_t ka, kb;
+};
+__device__ __forceinline__ RopePair rope_pair(float fqa, float fqb, float fka, float fkb, float wqa, float wqb,
+                                              float wka, float wkb, float fr, int64_t pos, float rq, float rk) {
+  const float f = fr * static_cast<float>(pos);
+  const float c = cosf(f), sn = sinf(f);
+  const float qa = round_to_bf16(wqa * (fqa * rq));
+  const float qb = round_to_bf16(wqb * (fqb * rq));
+  const float ka = round_to_bf16(wka * (fka * rk));
+  const float kb = round_to_bf16(wkb * (fkb * rk));
+  RopePair r;
+  r.qa = round_to_bf16(qa * c + (-qb) * sn);
+  r.qb = round_to_bf16(qb * c + qa * sn);
+  r.ka = float_to_bf16_bits(ka * c + (-kb) * sn);
+  r.kb = float_to_bf16_bits(kb * c + ka * sn);
+  return r;
+}
+
+// grid = rows: row r of qkv [rows, 3H] at position *pos_p + r: q, k normalised over the whole projection (qk_rms)
+// and rotated (rope_pair) for every head; q -> q_out[r]; k, v -> the caches at that position (if inside them).
+__global__ __launch_bounds__(kAttnThreads) void qk_rope_cache_kernel(const uint16_t* __restrict__ qkv,
+                                                                     const uint16_t* __restrict__ qw,
+                                                                     const uint16_t* __restrict__ kw,
+                                                                     const float* __restrict__ inv_freq,
+                                                                     const int64_t* __restrict__ pos_p,
+                                                                     uint16_t* __restrict__ q_out,
+                                                                     uint16_t* __restrict__ kc,
+                                                                     uint16_t* __restrict__ vc, int heads, int D,
+                                                                     int max_len, float eps) {
+  __shared__ float red_q[kAttnWaves], red_k[kAttnWaves];
+  const int r = blockIdx.x;
+  const int H = heads * D, half = D / 2;
+  const int64_t pos = *pos_p + r;
+  const bool in_cache = pos >= 0 && pos < max_len;
+  const uint16_t* q = qkv + static_cast<int64_t>(r) * 3 * H;
+  const uint16_t* k = q + H;
+  const uint16_t* v = q + 2 * H;
+  uint16_t* qo = q_out + static_cast<int64_t>(r) * H;
+  float rq, rk;
+  qk_rms(q, k, H, eps, red_q, red_k, rq, rk);
+  for (int i = threadIdx.x; i < H / 2; i += kAttnThreads) {
+    const int h = i / half, j = i % half;
+    const int a = h * D + j, b = a + half;
+    const RopePair rp = rope_pair(ld_bf16(q, a), ld_bf16(q, b), ld_bf16(k, a), ld_bf16(k, b), ld_bf16(qw, a),
+                                  ld_bf16(qw, b), ld_bf16(kw, a), ld_bf16(kw, b), inv_freq[j], pos, rq, rk);
+    qo[a] = float_to_bf16_bits(rp.qa);
+    qo[b] = float_to_bf16_bits(rp.qb);
+    if (in_cache) {
+      const int64_t row = (static_cast<int64_t>(h) * max_len + pos) * D;
+      kc[row + j] = rp.ka;
+      kc[row + j + half] = rp.kb;
+      vc[row + j] = v[a];
+      vc[row + j + half] = v[b];
+    }
+  }
+}
+
+// grid = (heads, rows); row r of q / out [rows, heads * D] attends over positions 0 .. *pos_p + r of the head's
+// cache rows [max_len, D], D = 8 * LPR.
 template <int LPR>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ kc,
@@ -304,20 +360,21 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const uint16_t*
   __shared__ float qs[D];
   __shared__ float red_m[kAttnWaves], red_l[kAttnWaves];
   __shared__ float part[kAttnPart];
-  const int h = blockIdx.x;
-  int64_t pos = *pos_p;
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int64_t row = (static_cast<int64_t>(r) * gridDim.x + h) * D;
+  int64_t pos = *pos_p + r;
   pos = pos < 0 ? 0 : (pos >= max_len ? max_len - 1 : pos);
   HeadAttention<LPR, false> att(kc + static_cast<int64_t>(h) * max_len * D,
                                 vc + static_cast<int64_t>(h) * max_len * D, static_cast<int>(pos) + 1);
   att.prefetch();
-  for (int d = threadIdx.x; d < D; d += kAttnThreads) qs[d] = ld_bf16(q, static_cast<int64_t>(h) * D + d);
+  for (int d = threadIdx.x; d < D; d += kAttnThreads) qs[d] = ld_bf16(q, row + d);
   __syncthreads();
-  att.run(qs, nullptr, nullptr, -1, scale, sc, red_m, red_l, part, out + static_cast<int64_t>(h) * D);
+  att.run(qs, nullptr, nullptr, -1, scale, sc, red_m, red_l, part, out + row);
 }
 
 // qk_rope_cache and attention in one launch: every workgroup h computes the q / k norms over the whole projections
-// (the same sums in every workgroup; their summation order differs from qk_rope_cache_kernel's, so a value may land
-// one bf16 step apart), rotates its own head, writes its k and v at pos to the cache, and attends over positions
+// (the same sums in every workgroup, in qk_rope_cache_kernel's order: the results are equal bit for bit to the two
+// launches), rotates its own head, writes its k and v at pos to the cache, and attends over positions
 // 0 .. pos with that row taken from LDS. Every load that does not depend on the norms (the projections, the RoPE
 // operands, the first batch of cache rows) is issued before the first reduction.
 template <int LPR>
@@ -372,48 +429,15 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint
   HeadAttention<LPR, true> att(K, V, static_cast<int>(pos) + 1);
   att.prefetch();
 
-  // the norms over the whole projections: 8 elements (one 16-byte load) of q and of k per thread and pass
-  float sq = 0.f, sk = 0.f;
-  for (int i = 8 * threadIdx.x; i < H; i += 8 * kAttnThreads) {
-    const u32x4 qa = *reinterpret_cast<const u32x4*>(q + i);
-    const u32x4 ka = *reinterpret_cast<const u32x4*>(k + i);
-    const uint32_t qd[4] = {qa.x, qa.y, qa.z, qa.w}, kd[4] = {ka.x, ka.y, ka.z, ka.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float q0 = bf16_bits_to_float(qd[e] & 0xffffu), q1 = bf16_bits_to_float(qd[e] >> 16);
-      const float k0 = bf16_bits_to_float(kd[e] & 0xffffu), k1 = bf16_bits_to_float(kd[e] >> 16);
-      sq += q0 * q0;
-      sq += q1 * q1;
-      sk += k0 * k0;
-      sk += k1 * k1;
-    }
-  }
-  sq = wave_sum(sq);
-  sk = wave_sum(sk);
-  if (lane == 0) {
-    red_q[wave] = sq;
-    red_k[wave] = sk;
-  }
-  __syncthreads();
-  sq = red_q[0];
-  sk = red_k[0];
-  for (int w = 1; w < kAttnWaves; ++w) {
-    sq += red_q[w];
-    sk += red_k[w];
-  }
-  const float rq = 1.f / sqrtf(sq / static_cast<float>(H) + eps);
-  const float rk = 1.f / sqrtf(sk / static_cast<float>(H) + eps);
+  // the norms over the whole projections
+  float rq, rk;
+  qk_rms(q, k, H, eps, red_q, red_k, rq, rk);
   if (roper) {
-    const float f = fr * static_cast<float>(pos_in);
-    const float c = cosf(f), sn = sinf(f);
-    const float qa = round_to_bf16(w_qa * (f_qa * rq));
-    const float qb = round_to_bf16(w_qb * (f_qb * rq));
-    const float ka = round_to_bf16(w_ka * (f_ka * rk));
-    const float kb = round_to_bf16(w_kb * (f_kb * rk));
-    qs[j] = round_to_bf16(qa * c + (-qb) * sn);
-    qs[j + half] = round_to_bf16(qb * c + qa * sn);
-    const uint16_t k_lo = float_to_bf16_bits(ka * c + (-kb) * sn);
-    const uint16_t k_hi = float_to_bf16_bits(kb * c + ka * sn);
+    const RopePair rp = rope_pair(f_qa, f_qb, f_ka, f_kb, w_qa, w_qb, w_ka, w_kb, fr, pos_in, rq, rk);
+    qs[j] = rp.qa;
+    qs[j + half] = rp.qb;
+    const uint16_t k_lo = rp.ka;
+    const uint16_t k_hi = rp.kb;
     ks[j] = k_lo;
     ks[j + half] = k_hi;
     vs[j] = v_a;
@@ -434,8 +458,8 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint
 // Launches of the attention kernels for head_dim = 8 * LPR (LPR = 1, 2, 4, 8, 16 or 32).
 template <int LPR>
 void launch_attention(const void* q, const void* kc, const void* vc, const int64_t* pos, void* out, int heads,
-                      int max_len, float scale, hipStream_t st) {
-  attention_kernel<LPR><<<heads, kAttnThreads, 0, st>>>(static_cast<const uint16_t*>(q),
+                      int rows, int max_len, float scale, hipStream_t st) {
+  attention_kernel<LPR><<<dim3(heads, rows), kAttnThreads, 0, st>>>(static_cast<const uint16_t*>(q),
                                                         static_cast<const uint16_t*>(kc),
                                                         static_cast<const uint16_t*>(vc), pos,
                                                         static_cast<uint16_t*>(out), max_len, scale);
@@ -453,13 +477,18 @@ void launch_rope_attention(const void* qkv, const void* qw, const void* kw, cons
 
 constexpr int kNormPer = 8;  // elements per thread kept in registers by norm_residual (n <= kBlock * kNormPer)
 
-// One workgroup. For n <= kBlock * kNormPer, x, the weight and the residual are loaded once, together, before the
-// reduction (one round trip to memory); longer vectors take a second pass over memory.
+// grid = rows, one workgroup per row of x / residual / out [rows, n]. For n <= kBlock * kNormPer, x, the weight
+// and the residual are loaded once, together, before the reduction (one round trip to memory); longer vectors take
+// a second pass over memory.
 __global__ __launch_bounds__(kBlock) void norm_residual_kernel(const uint16_t* __restrict__ x,
                                                                const uint16_t* __restrict__ w,
                                                                const uint16_t* residual, uint16_t* out, int n,
                                                                float eps) {
   __shared__ float red[kBlock / kWave];
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * n;
+  x += row;
+  out += row;
+  if (residual != nullptr) residual += row;
   if (n <= static_cast<int>(blockDim.x) * kNormPer) {
     float xv[kNormPer], wv[kNormPer], rv[kNormPer];
     float ss = 0.f;
@@ -498,11 +527,19 @@ __global__ __launch_bounds__(kBlock) void norm_residual_kernel(const uint16_t* _
   }
 }
 
-__global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out, int F) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < F; i += gridDim.x * blockDim.x) {
-    const float g = ld_bf16(gu, i);
+// out[r, f] = bf16(bf16(silu(g)) * u) for rows r of gu [rows, 2F]: g = gu[r, f], u = gu[r, F + f] (concatenated
+// halves) or g = gu[r, 2f], u = gu[r, 2f + 1] (interleaved rows of the weight).
+__global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out, int F, int rows,
+                                int interleaved) {
+  const int64_t total = static_cast<int64_t>(rows) * F;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / F, f = i % F;
+    const uint16_t* g2 = gu + r * 2 * F;
+    const float g = interleaved ? ld_bf16(g2, 2 * f) : ld_bf16(g2, f);
+    const float u = interleaved ? ld_bf16(g2, 2 * f + 1) : ld_bf16(g2, F + f);
     const float a = round_to_bf16(g / (1.f + expf(-g)));
-    out[i] = float_to_bf16_bits(a * ld_bf16(gu, F + i));
+    out[i] = float_to_bf16_bits(a * u);
   }
 }
 
@@ -593,11 +630,14 @@ __device__ __forceinline__ void wave_take(float& best, int& idx) {
   }
 }
 
-// kArgmaxBlocks workgroups, each over an even share of the logits (vec: 16-byte aligned logits, 8 per load; the
-// V % 8 tail and, when not vec, every element one at a time); each writes its (value, index) to the scratch, and
-// the last workgroup to finish (a ticket counter, reset by that workgroup) folds them, writes the token and
-// advances the position. better() is a total order, so the result does not depend on the split. Scratch: values
-// [kArgmaxBlocks] float, indices [kArgmaxBlocks] int, then the counter (zero before the first launch).
+constexpr int kArgmaxRowWords = 2 * kArgmaxBlocks + 1;  // scratch words per row: values, indices, counter
+
+// grid = (kArgmaxBlocks, rows): for row r of logits [rows, V], kArgmaxBlocks workgroups each take an even share
+// (vec: 16-byte aligned rows, 8 logits per load; the V % 8 tail and, when not vec, every element one at a time);
+// each writes its (value, index) to the row's scratch, and the last workgroup of the row to finish (a ticket
+// counter, reset by that workgroup) folds them and writes tok[r]; with pos (one row only), it also advances *pos.
+// better() is a total order, so the result does not depend on the split. Scratch per row: values [kArgmaxBlocks]
+// float, indices [kArgmaxBlocks] int, then the counter (zero before the first launch).
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint16_t* __restrict__ logits, int V,
                                                                      int vec, int64_t* __restrict__ tok,
                                                                      int64_t* __restrict__ pos,
@@ -605,6 +645,9 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint1
   __shared__ float bv[kArgmaxThreads / kWave];
   __shared__ int bi[kArgmaxThreads / kWave];
   __shared__ uint32_t ticket;
+  const int row = blockIdx.y;
+  logits += static_cast<int64_t>(row) * V;
+  scratch += static_cast<int64_t>(row) * kArgmaxRowWords;
   float* part_v = reinterpret_cast<float*>(scratch);
   int* part_i = reinterpret_cast<int*>(scratch + kArgmaxBlocks);
   uint32_t* counter = scratch + 2 * kArgmaxBlocks;
@@ -662,8 +705,8 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint1
   for (int k = threadIdx.x; k < G; k += kWave) take(best, idx, part_v[k], part_i[k]);
   wave_take(best, idx);
   if (threadIdx.x == 0) {
-    *tok = idx == 0x7fffffff ? 0 : idx;
-    *pos += 1;
+    tok[row] = idx == 0x7fffffff ? 0 : idx;
+    if (pos != nullptr) *pos += 1;
     *counter = 0u;  // ready for the next launch
   }
 }
@@ -680,6 +723,15 @@ int status() {
 
 extern "C" {
 
+int bp_decode_embed_rows(const int64_t* tok, const void* table, void* x, int rows, int hidden, int64_t vocab,
+                         void* stream) {
+  if (tok == nullptr || table == nullptr || x == nullptr || rows <= 0 || hidden <= 0 || vocab <= 0)
+    return BP_E_INVALID_ARG;
+  bp::embed_kernel<<<rows, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+      tok, static_cast<const uint16_t*>(table), static_cast<uint16_t*>(x), hidden, vocab);
+  return bp::status();
+}
+
 int bp_decode_embed(const int64_t* tok, const void* table, void* x, int hidden, int64_t vocab, void* stream) {
   if (tok == nullptr || table == nullptr || x == nullptr || hidden <= 0 || vocab <= 0) return BP_E_INVALID_ARG;
   bp::embed_kernel<<<1, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
@@ -687,24 +739,37 @@ int bp_decode_embed(const int64_t* tok, const void* table, void* x, int hidden, 
   return bp::status();
 }
 
-int bp_decode_qk_rope_cache(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
-                            const int64_t* pos, void* q_out, void* k_cache, void* v_cache, int heads, int head_dim,
-                            int max_len, float eps, void* stream) {
+int bp_decode_qk_rope_cache_rows(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                                 const int64_t* pos, void* q_out, void* k_cache, void* v_cache, int heads,
+                                 int head_dim, int max_len, float eps, int rows, void* stream) {
   if (qkv == nullptr || q_norm_w == nullptr || k_norm_w == nullptr || inv_freq == nullptr || pos == nullptr ||
-      q_out == nullptr || k_cache == nullptr || v_cache == nullptr || heads <= 0 || max_len <= 0)
+      q_out == nullptr || k_cache == nullptr || v_cache == nullptr || heads <= 0 || max_len <= 0 || rows <= 0)
     return BP_E_INVALID_ARG;
-  if (head_dim <= 0 || head_dim % 2 != 0) return BP_E_UNSUPPORTED;
-  bp::qk_rope_cache_kernel<<<1, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+  if (head_dim <= 0 || head_dim % 8 != 0) return BP_E_UNSUPPORTED;
+  if (!bp::aligned16(qkv)) return BP_E_INVALID_ARG;
+  bp::qk_rope_cache_kernel<<<rows, bp::kAttnThreads, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(q_norm_w),
       static_cast<const uint16_t*>(k_norm_w), inv_freq, pos, static_cast<uint16_t*>(q_out),
       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), heads, head_dim, max_len, eps);
   return bp::status();
 }
 
+int bp_decode_qk_rope_cache(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                            const int64_t* pos, void* q_out, void* k_cache, void* v_cache, int heads, int head_dim,
+                            int max_len, float eps, void* stream) {
+  return bp_decode_qk_rope_cache_rows(qkv, q_norm_w, k_norm_w, inv_freq, pos, q_out, k_cache, v_cache, heads,
+                                      head_dim, max_len, eps, 1, stream);
+}
+
 int bp_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos, void* out,
                         int heads, int head_dim, int max_len, float scale, void* stream) {
+  return bp_decode_attention_rows(q, k_cache, v_cache, pos, out, heads, head_dim, max_len, scale, 1, stream);
+}
+
+int bp_decode_attention_rows(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos, void* out,
+                             int heads, int head_dim, int max_len, float scale, int rows, void* stream) {
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr || pos == nullptr || out == nullptr || heads <= 0 ||
-      max_len <= 0)
+      max_len <= 0 || rows <= 0)
     return BP_E_INVALID_ARG;
   if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256 || bp::kAttnThreads % head_dim != 0 ||
       max_len > bp::kAttnMaxLen)
@@ -712,12 +777,12 @@ int bp_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   if (!bp::aligned16(k_cache) || !bp::aligned16(v_cache)) return BP_E_INVALID_ARG;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (head_dim / 8) {
-    case 1: bp::launch_attention<1>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
-    case 2: bp::launch_attention<2>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
-    case 4: bp::launch_attention<4>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
-    case 8: bp::launch_attention<8>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
-    case 16: bp::launch_attention<16>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
-    case 32: bp::launch_attention<32>(q, k_cache, v_cache, pos, out, heads, max_len, scale, st); break;
+    case 1: bp::launch_attention<1>(q, k_cache, v_cache, pos, out, heads, rows, max_len, scale, st); break;
+    case 2: bp::launch_attention<2>(q, k_cache, v_cache, pos, out, heads, rows, max_len, scale, st); break;
+    case 4: bp::launch_attention<4>(q, k_cache, v_cache, pos, out, heads, rows, max_len, scale, st); break;
+    case 8: bp::launch_attention<8>(q, k_cache, v_cache, pos, out, heads, rows, max_len, scale, st); break;
+    case 16: bp::launch_attention<16>(q, k_cache, v_cache, pos, out, heads, rows, max_len, scale, st); break;
+    case 32: bp::launch_attention<32>(q, k_cache, v_cache, pos, out, heads, rows, max_len, scale, st); break;
     default: return BP_E_UNSUPPORTED;
   }
   return bp::status();
@@ -750,13 +815,18 @@ int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* 
   return bp::status();
 }
 
-int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
-                            void* stream) {
-  if (x == nullptr || weight == nullptr || out == nullptr || n <= 0) return BP_E_INVALID_ARG;
-  bp::norm_residual_kernel<<<1, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* residual, void* out, int n,
+                                 float eps, int rows, void* stream) {
+  if (x == nullptr || weight == nullptr || out == nullptr || n <= 0 || rows <= 0) return BP_E_INVALID_ARG;
+  bp::norm_residual_kernel<<<rows, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight),
       static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), n, eps);
   return bp::status();
+}
+
+int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
+                            void* stream) {
+  return bp_decode_norm_residual_rows(x, weight, residual, out, n, eps, 1, stream);
 }
 
 int bp_decode_gate_up_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
@@ -776,22 +846,40 @@ int bp_decode_gate_up_silu(int wkind, const void* x, const void* w, const void* 
   return bp::status();
 }
 
-int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream) {
-  if (gate_up == nullptr || out == nullptr || ffn <= 0) return BP_E_INVALID_ARG;
-  const int blocks = (ffn + 255) / 256 < 1024 ? (ffn + 255) / 256 : 1024;
+int bp_decode_silu_mul_rows(const void* gate_up, void* out, int ffn, int rows, int interleaved, void* stream) {
+  if (gate_up == nullptr || out == nullptr || ffn <= 0 || rows <= 0) return BP_E_INVALID_ARG;
+  const int64_t total = static_cast<int64_t>(ffn) * rows;
+  const int blocks = static_cast<int>((total + 255) / 256 < 1024 ? (total + 255) / 256 : 1024);
   bp::silu_mul_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), ffn);
+      static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), ffn, rows, interleaved ? 1 : 0);
   return bp::status();
 }
 
-size_t bp_decode_argmax_scratch_bytes(void) { return (2 * bp::kArgmaxBlocks + 1) * sizeof(uint32_t); }
+int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream) {
+  return bp_decode_silu_mul_rows(gate_up, out, ffn, 1, 0, stream);
+}
+
+size_t bp_decode_argmax_scratch_bytes(void) { return bp::kArgmaxRowWords * sizeof(uint32_t); }
+
+size_t bp_decode_argmax_rows_scratch_bytes(int rows) {
+  return rows <= 0 ? 0 : static_cast<size_t>(rows) * bp::kArgmaxRowWords * sizeof(uint32_t);
+}
 
 int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream) {
   if (logits == nullptr || tok == nullptr || pos == nullptr || scratch == nullptr || vocab <= 0)
     return BP_E_INVALID_ARG;
-  bp::argmax_next_kernel<<<bp::kArgmaxBlocks, bp::kArgmaxThreads, 0, static_cast<hipStream_t>(stream)>>>(
+  bp::argmax_next_kernel<<<dim3(bp::kArgmaxBlocks, 1), bp::kArgmaxThreads, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(logits), vocab, bp::aligned16(logits) ? 1 : 0, tok, pos,
       static_cast<uint32_t*>(scratch));
+  return bp::status();
+}
+
+int bp_decode_argmax_rows(const void* logits, int vocab, int rows, int64_t* tok, void* scratch, void* stream) {
+  if (logits == nullptr || tok == nullptr || scratch == nullptr || vocab <= 0 || rows <= 0) return BP_E_INVALID_ARG;
+  const int vec = bp::aligned16(logits) && (rows == 1 || vocab % 8 == 0) ? 1 : 0;
+  bp::argmax_next_kernel<<<dim3(bp::kArgmaxBlocks, rows), bp::kArgmaxThreads, 0,
+                           static_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t*>(logits), vocab, vec, tok,
+                                                               nullptr, static_cast<uint32_t*>(scratch));
   return bp::status();
 }
 

@@ -10,11 +10,9 @@
 namespace bp {
 namespace {
 
-// out[:S] <- tok[:S]; out[SMAX] <- L = the number of leading drafts ids[1 + j] equal to tok[j] (j < S - 1).
-// One wave: 64 comparisons per ballot, the first mismatch ends the count.
-__global__ __launch_bounds__(kWave) void draft_accept_kernel(const int64_t* __restrict__ ids,
-                                                             const int64_t* __restrict__ tok,
-                                                             int64_t* __restrict__ out, int S, int SMAX) {
+// L = the number of leading drafts ids[1 + j] equal to tok[j] (j < S - 1), by one wave: 64 comparisons per
+// ballot, the first mismatch ends the count. Wave-uniform result.
+__device__ int64_t accepted_length(const int64_t* __restrict__ ids, const int64_t* __restrict__ tok, int S) {
   const int lane = threadIdx.x;
   int64_t accepted = 0;
   bool open = true;  // wave-uniform: no mismatch seen yet
@@ -30,8 +28,31 @@ __global__ __launch_bounds__(kWave) void draft_accept_kernel(const int64_t* __re
       accepted += in_range;
     }
   }
-  for (int j = lane; j < S; j += kWave) out[j] = tok[j];
-  if (lane == 0) out[SMAX] = accepted;
+  return accepted;
+}
+
+// out[:S] <- tok[:S]; out[SMAX] <- L.
+__global__ __launch_bounds__(kWave) void draft_accept_kernel(const int64_t* __restrict__ ids,
+                                                             const int64_t* __restrict__ tok,
+                                                             int64_t* __restrict__ out, int S, int SMAX) {
+  const int64_t accepted = accepted_length(ids, tok, S);
+  for (int j = threadIdx.x; j < S; j += kWave) out[j] = tok[j];
+  if (threadIdx.x == 0) out[SMAX] = accepted;
+}
+
+// As draft_accept_kernel, then ids[0] <- tok[L] and *pos += L + 1 (the next verify round's inputs). The drafts
+// ids[1 ..] are read before ids[0] is written (the comparisons never read ids[0]).
+__global__ __launch_bounds__(kWave) void draft_verify_next_kernel(int64_t* __restrict__ ids,
+                                                                  const int64_t* __restrict__ tok,
+                                                                  int64_t* __restrict__ out, int64_t* __restrict__ pos,
+                                                                  int S, int SMAX) {
+  const int64_t accepted = accepted_length(ids, tok, S);
+  for (int j = threadIdx.x; j < S; j += kWave) out[j] = tok[j];
+  if (threadIdx.x == 0) {
+    out[SMAX] = accepted;
+    ids[0] = tok[accepted];
+    *pos += accepted + 1;
+  }
 }
 
 // cur <- hist[slot] for one layer's state (c, n, m), slot = *length read on the device (clamped to the history).
@@ -54,6 +75,15 @@ __global__ void draft_commit_kernel(const float* __restrict__ c_hist, float* __r
 }  // namespace bp
 
 extern "C" {
+
+int bp_draft_verify_next(void* ids, const void* tok, void* out, int64_t* pos, int S, int SMAX, void* stream) {
+  if (ids == nullptr || tok == nullptr || out == nullptr || pos == nullptr || S < 1 || SMAX < S)
+    return BP_E_INVALID_ARG;
+  bp::draft_verify_next_kernel<<<1, bp::kWave, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<int64_t*>(ids), static_cast<const int64_t*>(tok), static_cast<int64_t*>(out), pos, S, SMAX);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? BP_OK : static_cast<int>(e);
+}
 
 int bp_draft_accept(const void* ids, const void* tok, void* out, int S, int SMAX, void* stream) {
   if (ids == nullptr || tok == nullptr || out == nullptr || S < 0 || SMAX < S) return BP_E_INVALID_ARG;

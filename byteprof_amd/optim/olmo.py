@@ -186,6 +186,66 @@ class OlmoDecoder:
         """Kernel launches of one step: embed, 7 or 8 per layer, final norm, LM head, argmax."""
         return 4 + (7 if self.gate_up_interleaved else 8) * self.cfg.layers
 
+    def verify_buffers(self, smax: int) -> None:
+        """Allocates the buffers of verify passes of up to `smax` rows (once; a larger smax reallocates). ids
+        [smax] and pos [1] (int64) are the round's inputs: ids[0] the last accepted token, ids[1 ..] the drafts,
+        pos the cache position of ids[0]; out [smax + 1] receives the row tokens and, at smax, the accepted length."""
+        if getattr(self, "smax", 0) >= smax:
+            return
+        cfg, dev = self.cfg, self.device
+        H, F, V = cfg.hidden, cfg.ffn, cfg.vocab
+        z = lambda *shape, dtype=torch.bfloat16: torch.zeros(*shape, dtype=dtype, device=dev)  # noqa: E731
+        self.smax = smax
+        self.v_ids, self.v_tok, self.v_out = z(smax, dtype=torch.int64), z(smax, dtype=torch.int64), \
+            z(smax + 1, dtype=torch.int64)
+        self.v_pos = z(1, dtype=torch.int64)
+        self.vx, self.vq, self.vattn, self.vo, self.vdn, self.vxn = (z(smax, H) for _ in range(6))
+        self.vqkv, self.vgu, self.vact, self.vlogits = z(smax, 3 * H), z(smax, 2 * F), z(smax, F), z(smax, V)
+        self.v_argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_rows_scratch_bytes(smax) // 4), dtype=torch.int32)
+
+    def verify(self, s: int) -> None:
+        """One verify pass of s = 1 + drafts rows (the reference's captured draft step, olmo_draft.py
+        make_generate_draft): ids[:s] at positions pos .. pos + s - 1 through the model with the static cache (the
+        rows' k / v written first, row r attending over positions <= pos + r), the argmax of every row, the accepted
+        length L (drafts ids[1 + j] equal to the prediction of row j) and the next round's inputs: ids[0] <- the
+        token after the accepted prefix, pos += L + 1. Every row is computed as the one-token step at its position
+        computes it; the linears run at s activation rows (the matrix-core kernels from 5 rows on)."""
+        if not 1 <= s <= getattr(self, "smax", 0):
+            raise ValueError(f"s must be in 1..{getattr(self, 'smax', 0)} (verify_buffers)")
+        cfg, L = self.cfg, _lib.lib()
+        H, F, D = cfg.hidden, cfg.ffn, cfg.head_dim
+        st = _lib.stream_ptr(self.device)
+        c = _lib.check
+        c(L.bp_decode_embed_rows(self.v_ids.data_ptr(), self.embed.data_ptr(), self.vx.data_ptr(), s, H, cfg.vocab,
+                                 st), "bp_decode_embed_rows")
+        x = self.vx[:s]
+        for i, w in enumerate(self.layers):
+            kc, vc = self.k_cache[i], self.v_cache[i]
+            self._mm(x, w["qkv"], self.vqkv[:s])
+            c(L.bp_decode_qk_rope_cache_rows(self.vqkv.data_ptr(), w["q_norm"].data_ptr(), w["k_norm"].data_ptr(),
+                                             self.inv_freq.data_ptr(), self.v_pos.data_ptr(), self.vq.data_ptr(),
+                                             kc.data_ptr(), vc.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, s,
+                                             st), "bp_decode_qk_rope_cache_rows")
+            c(L.bp_decode_attention_rows(self.vq.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.v_pos.data_ptr(),
+                                         self.vattn.data_ptr(), cfg.heads, D, cfg.max_len, self.scale, s, st),
+              "bp_decode_attention_rows")
+            self._mm(self.vattn[:s], w["o"], self.vo[:s])
+            c(L.bp_decode_norm_residual_rows(self.vo.data_ptr(), w["post_attn"].data_ptr(), self.vx.data_ptr(),
+                                             self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
+            self._mm(x, w["gate_up"], self.vgu[:s])
+            c(L.bp_decode_silu_mul_rows(self.vgu.data_ptr(), self.vact.data_ptr(), F, s,
+                                        int(self.gate_up_interleaved), st), "bp_decode_silu_mul_rows")
+            self._mm(self.vact[:s], w["down"], self.vdn[:s])
+            c(L.bp_decode_norm_residual_rows(self.vdn.data_ptr(), w["post_ff"].data_ptr(), self.vx.data_ptr(),
+                                             self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
+        c(L.bp_decode_norm_residual_rows(self.vx.data_ptr(), self.norm.data_ptr(), None, self.vxn.data_ptr(), H,
+                                         cfg.eps, s, st), "bp_decode_norm_residual_rows")
+        self._mm(self.vxn[:s], self.lm_head, self.vlogits[:s])
+        c(L.bp_decode_argmax_rows(self.vlogits.data_ptr(), cfg.vocab, s, self.v_tok.data_ptr(),
+                                  self.v_argmax_scratch.data_ptr(), st), "bp_decode_argmax_rows")
+        c(L.bp_draft_verify_next(self.v_ids.data_ptr(), self.v_tok.data_ptr(), self.v_out.data_ptr(),
+                                 self.v_pos.data_ptr(), s, self.smax, st), "bp_draft_verify_next")
+
     def weight_bytes(self) -> int:
         """Bytes of the linears' weights (and scales) a step streams."""
         lins = [self.lm_head] + [w[n] for w in self.layers for n in ("qkv", "o", "gate_up", "down")]

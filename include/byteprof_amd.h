@@ -180,6 +180,15 @@ int bp_mlstm_lazy_commit(void* c, void* n, void* m, const void* nstart, const vo
 int bp_draft_accept(const void* ids, const void* tok, void* out, int S, int SMAX, void* stream);
 
 /*
+ * The end of a verify round of the token decode loop, on the device: bp_draft_accept's out[:S], out[SMAX] = L, then
+ * the next round's inputs: ids[0] <- tok[L] (the token after the accepted prefix), *pos += L + 1. ids, tok, out,
+ * pos: int64.
+ * Replaces: the acceptance and set_state of byteprof/optim/olmo_draft.py (make_generate_draft's captured step:
+ *           core.accepted_length_t, out_dev, set_state(tok[L], cp[0] + L + 1)).
+ */
+int bp_draft_verify_next(void* ids, const void* tok, void* out, int64_t* pos, int S, int SMAX, void* stream);
+
+/*
  * cur <- hist[slot] for one layer's state, slot = *length (int64 in device memory, clamped to [0, slots)):
  * c_cur[i] = c_hist[slot * c_n + i] (i < c_n), likewise n (n_n <= c_n) and m (m_n <= c_n); fp32.
  * Replaces: byteprof/optim/draft_kernels.py (commit_kernel) via draft_core.py:92-111 (commit_state).
@@ -198,17 +207,22 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  * argmax and the in-graph update of the next step's inputs), with the linears done by bp_skinny_* launches.
  *
  * embed:          x[hidden] <- table[tok] (table [vocab, hidden]; tok clamped into range).
+ * *_rows:         the same step for `rows` consecutive positions of a verify pass (row r of each [rows, ...]
+ *                 operand at position *pos + r; the attention of row r covers positions 0 .. *pos + r, so the rows'
+ *                 own cache entries, written by qk_rope_cache_rows before, take part causally); every row is
+ *                 computed exactly as the one-row call at that position computes it.
  * qk_rope_cache:  qkv = [q | k | v] (3 * heads * head_dim); q, k RMSNorm'd over their whole length with their
  *                 weights, rotated by RoPE at *pos (inv_freq[head_dim / 2] fp32, cos / sin in fp32); q -> q_out;
- *                 k, v -> k_cache, v_cache [heads, max_len, head_dim] at row *pos (no write if *pos >= max_len).
+ *                 k, v -> k_cache, v_cache [heads, max_len, head_dim] at row *pos (no write if *pos >= max_len);
+ *                 head_dim a multiple of 8, qkv 16-byte aligned.
  * attention:      per head, positions 0 .. *pos: out = bf16(softmax_fp32(bf16(bf16(q . k) * scale)) as bf16 . v);
  *                 head_dim a multiple of 8 dividing 256, max_len <= 4096; caches 16-byte aligned.
- * rope_attention: qk_rope_cache and attention in one launch (one workgroup per head; the q / k norms summed in
- *                 another order, so a value may differ by one bf16 step from the two-launch path); qkv 16-byte
- *                 aligned.
+ * rope_attention: qk_rope_cache and attention in one launch (one workgroup per head), equal bit for bit to the
+ *                 two launches; qkv 16-byte aligned.
  * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
  *                 out may alias residual.
- * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn).
+ * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn); silu_mul_rows with
+ *                 interleaved = 1 reads the pairs (gate_up[2f], gate_up[2f + 1]) instead.
  * gate_up_silu:   the gate|up projection of x[hidden] and silu_mul in one launch: w [2 * ffn, hidden] (wkind
  *                 BP_DT_BF16 (0) bf16 or 1 int8 with per-row scale [2 * ffn] of scale_dtype) with row 2n the gate
  *                 row n and row 2n + 1 the up row n; out[ffn] equal bit for bit to bp_skinny_* on w with 2 rows and
@@ -218,23 +232,37 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  *                 share the logits and the last to finish writes the result; `scratch` holds their partials and
  *                 a counter: bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is
  *                 (each call leaves the counter at zero); calls sharing one scratch must not overlap.
+ * argmax_rows:    tok[r] = argmax of row r of logits [rows, vocab] (as argmax_next; no position update), with
+ *                 bp_decode_argmax_rows_scratch_bytes(rows) bytes of scratch (zero before the first call).
  */
 int bp_decode_embed(const int64_t* tok, const void* table, void* x, int hidden, int64_t vocab, void* stream);
+int bp_decode_embed_rows(const int64_t* tok, const void* table, void* x, int rows, int hidden, int64_t vocab,
+                         void* stream);
 int bp_decode_qk_rope_cache(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
                             const int64_t* pos, void* q_out, void* k_cache, void* v_cache, int heads, int head_dim,
                             int max_len, float eps, void* stream);
+int bp_decode_qk_rope_cache_rows(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                                 const int64_t* pos, void* q_out, void* k_cache, void* v_cache, int heads,
+                                 int head_dim, int max_len, float eps, int rows, void* stream);
 int bp_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos, void* out,
                         int heads, int head_dim, int max_len, float scale, void* stream);
+int bp_decode_attention_rows(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos, void* out,
+                             int heads, int head_dim, int max_len, float scale, int rows, void* stream);
 int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
                              const int64_t* pos, void* k_cache, void* v_cache, void* out, int heads, int head_dim,
                              int max_len, float eps, float scale, void* stream);
 int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
                             void* stream);
+int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* residual, void* out, int n,
+                                 float eps, int rows, void* stream);
 int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream);
+int bp_decode_silu_mul_rows(const void* gate_up, void* out, int ffn, int rows, int interleaved, void* stream);
 int bp_decode_gate_up_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
                            int ffn, int hidden, int waves, void* stream);
 size_t bp_decode_argmax_scratch_bytes(void);
 int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream);
+size_t bp_decode_argmax_rows_scratch_bytes(int rows);
+int bp_decode_argmax_rows(const void* logits, int vocab, int rows, int64_t* tok, void* scratch, void* stream);
 
 /*
  * Decode-step linear set: a chain of skinny linears at one activation row run by one persistent launch.
