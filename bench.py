@@ -264,6 +264,57 @@ def sweep(device) -> dict:
     return out
 
 
+def draft_figures(dec, prompt, ref, new_tokens: int) -> dict:
+    """The drafting loop (byteprof_amd/optim/olmo_draft.py) on the same decoder: the captured verify round's GPU
+    time for K drafts (K + 1 rows; replays back to back, events), and the loop's time per token with the oracle
+    drafter (the recorded greedy continuation: every draft accepted, the upper bound of a drafter), K up to 8. The
+    recorded continuation is the drafting loop's own: its rows from 5 on use the matrix-core linears, which can
+    part from the one-token loop at a near tie, so the graph loop's tokens are re-recorded through the drafting
+    loop until they repeat (at most 3 passes)."""
+    import torch
+
+    from byteprof_amd.optim import olmo_draft as OD
+
+    key = tuple(prompt[0].tolist())
+    truth = {key: ref[0, prompt.shape[1]:].tolist()}
+    stats = OD.Stats()
+    gen, st = OD.make_generate_draft(dec, {"kind": "oracle", "truth": truth}, stats)
+    out = gen(prompt, max_new_tokens=4)  # captures the rounds' graphs
+    same = 1
+    for _ in range(3):
+        out = gen(prompt, max_new_tokens=1 + new_tokens)
+        toks = out[0, prompt.shape[1]:].tolist()
+        if toks == truth[key]:
+            break
+        same = 0
+        truth[key] = toks
+    stats.__init__()
+    t0 = time.perf_counter()
+    gen(prompt, max_new_tokens=1)
+    t1 = time.perf_counter()
+    out = gen(prompt, max_new_tokens=1 + new_tokens)
+    t2 = time.perf_counter()
+    rounds = {}
+    for k, g in st["graphs"].items():
+        dec.v_pos.fill_(prompt.shape[1])
+        g.replay()
+        torch.cuda.synchronize()
+        dec.v_pos.fill_(prompt.shape[1])
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        reps = 20
+        ev[0].record()
+        for _ in range(reps):
+            g.replay()
+        ev[1].record()
+        ev[1].synchronize()
+        rounds[str(k + 1)] = ev[0].elapsed_time(ev[1]) / reps * 1e3
+    per_token = ((t2 - t1) - (t1 - t0)) / new_tokens * 1e6
+    return {"us_per_round_by_rows": rounds, "oracle_drafter_us_per_token": per_token,
+            "oracle_drafter_tokens_per_s": 1e6 / per_token, "same_tokens_as_graph_loop": same,
+            "rounds": stats.rounds, "tokens": stats.emitted,
+            "note": "oracle drafter: every draft accepted (the recorded continuation of this loop); rounds of 9 rows"}
+
+
 def decode_loop(device, new_tokens: int = 128) -> dict:
     """The graph-captured greedy decode loop (byteprof_amd/optim/olmo.py) on the OLMo-2-1B shape with synthetic
     weights: per kind, the GPU time of one captured decode step (replays timed with events), the loop's time per
@@ -286,7 +337,7 @@ def decode_loop(device, new_tokens: int = 128) -> dict:
         t0 = time.perf_counter()
         graph(prompt, max_new_tokens=1)
         t1 = time.perf_counter()
-        graph(prompt, max_new_tokens=1 + new_tokens)
+        ref = graph(prompt, max_new_tokens=1 + new_tokens)
         t2 = time.perf_counter()
         loop_us = ((t2 - t1) - (t1 - t0)) / new_tokens * 1e6
         eager = OG.make_generate(dec)
@@ -320,7 +371,7 @@ def decode_loop(device, new_tokens: int = 128) -> dict:
         nb = dec.weight_bytes()
         out[kind] = {"us_per_token_loop": loop_us, "us_per_step_graph": step_us, "us_per_token_eager": eager_us,
                      "weight_bytes_per_step": nb, "weight_gbs_graph_step": nb / step_us / 1e3,
-                     "tokens_per_s_loop": 1e6 / loop_us}
+                     "tokens_per_s_loop": 1e6 / loop_us, "draft": draft_figures(dec, prompt, ref, new_tokens)}
         del dec, graph, eager, g
         torch.cuda.empty_cache()
     return out
