@@ -222,19 +222,33 @@ class OlmoDecoder:
         for i, w in enumerate(self.layers):
             kc, vc = self.k_cache[i], self.v_cache[i]
             self._mm(x, w["qkv"], self.vqkv[:s])
-            c(L.bp_decode_qk_rope_cache_rows(self.vqkv.data_ptr(), w["q_norm"].data_ptr(), w["k_norm"].data_ptr(),
-                                             self.inv_freq.data_ptr(), self.v_pos.data_ptr(), self.vq.data_ptr(),
-                                             kc.data_ptr(), vc.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, s,
-                                             st), "bp_decode_qk_rope_cache_rows")
-            c(L.bp_decode_attention_rows(self.vq.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.v_pos.data_ptr(),
-                                         self.vattn.data_ptr(), cfg.heads, D, cfg.max_len, self.scale, s, st),
-              "bp_decode_attention_rows")
+            if s == 1:  # one row: the one-token step's fused launch (equal bit for bit to the two below)
+                c(L.bp_decode_rope_attention(self.vqkv.data_ptr(), w["q_norm"].data_ptr(), w["k_norm"].data_ptr(),
+                                             self.inv_freq.data_ptr(), self.v_pos.data_ptr(), kc.data_ptr(),
+                                             vc.data_ptr(), self.vattn.data_ptr(), cfg.heads, D, cfg.max_len,
+                                             cfg.eps, self.scale, st), "bp_decode_rope_attention")
+            else:
+                c(L.bp_decode_qk_rope_cache_rows(self.vqkv.data_ptr(), w["q_norm"].data_ptr(),
+                                                 w["k_norm"].data_ptr(), self.inv_freq.data_ptr(),
+                                                 self.v_pos.data_ptr(), self.vq.data_ptr(), kc.data_ptr(),
+                                                 vc.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, s, st),
+                  "bp_decode_qk_rope_cache_rows")
+                c(L.bp_decode_attention_rows(self.vq.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.v_pos.data_ptr(),
+                                             self.vattn.data_ptr(), cfg.heads, D, cfg.max_len, self.scale, s, st),
+                  "bp_decode_attention_rows")
             self._mm(self.vattn[:s], w["o"], self.vo[:s])
             c(L.bp_decode_norm_residual_rows(self.vo.data_ptr(), w["post_attn"].data_ptr(), self.vx.data_ptr(),
                                              self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
-            self._mm(x, w["gate_up"], self.vgu[:s])
-            c(L.bp_decode_silu_mul_rows(self.vgu.data_ptr(), self.vact.data_ptr(), F, s,
-                                        int(self.gate_up_interleaved), st), "bp_decode_silu_mul_rows")
+            if s == 1 and self.gate_up_interleaved:  # the one-token step's fused gate|up + SiLU launch
+                gw = w["gate_up"]
+                sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
+                c(L.bp_decode_gate_up_silu(0 if self.kind == "bf16" else 1, self.vx.data_ptr(), gw[0].data_ptr(),
+                                           sc, sdt, self.vact.data_ptr(), F, H, GATE_UP_WAVES[self.kind], st),
+                  "bp_decode_gate_up_silu")
+            else:
+                self._mm(x, w["gate_up"], self.vgu[:s])
+                c(L.bp_decode_silu_mul_rows(self.vgu.data_ptr(), self.vact.data_ptr(), F, s,
+                                            int(self.gate_up_interleaved), st), "bp_decode_silu_mul_rows")
             self._mm(self.vact[:s], w["down"], self.vdn[:s])
             c(L.bp_decode_norm_residual_rows(self.vdn.data_ptr(), w["post_ff"].data_ptr(), self.vx.data_ptr(),
                                              self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
