@@ -5,8 +5,11 @@
                                                                          the set as one persistent launch, R launches
   python -m byteprof_amd.profiling group [--kind bf16|int8] [--replays R]
                                                                          the set as one grouped launch, R launches
-  python -m byteprof_amd.profiling decode [--kind bf16|int8] [--tokens N]  the graph-captured greedy decode loop
-                                                                         of the OLMo-2-1B shape, 8 prompt + N tokens
+  python -m byteprof_amd.profiling decode [--kind bf16|int8] [--tokens N] [--draft]
+                                                                         the graph-captured greedy decode loop
+                                                                         of the OLMo-2-1B shape, 8 prompt + N tokens;
+                                                                         --draft: then the drafting loop with the
+                                                                         oracle drafter (K up to 8)
   python -m byteprof_amd.profiling skinny [--kind bf16|int8] [--n N] [--k K] [--m M] [--replays R]
                                                                          skinny_mm over a ring of distinct weights
   python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
@@ -158,6 +161,7 @@ def main(argv=None) -> int:
     ap.add_argument("--k", type=int, default=2048, help="skinny: input length")
     ap.add_argument("--m", type=int, default=16, help="skinny: activation rows")
     ap.add_argument("--tokens", type=int, default=128, help="decode: new tokens")
+    ap.add_argument("--draft", action="store_true", help="decode: also the drafting loop (oracle drafter)")
     ap.add_argument("--mib", type=int, default=256)
     ap.add_argument("--reps", type=int, default=5)
     a = ap.parse_args(argv)
@@ -216,6 +220,18 @@ def main(argv=None) -> int:
         out = generate(prompt, max_new_tokens=a.tokens)
         torch.cuda.synchronize()
         print(f"decoded {out.shape[1] - prompt.shape[1]} tokens ({a.kind}, graph loop)", flush=True)
+        if a.draft:
+            from .optim import olmo_draft as OD
+
+            key = tuple(prompt[0].tolist())
+            truth = {key: out[0, prompt.shape[1]:].tolist()}
+            stats = OD.Stats()
+            gen, _ = OD.make_generate_draft(dec, {"kind": "oracle", "truth": truth}, stats)
+            for _ in range(2):  # the second pass drafts the first pass's own continuation
+                res = gen(prompt, max_new_tokens=a.tokens)
+                truth[key] = res[0, prompt.shape[1]:].tolist()
+            torch.cuda.synchronize()
+            print(f"drafting loop: {stats.dump()}", flush=True)
         return 0
     if a.what == "group":
         ops = D.build(a.kind, 1, device)

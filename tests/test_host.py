@@ -328,3 +328,38 @@ def test_int4_skinny_linear_holds_the_packed_format():
     x = torch.randn(3, 256, dtype=torch.bfloat16)
     y = m(x)  # CPU input: dequantized F.linear, as the reference
     assert torch.equal(y, torch.nn.functional.linear(x, m.dequantized(torch.bfloat16)))
+
+
+def test_drafting_host_logic_matches_the_reference_definitions():
+    """accepted_length / choose_k / the drafters, against hand-worked cases of the reference's definitions
+    (byteprof/optim/draft_core.py:27-37,182-188; byteprof/drafting/drafters.py:14-45)."""
+    from byteprof_amd.optim import olmo_draft as OD
+
+    # drafts ids[1..k] against the predictions toks[0..k-1]; the first mismatch ends the count
+    assert OD.accepted_length([9, 1, 2, 3], [1, 2, 3, 4], 3) == 3
+    assert OD.accepted_length([9, 1, 2, 3], [1, 5, 3, 4], 3) == 1
+    assert OD.accepted_length([9, 1, 2, 3], [7, 2, 3, 4], 3) == 0
+    assert OD.accepted_length([9, 1, 2, 3], [1, 2, 3, 4], 2) == 2  # only k drafts count
+    assert OD.accepted_length([9], [4], 0) == 0
+    # the same count as the reference's device form: cumprod of the matches, summed
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        k = int(rng.integers(0, 9))
+        ids = rng.integers(0, 3, k + 1).tolist()
+        toks = rng.integers(0, 3, k + 1).tolist()
+        m = torch.tensor([ids[j + 1] == toks[j] for j in range(k)], dtype=torch.int32)
+        want = int(torch.cumprod(m, 0).sum()) if k else 0
+        assert OD.accepted_length(ids, toks, k) == want
+    # the largest available K not above the draft length and the cap
+    ks = (0, 1, 2, 4, 6, 8)
+    assert [OD.choose_k(n, ks, 8) for n in range(10)] == [0, 1, 2, 2, 4, 4, 6, 6, 8, 8]
+    assert OD.choose_k(9, ks, 5) == 4
+    # the oracle drafter proposes the continuation after what it has been told was emitted
+    d = OD.OracleDrafter()
+    d.reset([1, 2, 3], truth=[50, 51, 52, 53, 54])
+    assert d.propose(2) == [51, 52]
+    d.push([51, 52])  # a round that emitted two tokens after t0 = truth[0]
+    assert d.propose(8) == [53, 54]
+    with pytest.raises(ValueError):
+        OD.OracleDrafter().reset([1], None)
+    assert OD.NullDrafter().propose(4) == []
