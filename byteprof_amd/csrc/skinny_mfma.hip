@@ -24,7 +24,8 @@
 // of how many activation rows share the launch.
 //
 // Reference semantics: byteprof/optim/skinny.py:36-90 (the kernel's bf16 / int8 modes and split reduce), used by
-// skinny_mm (skinny.py:136-166) at the speculative-verify widths (BASELINE sweep M in {1, 2, 4, 8, 16}).
+// skinny_mm (skinny.py:136-166) at the speculative-verify widths (activation rows 5..16 of the sweep M in
+// {1, 2, 4, 8, 16}).
 
 #include "byteprof_amd.h"
 #include "skinny_kernel.h"

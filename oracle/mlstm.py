@@ -3,8 +3,8 @@
 multistep: the stabilised recurrence of byteprof/optim/mlstm_multistep.py:21-86 in float64, with the reference's
     roundings to the io dtype at the points it casts (mlstm_multistep.py:27-29 gate activations; :78-83 state before
     the q products; :85 the stored h). Per position t, per head:
-        fl = log(sigmoid(f_t))                          (literal_gate=True: fl = f_t, the formula as BASELINE
-                                                          writes it, kept only to show the two readings differ)
+        fl = log(sigmoid(f_t))                          (literal_gate=True: fl = f_t, f read literally as a
+                                                          log forget gate, kept only to show the two readings differ)
         m_t = max(fl + m_{t-1}, i_t)
         fa = io(exp(fl + m_{t-1} - m_t)); ia = io(exp(i_t - m_t)); mv = io(exp(-m_t))
         C_t = fa C_{t-1} + ia k_t v_t^T;  n_t = fa n_{t-1} + ia k_t

@@ -11,7 +11,7 @@ from oracle import numerics as ON
 from oracle import skinny as OS
 
 TOL_COMPONENTWISE = 4e-3  # byteprof tests/test_skinny.py:17
-TOL_NORMWISE = 1e-2  # BASELINE / tests/test_quant_int8.py:53-56
+TOL_NORMWISE = 1e-2  # the bf16 max relative error gate; byteprof tests/test_quant_int8.py:53-56
 
 
 def make_weights(kind: str, n: int, k: int, seed: int = 0, device: str = "cuda", scale_dtype=None, std=0.02):

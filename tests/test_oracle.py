@@ -211,7 +211,7 @@ def test_mlstm_io_rounding_is_applied_to_h():
 
 
 def test_literal_gate_reading_differs_from_the_reference_reading():
-    """BASELINE writes m_t = max(f + m, i) with f ~ N(3, 1); the reference applies logsigmoid(f) first
+    """Read literally, the stabiliser is m_t = max(f + m, i) with f ~ N(3, 1); the reference applies logsigmoid(f) first
     (mlstm_multistep.py:25-26). With f taken literally as a log forget gate the state grows ~e^3 per step
     (in the stabilised form: m grows by ~3 per step while C keeps its scale), so the two readings give different h."""
     c, n, m, q, k, v, i, f = _mlstm_inputs(6, 2, 8, 4, seed=13)
