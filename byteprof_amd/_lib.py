@@ -62,6 +62,8 @@ SIGNATURES: dict[str, tuple] = {
     "bp_decode_attention": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_float, _c_vp]),
     "bp_decode_rope_attention": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int,
                                           _c_int, _c_float, _c_float, _c_vp]),
+    "bp_decode_rope_attention_rows": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int,
+                                               _c_int, _c_int, _c_int, _c_float, _c_float, _c_vp]),
     "bp_decode_norm_residual": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_float, _c_vp]),
     "bp_decode_silu_mul": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp]),
     "bp_decode_argmax_scratch_bytes": (_c_size, []),

@@ -18,6 +18,8 @@
 // forward the reference's decode loop replays (byteprof/optim/olmo.py:122-219: make_generate_graph captures the
 // forward, the argmax and the next-step input updates in one graph).
 
+#include <climits>
+
 #include "byteprof_amd.h"
 #include "common.h"
 #include "skinny_kernel.h"
@@ -144,12 +146,13 @@ struct HeadAttention {
   }
 
   __device__ __forceinline__ void scores(const u32x4 (&kv)[kAttnUnroll], int t0, const float (&qv)[8],
-                                         const uint16_t* ksub, int sub_t, float scale, float* sc, float& m) const {
+                                         const uint16_t* ksub, int sub_lo, float scale, float* sc, float& m) const {
     float dot[kAttnUnroll];
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
       const int t = t0 + u * STEP + slot;
-      const u32x4 w = SUB && t == sub_t ? *reinterpret_cast<const u32x4*>(ksub + 8 * s) : kv[u];
+      const u32x4 w = SUB && t >= sub_lo && t < T ? *reinterpret_cast<const u32x4*>(ksub + (t - sub_lo) * D + 8 * s)
+                                                  : kv[u];
       dot[u] = dot8(w, qv);
     }
 #pragma unroll
@@ -165,13 +168,13 @@ struct HeadAttention {
     }
   }
 
-  __device__ __forceinline__ void values(const u32x4 (&vv)[kAttnUnroll], int t0, const uint16_t* vsub, int sub_t,
+  __device__ __forceinline__ void values(const u32x4 (&vv)[kAttnUnroll], int t0, const uint16_t* vsub, int sub_lo,
                                          const float* sc, float inv, float (&acc)[8]) const {
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
       const int t = t0 + u * STEP + slot;
       if (t < T) {
-        const u32x4 w = SUB && t == sub_t ? *reinterpret_cast<const u32x4*>(vsub + 8 * s) : vv[u];
+        const u32x4 w = SUB && t >= sub_lo ? *reinterpret_cast<const u32x4*>(vsub + (t - sub_lo) * D + 8 * s) : vv[u];
         const float p = round_to_bf16(sc[t] * inv);
         const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -183,10 +186,11 @@ struct HeadAttention {
     }
   }
 
-  // q: bf16 values in LDS qs[0 .. D). Row sub_t (-1: none) is read from ksub / vsub (bf16, LDS, 16-byte aligned)
-  // instead of the cache. Writes out[0 .. D). The caller has made qs, ksub and vsub visible (a barrier).
+  // q: bf16 values in LDS qs[0 .. D). Rows t >= sub_lo (INT_MAX: none) are read from ksub / vsub [t - sub_lo][D]
+  // (bf16, LDS, 16-byte aligned rows) instead of the cache. Writes out[0 .. D). The caller has made qs, ksub and
+  // vsub visible (a barrier).
   // LDS: sc[T] scores, red_m / red_l [kAttnWaves], part [kAttnWaves * D].
-  __device__ __forceinline__ void run(const float* qs, const uint16_t* ksub, const uint16_t* vsub, int sub_t,
+  __device__ __forceinline__ void run(const float* qs, const uint16_t* ksub, const uint16_t* vsub, int sub_lo,
                                       float scale, float* sc, float* red_m, float* red_l, float* part,
                                       uint16_t* __restrict__ out) {
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -194,11 +198,11 @@ struct HeadAttention {
 #pragma unroll
     for (int e = 0; e < 8; ++e) qv[e] = qs[8 * s + e];
     float m = -INFINITY;
-    scores(k0, 0, qv, ksub, sub_t, scale, sc, m);
+    scores(k0, 0, qv, ksub, sub_lo, scale, sc, m);
     for (int t0 = BATCH; t0 < T; t0 += BATCH) {
       u32x4 kv[kAttnUnroll];
       load_batch(K, t0, kv);
-      scores(kv, t0, qv, ksub, sub_t, scale, sc, m);
+      scores(kv, t0, qv, ksub, sub_lo, scale, sc, m);
     }
     m = wave_max(m);
     if (lane == 0) red_m[wave] = m;
@@ -220,11 +224,11 @@ struct HeadAttention {
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    values(v0, 0, vsub, sub_t, sc, inv, acc);
+    values(v0, 0, vsub, sub_lo, sc, inv, acc);
     for (int t0 = BATCH; t0 < T; t0 += BATCH) {
       u32x4 vv[kAttnUnroll];
       load_batch(V, t0, vv);
-      values(vv, t0, vsub, sub_t, sc, inv, acc);
+      values(vv, t0, vsub, sub_lo, sc, inv, acc);
     }
     // the wave's row groups (lanes s, s + LPR, s + 2 LPR, ...) added by butterflies over the group bits
 #pragma unroll
@@ -369,7 +373,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const uint16_t*
   att.prefetch();
   for (int d = threadIdx.x; d < D; d += kAttnThreads) qs[d] = ld_bf16(q, row + d);
   __syncthreads();
-  att.run(qs, nullptr, nullptr, -1, scale, sc, red_m, red_l, part, out + row);
+  att.run(qs, nullptr, nullptr, INT_MAX, scale, sc, red_m, red_l, part, out + row);
 }
 
 // qk_rope_cache and attention in one launch: every workgroup h computes the q / k norms over the whole projections
@@ -451,8 +455,128 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint
     }
   }
   __syncthreads();  // qs, ks and vs, written above, are read below
-  att.run(qs, ks, vs, in_cache ? static_cast<int>(pos_in) : -1, scale, sc, red_m, red_l, part,
+  att.run(qs, ks, vs, in_cache ? static_cast<int>(pos_in) : INT_MAX, scale, sc, red_m, red_l, part,
           out + static_cast<int64_t>(h) * D);
+}
+
+constexpr int kRowsMax = 16;  // rows of one fused verify launch
+
+// grid = (heads, rows): workgroup (h, r) attends for row r of qkv [rows, 3H], at position *pos_p + r, over positions
+// 0 .. *pos_p + r. The rows 0 .. r of the launch for its own head are normalised (qk_rms's order) and rotated
+// (rope_pair) in this workgroup and read from LDS, the positions before them from the cache; the workgroup writes
+// only its own row's k and v to the cache. Equal bit for bit to qk_rope_cache_kernel + attention_kernel on the same
+// rows (the same sums in the same order).
+template <int LPR>
+__global__ __launch_bounds__(kAttnThreads) void rope_attention_rows_kernel(const uint16_t* __restrict__ qkv,
+                                                                           const uint16_t* __restrict__ qw,
+                                                                           const uint16_t* __restrict__ kw,
+                                                                           const float* __restrict__ inv_freq,
+                                                                           const int64_t* __restrict__ pos_p,
+                                                                           uint16_t* __restrict__ kc,
+                                                                           uint16_t* __restrict__ vc,
+                                                                           uint16_t* __restrict__ out, int heads,
+                                                                           int max_len, float eps, float scale) {
+  constexpr int D = 8 * LPR;
+  constexpr int half = D / 2;
+  __shared__ float sc[kAttnMaxLen];
+  __shared__ float qs[D];
+  __shared__ __align__(16) uint16_t ks[kRowsMax * D];
+  __shared__ __align__(16) uint16_t vs[kRowsMax * D];
+  __shared__ float red_q[kAttnWaves], red_k[kRowsMax][kAttnWaves], red_m[kAttnWaves], red_l[kAttnWaves];
+  __shared__ float part[kAttnPart];
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int H = heads * D;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int64_t pos0 = *pos_p;
+  const int64_t pos_r = pos0 + r;
+  const bool in_cache = pos_r >= 0 && pos_r < max_len;
+  const int64_t posc = pos_r < 0 ? 0 : (pos_r >= max_len ? max_len - 1 : pos_r);
+  uint16_t* K = kc + static_cast<int64_t>(h) * max_len * D;
+  uint16_t* V = vc + static_cast<int64_t>(h) * max_len * D;
+  HeadAttention<LPR, true> att(K, V, static_cast<int>(posc) + 1);
+  att.prefetch();
+
+  // sums of squares of q (row r) and k (rows 0 .. r), each in qk_rms's order
+  const int64_t row3 = 3 * static_cast<int64_t>(H);
+  float sq = 0.f;
+  float sk[kRowsMax];
+#pragma unroll
+  for (int j = 0; j < kRowsMax; ++j) sk[j] = 0.f;
+  for (int i = 8 * threadIdx.x; i < H; i += 8 * kAttnThreads) {
+    const u32x4 qa = *reinterpret_cast<const u32x4*>(qkv + r * row3 + i);
+    const uint32_t qd[4] = {qa.x, qa.y, qa.z, qa.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float q0 = bf16_bits_to_float(qd[e] & 0xffffu), q1 = bf16_bits_to_float(qd[e] >> 16);
+      sq += q0 * q0;
+      sq += q1 * q1;
+    }
+#pragma unroll
+    for (int j = 0; j < kRowsMax; ++j) {
+      if (j <= r) {
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(qkv + j * row3 + H + i);
+        const uint32_t kd[4] = {ka.x, ka.y, ka.z, ka.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float k0 = bf16_bits_to_float(kd[e] & 0xffffu), k1 = bf16_bits_to_float(kd[e] >> 16);
+          sk[j] += k0 * k0;
+          sk[j] += k1 * k1;
+        }
+      }
+    }
+  }
+  sq = wave_sum(sq);
+#pragma unroll
+  for (int j = 0; j < kRowsMax; ++j)
+    if (j <= r) sk[j] = wave_sum(sk[j]);
+  if (lane == 0) {
+    red_q[wave] = sq;
+#pragma unroll
+    for (int j = 0; j < kRowsMax; ++j)
+      if (j <= r) red_k[j][wave] = sk[j];
+  }
+  __syncthreads();
+  sq = red_q[0];
+  for (int w = 1; w < kAttnWaves; ++w) sq += red_q[w];
+  const float rq = 1.f / sqrtf(sq / static_cast<float>(H) + eps);
+  const int jp = threadIdx.x;
+  if (jp < half) {
+    const int a = h * D + jp, b = a + half;
+    const float wqa = ld_bf16(qw, a), wqb = ld_bf16(qw, b), wka = ld_bf16(kw, a), wkb = ld_bf16(kw, b);
+    const float fr = inv_freq[jp];
+    for (int j = 0; j <= r; ++j) {
+      const uint16_t* qj = qkv + j * row3;
+      float skj = red_k[j][0];
+      for (int w = 1; w < kAttnWaves; ++w) skj += red_k[j][w];
+      const float rk = 1.f / sqrtf(skj / static_cast<float>(H) + eps);
+      const RopePair rp = rope_pair(ld_bf16(qj, a), ld_bf16(qj, b), ld_bf16(qj + H, a), ld_bf16(qj + H, b), wqa, wqb,
+                                    wka, wkb, fr, pos0 + j, rq, rk);
+      const uint16_t va = qj[2 * H + a], vb = qj[2 * H + b];
+      ks[j * D + jp] = rp.ka;
+      ks[j * D + jp + half] = rp.kb;
+      vs[j * D + jp] = va;
+      vs[j * D + jp + half] = vb;
+      if (j == r) {
+        qs[jp] = rp.qa;
+        qs[jp + half] = rp.qb;
+        if (in_cache) {
+          const int64_t rr = pos_r * D;
+          K[rr + jp] = rp.ka;
+          K[rr + jp + half] = rp.kb;
+          V[rr + jp] = va;
+          V[rr + jp + half] = vb;
+        }
+      }
+    }
+  }
+  __syncthreads();  // qs, ks and vs, written above, are read below
+  // positions pos0 .. pos0 + r (those >= 0) from LDS: ks row t - pos0
+  // (positions at or beyond max_len are not in the cache: none of them is read)
+  const int64_t lo = pos0 < 0 ? 0 : pos0;
+  const bool sub = lo <= pos_r && lo < max_len;
+  const int64_t off = sub ? (lo - pos0) * D : 0;
+  att.run(qs, ks + off, vs + off, sub ? static_cast<int>(lo) : INT_MAX, scale, sc, red_m, red_l, part,
+          out + static_cast<int64_t>(r) * H + static_cast<int64_t>(h) * D);
 }
 
 // Launches of the attention kernels for head_dim = 8 * LPR (LPR = 1, 2, 4, 8, 16 or 32).
@@ -467,12 +591,19 @@ void launch_attention(const void* q, const void* kc, const void* vc, const int64
 
 template <int LPR>
 void launch_rope_attention(const void* qkv, const void* qw, const void* kw, const float* inv_freq, const int64_t* pos,
-                           void* kc, void* vc, void* out, int heads, int max_len, float eps, float scale,
+                           void* kc, void* vc, void* out, int heads, int rows, int max_len, float eps, float scale,
                            hipStream_t st) {
-  rope_attention_kernel<LPR><<<heads, kAttnThreads, 0, st>>>(
-      static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(qw), static_cast<const uint16_t*>(kw),
-      inv_freq, pos, static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), static_cast<uint16_t*>(out), heads,
-      max_len, eps, scale);
+  if (rows == 1) {
+    rope_attention_kernel<LPR><<<heads, kAttnThreads, 0, st>>>(
+        static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(qw), static_cast<const uint16_t*>(kw),
+        inv_freq, pos, static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), static_cast<uint16_t*>(out), heads,
+        max_len, eps, scale);
+  } else {
+    rope_attention_rows_kernel<LPR><<<dim3(heads, rows), kAttnThreads, 0, st>>>(
+        static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(qw), static_cast<const uint16_t*>(kw),
+        inv_freq, pos, static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), static_cast<uint16_t*>(out), heads,
+        max_len, eps, scale);
+  }
 }
 
 constexpr int kNormPer = 8;  // elements per thread kept in registers by norm_residual (n <= kBlock * kNormPer)
@@ -791,17 +922,25 @@ int bp_decode_attention_rows(const void* q, const void* k_cache, const void* v_c
 int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
                              const int64_t* pos, void* k_cache, void* v_cache, void* out, int heads, int head_dim,
                              int max_len, float eps, float scale, void* stream) {
+  return bp_decode_rope_attention_rows(qkv, q_norm_w, k_norm_w, inv_freq, pos, k_cache, v_cache, out, heads, head_dim,
+                                       1, max_len, eps, scale, stream);
+}
+
+int bp_decode_rope_attention_rows(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                                  const int64_t* pos, void* k_cache, void* v_cache, void* out, int heads, int head_dim,
+                                  int rows, int max_len, float eps, float scale, void* stream) {
   if (qkv == nullptr || q_norm_w == nullptr || k_norm_w == nullptr || inv_freq == nullptr || pos == nullptr ||
-      k_cache == nullptr || v_cache == nullptr || out == nullptr || heads <= 0 || max_len <= 0)
+      k_cache == nullptr || v_cache == nullptr || out == nullptr || heads <= 0 || max_len <= 0 || rows <= 0)
     return BP_E_INVALID_ARG;
+  if (rows > bp::kRowsMax) return BP_E_UNSUPPORTED;
   if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256 || bp::kAttnThreads % head_dim != 0 ||
       max_len > bp::kAttnMaxLen)
     return BP_E_UNSUPPORTED;
   if (!bp::aligned16(qkv) || !bp::aligned16(k_cache) || !bp::aligned16(v_cache)) return BP_E_INVALID_ARG;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define BP_ROPE_ATT(L)                                                                                           \
-  bp::launch_rope_attention<L>(qkv, q_norm_w, k_norm_w, inv_freq, pos, k_cache, v_cache, out, heads, max_len, eps, \
-                               scale, st)
+  bp::launch_rope_attention<L>(qkv, q_norm_w, k_norm_w, inv_freq, pos, k_cache, v_cache, out, heads, rows, max_len, \
+                               eps, scale, st)
   switch (head_dim / 8) {
     case 1: BP_ROPE_ATT(1); break;
     case 2: BP_ROPE_ATT(2); break;

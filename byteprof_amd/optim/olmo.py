@@ -33,6 +33,7 @@ from . import skinny as S
 MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
 GATE_UP_WAVES = {"bf16": 4, "int8": 2}  # waves per workgroup of the fused gate|up + SiLU launch
 _CHUNK = {"bf16": 512, "int8": 1024}  # K granularity of the skinny kernels' 16-byte loads
+ROPE_ATTENTION_ROWS = 16  # most rows of one fused q/k-norm + RoPE + cache + attention launch
 
 
 class OptimizeError(RuntimeError):
@@ -222,11 +223,12 @@ class OlmoDecoder:
         for i, w in enumerate(self.layers):
             kc, vc = self.k_cache[i], self.v_cache[i]
             self._mm(x, w["qkv"], self.vqkv[:s])
-            if s == 1:  # one row: the one-token step's fused launch (equal bit for bit to the two below)
-                c(L.bp_decode_rope_attention(self.vqkv.data_ptr(), w["q_norm"].data_ptr(), w["k_norm"].data_ptr(),
-                                             self.inv_freq.data_ptr(), self.v_pos.data_ptr(), kc.data_ptr(),
-                                             vc.data_ptr(), self.vattn.data_ptr(), cfg.heads, D, cfg.max_len,
-                                             cfg.eps, self.scale, st), "bp_decode_rope_attention")
+            if s <= ROPE_ATTENTION_ROWS:  # one fused launch (equal bit for bit to the two below)
+                c(L.bp_decode_rope_attention_rows(self.vqkv.data_ptr(), w["q_norm"].data_ptr(),
+                                                  w["k_norm"].data_ptr(), self.inv_freq.data_ptr(),
+                                                  self.v_pos.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                                  self.vattn.data_ptr(), cfg.heads, D, s, cfg.max_len, cfg.eps,
+                                                  self.scale, st), "bp_decode_rope_attention_rows")
             else:
                 c(L.bp_decode_qk_rope_cache_rows(self.vqkv.data_ptr(), w["q_norm"].data_ptr(),
                                                  w["k_norm"].data_ptr(), self.inv_freq.data_ptr(),

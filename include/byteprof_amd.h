@@ -218,7 +218,9 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  * attention:      per head, positions 0 .. *pos: out = bf16(softmax_fp32(bf16(bf16(q . k) * scale)) as bf16 . v);
  *                 head_dim a multiple of 8 dividing 256, max_len <= 4096; caches 16-byte aligned.
  * rope_attention: qk_rope_cache and attention in one launch (one workgroup per head), equal bit for bit to the
- *                 two launches; qkv 16-byte aligned.
+ *                 two launches; qkv 16-byte aligned. rope_attention_rows: rows (<= 16) consecutive positions
+ *                 *pos .. *pos + rows - 1 (>= 0) in one launch (one workgroup per head and row), equal bit for bit
+ *                 to qk_rope_cache_rows + attention_rows.
  * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
  *                 out may alias residual.
  * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn); silu_mul_rows with
@@ -251,6 +253,9 @@ int bp_decode_attention_rows(const void* q, const void* k_cache, const void* v_c
 int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
                              const int64_t* pos, void* k_cache, void* v_cache, void* out, int heads, int head_dim,
                              int max_len, float eps, float scale, void* stream);
+int bp_decode_rope_attention_rows(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                                  const int64_t* pos, void* k_cache, void* v_cache, void* out, int heads, int head_dim,
+                                  int rows, int max_len, float eps, float scale, void* stream);
 int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
                             void* stream);
 int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* residual, void* out, int n,

@@ -2,7 +2,7 @@
 decode kernels and bp_draft_verify_next).
 
   - every *_rows kernel equals the one-row kernel called at each row's position, bit for bit, and the fused
-    rope_attention equals qk_rope_cache + attention bit for bit;
+    rope_attention (one row) and rope_attention_rows equal qk_rope_cache(_rows) + attention(_rows) bit for bit;
   - the round's end on the device: accepted length, the row tokens, the next round's first token and position;
   - a verify pass of s rows, teacher-forced, against the oracle's sequential decode steps (the decode gate), every s
     from 1 to 9 (the linears on the matrix cores from 5 rows on);
@@ -78,6 +78,46 @@ def test_rope_cache_and_attention_rows_equal_the_one_row_calls(shape):
     torch.cuda.synchronize()
     assert torch.equal(o_c.view(torch.int16), o_b[S - 1].view(torch.int16))
     assert torch.equal(kc_c.view(torch.int16), kc_b.view(torch.int16))
+
+
+ROWS_CFGS = dict(ROPE_CFGS, d256=OG.OlmoConfig(hidden=512, ffn=512, layers=1, heads=2, vocab=512, max_len=300),
+                 d8=OG.OlmoConfig(hidden=64, ffn=512, layers=1, heads=8, vocab=512, max_len=600))
+
+
+@pytest.mark.parametrize("shape,rows,base", [("d64", 1, 0), ("d64", 2, 0), ("d64", 9, 37), ("d64", 16, 100),
+                                             ("d128", 2, 40), ("d128", 9, 40), ("d128", 16, 500),
+                                             ("d256", 5, 296), ("d8", 9, 3), ("d128", 9, 506)])
+def test_fused_rope_attention_rows_equal_the_two_launch_rows(shape, rows, base):
+    """rope_attention_rows (norms, RoPE, cache write and attention of every row in one launch) against
+    qk_rope_cache_rows + attention_rows on the same inputs: outputs and both caches equal bit for bit, also where
+    the last rows fall beyond the cache (base 296 + 5 > 300, 506 + 9 > 512)."""
+    cfg = ROWS_CFGS[shape]
+    oc = _ocfg(cfg)
+    L = _lib.lib()
+    H, D = cfg.hidden, cfg.head_dim
+    rng = np.random.default_rng(rows * 1000 + base)
+    qkv = _bf16(ON.bf16_round(rng.standard_normal((rows, 3 * H)).astype(np.float32)))
+    qw, kw = (_bf16(ON.bf16_round(1 + 0.1 * rng.standard_normal(H).astype(np.float32))) for _ in range(2))
+    cache0 = ON.bf16_round(rng.standard_normal((cfg.heads, cfg.max_len, D)).astype(np.float32))
+    inv = torch.from_numpy(OO.inv_freq(oc)).to(DEV)
+    kc_a, vc_a, kc_b, vc_b = (_bf16(cache0) for _ in range(4))
+    q_a = torch.empty(rows, H, dtype=torch.bfloat16, device=DEV)
+    o_a, o_b = (torch.full((rows, H), 7.0, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+    pos = torch.tensor([base], dtype=torch.int64, device=DEV)
+    _lib.check(L.bp_decode_qk_rope_cache_rows(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), inv.data_ptr(),
+                                              pos.data_ptr(), q_a.data_ptr(), kc_a.data_ptr(), vc_a.data_ptr(),
+                                              cfg.heads, D, cfg.max_len, cfg.eps, rows, _st()), "rows")
+    _lib.check(L.bp_decode_attention_rows(q_a.data_ptr(), kc_a.data_ptr(), vc_a.data_ptr(), pos.data_ptr(),
+                                          o_a.data_ptr(), cfg.heads, D, cfg.max_len, D ** -0.5, rows, _st()), "rows")
+    _lib.check(L.bp_decode_rope_attention_rows(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), inv.data_ptr(),
+                                               pos.data_ptr(), kc_b.data_ptr(), vc_b.data_ptr(), o_b.data_ptr(),
+                                               cfg.heads, D, rows, cfg.max_len, cfg.eps, D ** -0.5, _st()), "fused")
+    torch.cuda.synchronize()
+    for a, b in ((o_a, o_b), (kc_a, kc_b), (vc_a, vc_b)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert _lib.lib().bp_decode_rope_attention_rows(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), inv.data_ptr(),
+                                                    pos.data_ptr(), kc_b.data_ptr(), vc_b.data_ptr(), o_b.data_ptr(),
+                                                    cfg.heads, D, 17, cfg.max_len, cfg.eps, D ** -0.5, _st()) != 0
 
 
 def test_norm_silu_embed_argmax_rows_equal_the_one_row_calls():
