@@ -496,14 +496,39 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_rows_kernel(const
   HeadAttention<LPR, true> att(K, V, static_cast<int>(posc) + 1);
   att.prefetch();
 
+  // RoPE operands of this thread's (row, pair) items: item i = threadIdx.x + p * kAttnThreads is pair i % (D/2) of
+  // row i / (D/2); rows past r load row r (in bounds; not used). All loaded before the first reduction.
+  constexpr int kPass = (kRowsMax * half + kAttnThreads - 1) / kAttnThreads;
+  const int row3 = 3 * H;
+  const int jp = threadIdx.x % half;
+  const int a = h * D + jp, b = a + half;
+  const float wqa = ld_bf16(qw, a), wqb = ld_bf16(qw, b), wka = ld_bf16(kw, a), wkb = ld_bf16(kw, b);
+  const float fr = inv_freq[jp];
+  float f_qa[kPass], f_qb[kPass], f_ka[kPass], f_kb[kPass];
+  uint16_t v_a[kPass], v_b[kPass];
+#pragma unroll
+  for (int p = 0; p < kPass; ++p) {
+    const int j = (threadIdx.x + p * kAttnThreads) / half;
+    const uint16_t* qj = qkv + static_cast<int64_t>(j <= r ? j : r) * row3;
+    f_qa[p] = ld_bf16(qj, a);
+    f_qb[p] = ld_bf16(qj, b);
+    f_ka[p] = ld_bf16(qj + H, a);
+    f_kb[p] = ld_bf16(qj + H, b);
+    v_a[p] = qj[2 * H + a];
+    v_b[p] = qj[2 * H + b];
+  }
+
   // sums of squares of q (row r) and k (rows 0 .. r), each in qk_rms's order
-  const int64_t row3 = 3 * static_cast<int64_t>(H);
   float sq = 0.f;
   float sk[kRowsMax];
 #pragma unroll
   for (int j = 0; j < kRowsMax; ++j) sk[j] = 0.f;
   for (int i = 8 * threadIdx.x; i < H; i += 8 * kAttnThreads) {
-    const u32x4 qa = *reinterpret_cast<const u32x4*>(qkv + r * row3 + i);
+    u32x4 kx[kRowsMax];
+#pragma unroll
+    for (int j = 0; j < kRowsMax; ++j)
+      kx[j] = *reinterpret_cast<const u32x4*>(qkv + static_cast<int64_t>(j <= r ? j : r) * row3 + H + i);
+    const u32x4 qa = *reinterpret_cast<const u32x4*>(qkv + static_cast<int64_t>(r) * row3 + i);
     const uint32_t qd[4] = {qa.x, qa.y, qa.z, qa.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -513,49 +538,41 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_rows_kernel(const
     }
 #pragma unroll
     for (int j = 0; j < kRowsMax; ++j) {
-      if (j <= r) {
-        const u32x4 ka = *reinterpret_cast<const u32x4*>(qkv + j * row3 + H + i);
-        const uint32_t kd[4] = {ka.x, ka.y, ka.z, ka.w};
+      const uint32_t kd[4] = {kx[j].x, kx[j].y, kx[j].z, kx[j].w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float k0 = bf16_bits_to_float(kd[e] & 0xffffu), k1 = bf16_bits_to_float(kd[e] >> 16);
-          sk[j] += k0 * k0;
-          sk[j] += k1 * k1;
-        }
+      for (int e = 0; e < 4; ++e) {
+        const float k0 = bf16_bits_to_float(kd[e] & 0xffffu), k1 = bf16_bits_to_float(kd[e] >> 16);
+        sk[j] += k0 * k0;
+        sk[j] += k1 * k1;
       }
     }
   }
   sq = wave_sum(sq);
+  if (lane == 0) red_q[wave] = sq;
 #pragma unroll
-  for (int j = 0; j < kRowsMax; ++j)
-    if (j <= r) sk[j] = wave_sum(sk[j]);
-  if (lane == 0) {
-    red_q[wave] = sq;
-#pragma unroll
-    for (int j = 0; j < kRowsMax; ++j)
-      if (j <= r) red_k[j][wave] = sk[j];
+  for (int j = 0; j < kRowsMax; ++j) {
+    if (j <= r) {
+      const float t = wave_sum(sk[j]);
+      if (lane == 0) red_k[j][wave] = t;
+    }
   }
   __syncthreads();
   sq = red_q[0];
   for (int w = 1; w < kAttnWaves; ++w) sq += red_q[w];
   const float rq = 1.f / sqrtf(sq / static_cast<float>(H) + eps);
-  const int jp = threadIdx.x;
-  if (jp < half) {
-    const int a = h * D + jp, b = a + half;
-    const float wqa = ld_bf16(qw, a), wqb = ld_bf16(qw, b), wka = ld_bf16(kw, a), wkb = ld_bf16(kw, b);
-    const float fr = inv_freq[jp];
-    for (int j = 0; j <= r; ++j) {
-      const uint16_t* qj = qkv + j * row3;
+#pragma unroll
+  for (int p = 0; p < kPass; ++p) {
+    const int j = (threadIdx.x + p * kAttnThreads) / half;
+    if (j <= r) {
       float skj = red_k[j][0];
       for (int w = 1; w < kAttnWaves; ++w) skj += red_k[j][w];
       const float rk = 1.f / sqrtf(skj / static_cast<float>(H) + eps);
-      const RopePair rp = rope_pair(ld_bf16(qj, a), ld_bf16(qj, b), ld_bf16(qj + H, a), ld_bf16(qj + H, b), wqa, wqb,
-                                    wka, wkb, fr, pos0 + j, rq, rk);
-      const uint16_t va = qj[2 * H + a], vb = qj[2 * H + b];
+      const RopePair rp =
+          rope_pair(f_qa[p], f_qb[p], f_ka[p], f_kb[p], wqa, wqb, wka, wkb, fr, pos0 + j, rq, rk);
       ks[j * D + jp] = rp.ka;
       ks[j * D + jp + half] = rp.kb;
-      vs[j * D + jp] = va;
-      vs[j * D + jp + half] = vb;
+      vs[j * D + jp] = v_a[p];
+      vs[j * D + jp + half] = v_b[p];
       if (j == r) {
         qs[jp] = rp.qa;
         qs[jp + half] = rp.qb;
@@ -563,8 +580,8 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_rows_kernel(const
           const int64_t rr = pos_r * D;
           K[rr + jp] = rp.ka;
           K[rr + jp + half] = rp.kb;
-          V[rr + jp] = va;
-          V[rr + jp + half] = vb;
+          V[rr + jp] = v_a[p];
+          V[rr + jp + half] = v_b[p];
         }
       }
     }
