@@ -42,6 +42,8 @@ SIGNATURES: dict[str, tuple] = {
                                      _c_vp, _c_size, _c_vp]),
     "bp_skinny_mfma_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                      _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "bp_skinny_mfma_silu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
+                                     _c_int, _c_int, _c_vp]),
     "bp_skinny_int4_config_supported": (_c_int, [_c_int, _c_int, _c_int]),
     "bp_skinny_int4": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                 _c_int, _c_vp, _c_size, _c_vp]),

@@ -24,6 +24,8 @@ extern template SkinnyFn skinny_pick<kInt8, 16>(int, int, bool);
 // Matrix-core variant (skinny_mfma.hip): kernel for (kind, 16-row blocks per workgroup, waves, steps in flight
 // per wave), K per step.
 SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth);
+// The same kernels with the SiLU product of interleaved gate|up rows as the epilogue (split 1).
+SkinnyFn mfma_silu_pick(int wkind, int rb, int waves, int depth);
 int mfma_k_step(int wkind);
 // LDS-staged matrix-core variant (depth 3: each wave owns whole blocks; 4: the waves share each block's steps):
 // kernel for (kind, waves, share), largest K slice per workgroup.
@@ -286,6 +288,26 @@ int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int sca
   if (block_rows <= 0 || block_rows % 16 != 0) return BP_E_UNSUPPORTED;
   return bp::skinny_mfma_launch(bp::kInt8, x, q, scale, scale_dtype, y, M, N, K, block_rows / 16, waves, depth,
                                 split, workspace, workspace_bytes, stream);
+}
+
+int bp_skinny_mfma_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
+                        int64_t M, int64_t ffn, int64_t K, int block_rows, int waves, int depth, void* stream) {
+  if (M <= 0 || M > 16 || ffn <= 0 || K <= 0 || x == nullptr || w == nullptr || out == nullptr)
+    return BP_E_INVALID_ARG;
+  if (wkind != bp::kBf16 && wkind != bp::kInt8) return BP_E_UNSUPPORTED;
+  if (wkind == bp::kInt8 && (scale == nullptr || scale_dtype < BP_DT_BF16 || scale_dtype > BP_DT_F32))
+    return BP_E_INVALID_ARG;
+  if (block_rows <= 0 || block_rows % 16 != 0 || K % bp::mfma_k_step(wkind) != 0) return BP_E_UNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0) return BP_E_UNSUPPORTED;
+  bp::SkinnyFn fn = bp::mfma_silu_pick(wkind, block_rows / 16, waves, depth);
+  if (fn == nullptr) return BP_E_UNSUPPORTED;
+  const int64_t N = 2 * ffn;
+  const int64_t tiles = (N + block_rows - 1) / block_rows;
+  if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
+  fn<<<dim3(static_cast<unsigned>(tiles), 1), waves * bp::kWave, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale, scale_dtype,
+      static_cast<uint16_t*>(out), nullptr, static_cast<int>(M), N, K, 1);
+  return bp::launch_status();
 }
 
 int bp_version(void) { return 100; }

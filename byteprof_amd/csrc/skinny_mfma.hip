@@ -99,7 +99,10 @@ struct Operands {
   }
 };
 
-template <int KIND, int RB, int WAVES, int DEPTH>
+// SILU: the gate|up projection with the SiLU product as the epilogue (split 1): w rows 2f / 2f + 1 are the gate /
+// up rows of output f, and y [M, N / 2] receives bf16(bf16(silu(g)) * u) of the rows' bf16-rounded sums g, u (the
+// rounding and formula of the decode loop's silu_mul). A lane's four channels of a tile are two such pairs.
+template <int KIND, int RB, int WAVES, int DEPTH, bool SILU = false>
 __global__ __launch_bounds__(WAVES * kWave) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
                                                                     const uint8_t* __restrict__ w,
                                                                     const void* __restrict__ scale, int scale_dt,
@@ -185,6 +188,22 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mfma_kernel(const uint16
     const int m = l & 15;
     if (m >= M) continue;
     const float tv[4] = {t.x, t.y, t.z, t.w};
+    if constexpr (SILU) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int64_t n = n0 + 16 * rb + 4 * (l >> 4) + 2 * p;  // even: the gate row; n + 1 the up row
+        if (n + 1 >= N) continue;
+        float gv = tv[2 * p], uv = tv[2 * p + 1];
+        if constexpr (KIND == kInt8) {
+          gv *= load_scale(scale, n, scale_dt);
+          uv *= load_scale(scale, n + 1, scale_dt);
+        }
+        const float gb = round_to_bf16(gv);
+        const float a = round_to_bf16(gb / (1.f + expf(-gb)));
+        y[static_cast<int64_t>(m) * (N / 2) + n / 2] = float_to_bf16_bits(a * round_to_bf16(uv));
+      }
+      continue;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t n = n0 + 16 * rb + 4 * (l >> 4) + r;
@@ -390,11 +409,12 @@ SkinnyFn mfma_staged_pick(int wkind, int waves, bool share) {
 
 int mfma_staged_k_max() { return kStageXMax; }
 
-SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth) {
+template <bool SILU>
+SkinnyFn mfma_pick_t(int wkind, int rb, int waves, int depth) {
 #define BP_MFMA_DEPTH(KIND, RB, W)                                     \
   switch (depth) {                                                     \
-    case 1: return &skinny_mfma_kernel<KIND, RB, W, 1>;                \
-    case 2: return &skinny_mfma_kernel<KIND, RB, W, 2>;                \
+    case 1: return &skinny_mfma_kernel<KIND, RB, W, 1, SILU>;          \
+    case 2: return &skinny_mfma_kernel<KIND, RB, W, 2, SILU>;          \
     default: return nullptr;                                           \
   }
 #define BP_MFMA_WAVES(KIND, RB)                \
@@ -419,6 +439,10 @@ SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth) {
 #undef BP_MFMA_WAVES
 #undef BP_MFMA_DEPTH
 }
+
+SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth) { return mfma_pick_t<false>(wkind, rb, waves, depth); }
+
+SkinnyFn mfma_silu_pick(int wkind, int rb, int waves, int depth) { return mfma_pick_t<true>(wkind, rb, waves, depth); }
 
 int mfma_k_step(int wkind) { return wkind == kBf16 ? MfmaLayout<kBf16>::kStep : MfmaLayout<kInt8>::kStep; }
 

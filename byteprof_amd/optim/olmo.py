@@ -187,6 +187,16 @@ class OlmoDecoder:
         """Kernel launches of one step: embed, 7 or 8 per layer, final norm, LM head, argmax."""
         return 4 + (7 if self.gate_up_interleaved else 8) * self.cfg.layers
 
+    def _mfma_silu(self, s: int) -> tuple[int, int, int] | None:
+        """(block_rows, waves, depth) of the matrix-core gate|up launch that skinny_mm makes at s rows when it can
+        take the SiLU epilogue (interleaved rows, depth 1 or 2, split 1), else None."""
+        if not self.gate_up_interleaved or S._bm(s) not in S.MFMA_BUCKETS:
+            return None
+        mc = S.mfma_cfg(self.kind, 2 * self.cfg.ffn, self.cfg.hidden)
+        if mc is None or mc[2] not in (1, 2) or mc[3] != 1:
+            return None
+        return mc[0], mc[1], mc[2]
+
     def verify_buffers(self, smax: int) -> None:
         """Allocates the buffers of verify passes of up to `smax` rows (once; a larger smax reallocates). ids
         [smax] and pos [1] (int64) are the round's inputs: ids[0] the last accepted token, ids[1 ..] the drafts,
@@ -247,6 +257,11 @@ class OlmoDecoder:
                 c(L.bp_decode_gate_up_silu(0 if self.kind == "bf16" else 1, self.vx.data_ptr(), gw[0].data_ptr(),
                                            sc, sdt, self.vact.data_ptr(), F, H, GATE_UP_WAVES[self.kind], st),
                   "bp_decode_gate_up_silu")
+            elif self._mfma_silu(s) is not None:  # the matrix-core gate|up with the SiLU product as its epilogue
+                gw = w["gate_up"]
+                sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
+                c(L.bp_skinny_mfma_silu(0 if self.kind == "bf16" else 1, x.data_ptr(), gw[0].data_ptr(), sc, sdt,
+                                        self.vact.data_ptr(), s, F, H, *self._mfma_silu(s), st), "bp_skinny_mfma_silu")
             else:
                 self._mm(x, w["gate_up"], self.vgu[:s])
                 c(L.bp_decode_silu_mul_rows(self.vgu.data_ptr(), self.vact.data_ptr(), F, s,

@@ -102,6 +102,14 @@ int bp_skinny_mfma_bf16(const void* x, const void* w, void* y, int64_t M, int64_
 int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y,
                         int64_t M, int64_t N, int64_t K, int block_rows, int waves, int depth, int split,
                         void* workspace, size_t workspace_bytes, void* stream);
+/* The gate|up projection of a verify pass (M = 1..16 rows) with the SiLU product as the epilogue of the depth 1 / 2
+ * kernels (split 1): w [2 * ffn, K] (wkind 0 bf16, 1 int8 with per-row scale) with row 2f the gate row f and row
+ * 2f + 1 the up row f; out [M, ffn] = bf16(bf16(silu(g)) * u) of the bf16-rounded row sums, equal bit for bit to
+ * bp_skinny_mfma_* (same block_rows, waves, depth, split 1) followed by bp_decode_silu_mul_rows (interleaved).
+ * Replaces: the gate / up projections and act_fn(gate) * up of HF Olmo2MLP in the verify forward that
+ *           byteprof/optim/olmo_draft.py captures (make_generate_draft). */
+int bp_skinny_mfma_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
+                        int64_t M, int64_t ffn, int64_t K, int block_rows, int waves, int depth, void* stream);
 
 /*
  * int4 group-128 weights in the tile-major format of byteprof's skinny kernels:

@@ -20,6 +20,7 @@ import torch
 from byteprof_amd import _lib
 from byteprof_amd.optim import olmo as OG
 from byteprof_amd.optim import olmo_draft as OD
+from byteprof_amd.quant.hip_int8 import quantize_rowwise_int8
 from oracle import numerics as ON
 from oracle import olmo as OO
 from tests.test_olmo_gpu import GATE, SMALL, _bf16, _np, _ocfg, _small_decoder
@@ -118,6 +119,41 @@ def test_fused_rope_attention_rows_equal_the_two_launch_rows(shape, rows, base):
     assert _lib.lib().bp_decode_rope_attention_rows(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), inv.data_ptr(),
                                                     pos.data_ptr(), kc_b.data_ptr(), vc_b.data_ptr(), o_b.data_ptr(),
                                                     cfg.heads, D, 17, cfg.max_len, cfg.eps, D ** -0.5, _st()) != 0
+
+
+@pytest.mark.parametrize("cfg", [(64, 2, 2), (64, 8, 1), (32, 4, 1), (16, 1, 2)])
+@pytest.mark.parametrize("m", [5, 9, 16])
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_mfma_silu_equals_mfma_then_silu_mul(kind, m, cfg):
+    """The matrix-core gate|up launch with the SiLU epilogue against the same launch (split 1) followed by
+    silu_mul_rows on the interleaved rows: equal bit for bit. F = 1000 leaves a partial last tile."""
+    L = _lib.lib()
+    F, K = 1000, 2048
+    block_rows, waves, depth = cfg
+    rng = np.random.default_rng(m * 7 + waves)
+    x = _bf16(ON.bf16_round(rng.standard_normal((m, K)).astype(np.float32)))
+    w = _bf16(ON.bf16_round(rng.standard_normal((2 * F, K)).astype(np.float32) * 0.05))
+    args = (w,) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
+    sc, sdt = (args[1].data_ptr(), _lib.TORCH_DT[torch.float16]) if kind == "int8" else (None, 0)
+    out = torch.full((m, F), 3.0, dtype=torch.bfloat16, device=DEV)
+    _lib.check(L.bp_skinny_mfma_silu(0 if kind == "bf16" else 1, x.data_ptr(), args[0].data_ptr(), sc, sdt,
+                                     out.data_ptr(), m, F, K, block_rows, waves, depth, _st()), "mfma_silu")
+    gu = torch.empty(m, 2 * F, dtype=torch.bfloat16, device=DEV)
+    if kind == "bf16":
+        rc = L.bp_skinny_mfma_bf16(x.data_ptr(), w.data_ptr(), gu.data_ptr(), m, 2 * F, K, block_rows, waves,
+                                   depth, 1, None, 0, _st())
+    else:
+        rc = L.bp_skinny_mfma_int8(x.data_ptr(), args[0].data_ptr(), sc, sdt, gu.data_ptr(), m, 2 * F, K,
+                                   block_rows, waves, depth, 1, None, 0, _st())
+    _lib.check(rc, "mfma")
+    ref = torch.empty(m, F, dtype=torch.bfloat16, device=DEV)
+    _lib.check(L.bp_decode_silu_mul_rows(gu.data_ptr(), ref.data_ptr(), F, m, 1, _st()), "silu_mul_rows")
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert L.bp_skinny_mfma_silu(0, x.data_ptr(), w.data_ptr(), None, 0, out.data_ptr(), m, F, K, block_rows, waves,
+                                 3, _st()) == -2
+    assert L.bp_skinny_mfma_silu(0, x.data_ptr(), w.data_ptr(), None, 0, out.data_ptr(), 17, F, K, block_rows,
+                                 waves, depth, _st()) == -1
 
 
 def test_norm_silu_embed_argmax_rows_equal_the_one_row_calls():
