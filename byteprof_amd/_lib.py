@@ -42,6 +42,8 @@ SIGNATURES: dict[str, tuple] = {
                                      _c_vp, _c_size, _c_vp]),
     "bp_skinny_mfma_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                      _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "bp_skinny_mfma_partials": (_c_int, [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+                                         _c_int, _c_vp, _c_size, _c_vp]),
     "bp_skinny_mfma_silu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                      _c_int, _c_int, _c_vp]),
     "bp_skinny_int4_config_supported": (_c_int, [_c_int, _c_int, _c_int]),
@@ -66,6 +68,8 @@ SIGNATURES: dict[str, tuple] = {
                                           _c_int, _c_float, _c_float, _c_vp]),
     "bp_decode_rope_attention_rows": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int,
                                                _c_int, _c_int, _c_int, _c_float, _c_float, _c_vp]),
+    "bp_decode_splitk_norm_residual_rows": (_c_int, [_c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_int,
+                                                     _c_float, _c_int, _c_vp]),
     "bp_decode_norm_residual": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_float, _c_vp]),
     "bp_decode_silu_mul": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp]),
     "bp_decode_argmax_scratch_bytes": (_c_size, []),

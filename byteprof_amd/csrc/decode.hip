@@ -675,6 +675,46 @@ __global__ __launch_bounds__(kBlock) void norm_residual_kernel(const uint16_t* _
   }
 }
 
+// The split-K reduce of a projection's partials (ws [split][rows][n], added in split order, the int8 scale applied
+// to the sum, rounded to bf16: splitk_reduce_kernel's arithmetic) feeding norm_residual_kernel's register path in the
+// same workgroup (grid = rows, n <= kBlock * kNormPer): out = bf16(residual + bf16(w * y * rsqrt(mean(y^2) + eps))),
+// equal bit for bit to the two launches; out may alias residual.
+__global__ __launch_bounds__(kBlock) void splitk_norm_residual_kernel(const float* __restrict__ ws, int split,
+                                                                      const void* __restrict__ scale, int scale_dt,
+                                                                      const uint16_t* __restrict__ w,
+                                                                      const uint16_t* residual, uint16_t* out, int n,
+                                                                      float eps) {
+  __shared__ float red[kBlock / kWave];
+  const int64_t total = static_cast<int64_t>(gridDim.x) * n;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * n;
+  float xv[kNormPer], wv[kNormPer], rv[kNormPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < kNormPer; ++e) {
+    const int i = threadIdx.x + e * blockDim.x;
+    xv[e] = wv[e] = rv[e] = 0.f;
+    if (i < n) {
+      float t = ws[row + i];
+      for (int s = 1; s < split; ++s) t += ws[s * total + row + i];
+      if (scale != nullptr) t *= load_scale(scale, i, scale_dt);
+      xv[e] = round_to_bf16(t);
+      wv[e] = ld_bf16(w, i);
+      if (residual != nullptr) rv[e] = ld_bf16(residual, row + i);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < kNormPer; ++e) ss += xv[e] * xv[e];
+  const float r = 1.f / sqrtf(block_sum(ss, red) / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int e = 0; e < kNormPer; ++e) {
+    const int i = threadIdx.x + e * blockDim.x;
+    if (i < n) {
+      const float y = round_to_bf16(wv[e] * (xv[e] * r));
+      out[row + i] = float_to_bf16_bits(residual != nullptr ? rv[e] + y : y);
+    }
+  }
+}
+
 // out[r, f] = bf16(bf16(silu(g)) * u) for rows r of gu [rows, 2F]: g = gu[r, f], u = gu[r, F + f] (concatenated
 // halves) or g = gu[r, 2f], u = gu[r, 2f + 1] (interleaved rows of the weight).
 __global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out, int F, int rows,
@@ -976,6 +1016,19 @@ int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* 
   if (x == nullptr || weight == nullptr || out == nullptr || n <= 0 || rows <= 0) return BP_E_INVALID_ARG;
   bp::norm_residual_kernel<<<rows, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight),
+      static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), n, eps);
+  return bp::status();
+}
+
+int bp_decode_splitk_norm_residual_rows(const float* workspace, int split, const void* scale, int scale_dtype,
+                                        const void* weight, const void* residual, void* out, int n, float eps,
+                                        int rows, void* stream) {
+  if (workspace == nullptr || weight == nullptr || out == nullptr || n <= 0 || rows <= 0 || split < 1)
+    return BP_E_INVALID_ARG;
+  if (scale != nullptr && (scale_dtype < BP_DT_BF16 || scale_dtype > BP_DT_F32)) return BP_E_INVALID_ARG;
+  if (n > bp::kBlock * bp::kNormPer) return BP_E_UNSUPPORTED;
+  bp::splitk_norm_residual_kernel<<<rows, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+      workspace, split, scale, scale_dtype, static_cast<const uint16_t*>(weight),
       static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), n, eps);
   return bp::status();
 }

@@ -175,13 +175,15 @@ int skinny_mfma_staged_launch(int wkind, const void* x, const void* w, const voi
   return launch_status();
 }
 
+// partials_only: with split > 1, stop after the partial sums (the caller reduces the workspace).
 int skinny_mfma_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y,
                        int64_t M, int64_t N, int64_t K, int rb, int waves, int depth, int split, void* ws,
-                       size_t ws_bytes, void* stream) {
+                       size_t ws_bytes, void* stream, bool partials_only = false) {
   if (M < 0 || N < 0 || K < 0 || M > 16) return BP_E_INVALID_ARG;
   if (M == 0 || N == 0) return BP_OK;
   if (x == nullptr || w == nullptr || y == nullptr) return BP_E_INVALID_ARG;
-  if (wkind == kInt8 && (scale == nullptr || scale_dt < BP_DT_BF16 || scale_dt > BP_DT_F32)) return BP_E_INVALID_ARG;
+  if (wkind == kInt8 && !partials_only && (scale == nullptr || scale_dt < BP_DT_BF16 || scale_dt > BP_DT_F32))
+    return BP_E_INVALID_ARG;
   if (split < 1 || split > 1024) return BP_E_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (K == 0) {
@@ -207,7 +209,7 @@ int skinny_mfma_launch(int wkind, const void* x, const void* w, const void* scal
                                      scale_dt, static_cast<uint16_t*>(y), static_cast<float*>(ws),
                                      static_cast<int>(M), N, K, split);
   const int rc = launch_status();
-  if (rc != BP_OK || split == 1) return rc;
+  if (rc != BP_OK || split == 1 || partials_only) return rc;
   splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
                                                        wkind == kInt8 ? scale : nullptr, scale_dt, M, N, split);
   return launch_status();
@@ -288,6 +290,19 @@ int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int sca
   if (block_rows <= 0 || block_rows % 16 != 0) return BP_E_UNSUPPORTED;
   return bp::skinny_mfma_launch(bp::kInt8, x, q, scale, scale_dtype, y, M, N, K, block_rows / 16, waves, depth,
                                 split, workspace, workspace_bytes, stream);
+}
+
+int bp_skinny_mfma_partials(int wkind, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int block_rows,
+                            int waves, int depth, int split, void* workspace, size_t workspace_bytes, void* stream) {
+  if (block_rows <= 0 || block_rows % 16 != 0 || (depth != 1 && depth != 2) || M <= 0 || N <= 0) return BP_E_UNSUPPORTED;
+  if (wkind != bp::kBf16 && wkind != bp::kInt8) return BP_E_UNSUPPORTED;
+  if (K <= 0 || K % bp::mfma_k_step(wkind) != 0 || split < 2 || split > K / bp::mfma_k_step(wkind))
+    return BP_E_UNSUPPORTED;
+  if (workspace == nullptr) return BP_E_WORKSPACE;
+  // y is not written with partials_only (the launch's checks want a non-null pointer); the int8 scale is the
+  // reducer's to apply
+  return bp::skinny_mfma_launch(wkind, x, w, nullptr, 0, workspace, M, N, K, block_rows / 16, waves, depth, split,
+                                workspace, workspace_bytes, stream, true);
 }
 
 int bp_skinny_mfma_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,

@@ -197,6 +197,18 @@ class OlmoDecoder:
             return None
         return mc[0], mc[1], mc[2]
 
+    def _mfma_splitk(self, s: int) -> tuple[int, int, int, int] | None:
+        """(block_rows, waves, depth, split) of the matrix-core down launch that skinny_mm makes at s rows when it
+        is a split-K launch of depth 1 or 2 (its reduce can feed the norm), else None."""
+        H, F = self.cfg.hidden, self.cfg.ffn
+        if S._bm(s) not in S.MFMA_BUCKETS or H > 8192 or self.vact.data_ptr() % 16:
+            return None
+        mc = S.mfma_cfg(self.kind, H, F)
+        if mc is None or mc[2] not in (1, 2):
+            return None
+        split = max(1, min(mc[3], F // S.mfma_k_step(self.kind)))
+        return (mc[0], mc[1], mc[2], split) if split > 1 else None
+
     def verify_buffers(self, smax: int) -> None:
         """Allocates the buffers of verify passes of up to `smax` rows (once; a larger smax reallocates). ids
         [smax] and pos [1] (int64) are the round's inputs: ids[0] the last accepted token, ids[1 ..] the drafts,
@@ -213,6 +225,9 @@ class OlmoDecoder:
         self.vx, self.vq, self.vattn, self.vo, self.vdn, self.vxn = (z(smax, H) for _ in range(6))
         self.vqkv, self.vgu, self.vact, self.vlogits = z(smax, 3 * H), z(smax, 2 * F), z(smax, F), z(smax, V)
         self.v_argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_rows_scratch_bytes(smax) // 4), dtype=torch.int32)
+        mc = S.mfma_cfg(self.kind, H, F)
+        split = max(1, min(mc[3], F // S.mfma_k_step(self.kind))) if mc is not None else 1
+        self.vws = torch.empty(split * smax * H, dtype=torch.float32, device=dev)  # the down launch's partials
 
     def verify(self, s: int) -> None:
         """One verify pass of s = 1 + drafts rows (the reference's captured draft step, olmo_draft.py
@@ -266,9 +281,20 @@ class OlmoDecoder:
                 self._mm(x, w["gate_up"], self.vgu[:s])
                 c(L.bp_decode_silu_mul_rows(self.vgu.data_ptr(), self.vact.data_ptr(), F, s,
                                             int(self.gate_up_interleaved), st), "bp_decode_silu_mul_rows")
-            self._mm(self.vact[:s], w["down"], self.vdn[:s])
-            c(L.bp_decode_norm_residual_rows(self.vdn.data_ptr(), w["post_ff"].data_ptr(), self.vx.data_ptr(),
-                                             self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
+            dc = self._mfma_splitk(s)
+            if dc is not None:  # split-K on the matrix cores; the reduce feeds the norm in one launch
+                dw = w["down"]
+                c(L.bp_skinny_mfma_partials(0 if self.kind == "bf16" else 1, self.vact.data_ptr(), dw[0].data_ptr(),
+                                            s, H, F, *dc, self.vws.data_ptr(), self.vws.numel() * 4, st),
+                  "bp_skinny_mfma_partials")
+                sc, sdt = (dw[1].data_ptr(), _lib.TORCH_DT[dw[1].dtype]) if self.kind == "int8" else (None, 0)
+                c(L.bp_decode_splitk_norm_residual_rows(self.vws.data_ptr(), dc[3], sc, sdt, w["post_ff"].data_ptr(),
+                                                        self.vx.data_ptr(), self.vx.data_ptr(), H, cfg.eps, s, st),
+                  "bp_decode_splitk_norm_residual_rows")
+            else:
+                self._mm(self.vact[:s], w["down"], self.vdn[:s])
+                c(L.bp_decode_norm_residual_rows(self.vdn.data_ptr(), w["post_ff"].data_ptr(), self.vx.data_ptr(),
+                                                 self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
         c(L.bp_decode_norm_residual_rows(self.vx.data_ptr(), self.norm.data_ptr(), None, self.vxn.data_ptr(), H,
                                          cfg.eps, s, st), "bp_decode_norm_residual_rows")
         self._mm(self.vxn[:s], self.lm_head, self.vlogits[:s])

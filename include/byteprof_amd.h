@@ -108,6 +108,10 @@ int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int sca
  * bp_skinny_mfma_* (same block_rows, waves, depth, split 1) followed by bp_decode_silu_mul_rows (interleaved).
  * Replaces: the gate / up projections and act_fn(gate) * up of HF Olmo2MLP in the verify forward that
  *           byteprof/optim/olmo_draft.py captures (make_generate_draft). */
+/* bp_skinny_mfma_* (depth 1 or 2, split >= 2) stopped after the partial sums: workspace [split][M][N] fp32 (unscaled
+ * for int8: the reducer applies the scale), e.g. for bp_decode_splitk_norm_residual_rows. */
+int bp_skinny_mfma_partials(int wkind, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int block_rows,
+                            int waves, int depth, int split, void* workspace, size_t workspace_bytes, void* stream);
 int bp_skinny_mfma_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
                         int64_t M, int64_t ffn, int64_t K, int block_rows, int waves, int depth, void* stream);
 
@@ -230,7 +234,9 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  *                 *pos .. *pos + rows - 1 (>= 0) in one launch (one workgroup per head and row), equal bit for bit
  *                 to qk_rope_cache_rows + attention_rows.
  * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
- *                 out may alias residual.
+ *                 out may alias residual. splitk_norm_residual_rows: x = the split-K reduce of a projection's
+ *                 partials (workspace [split][rows][n] from bp_skinny_mfma_partials, the int8 scale [n] applied,
+ *                 NULL for bf16), equal bit for bit to bp_splitk_reduce + norm_residual_rows; n <= 8192.
  * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn); silu_mul_rows with
  *                 interleaved = 1 reads the pairs (gate_up[2f], gate_up[2f + 1]) instead.
  * gate_up_silu:   the gate|up projection of x[hidden] and silu_mul in one launch: w [2 * ffn, hidden] (wkind
@@ -264,6 +270,9 @@ int bp_decode_rope_attention(const void* qkv, const void* q_norm_w, const void* 
 int bp_decode_rope_attention_rows(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
                                   const int64_t* pos, void* k_cache, void* v_cache, void* out, int heads, int head_dim,
                                   int rows, int max_len, float eps, float scale, void* stream);
+int bp_decode_splitk_norm_residual_rows(const float* workspace, int split, const void* scale, int scale_dtype,
+                                        const void* weight, const void* residual, void* out, int n, float eps,
+                                        int rows, void* stream);
 int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
                             void* stream);
 int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* residual, void* out, int n,

@@ -156,6 +156,49 @@ def test_mfma_silu_equals_mfma_then_silu_mul(kind, m, cfg):
                                  waves, depth, _st()) == -1
 
 
+@pytest.mark.parametrize("cfg", [(32, 2, 2, 4), (32, 8, 2, 4), (16, 4, 1, 8), (64, 1, 1, 2)])
+@pytest.mark.parametrize("m", [5, 9, 16])
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_splitk_norm_residual_equals_reduce_then_norm(kind, m, cfg):
+    """The down projection of a verify pass: the split-K partials reduced inside the norm launch, against the
+    matrix-core launch with its own reduce followed by norm_residual_rows: equal bit for bit (in place on the
+    residual, as the decoder runs it)."""
+    L = _lib.lib()
+    H, F = 2048, 8192
+    block_rows, waves, depth, split = cfg
+    rng = np.random.default_rng(m * 11 + waves + split)
+    x = _bf16(ON.bf16_round(rng.standard_normal((m, F)).astype(np.float32)))
+    w = _bf16(ON.bf16_round(rng.standard_normal((H, F)).astype(np.float32) * 0.02))
+    nw = _bf16(ON.bf16_round(1 + 0.1 * rng.standard_normal(H).astype(np.float32)))
+    r0 = _bf16(ON.bf16_round(rng.standard_normal((m, H)).astype(np.float32)))
+    args = (w,) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
+    sc, sdt = (args[1].data_ptr(), _lib.TORCH_DT[torch.float16]) if kind == "int8" else (None, 0)
+    kc = 0 if kind == "bf16" else 1
+    ws = torch.empty(split * m * H, dtype=torch.float32, device=DEV)
+    ra, rb = r0.clone(), r0.clone()
+    _lib.check(L.bp_skinny_mfma_partials(kc, x.data_ptr(), args[0].data_ptr(), m, H, F, block_rows, waves, depth,
+                                         split, ws.data_ptr(), ws.numel() * 4, _st()), "partials")
+    _lib.check(L.bp_decode_splitk_norm_residual_rows(ws.data_ptr(), split, sc, sdt, nw.data_ptr(), ra.data_ptr(),
+                                                     ra.data_ptr(), H, 1e-6, m, _st()), "splitk_norm")
+    y = torch.empty(m, H, dtype=torch.bfloat16, device=DEV)
+    ws2 = torch.empty_like(ws)
+    if kind == "bf16":
+        rc = L.bp_skinny_mfma_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, H, F, block_rows, waves, depth,
+                                   split, ws2.data_ptr(), ws2.numel() * 4, _st())
+    else:
+        rc = L.bp_skinny_mfma_int8(x.data_ptr(), args[0].data_ptr(), sc, sdt, y.data_ptr(), m, H, F, block_rows,
+                                   waves, depth, split, ws2.data_ptr(), ws2.numel() * 4, _st())
+    _lib.check(rc, "mfma")
+    _lib.check(L.bp_decode_norm_residual_rows(y.data_ptr(), nw.data_ptr(), rb.data_ptr(), rb.data_ptr(), H, 1e-6, m,
+                                              _st()), "norm_rows")
+    torch.cuda.synchronize()
+    assert torch.equal(ra.view(torch.int16), rb.view(torch.int16))
+    assert L.bp_skinny_mfma_partials(kc, x.data_ptr(), args[0].data_ptr(), m, H, F, block_rows, waves, depth, 1,
+                                     ws.data_ptr(), ws.numel() * 4, _st()) == -2
+    assert L.bp_skinny_mfma_partials(kc, x.data_ptr(), args[0].data_ptr(), m, H, F, block_rows, waves, depth, split,
+                                     ws.data_ptr(), 16, _st()) == -3
+
+
 def test_norm_silu_embed_argmax_rows_equal_the_one_row_calls():
     L = _lib.lib()
     rng = np.random.default_rng(5)
