@@ -820,7 +820,7 @@ __device__ __forceinline__ void wave_take(float& best, int& idx) {
 
 constexpr int kArgmaxRowWords = 2 * kArgmaxBlocks + 1;  // scratch words per row: values, indices, counter
 
-// grid = (kArgmaxBlocks, rows): for row r of logits [rows, V], kArgmaxBlocks workgroups each take an even share
+// grid = (G, rows), G <= kArgmaxBlocks: for row r of logits [rows, V], G workgroups each take an even share
 // (vec: 16-byte aligned rows, 8 logits per load; the V % 8 tail and, when not vec, every element one at a time);
 // each writes its (value, index) to the row's scratch, and the last workgroup of the row to finish (a ticket
 // counter, reset by that workgroup) folds them and writes tok[r]; with pos (one row only), it also advances *pos.
@@ -1086,7 +1086,10 @@ int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* 
 int bp_decode_argmax_rows(const void* logits, int vocab, int rows, int64_t* tok, void* scratch, void* stream) {
   if (logits == nullptr || tok == nullptr || scratch == nullptr || vocab <= 0 || rows <= 0) return BP_E_INVALID_ARG;
   const int vec = bp::aligned16(logits) && (rows == 1 || vocab % 8 == 0) ? 1 : 0;
-  bp::argmax_next_kernel<<<dim3(bp::kArgmaxBlocks, rows), bp::kArgmaxThreads, 0,
+  // about kArgmaxBlocks workgroups in all: each ends with a device-scope release fence, whose cost grows with their
+  // number (the result does not depend on the split: the fold is exact)
+  const int per_row = bp::kArgmaxBlocks / rows > 4 ? bp::kArgmaxBlocks / rows : 4;
+  bp::argmax_next_kernel<<<dim3(per_row, rows), bp::kArgmaxThreads, 0,
                            static_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t*>(logits), vocab, vec, tok,
                                                                nullptr, static_cast<uint32_t*>(scratch));
   return bp::status();
