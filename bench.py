@@ -256,7 +256,7 @@ def sweep(device) -> dict:
                 g = D.capture([lambda w=w: S.skinny_mm(x, w, out=y) for w in ring])
                 us = statistics.median(D.time_replays(g, 2, 5)) * 1000.0 / len(ring)
                 del g
-                fam = "mfma" if S._bm(m) in S.MFMA_BUCKETS and S.mfma_cfg("bf16", n, k) is not None else "valu"
+                fam = "mf"
                 cell[str(m)] = {"us": round(us, 2), "gbs": round((per + 2 * m * (n + k)) / us / 1e3), "kernel": fam}
             out[f"{n}x{k}"] = cell
             del ring

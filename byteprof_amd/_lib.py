@@ -36,16 +36,15 @@ SIGNATURES: dict[str, tuple] = {
                                 _c_vp]),
     "bp_skinny_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
                                 _c_vp, _c_size, _c_vp]),
-    "bp_skinny_mfma_config_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
-    "bp_skinny_mfma_k_step": (_c_int, [_c_int]),
-    "bp_skinny_mfma_bf16": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
-                                     _c_vp, _c_size, _c_vp]),
-    "bp_skinny_mfma_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
-                                     _c_int, _c_int, _c_vp, _c_size, _c_vp]),
-    "bp_skinny_mfma_partials": (_c_int, [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
-                                         _c_int, _c_vp, _c_size, _c_vp]),
-    "bp_skinny_mfma_silu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
-                                     _c_int, _c_int, _c_vp]),
+    "bp_skinny_mf_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "bp_skinny_mf_k_segment": (_c_int, [_c_int]),
+    "bp_skinny_mf_stage_bytes": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
+    "bp_skinny_mf": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+                              _c_int, _c_vp, _c_size, _c_vp]),
+    "bp_skinny_mf_partials": (_c_int, [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                       _c_vp, _c_size, _c_vp]),
+    "bp_skinny_mf_silu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                   _c_int, _c_vp]),
     "bp_skinny_int4_config_supported": (_c_int, [_c_int, _c_int, _c_int]),
     "bp_skinny_int4": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                 _c_int, _c_vp, _c_size, _c_vp]),
@@ -73,7 +72,6 @@ SIGNATURES: dict[str, tuple] = {
     "bp_decode_norm_residual": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_float, _c_vp]),
     "bp_decode_silu_mul": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp]),
     "bp_decode_argmax_scratch_bytes": (_c_size, []),
-    "bp_decode_gate_up_silu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
     "bp_decode_argmax_next": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp]),
     "bp_decode_embed_rows": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_i64, _c_vp]),
     "bp_decode_qk_rope_cache_rows": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int,

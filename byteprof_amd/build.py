@@ -46,11 +46,11 @@ def units() -> list[tuple[Path, list[str], Path]]:
     out = [(CSRC / "skinny.hip", [], BUILD_DIR / "skinny.o"),
            (CSRC / "mlstm.hip", [], BUILD_DIR / "mlstm.o"),
            (CSRC / "linear_set.hip", [], BUILD_DIR / "linear_set.o"),
-           (CSRC / "skinny_mfma.hip", [], BUILD_DIR / "skinny_mfma.o"),
            (CSRC / "skinny_int4.hip", [], BUILD_DIR / "skinny_int4.o"),
            (CSRC / "draft.hip", [], BUILD_DIR / "draft.o"),
            (CSRC / "decode.hip", [], BUILD_DIR / "decode.o"),
-           (CSRC / "skinny_group.hip", [], BUILD_DIR / "skinny_group.o")]
+           (CSRC / "skinny_group.hip", [], BUILD_DIR / "skinny_group.o"),
+           (CSRC / "skinny_mf.hip", [], BUILD_DIR / "skinny_mf.o")]
     for kind in KINDS:
         for mt in ROW_BUCKETS:
             out.append((CSRC / "skinny_inst.hip", [f"-DBP_KIND={kind}", f"-DBP_MT={mt}"],

@@ -10,8 +10,6 @@
 //                   out = bf16(sum_t p_t v_t)
 //   norm_residual   out <- bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))) (no residual: the plain norm)
 //   silu_mul        out <- bf16(bf16(silu(g)) * u), g and u the two halves of the fused gate|up projection
-//   gate_up_silu    the gate|up projection and silu_mul in one launch, over a weight whose rows interleave gate
-//                   and up (row 2n gate n, row 2n + 1 up n): each workgroup computes one (gate, up) pair
 //   argmax_next     tok <- first index of the largest logit (NaN counts as largest); pos <- pos + 1
 //
 // The roundings are those of transformers' Olmo2ForCausalLM run in bf16 with the eager attention, the model whose
@@ -731,65 +729,6 @@ __global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __res
   }
 }
 
-// The gate|up projection at one activation row with the SiLU product as its epilogue. w: [2F, K] with row 2n the
-// gate row n and row 2n + 1 the up row n (int8: scale [2F] in the same order). Workgroup n computes rows 2n and
-// 2n + 1 exactly as skinny_dot_kernel<KIND, 1, 2, WAVES> does (the same helpers in the same order: bitwise the
-// skinny outputs g_n, u_n, each rounded to bf16), then out[n] = bf16(bf16(silu(g_n)) * u_n) as silu_mul_kernel.
-// K a multiple of the 1 KiB chunk (512 bf16 / 1024 int8), x and w 16-byte aligned.
-template <int KIND, int WAVES>
-__global__ __launch_bounds__(WAVES * kWave) void gate_up_silu_kernel(const uint16_t* __restrict__ x,
-                                                                     const uint8_t* __restrict__ w,
-                                                                     const void* __restrict__ scale, int scale_dt,
-                                                                     uint16_t* __restrict__ out, int K) {
-  using L = Layout<KIND>;
-  __shared__ float red[WAVES][2];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int64_t row0 = 2 * static_cast<int64_t>(blockIdx.x);
-  const int nch = K / L::kChunk;
-  float acc[2] = {0.f, 0.f};
-  for (int c = wave; c < nch; c += WAVES) {
-    const int64_t k0 = static_cast<int64_t>(c) * L::kChunk + static_cast<int64_t>(lane) * L::kEpl;
-    const u32x4 w0 = load_w<KIND, true>(w, row0, K, k0);
-    const u32x4 w1 = load_w<KIND, true>(w, row0 + 1, K, k0);
-    uint32_t xv[L::kXDwords];
-    load_x<KIND, true>(x, K, k0, xv);
-    acc[0] = chunk_dot<KIND>(w0, xv, acc[0]);
-    acc[1] = chunk_dot<KIND>(w1, xv, acc[1]);
-  }
-  wave_transpose_reduce<2>(acc, lane);
-  // lane l holds the wave total of row l / 32
-  if ((lane & 31) == 0) red[wave][lane / 32] = acc[0];
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float t[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      t[r] = red[0][r];
-#pragma unroll
-      for (int v = 1; v < WAVES; ++v) t[r] += red[v][r];
-      if constexpr (KIND == kInt8) t[r] *= load_scale(scale, row0 + r, scale_dt);
-    }
-    const float g = round_to_bf16(t[0]);
-    const float u = round_to_bf16(t[1]);
-    const float a = round_to_bf16(g / (1.f + expf(-g)));
-    out[blockIdx.x] = float_to_bf16_bits(a * u);
-  }
-}
-
-using GateUpFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, uint16_t*, int);
-
-template <int KIND>
-GateUpFn gate_up_pick(int waves) {
-  switch (waves) {
-    case 1: return &gate_up_silu_kernel<KIND, 1>;
-    case 2: return &gate_up_silu_kernel<KIND, 2>;
-    case 4: return &gate_up_silu_kernel<KIND, 4>;
-    case 8: return &gate_up_silu_kernel<KIND, 8>;
-    default: return nullptr;
-  }
-}
-
 // (value, index) order of torch.argmax: NaN first, then the larger value, then the smaller index.
 __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
   const bool na = a != a, nb = b != b;
@@ -1036,23 +975,6 @@ int bp_decode_splitk_norm_residual_rows(const float* workspace, int split, const
 int bp_decode_norm_residual(const void* x, const void* weight, const void* residual, void* out, int n, float eps,
                             void* stream) {
   return bp_decode_norm_residual_rows(x, weight, residual, out, n, eps, 1, stream);
-}
-
-int bp_decode_gate_up_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
-                           int ffn, int hidden, int waves, void* stream) {
-  if (x == nullptr || w == nullptr || out == nullptr || ffn <= 0 || hidden <= 0) return BP_E_INVALID_ARG;
-  if (wkind != bp::kBf16 && wkind != bp::kInt8) return BP_E_UNSUPPORTED;
-  if (wkind == bp::kInt8 && (scale == nullptr || scale_dtype < BP_DT_BF16 || scale_dtype > BP_DT_F32))
-    return BP_E_INVALID_ARG;
-  const int chunk = wkind == bp::kBf16 ? bp::Layout<bp::kBf16>::kChunk : bp::Layout<bp::kInt8>::kChunk;
-  if (hidden % chunk != 0) return BP_E_UNSUPPORTED;
-  if (!bp::aligned16(x) || !bp::aligned16(w)) return BP_E_INVALID_ARG;
-  bp::GateUpFn fn = wkind == bp::kBf16 ? bp::gate_up_pick<bp::kBf16>(waves) : bp::gate_up_pick<bp::kInt8>(waves);
-  if (fn == nullptr) return BP_E_UNSUPPORTED;
-  fn<<<ffn, waves * bp::kWave, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale, scale_dtype,
-      static_cast<uint16_t*>(out), hidden);
-  return bp::status();
 }
 
 int bp_decode_silu_mul_rows(const void* gate_up, void* out, int ffn, int rows, int interleaved, void* stream) {

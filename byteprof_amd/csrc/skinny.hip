@@ -21,17 +21,6 @@ extern template SkinnyFn skinny_pick<kInt8, 4>(int, int, bool);
 extern template SkinnyFn skinny_pick<kInt8, 8>(int, int, bool);
 extern template SkinnyFn skinny_pick<kInt8, 16>(int, int, bool);
 
-// Matrix-core variant (skinny_mfma.hip): kernel for (kind, 16-row blocks per workgroup, waves, steps in flight
-// per wave), K per step.
-SkinnyFn mfma_pick(int wkind, int rb, int waves, int depth);
-// The same kernels with the SiLU product of interleaved gate|up rows as the epilogue (split 1).
-SkinnyFn mfma_silu_pick(int wkind, int rb, int waves, int depth);
-int mfma_k_step(int wkind);
-// LDS-staged matrix-core variant (depth 3: each wave owns whole blocks; 4: the waves share each block's steps):
-// kernel for (kind, waves, share), largest K slice per workgroup.
-SkinnyFn mfma_staged_pick(int wkind, int waves, bool share);
-int mfma_staged_k_max();
-
 // int4 group-128 kernels (skinny_int4.hip).
 using Int4Fn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
                         int64_t, int64_t, int);
@@ -133,88 +122,6 @@ int skinny_launch(int wkind, const void* x, const void* w, const void* scale, in
   return launch_status();
 }
 
-// Compute units of the current device (cached per device; 0 when the query fails).
-int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < 64 && cache[dev] > 0) return cache[dev];
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev < 64) cache[dev] = cus;
-  return cus;
-}
-
-// The staged variant: 16-row blocks only; each workgroup stages K / split activations (at most mfma_staged_k_max(),
-// K / split a multiple of the 1 KiB step, and the steps of a slice a multiple or a divisor of the waves) and loops
-// over rounds of row blocks; one workgroup per CU (LDS).
-int skinny_mfma_staged_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y,
-                              int64_t M, int64_t N, int64_t K, int rb, int waves, bool share, int split, void* ws,
-                              size_t ws_bytes, hipStream_t st) {
-  SkinnyFn fn = mfma_staged_pick(wkind, waves, share);
-  if (fn == nullptr || rb != 1) return BP_E_UNSUPPORTED;
-  const int64_t step = wkind == kBf16 ? 512 : 1024;
-  if (K % (static_cast<int64_t>(split) * step) != 0 || K / split > mfma_staged_k_max()) return BP_E_UNSUPPORTED;
-  const int64_t nsteps = K / split / step;
-  if (share && nsteps % waves != 0 && waves % nsteps != 0) return BP_E_UNSUPPORTED;
-  const int64_t per_round = share ? waves / std::min<int64_t>(waves, nsteps) : waves;  // blocks per round
-  if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
-    return BP_E_WORKSPACE;
-  const int cus = device_cus();
-  if (cus <= 0) return static_cast<int>(hipErrorInvalidDevice);
-  const int64_t blocks = (N + 15) / 16;
-  const int64_t gx = std::min<int64_t>((blocks + per_round - 1) / per_round, std::max(1, cus / split));
-  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(split));
-  fn<<<grid, waves * kWave, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale,
-                                     scale_dt, static_cast<uint16_t*>(y), static_cast<float*>(ws),
-                                     static_cast<int>(M), N, K, split);
-  const int rc = launch_status();
-  if (rc != BP_OK || split == 1) return rc;
-  splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
-                                                       wkind == kInt8 ? scale : nullptr, scale_dt, M, N, split);
-  return launch_status();
-}
-
-// partials_only: with split > 1, stop after the partial sums (the caller reduces the workspace).
-int skinny_mfma_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y,
-                       int64_t M, int64_t N, int64_t K, int rb, int waves, int depth, int split, void* ws,
-                       size_t ws_bytes, void* stream, bool partials_only = false) {
-  if (M < 0 || N < 0 || K < 0 || M > 16) return BP_E_INVALID_ARG;
-  if (M == 0 || N == 0) return BP_OK;
-  if (x == nullptr || w == nullptr || y == nullptr) return BP_E_INVALID_ARG;
-  if (wkind == kInt8 && !partials_only && (scale == nullptr || scale_dt < BP_DT_BF16 || scale_dt > BP_DT_F32))
-    return BP_E_INVALID_ARG;
-  if (split < 1 || split > 1024) return BP_E_UNSUPPORTED;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (K == 0) {
-    fill_zero_bf16_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<uint16_t*>(y), M * N);
-    return launch_status();
-  }
-  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0) return BP_E_UNSUPPORTED;
-  if (depth == 3 || depth == 4)
-    return skinny_mfma_staged_launch(wkind, x, w, scale, scale_dt, y, M, N, K, rb, waves, depth == 4, split, ws,
-                                     ws_bytes, st);
-  const int step = mfma_k_step(wkind);
-  if (K % step != 0) return BP_E_UNSUPPORTED;
-  SkinnyFn fn = mfma_pick(wkind, rb, waves, depth);
-  if (fn == nullptr) return BP_E_UNSUPPORTED;
-  const int64_t nst = K / step;
-  if (split > nst) split = static_cast<int>(nst);
-  if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
-    return BP_E_WORKSPACE;
-  const int64_t tiles = (N + 16 * rb - 1) / (16 * rb);
-  if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
-  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(split));
-  fn<<<grid, waves * kWave, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale,
-                                     scale_dt, static_cast<uint16_t*>(y), static_cast<float*>(ws),
-                                     static_cast<int>(M), N, K, split);
-  const int rc = launch_status();
-  if (rc != BP_OK || split == 1 || partials_only) return rc;
-  splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
-                                                       wkind == kInt8 ? scale : nullptr, scale_dt, M, N, split);
-  return launch_status();
-}
-
 int skinny_int4_launch(const void* x, const void* packed, const void* scale, int scale_dt, const void* zero, void* y,
                        int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int split, void* ws,
                        size_t ws_bytes, void* stream) {
@@ -252,6 +159,13 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
 }
 
 }  // namespace
+
+int splitk_reduce_launch(const float* ws, uint16_t* y, const void* scale, int scale_dt, int64_t M, int64_t N,
+                         int split, hipStream_t st) {
+  splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(ws, y, scale, scale_dt, M, N, split);
+  return launch_status();
+}
+
 }  // namespace bp
 
 extern "C" {
@@ -265,64 +179,6 @@ int bp_skinny_int4(const void* x, const void* packed, const void* scale, int sca
                    size_t workspace_bytes, void* stream) {
   return bp::skinny_int4_launch(x, packed, scale, scale_dtype, zero, y, M, N, K, tile_rows, waves, split, workspace,
                                 workspace_bytes, stream);
-}
-
-int bp_skinny_mfma_config_supported(int wkind, int block_rows, int waves, int depth) {
-  if (depth == 3 || depth == 4)
-    return block_rows == 16 && bp::mfma_staged_pick(wkind, waves, depth == 4) != nullptr ? 1 : 0;
-  return block_rows % 16 == 0 && bp::mfma_pick(wkind, block_rows / 16, waves, depth) != nullptr ? 1 : 0;
-}
-
-int bp_skinny_mfma_k_step(int wkind) {
-  return wkind == bp::kBf16 || wkind == bp::kInt8 ? bp::mfma_k_step(wkind) : 0;
-}
-
-int bp_skinny_mfma_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int block_rows,
-                        int waves, int depth, int split, void* workspace, size_t workspace_bytes, void* stream) {
-  if (block_rows <= 0 || block_rows % 16 != 0) return BP_E_UNSUPPORTED;
-  return bp::skinny_mfma_launch(bp::kBf16, x, w, nullptr, 0, y, M, N, K, block_rows / 16, waves, depth, split,
-                                workspace, workspace_bytes, stream);
-}
-
-int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y, int64_t M,
-                        int64_t N, int64_t K, int block_rows, int waves, int depth, int split, void* workspace,
-                        size_t workspace_bytes, void* stream) {
-  if (block_rows <= 0 || block_rows % 16 != 0) return BP_E_UNSUPPORTED;
-  return bp::skinny_mfma_launch(bp::kInt8, x, q, scale, scale_dtype, y, M, N, K, block_rows / 16, waves, depth,
-                                split, workspace, workspace_bytes, stream);
-}
-
-int bp_skinny_mfma_partials(int wkind, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int block_rows,
-                            int waves, int depth, int split, void* workspace, size_t workspace_bytes, void* stream) {
-  if (block_rows <= 0 || block_rows % 16 != 0 || (depth != 1 && depth != 2) || M <= 0 || N <= 0) return BP_E_UNSUPPORTED;
-  if (wkind != bp::kBf16 && wkind != bp::kInt8) return BP_E_UNSUPPORTED;
-  if (K <= 0 || K % bp::mfma_k_step(wkind) != 0 || split < 2 || split > K / bp::mfma_k_step(wkind))
-    return BP_E_UNSUPPORTED;
-  if (workspace == nullptr) return BP_E_WORKSPACE;
-  // y is not written with partials_only (the launch's checks want a non-null pointer); the int8 scale is the
-  // reducer's to apply
-  return bp::skinny_mfma_launch(wkind, x, w, nullptr, 0, workspace, M, N, K, block_rows / 16, waves, depth, split,
-                                workspace, workspace_bytes, stream, true);
-}
-
-int bp_skinny_mfma_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
-                        int64_t M, int64_t ffn, int64_t K, int block_rows, int waves, int depth, void* stream) {
-  if (M <= 0 || M > 16 || ffn <= 0 || K <= 0 || x == nullptr || w == nullptr || out == nullptr)
-    return BP_E_INVALID_ARG;
-  if (wkind != bp::kBf16 && wkind != bp::kInt8) return BP_E_UNSUPPORTED;
-  if (wkind == bp::kInt8 && (scale == nullptr || scale_dtype < BP_DT_BF16 || scale_dtype > BP_DT_F32))
-    return BP_E_INVALID_ARG;
-  if (block_rows <= 0 || block_rows % 16 != 0 || K % bp::mfma_k_step(wkind) != 0) return BP_E_UNSUPPORTED;
-  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0) return BP_E_UNSUPPORTED;
-  bp::SkinnyFn fn = bp::mfma_silu_pick(wkind, block_rows / 16, waves, depth);
-  if (fn == nullptr) return BP_E_UNSUPPORTED;
-  const int64_t N = 2 * ffn;
-  const int64_t tiles = (N + block_rows - 1) / block_rows;
-  if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
-  fn<<<dim3(static_cast<unsigned>(tiles), 1), waves * bp::kWave, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale, scale_dtype,
-      static_cast<uint16_t*>(out), nullptr, static_cast<int>(M), N, K, 1);
-  return bp::launch_status();
 }
 
 int bp_version(void) { return 100; }

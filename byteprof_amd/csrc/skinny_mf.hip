@@ -1,0 +1,324 @@
+// Kernels and C ABI of the matrix-core skinny matmul with the 8-row segment layout (skinny_mf.h): the plain launch
+// (any M up to 64, split-K through the fixed-order reduce), its gate|up + SiLU epilogue and its partial sums for a
+// caller-side reduce.
+//
+// Reference semantics: byteprof/optim/skinny.py:36-90 (kernel and _split_reduce), :93-133 (_launch), via skinny_mm
+// (skinny.py:136-166).
+
+#include <algorithm>
+
+#include "byteprof_amd.h"
+#include "skinny_mf.h"
+
+namespace bp {
+
+// Fixed-order split reduce of skinny.hip.
+int splitk_reduce_launch(const float* ws, uint16_t* y, const void* scale, int scale_dt, int64_t M, int64_t N,
+                         int split, hipStream_t st);
+
+namespace {
+
+// EPI: 0 = y[m][n] (split 1) or fp32 partials ws[split][m][n]; 1 = the SiLU product of interleaved gate|up rows
+// (rows 2f / 2f + 1 the gate / up rows of output f): y[m][f] = bf16(bf16(silu(bf16(g))) * bf16(u)).
+// XL: the workgroup's activation rows and K range are staged in LDS (dynamic shared memory of
+// min(M, 8 MB) x K-range x 2 bytes), their loads issued before the first weight loads; otherwise every segment's
+// activation operand is loaded from memory with its weights. Same operands either way: the results are equal bit
+// for bit.
+template <int KIND, int MB, int RB, int WAVES, bool VEC, int EPI, bool XL>
+__global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t* __restrict__ x,
+                                                                  const uint8_t* __restrict__ w,
+                                                                  const void* __restrict__ scale, int scale_dt,
+                                                                  uint16_t* __restrict__ y, float* __restrict__ ws,
+                                                                  int M, int64_t N, int64_t K, int split) {
+  using G = MfGeom<KIND>;
+  constexpr int D = VEC ? mf_depth<KIND, MB, RB, !XL>() : 1;
+  __shared__ MfRed<WAVES, RB, MB> red;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  // wave-uniform (a scalar value): the segment count below decides whether MFMAs run, and MFMAs ignore EXEC, so the
+  // compiler must see those branches as uniform and make them scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const MfLane ln(lane);
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 8 * RB;
+  const int sp = blockIdx.y;
+  const int64_t nseg_all = (K + G::kSeg - 1) / G::kSeg;
+  const int64_t s_lo = sp * nseg_all / split;
+  const int64_t s_hi = (sp + 1) * nseg_all / split;
+  const int64_t s_first = s_lo + wave;
+  const int64_t nseg = mf_uniform(s_first < s_hi ? (s_hi - s_first + WAVES - 1) / WAVES : 0);
+
+  // the lane's weight rows (rows past N read row N - 1; their outputs are never stored), advanced to the lane's
+  // 16 bytes of a segment (VEC = false: the row start; the element loads add the lane's K offset kl)
+  const int64_t kl = static_cast<int64_t>(G::kLaneK) * ln.slot();
+  const uint8_t* wrow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int64_t row = std::min<int64_t>(n0 + 8 * rb + ln.r, N - 1);
+    wrow[rb] = w + row * K * G::kEB + (VEC ? 16 * ln.slot() : 0);
+  }
+  floatx4 acc[RB][MB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[rb][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  if constexpr (XL) {
+    constexpr int kNT = WAVES * kWave;
+    constexpr int kPer = 4;
+    const int mrows = M < 8 * MB ? M : 8 * MB;
+    const int kn = static_cast<int>((s_hi - s_lo) * G::kSeg);
+    const int64_t k_lo = s_lo * G::kSeg;
+    const int passes = (mrows * (kn / 8) + kPer * kNT - 1) / (kPer * kNT);
+    MfStage<kNT, kPer> stage;
+    stage.issue(x, mrows, K, k_lo, kn, 0);  // ahead of the weight loads: the commit waits for these only
+    MfXLds<KIND, MB> xs;
+    xs.init(xs_lds, mrows, kn, k_lo, ln);
+    auto commit = [&]() {
+      stage.commit(xs_lds, mrows, kn, 0);
+      for (int pass = 1; pass < passes; ++pass) {
+        stage.issue(x, mrows, K, k_lo, kn, pass);
+        stage.commit(xs_lds, mrows, kn, pass);
+      }
+      __syncthreads();
+    };
+    MfMain<KIND, MB, RB, D, true, false, MfXLds<KIND, MB>>::run(wrow, xs, x, K, kl, s_first, WAVES, nseg, acc,
+                                                               commit);
+  } else if constexpr (VEC) {
+    MfXGlobal<KIND, MB, true> xs;
+    xs.init(x, M, K, ln);
+    MfMain<KIND, MB, RB, D, true, true, MfXGlobal<KIND, MB, true>>::run(wrow, xs, x, K, kl, s_first, WAVES, nseg,
+                                                                        acc);
+  } else {
+    // element loads with bounds (K not a multiple of the segment or unaligned operands): same segments, same order
+    MfXGlobal<KIND, MB, false> xs;
+    xs.init(x, M, K, ln);
+    MfMain<KIND, MB, RB, 1, false, true, MfXGlobal<KIND, MB, false>>::run(wrow, xs, x, K, kl, s_first, WAVES, nseg,
+                                                                          acc);
+  }
+  mf_fold_halves<RB, MB>(acc);
+  mf_store_red<WAVES, RB, MB>(red, acc, wave, lane);
+  __syncthreads();
+
+  constexpr int kRows = 8 * RB;
+  if constexpr (EPI == 0) {
+    const int cols = M < 8 * MB ? M : 8 * MB;
+    for (int e = threadIdx.x; e < kRows * cols; e += WAVES * kWave) {
+      const int m = e / kRows;
+      const int rr = e % kRows;
+      const int64_t n = n0 + rr;
+      if (n >= N) continue;
+      float t = mf_total<WAVES, RB, MB>(red, rr, m);
+      if (split == 1) {
+        if constexpr (KIND == kInt8) t *= load_scale(scale, n, scale_dt);
+        y[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);
+      } else {
+        ws[(static_cast<int64_t>(sp) * M + m) * N + n] = t;
+      }
+    }
+  } else {
+    const int cols = M < 8 * MB ? M : 8 * MB;
+    for (int e = threadIdx.x; e < (kRows / 2) * cols; e += WAVES * kWave) {
+      const int m = e / (kRows / 2);
+      const int rr = 2 * (e % (kRows / 2));
+      const int64_t n = n0 + rr;  // the gate row; n + 1 the up row
+      if (n + 1 >= N) continue;
+      float gv = mf_total<WAVES, RB, MB>(red, rr, m);
+      float uv = mf_total<WAVES, RB, MB>(red, rr + 1, m);
+      if constexpr (KIND == kInt8) {
+        gv *= load_scale(scale, n, scale_dt);
+        uv *= load_scale(scale, n + 1, scale_dt);
+      }
+      const float gb = round_to_bf16(gv);
+      const float a = round_to_bf16(gb / (1.f + expf(-gb)));
+      y[static_cast<int64_t>(m) * (N / 2) + n / 2] = float_to_bf16_bits(a * round_to_bf16(uv));
+    }
+  }
+}
+
+using MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, uint16_t*, float*, int, int64_t, int64_t,
+                      int);
+
+// Compiled menu: activation blocks MB in {1, 2, 4, 8} (M <= 8, 16, 32, 64) x row blocks RB in {1, 2, 4} (RB 4 up
+// to MB 2) x waves in {1, 2, 4, 8}; the SiLU epilogue and the LDS-staged activations up to MB 2; the element-load
+// variant at RB 1, 4 waves.
+template <int KIND, int MB, int RB, int EPI, bool XL>
+MfFn pick_waves(int waves) {
+  switch (waves) {
+    case 1: return &skinny_mf_kernel<KIND, MB, RB, 1, true, EPI, XL>;
+    case 2: return &skinny_mf_kernel<KIND, MB, RB, 2, true, EPI, XL>;
+    case 4: return &skinny_mf_kernel<KIND, MB, RB, 4, true, EPI, XL>;
+    case 8: return &skinny_mf_kernel<KIND, MB, RB, 8, true, EPI, XL>;
+    default: return nullptr;
+  }
+}
+
+template <int KIND, int MB, int EPI, bool XL>
+MfFn pick_rb(int rb, int waves) {
+  switch (rb) {
+    case 1: return pick_waves<KIND, MB, 1, EPI, XL>(waves);
+    case 2: return pick_waves<KIND, MB, 2, EPI, XL>(waves);
+    case 4:
+      if constexpr (MB <= 2) return pick_waves<KIND, MB, 4, EPI, XL>(waves);
+      return nullptr;
+    default: return nullptr;
+  }
+}
+
+template <int KIND, int EPI, bool XL>
+MfFn pick_mb(int mb, int rb, int waves, bool vec) {
+  if (!vec) {
+    if constexpr (EPI == 0 && !XL) {
+      if (waves != 4) return nullptr;
+      switch (mb) {
+        case 1: return &skinny_mf_kernel<KIND, 1, 1, 4, false, 0, false>;
+        case 2: return &skinny_mf_kernel<KIND, 2, 1, 4, false, 0, false>;
+        case 4: return &skinny_mf_kernel<KIND, 4, 1, 4, false, 0, false>;
+        case 8: return &skinny_mf_kernel<KIND, 8, 1, 4, false, 0, false>;
+        default: return nullptr;
+      }
+    }
+    return nullptr;
+  }
+  switch (mb) {
+    case 1: return pick_rb<KIND, 1, EPI, XL>(rb, waves);
+    case 2: return pick_rb<KIND, 2, EPI, XL>(rb, waves);
+    case 4:
+      if constexpr (EPI == 0 && !XL) return pick_rb<KIND, 4, EPI, XL>(rb, waves);
+      return nullptr;
+    case 8:
+      if constexpr (EPI == 0 && !XL) return pick_rb<KIND, 8, EPI, XL>(rb, waves);
+      return nullptr;
+    default: return nullptr;
+  }
+}
+
+template <int KIND>
+MfFn mf_pick_kind(int mb, int rb, int waves, bool vec, int epi, bool xl) {
+  if (epi == 0) return xl ? pick_mb<KIND, 0, true>(mb, rb, waves, vec) : pick_mb<KIND, 0, false>(mb, rb, waves, vec);
+  return xl ? pick_mb<KIND, 1, true>(mb, rb, waves, vec) : pick_mb<KIND, 1, false>(mb, rb, waves, vec);
+}
+
+MfFn mf_pick(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl) {
+  if (wkind == kBf16) return mf_pick_kind<kBf16>(mb, rb, waves, vec, epi, xl);
+  if (wkind == kInt8) return mf_pick_kind<kInt8>(mb, rb, waves, vec, epi, xl);
+  return nullptr;
+}
+
+int mf_blocks(int64_t M) { return M <= 8 ? 1 : M <= 16 ? 2 : M <= 32 ? 4 : 8; }
+
+int mf_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? BP_OK : static_cast<int>(e);
+}
+
+__global__ void mf_fill_zero_kernel(uint16_t* __restrict__ y, int64_t count) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    y[i] = 0;
+}
+
+constexpr int64_t kMaxStageBytes = 32 * 1024;  // LDS for staged activations (dynamic shared memory)
+
+// LDS bytes of the staged activations of a launch (the largest K range of a workgroup), or -1 when they do not fit.
+int64_t mf_stage_bytes(int wkind, int64_t M, int64_t K, int split) {
+  const int64_t seg = wkind == kBf16 ? 64 : 128;
+  const int64_t nseg = (K + seg - 1) / seg;
+  const int64_t per = (nseg + split - 1) / split;
+  const int64_t rows = M < 8 * mf_blocks(M) ? M : 8 * mf_blocks(M);
+  const int64_t bytes = rows * per * seg * 2;
+  return bytes <= kMaxStageBytes ? bytes : -1;
+}
+
+// mode 0: y (split > 1: partials then the reduce); 1: partials only (split >= 2, y unused); 2: SiLU epilogue.
+int mf_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y, int64_t M,
+              int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* ws, size_t ws_bytes, void* stream,
+              int mode) {
+  if (wkind != kBf16 && wkind != kInt8) return BP_E_UNSUPPORTED;
+  if (M < 0 || N < 0 || K < 0 || M > 64) return BP_E_INVALID_ARG;
+  if (M == 0 || N == 0) return BP_OK;
+  if (x == nullptr || w == nullptr || (mode != 1 && y == nullptr)) return BP_E_INVALID_ARG;
+  if (wkind == kInt8 && mode != 1 && (scale == nullptr || scale_dt < BP_DT_BF16 || scale_dt > BP_DT_F32))
+    return BP_E_INVALID_ARG;
+  if (split < 1 || split > 1024) return BP_E_UNSUPPORTED;
+  if (mode == 2 && (N % 2 != 0 || split != 1 || M > 16)) return BP_E_UNSUPPORTED;
+  if (mode == 1 && split < 2) return BP_E_UNSUPPORTED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K == 0) {
+    if (mode == 1) return BP_E_UNSUPPORTED;
+    const int64_t count = mode == 2 ? M * (N / 2) : M * N;
+    mf_fill_zero_kernel<<<static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 2048)), 256, 0, st>>>(
+        static_cast<uint16_t*>(y), count);
+    return mf_status();
+  }
+  const int64_t seg = wkind == kBf16 ? 64 : 128;
+  // the vector loads read whole segments: K a multiple of the segment, 16-byte aligned operands
+  const bool vec = K % seg == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(w) % 16 == 0;
+  if (!vec) {
+    rb = 1;
+    waves = 4;
+    xstage = 0;
+  }
+  const int64_t nseg = (K + seg - 1) / seg;
+  if (split > nseg) split = static_cast<int>(nseg);
+  if (mode == 1 && split < 2) return BP_E_UNSUPPORTED;
+  int64_t lds = 0;
+  if (xstage) {
+    lds = mf_stage_bytes(wkind, M, K, split);
+    if (lds < 0) return BP_E_UNSUPPORTED;
+  }
+  MfFn fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0);
+  if (fn == nullptr) return BP_E_UNSUPPORTED;
+  if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
+    return BP_E_WORKSPACE;
+  const int64_t tiles = (N + 8 * rb - 1) / (8 * rb);
+  if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
+  fn<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(split)), waves * kWave, static_cast<size_t>(lds),
+       st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale, scale_dt,
+             static_cast<uint16_t*>(y), static_cast<float*>(ws), static_cast<int>(M), N, K, split);
+  const int rc = mf_status();
+  if (rc != BP_OK || split == 1 || mode == 1) return rc;
+  return splitk_reduce_launch(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
+                              wkind == kInt8 ? scale : nullptr, scale_dt, M, N, split, st);
+}
+
+}  // namespace
+}  // namespace bp
+
+extern "C" {
+
+int bp_skinny_mf_supported(int wkind, int M, int rb, int waves, int xstage) {
+  if (M < 1 || M > 64) return 0;
+  return bp::mf_pick(wkind, bp::mf_blocks(M), rb, waves, true, 0, xstage != 0) != nullptr ? 1 : 0;
+}
+
+int bp_skinny_mf_k_segment(int wkind) { return wkind == bp::kBf16 ? 64 : wkind == bp::kInt8 ? 128 : 0; }
+
+int64_t bp_skinny_mf_stage_bytes(int wkind, int64_t M, int64_t K, int split) {
+  if ((wkind != bp::kBf16 && wkind != bp::kInt8) || M < 1 || M > 64 || K < 1 || split < 1) return -1;
+  return bp::mf_stage_bytes(wkind, M, K, split);
+}
+
+int bp_skinny_mf(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y, int64_t M,
+                 int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  return bp::mf_launch(wkind, x, w, scale, scale_dtype, y, M, N, K, rb, waves, split, xstage, workspace,
+                       workspace_bytes, stream, 0);
+}
+
+int bp_skinny_mf_partials(int wkind, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int rb,
+                          int waves, int split, int xstage, void* workspace, size_t workspace_bytes, void* stream) {
+  if (workspace == nullptr) return BP_E_WORKSPACE;
+  return bp::mf_launch(wkind, x, w, nullptr, 0, nullptr, M, N, K, rb, waves, split, xstage, workspace,
+                       workspace_bytes, stream, 1);
+}
+
+int bp_skinny_mf_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
+                      int64_t M, int64_t ffn, int64_t K, int rb, int waves, int xstage, void* stream) {
+  if (ffn < 0) return BP_E_INVALID_ARG;
+  return bp::mf_launch(wkind, x, w, scale, scale_dtype, out, M, 2 * ffn, K, rb, waves, 1, xstage, nullptr, 0, stream,
+                       2);
+}
+
+}  // extern "C"

@@ -13,8 +13,8 @@ The model is the OLMo-2 architecture with synthetic weights (the checkpoint is n
 `OlmoDecoder` holds the weights of transformers' Olmo2ForCausalLM layout with q|k|v and gate|up fused into one
 linear each (one launch instead of three or two; the outputs are the same rows), bf16 or int8 (per-row scales).
 The gate and up rows are interleaved (row 2n gate n, row 2n + 1 up n) so that one launch computes the projection
-and the SiLU product (bp_decode_gate_up_silu), where the hidden size is a multiple of the kernels' 1 KiB chunk;
-otherwise gate|up is one skinny launch followed by silu_mul.
+and the SiLU product (bp_skinny_mf_silu). Every linear runs on the skinny matrix-core kernel, whose rows do not
+depend on how many rows share a launch: a verify pass of s rows computes each row exactly as the one-token step.
 The prompt is fed one position at a time through the same step (the reference prefills with one batched
 forward; the cache contents and the first new token are the same up to rounding).
 """
@@ -31,9 +31,8 @@ from ..quant.hip_int8 import quantize_rowwise_int8
 from . import skinny as S
 
 MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
-GATE_UP_WAVES = {"bf16": 4, "int8": 2}  # waves per workgroup of the fused gate|up + SiLU launch
-_CHUNK = {"bf16": 512, "int8": 1024}  # K granularity of the skinny kernels' 16-byte loads
 ROPE_ATTENTION_ROWS = 16  # most rows of one fused q/k-norm + RoPE + cache + attention launch
+VERIFY_ROWS = 16  # rows of the verify-pass buffers (allocated once per decoder, never reallocated)
 
 
 class OptimizeError(RuntimeError):
@@ -111,11 +110,9 @@ class OlmoDecoder:
             return (w,) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
 
         bf = torch.bfloat16
-        # one launch for gate|up and the SiLU product where the hidden size allows it (rows interleaved)
-        self.gate_up_interleaved = H % _CHUNK[kind] == 0
 
-        def gate_up(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
-            return torch.stack([g, u], dim=1).reshape(2 * F, H) if self.gate_up_interleaved else torch.cat([g, u])
+        def gate_up(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:  # rows interleaved: 2f gate f, 2f + 1 up f
+            return torch.stack([g, u], dim=1).reshape(2 * F, H)
 
         self.embed = weights["embed"].to(bf).contiguous()
         self.norm = weights["norm"].to(bf).contiguous()
@@ -164,15 +161,7 @@ class OlmoDecoder:
             self._mm(self.attn, w["o"], self.o)
             c(L.bp_decode_norm_residual(self.o.data_ptr(), w["post_attn"].data_ptr(), self.x.data_ptr(),
                                         self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")
-            if self.gate_up_interleaved:
-                gw = w["gate_up"]
-                sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
-                c(L.bp_decode_gate_up_silu(0 if self.kind == "bf16" else 1, self.x.data_ptr(), gw[0].data_ptr(), sc,
-                                           sdt, self.act.data_ptr(), cfg.ffn, H, GATE_UP_WAVES[self.kind], st),
-                  "bp_decode_gate_up_silu")
-            else:
-                self._mm(self.x, w["gate_up"], self.gu)
-                c(L.bp_decode_silu_mul(self.gu.data_ptr(), self.act.data_ptr(), cfg.ffn, st), "bp_decode_silu_mul")
+            self._gate_up_silu(self.x, w["gate_up"], self.act, self.gu, 1)
             self._mm(self.act, w["down"], self.dn)
             c(L.bp_decode_norm_residual(self.dn.data_ptr(), w["post_ff"].data_ptr(), self.x.data_ptr(),
                                         self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")
@@ -182,52 +171,61 @@ class OlmoDecoder:
         c(L.bp_decode_argmax_next(self.logits.data_ptr(), cfg.vocab, self.tok.data_ptr(), self.pos.data_ptr(),
                                   self.argmax_scratch.data_ptr(), st), "bp_decode_argmax_next")
 
+    def _plan(self, n: int, k: int, rows: int) -> tuple[int, int, int, int]:
+        """(weight blocks per workgroup, waves, split, staging) of the skinny launch skinny_mm makes."""
+        return S._resolve(self.kind, n, k, rows, None)
+
+    def _gate_up_silu(self, x: torch.Tensor, gw: tuple, act: torch.Tensor, gu: torch.Tensor, rows: int) -> None:
+        """act[:rows] = bf16(bf16(silu(g)) * u) of the interleaved gate|up projection: one launch with the SiLU
+        product as its epilogue when the shape's K order has no split, else skinny_mm + the SiLU kernel (the same
+        sums either way)."""
+        F, H = self.cfg.ffn, self.cfg.hidden
+        rb, waves, split, xs = self._plan(2 * F, H, rows)
+        L, st = _lib.lib(), _lib.stream_ptr(self.device)
+        if split == 1 and rows <= 16:
+            sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
+            _lib.check(L.bp_skinny_mf_silu(S._KIND_CODE[self.kind], x.data_ptr(), gw[0].data_ptr(), sc, sdt,
+                                           act.data_ptr(), rows, F, H, rb, waves, xs, st), "bp_skinny_mf_silu")
+            return
+        self._mm(x[:rows], gw, gu[:rows])
+        _lib.check(L.bp_decode_silu_mul_rows(gu.data_ptr(), act.data_ptr(), F, rows, 1, st), "bp_decode_silu_mul_rows")
+
     @property
     def launches_per_step(self) -> int:
-        """Kernel launches of one step: embed, 7 or 8 per layer, final norm, LM head, argmax."""
-        return 4 + (7 if self.gate_up_interleaved else 8) * self.cfg.layers
+        """Kernel launches of one step: embed, 7 per layer (+1 per split-K linear), final norm, LM head, argmax."""
+        H, F, V = self.cfg.hidden, self.cfg.ffn, self.cfg.vocab
+        extra = lambda n, k: int(self._plan(n, k, 1)[2] > 1)  # noqa: E731  (the split reduce)
+        per_layer = 7 + extra(3 * H, H) + extra(H, H) + extra(H, F) + 2 * extra(2 * F, H)
+        return 4 + per_layer * self.cfg.layers + extra(V, H)
 
-    def _mfma_silu(self, s: int) -> tuple[int, int, int] | None:
-        """(block_rows, waves, depth) of the matrix-core gate|up launch that skinny_mm makes at s rows when it can
-        take the SiLU epilogue (interleaved rows, depth 1 or 2, split 1), else None."""
-        if not self.gate_up_interleaved or S._bm(s) not in S.MFMA_BUCKETS:
-            return None
-        mc = S.mfma_cfg(self.kind, 2 * self.cfg.ffn, self.cfg.hidden)
-        if mc is None or mc[2] not in (1, 2) or mc[3] != 1:
-            return None
-        return mc[0], mc[1], mc[2]
-
-    def _mfma_splitk(self, s: int) -> tuple[int, int, int, int] | None:
-        """(block_rows, waves, depth, split) of the matrix-core down launch that skinny_mm makes at s rows when it
-        is a split-K launch of depth 1 or 2 (its reduce can feed the norm), else None."""
+    def _down_splitk(self, s: int) -> tuple[int, int, int, int] | None:
+        """The down projection's plan at s rows when it is split-K (its partials then feed the norm's launch)."""
         H, F = self.cfg.hidden, self.cfg.ffn
-        if S._bm(s) not in S.MFMA_BUCKETS or H > 8192 or self.vact.data_ptr() % 16:
-            return None
-        mc = S.mfma_cfg(self.kind, H, F)
-        if mc is None or mc[2] not in (1, 2):
-            return None
-        split = max(1, min(mc[3], F // S.mfma_k_step(self.kind)))
-        return (mc[0], mc[1], mc[2], split) if split > 1 else None
+        plan = self._plan(H, F, s)
+        return plan if plan[2] > 1 and H <= 8192 else None
 
     def verify_buffers(self, smax: int) -> None:
-        """Allocates the buffers of verify passes of up to `smax` rows (once; a larger smax reallocates). ids
-        [smax] and pos [1] (int64) are the round's inputs: ids[0] the last accepted token, ids[1 ..] the drafts,
-        pos the cache position of ids[0]; out [smax + 1] receives the row tokens and, at smax, the accepted length."""
-        if getattr(self, "smax", 0) >= smax:
+        """The buffers of verify passes (allocated once, for VERIFY_ROWS rows, and never reallocated, so graphs
+        captured by any drafting loop on this decoder keep valid pointers). ids [VERIFY_ROWS] and pos [1] (int64) are
+        a round's inputs: ids[0] the last accepted token, ids[1 ..] the drafts, pos the cache position of ids[0];
+        out [VERIFY_ROWS + 1] receives the row tokens and, at VERIFY_ROWS (= self.smax), the accepted length."""
+        if not 1 <= smax <= VERIFY_ROWS:
+            raise ValueError(f"verify passes take 1..{VERIFY_ROWS} rows, asked for {smax}")
+        if getattr(self, "smax", 0):
             return
         cfg, dev = self.cfg, self.device
         H, F, V = cfg.hidden, cfg.ffn, cfg.vocab
+        n = VERIFY_ROWS
         z = lambda *shape, dtype=torch.bfloat16: torch.zeros(*shape, dtype=dtype, device=dev)  # noqa: E731
-        self.smax = smax
-        self.v_ids, self.v_tok, self.v_out = z(smax, dtype=torch.int64), z(smax, dtype=torch.int64), \
-            z(smax + 1, dtype=torch.int64)
+        self.smax = n
+        self.v_ids, self.v_tok, self.v_out = z(n, dtype=torch.int64), z(n, dtype=torch.int64), \
+            z(n + 1, dtype=torch.int64)
         self.v_pos = z(1, dtype=torch.int64)
-        self.vx, self.vq, self.vattn, self.vo, self.vdn, self.vxn = (z(smax, H) for _ in range(6))
-        self.vqkv, self.vgu, self.vact, self.vlogits = z(smax, 3 * H), z(smax, 2 * F), z(smax, F), z(smax, V)
-        self.v_argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_rows_scratch_bytes(smax) // 4), dtype=torch.int32)
-        mc = S.mfma_cfg(self.kind, H, F)
-        split = max(1, min(mc[3], F // S.mfma_k_step(self.kind))) if mc is not None else 1
-        self.vws = torch.empty(split * smax * H, dtype=torch.float32, device=dev)  # the down launch's partials
+        self.vx, self.vq, self.vattn, self.vo, self.vdn, self.vxn = (z(n, H) for _ in range(6))
+        self.vqkv, self.vgu, self.vact, self.vlogits = z(n, 3 * H), z(n, 2 * F), z(n, F), z(n, V)
+        self.v_argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_rows_scratch_bytes(n) // 4), dtype=torch.int32)
+        split = max(p[2] for p in (self._plan(H, F, r) for r in range(1, n + 1)))
+        self.vws = torch.empty(split * n * H, dtype=torch.float32, device=dev)  # the down launch's partials
 
     def verify(self, s: int) -> None:
         """One verify pass of s = 1 + drafts rows (the reference's captured draft step, olmo_draft.py
@@ -235,7 +233,7 @@ class OlmoDecoder:
         rows' k / v written first, row r attending over positions <= pos + r), the argmax of every row, the accepted
         length L (drafts ids[1 + j] equal to the prediction of row j) and the next round's inputs: ids[0] <- the
         token after the accepted prefix, pos += L + 1. Every row is computed as the one-token step at its position
-        computes it; the linears run at s activation rows (the matrix-core kernels from 5 rows on)."""
+        computes it (the linears' rows do not depend on the row count)."""
         if not 1 <= s <= getattr(self, "smax", 0):
             raise ValueError(f"s must be in 1..{getattr(self, 'smax', 0)} (verify_buffers)")
         cfg, L = self.cfg, _lib.lib()
@@ -266,29 +264,16 @@ class OlmoDecoder:
             self._mm(self.vattn[:s], w["o"], self.vo[:s])
             c(L.bp_decode_norm_residual_rows(self.vo.data_ptr(), w["post_attn"].data_ptr(), self.vx.data_ptr(),
                                              self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
-            if s == 1 and self.gate_up_interleaved:  # the one-token step's fused gate|up + SiLU launch
-                gw = w["gate_up"]
-                sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
-                c(L.bp_decode_gate_up_silu(0 if self.kind == "bf16" else 1, self.vx.data_ptr(), gw[0].data_ptr(),
-                                           sc, sdt, self.vact.data_ptr(), F, H, GATE_UP_WAVES[self.kind], st),
-                  "bp_decode_gate_up_silu")
-            elif self._mfma_silu(s) is not None:  # the matrix-core gate|up with the SiLU product as its epilogue
-                gw = w["gate_up"]
-                sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
-                c(L.bp_skinny_mfma_silu(0 if self.kind == "bf16" else 1, x.data_ptr(), gw[0].data_ptr(), sc, sdt,
-                                        self.vact.data_ptr(), s, F, H, *self._mfma_silu(s), st), "bp_skinny_mfma_silu")
-            else:
-                self._mm(x, w["gate_up"], self.vgu[:s])
-                c(L.bp_decode_silu_mul_rows(self.vgu.data_ptr(), self.vact.data_ptr(), F, s,
-                                            int(self.gate_up_interleaved), st), "bp_decode_silu_mul_rows")
-            dc = self._mfma_splitk(s)
-            if dc is not None:  # split-K on the matrix cores; the reduce feeds the norm in one launch
+            self._gate_up_silu(x, w["gate_up"], self.vact, self.vgu, s)
+            dc = self._down_splitk(s)
+            if dc is not None:  # split-K partials; their reduce feeds the norm in one launch
                 dw = w["down"]
-                c(L.bp_skinny_mfma_partials(0 if self.kind == "bf16" else 1, self.vact.data_ptr(), dw[0].data_ptr(),
-                                            s, H, F, *dc, self.vws.data_ptr(), self.vws.numel() * 4, st),
-                  "bp_skinny_mfma_partials")
+                rb, waves, split, xs = dc
+                c(L.bp_skinny_mf_partials(S._KIND_CODE[self.kind], self.vact.data_ptr(), dw[0].data_ptr(), s, H, F,
+                                          rb, waves, split, xs, self.vws.data_ptr(), self.vws.numel() * 4, st),
+                  "bp_skinny_mf_partials")
                 sc, sdt = (dw[1].data_ptr(), _lib.TORCH_DT[dw[1].dtype]) if self.kind == "int8" else (None, 0)
-                c(L.bp_decode_splitk_norm_residual_rows(self.vws.data_ptr(), dc[3], sc, sdt, w["post_ff"].data_ptr(),
+                c(L.bp_decode_splitk_norm_residual_rows(self.vws.data_ptr(), split, sc, sdt, w["post_ff"].data_ptr(),
                                                         self.vx.data_ptr(), self.vx.data_ptr(), H, cfg.eps, s, st),
                   "bp_decode_splitk_norm_residual_rows")
             else:

@@ -118,7 +118,7 @@ def make_generate_draft(dec: OlmoDecoder, spec: dict[str, Any] | None = None,
     dec.verify_buffers(smax)
     dev = dec.device
     pinned_d = torch.zeros(smax, dtype=torch.long).pin_memory()
-    pinned_o = torch.zeros(smax + 1, dtype=torch.long).pin_memory()
+    pinned_o = torch.zeros(dec.smax + 1, dtype=torch.long).pin_memory()  # row tokens, accepted length at dec.smax
     pinned_one = torch.zeros(1, dtype=torch.long).pin_memory()
     d_np, o_np, one_np = pinned_d.numpy(), pinned_o.numpy(), pinned_one.numpy()
     done = torch.cuda.Event()
@@ -191,7 +191,7 @@ def make_generate_draft(dec: OlmoDecoder, spec: dict[str, Any] | None = None,
                 done.record()
                 done.synchronize()  # the single sync of this round
                 toks = o_np[:k + 1].tolist()
-                length = int(o_np[smax])
+                length = int(o_np[dec.smax])
                 if length != accepted_length([last] + list(draft[:k]), toks, k):
                     raise RuntimeError("host and device disagree on the accepted length")
                 emitted = toks[:length + 1]

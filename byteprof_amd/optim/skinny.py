@@ -1,24 +1,20 @@
 """Skinny weight-only matmul y[M, N] = x[M, K] @ W[N, K]^T on gfx950 (MI355X), through libbyteprof_amd.so.
 
-Drop-in for byteprof/optim/skinny.py: same names (`skinny_mm`, `get_cfg`, `dequantize`, `MAX_M`, `GROUP`), same
-argument meaning, same ValueError validation (skinny.py:136-166). bf16 activations, fp32 accumulation, bf16 output;
-weights bf16 [N, K] or int8 [N, K] with one scale per output row (bf16, fp16 or fp32).
+Drop-in for byteprof/optim/skinny.py: same names (`skinny_mm`, `get_cfg`, `_bm`, `dequantize`, `MAX_M`, `GROUP`,
+`quantize_int4`, `pack_int4`, `unpack_int4`), same argument meaning, same ValueError validation (skinny.py:136-166).
+bf16 activations, fp32 accumulation, bf16 output; weights bf16 [N, K], int8 [N, K] with one scale per output row
+(bf16, fp16 or fp32), or int4 group-128 in the reference's tile-major format.
 
-Differences from the reference, each forced by the hardware mapping or by raw-pointer kernels:
-  - one launch handles up to ROWS_PER_LAUNCH = 16 activation rows (the reference: 64); larger M is chunked here,
-    and `SkinnyLinear` still sends every input of 1..MAX_M rows to the kernel;
-  - x must be bfloat16 and on the GPU, w and scale contiguous (the reference assumes the latter silently);
-  - `cfg` is (rows, waves, split) for this kernel (rows: weight rows per workgroup; waves: wavefronts sharing the
-    K range of a workgroup; split: K ranges in separate workgroups, added in fixed order). The reference's
-    (BN, BK, num_warps, num_stages[, split]) tuples are accepted and mapped to (BN, num_warps, split);
-  - launches of 5..16 rows (the 8- and 16-row buckets: speculative-verify widths) run on the matrix cores
-    (skinny_mfma.hip) when K is a multiple of 128 (bf16) / 256 (int8), launches of 1..4 rows on the VALU dot2
-    kernels; bitwise row independence (test_skinny.py:114-121) holds within each family, i.e. for M = 1..4 and for
-    M = 5..16 (the reference's single M <= 16 bucket is split at the change of arithmetic unit). An explicit `cfg`
-    selects the VALU kernel;
-  - int4 group-128 weights (uint8 tile-major, `quantize_int4` / `pack_int4`, the reference's format byte for byte)
-    run on skinny_int4.hip, whose products use the codes, zeros and activations exactly (the reference rounds
-    code - zero to bf16 before its tensor-core product): closer to the dequantize-then-matmul result.
+bf16 and int8 run on one matrix-core kernel family for every row count (csrc/skinny_mf.h): one launch takes up to
+MAX_M = 64 activation rows and streams every weight byte once; the K order of every sum depends only on the shape's
+(waves, split), never on M, so output row i is bitwise the same whether it is computed alone or with up to 63 other
+rows (the reference's row-independence contract, test_skinny.py:110-120, here over M = 1..64). int4 runs on
+skinny_int4.hip (VALU dot products whose order also ignores M).
+
+`cfg` is (rows, waves, split) for the bf16 / int8 kernel (rows: weight rows per workgroup, a multiple of 8;
+waves: wavefronts sharing a workgroup's K range; split: K ranges in separate workgroups, added in fixed order) or
+the reference's (BN, BK, num_warps, num_stages[, split]), mapped to (BN, num_warps, split). Differences from the
+reference forced by raw-pointer kernels: x must be bfloat16 and on the GPU, w, scale and out contiguous.
 """
 
 from __future__ import annotations
@@ -32,16 +28,16 @@ import torch
 from .. import _lib
 
 GROUP = 128
-MAX_M = 64  # rows for which SkinnyLinear uses the kernel (skinny_linear.py:60); interface parity with the reference
-ROWS_PER_LAUNCH = 16  # activation rows per kernel launch on gfx950
+MAX_M = 64  # activation rows per launch; more rows are processed in chunks of MAX_M (skinny.py:32)
+ROWS_PER_LAUNCH = MAX_M
 
-_ROW_BUCKETS = (1, 2, 4, 8, 16)
-_ROWS_MENU = (2, 4, 8, 16, 32)
-_WAVES_MENU = (1, 2, 4, 8, 16)
 _KIND_CODE = {"bf16": 0, "int8": 1}
-_CHUNK = {"bf16": 512, "int8": 1024}  # K elements per wave-wide 16-byte load
+_RB_MENU = (1, 2, 4)        # 8-row weight blocks per workgroup
+_WAVES_MENU = (1, 2, 4, 8)
+_BUCKETS = (1, 8, 16, 32, 64)  # row buckets of the tuned plans (8-row activation blocks per launch: 1, 1, 2, 4, 8)
 
-# Tuned (waves, split) per (kind, N, K) and rows per activation-row bucket; see skinny_cfg.json.
+# Tuned (waves, split) per (kind, N, K) -- one K order for every row count -- and weight blocks per workgroup per
+# activation-row bucket; written by byteprof_amd.tune.
 _CFG_FILE = Path(__file__).with_name("skinny_cfg.json")
 _TABLE: dict[tuple[str, int, int], dict] = {}
 if _CFG_FILE.exists():
@@ -53,174 +49,116 @@ if _CFG_FILE.exists():
 
 
 def _bm(m: int) -> int:
-    """Activation-row bucket of a launch (M rounded up to 1, 2, 4, 8 or 16)."""
-    for b in _ROW_BUCKETS:
+    """The reference's row bucket of a launch (skinny.py:108-109): 16, 32 or 64."""
+    return 16 if m <= 16 else 32 if m <= 32 else 64
+
+
+def _bucket(m: int) -> int:
+    """Row bucket of a launch's tuned plan: 1 (the decode step), else M rounded up to 8, 16, 32 or 64. The plan
+    (weight blocks per workgroup, activation staging) may differ per bucket; the K order may not."""
+    for b in _BUCKETS:
         if m <= b:
             return b
-    return ROWS_PER_LAUNCH
+    return MAX_M
 
 
-@functools.lru_cache(maxsize=None)
-def _supported(kind: str, bm: int, rows: int, waves: int) -> bool:
-    return bool(_lib.lib().bp_skinny_config_supported(_KIND_CODE[kind], bm, rows, waves))
+def k_segment(kind: str) -> int:
+    """K elements of one weight row that one load instruction of the kernel covers (64 bf16, 128 int8)."""
+    return 64 if kind == "bf16" else 128
 
 
 def _default_waves(kind: str, k: int) -> int:
-    nch = -(-k // _CHUNK[kind])
+    nseg = -(-k // k_segment(kind))
     waves = 1
-    while waves * 2 <= min(nch, 8):
+    while waves * 2 <= 8 and nseg // (waves * 2) >= 4:  # at least 4 segments per wave
         waves *= 2
     return waves
 
 
-def _default_rows(n: int, bm: int) -> int:
-    rows = {1: 8, 2: 8, 4: 4, 8: 4, 16: 2}[bm]
-    while rows > 2 and -(-n // rows) < 512:  # keep at least ~2 workgroups per CU on 256 CUs
-        rows //= 2
-    return rows
+def _default_rb(n: int, bucket: int) -> int:
+    blocks = -(-n // 8)
+    if bucket > 16:
+        return 1
+    return 2 if blocks >= 2048 else 1
+
+
+def _default_split(kind: str, n: int, k: int, waves: int) -> int:
+    blocks = -(-n // 8)
+    nseg = -(-k // k_segment(kind))
+    split = 1
+    while blocks * split < 256 and nseg // (waves * split * 2) >= 2:
+        split *= 2
+    return split
 
 
 def get_cfg(kind: str, n: int, k: int, bm: int) -> tuple[int, int, int]:
-    """(rows, waves, split) for a launch of `bm` activation rows; tuned table first, then the heuristic."""
+    """(rows, waves, split) of a bf16 / int8 launch of `bm` activation rows (the bucket's upper bound): the tuned
+    table first, then a heuristic. waves and split (the K order) depend on the shape only."""
+    rb, waves, split, _ = _table_plan(kind, n, k, bm)
+    return 8 * rb, waves, split
+
+
+def _table_plan(kind: str, n: int, k: int, m: int) -> tuple[int, int, int, int]:
+    """(weight blocks per workgroup, waves, split, staged activations) from the table, else the heuristic."""
+    bucket = _bucket(m)
     entry = _TABLE.get((kind, n, k))
     if entry is not None:
-        rows = int(entry.get("rows", {}).get(str(bm), _default_rows(n, bm)))
-        return rows, int(entry["waves"]), int(entry.get("split", 1))
-    return _default_rows(n, bm), _default_waves(kind, k), 1
+        rb = int(entry.get("rb", {}).get(str(bucket), _default_rb(n, bucket)))
+        xs = int(entry.get("xs", {}).get(str(bucket), 0))
+        return rb, int(entry["waves"]), int(entry.get("split", 1)), xs
+    waves = _default_waves(kind, k)
+    return _default_rb(n, bucket), waves, _default_split(kind, n, k, waves), int(n >= 16384)
 
 
-def _resolve(kind: str, n: int, k: int, bm: int, cfg) -> tuple[int, int, int]:
-    """Map a user / table configuration onto the compiled menu (largest supported rows <= requested)."""
+def _resolve(kind: str, n: int, k: int, m: int, cfg) -> tuple[int, int, int, int]:
+    """(weight blocks per workgroup, waves, split, staged activations) of a launch from a user / table
+    configuration, mapped onto the compiled menu (largest supported value at or below the request)."""
+    xs = 0
     if cfg is None:
-        rows, waves, split = get_cfg(kind, n, k, bm)
+        rb, waves, split, xs = _table_plan(kind, n, k, m)
+        rows = 8 * rb
     elif len(cfg) == 3:
         rows, waves, split = (int(c) for c in cfg)
     elif len(cfg) in (4, 5):  # the reference's (BN, BK, num_warps, num_stages[, split])
         rows, waves, split = int(cfg[0]), int(cfg[2]), int(cfg[4]) if len(cfg) == 5 else 1
     else:
         raise ValueError(f"cfg must be (rows, waves, split) or (BN, BK, warps, stages[, split]), got {cfg!r}")
+    rb = max(r for r in _RB_MENU if r <= max(rows // 8, 1))
     waves = max(w for w in _WAVES_MENU if w <= max(waves, 1))
-    split = max(1, split)
-    cands = [r for r in _ROWS_MENU if r <= max(rows, 2)]
-    for r in sorted(cands, reverse=True):
-        if _supported(kind, bm, r, waves):
-            return r, waves, split
-    for w in sorted((w for w in _WAVES_MENU if w < waves), reverse=True):
-        for r in sorted(_ROWS_MENU, reverse=True):
-            if _supported(kind, bm, r, w):
-                return r, w, split
-    raise ValueError(f"no compiled kernel for {kind} rows<={rows} waves<={waves} at {bm} activation rows")
+    split = max(1, min(int(split), -(-k // k_segment(kind))))
+    if xs and (m > 16 or _stage_bytes(kind, m, k, split) < 0):
+        xs = 0
+    while rb > 1 and not _supported(kind, m, rb, waves, xs):
+        rb //= 2
+    if not _supported(kind, m, rb, waves, xs):
+        raise ValueError(f"no compiled kernel for {kind} at {m} rows, {8 * rb} weight rows, {waves} waves")
+    return rb, waves, split, xs
 
 
-MFMA_BUCKETS = (8, 16)  # row buckets (M = 5..16) served by the matrix-core kernels when the shape allows
+@functools.lru_cache(maxsize=None)
+def _supported(kind: str, m: int, rb: int, waves: int, xs: int = 0) -> bool:
+    return bool(_lib.lib().bp_skinny_mf_supported(_KIND_CODE[kind], m, rb, waves, xs))
 
 
-# The LDS-staged matrix-core kernel (depth 3: each wave owns whole 16-row blocks; depth 4: the waves of a workgroup
-# share each block's steps): K per 1 KiB step, activation elements a workgroup stages in LDS.
-STAGED_DEPTHS = (3, 4)
-STAGED_STEP = {"bf16": 512, "int8": 1024}
-STAGED_K_MAX = 2048
-
-
-def staged_split(kind: str, k: int, split: int = 1, waves: int = 1, depth: int = 3) -> int | None:
-    """The smallest split >= `split` that the LDS-staged kernel takes for K (K / split a multiple of the step and
-    at most STAGED_K_MAX; at depth 4 its steps a multiple or a divisor of the waves), or None."""
-    step = STAGED_STEP[kind]
-    if k <= 0 or k % step:
-        return None
-    for s in range(max(1, split), k // step + 1):
-        if k % (s * step) == 0 and k // s <= STAGED_K_MAX:
-            steps = k // s // step
-            if depth != 4 or steps % waves == 0 or waves % steps == 0:
-                return s
-    return None
-
-
-def mfma_cfg(kind: str, n: int, k: int) -> tuple[int, int, int, int] | None:
-    """(block_rows, waves, depth, split) of the matrix-core kernel for a shape's 8- and 16-row buckets, or None
-    when those buckets stay on the VALU kernel (table entry 'mfma', else a heuristic)."""
-    if k % mfma_k_step(kind) != 0:
-        return None
-    entry = _TABLE.get((kind, n, k), {}).get("mfma")
-    if entry is not None:
-        if not entry.get("use", True):
-            return None
-        depth = int(entry["depth"])
-        if depth in STAGED_DEPTHS and staged_split(kind, k, int(entry.get("split", 1)), int(entry["waves"]),
-                                                  depth) is None:
-            return None
-        return int(entry["block_rows"]), int(entry["waves"]), depth, int(entry.get("split", 1))
-    steps = k // mfma_k_step(kind)
-    waves = 1
-    while waves * 2 <= min(steps, 4):
-        waves *= 2
-    block_rows = 64 if n >= 32768 else 32 if n >= 4096 else 16
-    return block_rows, waves, 1 if n >= 32768 else 2, 1
+@functools.lru_cache(maxsize=None)
+def _stage_bytes(kind: str, m: int, k: int, split: int) -> int:
+    return int(_lib.lib().bp_skinny_mf_stage_bytes(_KIND_CODE[kind], m, k, split))
 
 
 def _launch(kind: str, x: torch.Tensor, w: torch.Tensor, scale, y: torch.Tensor, cfg=None) -> None:
     m, k = x.shape
     n = w.shape[0]
-    bm = _bm(m)
-    if cfg is None and bm in MFMA_BUCKETS and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0:
-        mc = mfma_cfg(kind, n, k)
-        if mc is not None:
-            launch_mfma(kind, x, w, scale, y, *mc)
-            return
-    rows, waves, split = _resolve(kind, n, k, bm, cfg)
-    split = min(split, -(-k // _CHUNK[kind]))
+    rb, waves, split, xs = _resolve(kind, n, k, m, cfg)
     L = _lib.lib()
     ws = None
     ws_bytes = 0
     if split > 1:
         ws_bytes = L.bp_skinny_workspace_bytes(m, n, split)
         ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=x.device)
-    stream = _lib.stream_ptr(x.device)
-    if kind == "bf16":
-        rc = L.bp_skinny_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, rows, waves, split,
-                              _lib.ptr(ws), ws_bytes, stream)
-    else:
-        rc = L.bp_skinny_int8(x.data_ptr(), w.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype],
-                              y.data_ptr(), m, n, k, rows, waves, split, _lib.ptr(ws), ws_bytes, stream)
-    _lib.check(rc, f"bp_skinny_{kind}")
-
-
-def mfma_k_step(kind: str) -> int:
-    """K granularity of the matrix-core kernels (K must be a multiple of it)."""
-    return _mfma_k_step_cached(kind)
-
-
-@functools.lru_cache(maxsize=None)
-def _mfma_k_step_cached(kind: str) -> int:
-    return int(_lib.lib().bp_skinny_mfma_k_step(_KIND_CODE[kind]))
-
-
-def launch_mfma(kind: str, x: torch.Tensor, w: torch.Tensor, scale, y: torch.Tensor, block_rows: int, waves: int,
-                depth: int = 1, split: int = 1) -> None:
-    """One launch of the matrix-core kernel on 1..16 activation rows (operands validated by the caller)."""
-    m, k = x.shape
-    n = w.shape[0]
-    if depth in STAGED_DEPTHS:
-        split = staged_split(kind, k, split, waves, depth)
-        if split is None:
-            raise ValueError(f"K = {k} does not fit the LDS-staged matrix-core kernel")
-    else:
-        split = max(1, min(split, k // mfma_k_step(kind)))
-    L = _lib.lib()
-    ws = None
-    ws_bytes = 0
-    if split > 1:
-        ws_bytes = L.bp_skinny_workspace_bytes(m, n, split)
-        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=x.device)
-    stream = _lib.stream_ptr(x.device)
-    if kind == "bf16":
-        rc = L.bp_skinny_mfma_bf16(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, block_rows, waves, depth,
-                                   split, _lib.ptr(ws), ws_bytes, stream)
-    else:
-        rc = L.bp_skinny_mfma_int8(x.data_ptr(), w.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype],
-                                   y.data_ptr(), m, n, k, block_rows, waves, depth, split, _lib.ptr(ws), ws_bytes,
-                                   stream)
-    _lib.check(rc, f"bp_skinny_mfma_{kind}")
+    sc, sdt = (scale.data_ptr(), _lib.TORCH_DT[scale.dtype]) if kind == "int8" else (None, 0)
+    rc = L.bp_skinny_mf(_KIND_CODE[kind], x.data_ptr(), w.data_ptr(), sc, sdt, y.data_ptr(), m, n, k, rb, waves,
+                        split, xs, _lib.ptr(ws), ws_bytes, _lib.stream_ptr(x.device))
+    _lib.check(rc, f"bp_skinny_mf ({kind})")
 
 
 def _check_device(x: torch.Tensor, *others: torch.Tensor | None) -> None:
@@ -234,7 +172,8 @@ def _check_device(x: torch.Tensor, *others: torch.Tensor | None) -> None:
 def skinny_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None = None,
               zero: torch.Tensor | None = None, out: torch.Tensor | None = None,
               cfg: tuple[int, ...] | None = None) -> torch.Tensor:
-    """x: [M, K] bf16 (contiguous); w: bf16 [N, K] | int8 [N, K] + scale [N]. Returns y [M, N] in x.dtype.
+    """x: [M, K] bf16 (contiguous); w: bf16 [N, K] | int8 [N, K] + scale [N] | int4 tile-major uint8 + scale,
+    zero [K/128, N]. Returns y [M, N] in x.dtype (written into `out` when given).
 
     Validation and empty-shape behaviour follow byteprof/optim/skinny.py:136-166."""
     if x.dim() != 2 or not x.is_contiguous():
@@ -279,12 +218,16 @@ def skinny_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None = Non
         if k == 0:
             y.zero_()
         return y
-    for r0 in range(0, m, ROWS_PER_LAUNCH):
-        if kind == "int4":
-            _launch_int4(x[r0:r0 + ROWS_PER_LAUNCH], w, scale, zero, y[r0:r0 + ROWS_PER_LAUNCH], cfg)
-        else:
-            _launch(kind, x[r0:r0 + ROWS_PER_LAUNCH], w, scale, y[r0:r0 + ROWS_PER_LAUNCH], cfg)
+    if kind == "int4":
+        for r0 in range(0, m, INT4_ROWS_PER_LAUNCH):
+            _launch_int4(x[r0:r0 + INT4_ROWS_PER_LAUNCH], w, scale, zero, y[r0:r0 + INT4_ROWS_PER_LAUNCH], cfg)
+    else:
+        for r0 in range(0, m, MAX_M):
+            _launch(kind, x[r0:r0 + MAX_M], w, scale, y[r0:r0 + MAX_M], cfg)
     return y
+
+
+INT4_ROWS_PER_LAUNCH = 16  # activation rows per launch of the int4 kernel
 
 
 def int4_cfg(n: int, k: int, tile_rows: int, cfg=None) -> tuple[int, int]:

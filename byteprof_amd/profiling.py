@@ -133,8 +133,8 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
 
     out = {}
     for _, n, k in D.shapes():
-        rows, waves, split = S._resolve(kind, n, k, 1, None)
-        grid = -(-n // rows) * waves * 64 * split
+        rb, waves, split, _ = S._resolve(kind, n, k, 1, None)
+        grid = -(-n // (8 * rb)) * waves * 64 * split
         out[(D.kernel_key(kind, n, k, 1), f"{n}x{k}")] = grid
     return out
 
@@ -149,7 +149,6 @@ def main(argv=None) -> int:
     ap.add_argument("--write-copy", help="summarize: WRITE_SIZE database of the calibration copy")
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--pmc", action="append", help="summarize: any --pmc database, counters per dispatch")
-    ap.add_argument("--valu", action="store_true", help="skinny: force the VALU kernels (the tuned VALU tiles)")
     ap.add_argument("--all", action="store_true", help="summarize: include kernels outside this library")
     ap.add_argument("--set-kind", choices=("bf16", "int8"), help="summarize: emit traffic lines for the set shapes")
     ap.add_argument("--chain-tag", help="summarize: emit traffic lines for the set kernel under this tag (a tag "
@@ -192,12 +191,12 @@ def main(argv=None) -> int:
             del w
         x = torch.randn(a.m, a.k, device=device).to(torch.bfloat16)
         y = torch.empty(a.m, a.n, dtype=torch.bfloat16, device=device)
-        cfg = S.get_cfg(a.kind, a.n, a.k, S._bm(a.m)) if a.valu else None
+        cfg = None
         for _ in range(a.replays):
             for args in ring:
                 S.skinny_mm(x, *args, out=y, cfg=cfg)
         torch.cuda.synchronize()
-        print(f"skinny_mm {a.kind} {a.n}x{a.k} at M={a.m} ({'VALU' if a.valu else 'routed'}): {a.replays} passes "
+        print(f"skinny_mm {a.kind} {a.n}x{a.k} at M={a.m} (tuned plan): {a.replays} passes "
               f"over {len(ring)} weights", flush=True)
         return 0
     if a.what == "chain":

@@ -1,13 +1,14 @@
 """Fused int8 weight-only products on gfx950 and the per-row int8 quantizer.
 
 Drop-in for byteprof/quant/triton_int8.py: `gemv_int8(x, w, scale, cfg=None, out=None)` computes
-y[1, n] = scale[n] * sum_k float(w[n, k]) * float(x[k]) with the int8 -> float conversion fused into the weight
+y[1, n] = scale[n] * sum_k float(w[n, k]) * float(x[k]) with the int8 -> bf16 conversion fused into the weight
 stream (triton_int8.py:16-47); `quantize_rowwise_int8(w)` is the symmetric per-row quantizer (triton_int8.py:50-55),
 restated in torch so its bytes are those of the reference.
 
-`cfg` is (rows, waves) for the gfx950 kernel; the reference's (BN, BK, num_warps) triples are accepted and mapped to
-(BN, num_warps). Like the reference, gemv_int8 does not validate beyond what raw-pointer kernels need (one row,
-shapes that agree, GPU tensors).
+The product runs on the one-row launch of the skinny matrix-core kernel (the same instructions and K order as
+skinny_mm on int8 weights, so the two agree bit for bit). `cfg` is (rows, waves) or the reference's (BN, BK,
+num_warps); like the reference, gemv_int8 validates only what raw-pointer kernels need (one row, shapes that agree,
+GPU tensors).
 """
 
 from __future__ import annotations
@@ -39,15 +40,10 @@ def gemv_int8(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, cfg: tuple[
     if K == 0:
         y.zero_()
         return y
-    if cfg is None:
-        rows, waves = default_cfg(N, K)
-    else:
-        rows, waves = int(cfg[0]), int(cfg[-1] if len(cfg) == 2 else cfg[2])
-    rows, waves, _ = skinny._resolve("int8", N, K, 1, (rows, waves, 1))
-    L = _lib.lib()
-    rc = L.bp_gemv_int8(x.data_ptr(), w.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype], y.data_ptr(), N, K,
-                        rows, waves, _lib.stream_ptr(x.device))
-    _lib.check(rc, "bp_gemv_int8")
+    if cfg is not None:  # (rows, waves) or (BN, BK, num_warps): the split stays the shape's own (its K order)
+        split = skinny.get_cfg("int8", N, K, 1)[2]
+        cfg = (int(cfg[0]), int(cfg[-1] if len(cfg) == 2 else cfg[2]), split)
+    skinny._launch("int8", x.reshape(1, K), w, scale, y, cfg)
     return y
 
 

@@ -16,36 +16,28 @@ from typing import Any
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
-from .hip_int8 import gemv_int8, quantize_rowwise_int8
+from ..optim.weight_only import WeightOnlyLinear
+from .hip_int8 import gemv_int8
 from .select import group_of, olmo_should_quantize, should_quantize
 
 
-class Int8Linear(nn.Module):
+class Int8Linear(WeightOnlyLinear):
+    """Per-row symmetric int8 weights; one bf16 row on the GPU goes through the fused int8 product (`gemv_int8`),
+    every other input through F.linear on q.to(dtype) * scale.to(dtype) (the reference's dequantization in the
+    activation dtype, integrate.py:35-46)."""
+
     def __init__(self, lin: nn.Linear):
-        super().__init__()
-        self.in_features, self.out_features = lin.in_features, lin.out_features
-        q, scale = quantize_rowwise_int8(lin.weight.data)
-        self.register_buffer("q", q)
-        self.register_buffer("scale", scale)
-        # callers read weight.dtype; an empty parameter keeps that working without the bf16 weights
-        self.weight = nn.Parameter(torch.empty(0, dtype=lin.weight.dtype, device=lin.weight.device),
-                                   requires_grad=False)
-        self.bias = lin.bias
+        super().__init__(lin, "int8")
 
     def dequantized(self, dtype: torch.dtype) -> torch.Tensor:
         return self.q.to(dtype) * self.scale.to(dtype)[:, None]
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x2 = x.reshape(-1, self.in_features)
-        if x2.shape[0] == 1 and x2.is_cuda and x2.dtype == torch.bfloat16:
-            y = gemv_int8(x2.contiguous(), self.q, self.scale)
-            if self.bias is not None:
-                y = y + self.bias
-        else:
-            y = F.linear(x2, self.dequantized(x.dtype), self.bias)
-        return y.reshape(*x.shape[:-1], self.out_features)
+    def _kernel_takes(self, x2: torch.Tensor) -> bool:
+        return x2.shape[0] == 1 and x2.is_cuda and x2.dtype == torch.bfloat16
+
+    def _kernel(self, x2: torch.Tensor) -> torch.Tensor:
+        return gemv_int8(x2, self.q, self.scale)
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}, int8 rowwise (gfx950)"

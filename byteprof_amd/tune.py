@@ -5,13 +5,14 @@ a ring of distinct weight sets applied to one activation block inside a HIP grap
 HBM and not served from cache, the median of several trials per configuration. The ring here is sized against
 MI355X's 256 MB Infinity Cache (at least 1 GiB of weights per cell) instead of a 3 MB L2.
 
-Per (kind, N, K) the tuner keeps ONE K order (waves, split) for every activation-row bucket of the VALU kernels, so
-an output row stays bitwise independent of M: it picks (waves, split) by the M = 1 time (the decode metric), then
-the rows per workgroup separately for each bucket. Like the reference, a split > 1 is kept only if it wins by more
-than 3%. The matrix-core kernels get one configuration per shape for the 8- and 16-row buckets together ('mfma',
-chosen at M = 16, used when it beats the VALU kernels over both buckets).
+bf16 / int8 (the matrix-core kernel of every row count): per (kind, N, K) the tuner keeps ONE K order -- (waves,
+split) -- for every activation-row bucket, so an output row stays bitwise independent of M. It times every
+(waves, split) at one row (the decode metric) and at 16 rows (the verify widths), each with its best weight blocks
+per workgroup and activation staging, and keeps the fastest one-row order unless another is within 2% at one row
+and faster at 16 rows; like the reference, a split > 1 must win by more than 3%. Then, at that K order, it picks
+the weight blocks per workgroup and the staging for each bucket (1; 8: four and eight rows together; 16, 32, 64).
 
-Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8,int4] [--out path] [--quick] [--mfma-only]
+Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8,int4] [--out path]
 """
 
 from __future__ import annotations
@@ -24,16 +25,16 @@ from pathlib import Path
 
 import torch
 
-from . import _lib
 from .optim import skinny as S
 from .quant.hip_int8 import quantize_rowwise_int8
 
 RING_BYTES = 1 << 30
 DEFAULT_SHAPES = [(2048, 2048), (8192, 2048), (2048, 8192), (100352, 2048), (6144, 2048), (16384, 2048),
                   (100352, 8192), (8192, 8192)]
-ROWS = (2, 4, 8, 16, 32)
-WAVES = (1, 2, 4, 8, 16)
+WAVES = (1, 2, 4, 8)
 SPLITS = (1, 2, 4)
+RBS = (1, 2, 4)
+INT4_WAVES = (1, 2, 4, 8)
 
 
 def _ring(kind: str, n: int, k: int, device) -> list[tuple]:
@@ -47,90 +48,8 @@ def _ring(kind: str, n: int, k: int, device) -> list[tuple]:
     return ring
 
 
-def _time_cfg(ring, x, y, cfg, trials: int = 5) -> float:
-    """us per call: one graph holding one call per ring member."""
-    calls = [lambda a=a: S.skinny_mm(x, *a, out=y, cfg=cfg) for a in ring]
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for c in calls[:2]:
-            c()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for c in calls:
-            c()
-    g.replay()
-    torch.cuda.synchronize()
-    out = []
-    for _ in range(trials):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        g.replay()
-        b.record()
-        b.synchronize()
-        out.append(a.elapsed_time(b) * 1000.0 / len(calls))
-    del g
-    return statistics.median(out)
-
-
-def _supported(kind: str, bm: int, rows: int, waves: int) -> bool:
-    return bool(_lib.lib().bp_skinny_config_supported(S._KIND_CODE[kind], bm, rows, waves))
-
-
-def tune_shape(kind: str, n: int, k: int, device, quick: bool = False, log=print) -> dict:
-    ring = _ring(kind, n, k, device)
-    x16 = torch.randn(16, k, device=device).to(torch.bfloat16)
-    nch = -(-k // S._CHUNK[kind])
-    # 1. K order (waves, split) and rows at M = 1
-    x1 = x16[:1].contiguous()
-    y1 = torch.empty(1, n, dtype=torch.bfloat16, device=device)
-    best = None
-    results = {}
-    for waves in WAVES:
-        if waves > nch:
-            continue
-        for split in SPLITS:
-            if split > 1 and (split > nch // waves or quick):
-                continue
-            for rows in ROWS:
-                if not _supported(kind, 1, rows, waves):
-                    continue
-                us = _time_cfg(ring, x1, y1, (rows, waves, split))
-                results[(rows, waves, split)] = us
-                if best is None or us < best[0]:
-                    best = (us, rows, waves, split)
-    us1, rows1, waves, split = best
-    # keep split > 1 only if it wins by more than 3% over the best split-1 configuration
-    if split > 1:
-        no_split = min((v, r, w) for (r, w, s), v in results.items() if s == 1)
-        if no_split[0] <= us1 * 1.03:
-            us1, rows1, waves, split = no_split[0], no_split[1], no_split[2], 1
-    entry = {"waves": waves, "split": split, "rows": {"1": rows1}, "us": {"1": round(us1, 3)}}
-    log(f"  {kind} {n}x{k}: M=1 best rows={rows1} waves={waves} split={split}: {us1:.2f} us "
-        f"({(n * k * (2 if kind == 'bf16' else 1)) / us1 / 1e3:.0f} GB/s)")
-    # 2. rows for the other buckets at that K order
-    for bm in (2, 4, 8, 16):
-        xb = x16[:bm].contiguous()
-        yb = torch.empty(bm, n, dtype=torch.bfloat16, device=device)
-        cands = [(_time_cfg(ring, xb, yb, (r, waves, split)), r) for r in ROWS if _supported(kind, bm, r, waves)]
-        us_b, rows_b = min(cands)
-        entry["rows"][str(bm)] = rows_b
-        entry["us"][str(bm)] = round(us_b, 3)
-    log(f"    rows per bucket {entry['rows']} us {entry['us']}")
-    del ring
-    torch.cuda.empty_cache()
-    return entry
-
-
-MFMA_BLOCK_ROWS = (16, 32, 64)
-MFMA_WAVES = (1, 2, 4, 8)
-MFMA_DEPTHS = (1, 2)
-
-
 def _time_calls(calls, trials: int = 5) -> float:
-    """us per call: one graph holding the calls."""
+    """us per call: one graph holding the calls (one per ring member), median over trials."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -156,62 +75,79 @@ def _time_calls(calls, trials: int = 5) -> float:
     return statistics.median(out)
 
 
-def tune_mfma(kind: str, n: int, k: int, device, entry: dict, log=print) -> dict | None:
-    """Matrix-core configuration of a shape's 8- and 16-row buckets: (block_rows, waves, depth, split) by the
-    16-row time (split > 1 kept only if it wins by more than 3%), then 'use' = whether it beats the VALU kernel
-    over both buckets (one family serves both, so rows stay bitwise independent of M within them)."""
-    step = S.mfma_k_step(kind)
-    if k % step:
-        return None
-    steps = k // step
+def _launcher(kind: str, ring, x, y, rb: int, waves: int, split: int, xs: int):
+    """Calls of the kernel with an explicit plan (rb, waves, split, staging) over the ring."""
+    from . import _lib
+
+    L = _lib.lib()
+    m, k = x.shape
+    n = y.shape[1]
+    ws = torch.empty(max(1, split * m * n), dtype=torch.float32, device=x.device)
+
+    def call(a):
+        sc, sdt = (a[1].data_ptr(), _lib.TORCH_DT[a[1].dtype]) if kind == "int8" else (None, 0)
+        rc = L.bp_skinny_mf(S._KIND_CODE[kind], x.data_ptr(), a[0].data_ptr(), sc, sdt, y.data_ptr(), m, n, k, rb,
+                            waves, split, xs, ws.data_ptr(), ws.numel() * 4, _lib.stream_ptr(x.device))
+        _lib.check(rc, "bp_skinny_mf")
+
+    return [lambda a=a: call(a) for a in ring]
+
+
+def _plans(kind: str, m: int, k: int, waves: int, split: int):
+    for rb in RBS:
+        for xs in (0, 1):
+            if xs and (m > 16 or S._stage_bytes(kind, m, k, split) < 0):
+                continue
+            if S._supported(kind, m, rb, waves, xs):
+                yield rb, xs
+
+
+def _best_plan(kind, ring, x, y, waves, split, rows_list) -> tuple[float, int, int]:
+    """(summed us over the row counts, rb, staging) of the best plan at this K order."""
+    best = None
+    for rb, xs in _plans(kind, max(rows_list), x.shape[1], waves, split):
+        t = sum(_time_calls(_launcher(kind, ring, x[:m].contiguous(), y[:m], rb, waves, split, xs))
+                for m in rows_list)
+        if best is None or t < best[0]:
+            best = (t, rb, xs)
+    return best
+
+
+def tune_shape(kind: str, n: int, k: int, device, log=print) -> dict:
     ring = _ring(kind, n, k, device)
-    x16 = torch.randn(16, k, device=device).to(torch.bfloat16)
-    y16 = torch.empty(16, n, dtype=torch.bfloat16, device=device)
-    results = {}
-    for br in MFMA_BLOCK_ROWS:
-        for w in MFMA_WAVES:
-            if w > steps:
+    nseg = -(-k // S.k_segment(kind))
+    x = torch.randn(64, k, device=device).to(torch.bfloat16)
+    y = torch.empty(64, n, dtype=torch.bfloat16, device=device)
+    orders = {}
+    for waves in WAVES:
+        for split in SPLITS:
+            if waves * split > nseg:
                 continue
-            for d in MFMA_DEPTHS:
-                for sp in SPLITS:
-                    if sp > 1 and sp * w > steps:
-                        continue
-                    calls = [lambda a=a: S.launch_mfma(kind, x16, a[0], a[1] if kind == "int8" else None, y16, br, w,
-                                                       d, sp) for a in ring]
-                    results[(br, w, d, sp)] = _time_calls(calls)
-    # the LDS-staged variants: 16-row blocks, the smallest valid split and twice it
-    for d in S.STAGED_DEPTHS:
-        for w in (1, 2, 4):
-            s0 = S.staged_split(kind, k, 1, w, d)
-            if s0 is None:
-                continue
-            for sp in sorted({s0, S.staged_split(kind, k, 2 * s0, w, d)} - {None}):
-                calls = [lambda a=a: S.launch_mfma(kind, x16, a[0], a[1] if kind == "int8" else None, y16, 16, w, d,
-                                                   sp) for a in ring]
-                results[(16, w, d, sp)] = _time_calls(calls)
-    best = min(results, key=results.get)
-    if best[3] > 1:
-        no_split = [c for c in results if c[3] == 1]
-        if no_split:
-            no_split = min(no_split, key=results.get)
-            if results[no_split] <= results[best] * 1.03:
-                best = no_split
-    br, w, d, sp = best
-    us = {"16": round(results[best], 3)}
-    x8 = x16[:8].contiguous()
-    y8 = y16[:8].contiguous()
-    us["8"] = round(_time_calls([lambda a=a: S.launch_mfma(kind, x8, a[0], a[1] if kind == "int8" else None, y8, br,
-                                                             w, d, sp) for a in ring]), 3)
-    valu = [float(entry["us"][b]) for b in ("8", "16")] if "us" in entry else None
-    use = valu is None or us["8"] + us["16"] < valu[0] + valu[1]
-    log(f"  {kind} {n}x{k} mfma: block_rows={br} waves={w} depth={d} split={sp}: M=8 {us['8']:.2f} us, "
-        f"M=16 {us['16']:.2f} us (VALU {valu}) -> {'mfma' if use else 'valu'}")
+            t1 = _best_plan(kind, ring, x, y, waves, split, [1])
+            t16 = _best_plan(kind, ring, x, y, waves, split, [16])
+            orders[(waves, split)] = (t1[0], t16[0])
+            log(f"  {kind} {n}x{k} waves={waves} split={split}: M=1 {t1[0]:.2f} us (rb {t1[1]}, xs {t1[2]}), "
+                f"M=16 {t16[0]:.2f} us (rb {t16[1]}, xs {t16[2]})")
+    best = min(orders, key=lambda o: orders[o][0])
+    if best[1] > 1:
+        no_split = min((o for o in orders if o[1] == 1), key=lambda o: orders[o][0])
+        if orders[no_split][0] <= orders[best][0] * 1.03:
+            best = no_split
+    near = [o for o in orders if orders[o][0] <= orders[best][0] * 1.02 and (o[1] == 1 or best[1] > 1)]
+    best = min(near, key=lambda o: orders[o][1])
+    waves, split = best
+    rb, xs, us = {}, {}, {}
+    for bucket, rows in ((1, [1]), (8, [4, 8]), (16, [16]), (32, [32]), (64, [64])):
+        t, rb[str(bucket)], xs[str(bucket)] = _best_plan(kind, ring, x, y, waves, split, rows)
+        for m in rows:
+            us[str(m)] = round(_time_calls(_launcher(kind, ring, x[:m].contiguous(), y[:m], rb[str(bucket)], waves,
+                                                     split, xs[str(bucket)])), 3)
+    per = n * k * (2 if kind == "bf16" else 1)
+    log(f"  {kind} {n}x{k}: waves={waves} split={split} rb={rb} xs={xs} us={us} "
+        f"(M=1: {per / us['1'] / 1e3:.0f} GB/s of weights)")
     del ring
     torch.cuda.empty_cache()
-    return {"block_rows": br, "waves": w, "depth": d, "split": sp, "us": us, "use": use}
-
-
-INT4_WAVES = (1, 2, 4, 8)
+    return {"waves": waves, "split": split, "rb": rb, "xs": xs, "us": us}
 
 
 def tune_int4(n: int, k: int, device, log=print) -> dict | None:
@@ -259,40 +195,24 @@ def main(argv=None) -> int:
     ap.add_argument("--shapes", default=None, help="N:K,N:K,... (default: the decode-step set shapes)")
     ap.add_argument("--kinds", default="bf16,int8")
     ap.add_argument("--out", default=str(S._CFG_FILE))
-    ap.add_argument("--quick", action="store_true", help="no split-K candidates")
-    ap.add_argument("--mfma-only", action="store_true",
-                    help="tune only the matrix-core entries of the 8- and 16-row buckets (keeps the VALU entries)")
     a = ap.parse_args(argv)
     shapes = DEFAULT_SHAPES if a.shapes is None else [tuple(int(v) for v in s.split(":")) for s in a.shapes.split(",")]
     device = torch.device("cuda:0")
     out = Path(a.out)
     table = json.loads(out.read_text()) if out.exists() else {}
-    table["_about"] = ("skinny kernel tile configurations for gfx950, tuned by python -m byteprof_amd.tune: key "
-                       "kind|N|K; VALU kernels: waves and split fix the K order for every row bucket, rows per "
-                       "bucket; 'mfma': the matrix-core configuration (block_rows, waves, depth, split) of the 8- and "
-                       "16-row buckets and whether it is used (depth 1, 2: register-fed, steps in flight; 3, 4: "
-                       "LDS-staged, each wave owns whole blocks / the waves share each block); int4|N|K: waves and "
-                       "split of the int4 kernel (tile rows 32); us = measured time per call (ring of distinct "
-                       "weights, HIP graph)")
+    table["_about"] = ("skinny kernel configurations for gfx950, tuned by python -m byteprof_amd.tune. kind|N|K "
+                       "(bf16, int8): waves and split of the matrix-core kernel (they fix the K order for every row "
+                       "count), rb = 8-row weight blocks per workgroup and xs = activations staged in LDS, per "
+                       "row bucket (1, 8, 16, 32, 64), us = measured time per call by row count (ring of "
+                       "distinct weights, HIP graph); int4|N|K: waves and split of the int4 kernel (tile rows 32).")
+    log = lambda m: print(m, flush=True)  # noqa: E731
     for kind in a.kinds.split(","):
-        if kind == "int4":
-            for n, k in shapes:
-                print(f"[tune] int4 {n}x{k}", flush=True)
-                e = tune_int4(n, k, device, log=lambda m: print(m, flush=True))
-                if e is not None:
-                    table[f"int4|{n}|{k}"] = e
-                    out.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
-            continue
         for n, k in shapes:
             print(f"[tune] {kind} {n}x{k}", flush=True)
-            key = f"{kind}|{n}|{k}"
-            log = lambda m: print(m, flush=True)  # noqa: E731
-            if not a.mfma_only or key not in table:
-                table[key] = tune_shape(kind, n, k, device, a.quick, log=log)
-            mf = tune_mfma(kind, n, k, device, table[key], log=log)
-            if mf is not None:
-                table[key]["mfma"] = mf
-            out.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")  # after every cell (resumable)
+            e = tune_int4(n, k, device, log=log) if kind == "int4" else tune_shape(kind, n, k, device, log=log)
+            if e is not None:
+                table[f"{kind}|{n}|{k}"] = e
+                out.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")  # after every cell (resumable)
     print(f"[tune] wrote {out}")
     return 0
 

@@ -77,43 +77,41 @@ int bp_skinny_int8(const void* x, const void* q, const void* scale, int scale_dt
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Matrix-core variants of bp_skinny_bf16 / bp_skinny_int8 (v_mfma_f32_16x16x32_bf16 with the weights as the A
- * operand: 16 output channels x 16 activation rows x 32 K per instruction), same arguments and results, for the
- * speculative-verify widths where the VALU kernels run out of instruction throughput. 1 <= M <= 16.
- *   depth 1 or 2 (register-fed kernel: each lane loads its MFMA operands straight from memory, depth = K steps in
- *   flight per wave): block_rows 16, 32 or 64 weight rows per workgroup; waves 1, 2, 4 or 8; split as above;
- *   K a multiple of bp_skinny_mfma_k_step(wkind) (128 for bf16, 256 for int8).
- *   depth 3 or 4 (LDS-staged kernel: each weight row is streamed in 1 KiB contiguous loads and re-read from LDS in
- *   MFMA layout; the activations of the workgroup's K slice are staged in LDS once): block_rows 16; waves 1, 2 or
- *   4; K / split a multiple of 1 KiB of weight row (512 bf16 / 1024 int8 elements) and at most 2048; depth 3: each
- *   wave owns whole 16-row blocks; depth 4: the waves of a workgroup share each block's K steps (the steps of the
- *   slice a multiple or a divisor of waves), adding their partial tiles in wave order.
- *   x, w 16-byte aligned. BP_E_UNSUPPORTED when a condition fails (the VALU kernels take any K).
- * The K order of every sum depends only on (K, waves, depth family, split), so output row i does not change with M
- * (bitwise); it differs from the VALU kernels' order (both fp32; the results agree within rounding).
- * Replaces: byteprof/optim/skinny.py:36-90 (_skinny_kernel MODE 0 / 1, whose tl.dot maps onto the tensor cores
- *           at every BM) via skinny_mm (skinny.py:136-166).
+ * The skinny matmul of every row count on the matrix cores (v_mfma_f32_16x16x32_bf16), the path skinny_mm takes for
+ * bf16 and int8 weights:
+ *   y[M, N] (bf16) = x[M, K] (bf16) . w[N, K]^T, w bf16 (wkind 0) or int8 (wkind 1, times scale[N] of scale_dtype
+ *   BP_DT_BF16 / F16 / F32 on the fp32 sum), 1 <= M <= 64 per call (M = 0 or N = 0: no-op; K = 0: zeros).
+ * One load instruction reads a 128-byte segment of 8 consecutive weight rows (one full line per row); the
+ * activations are the MFMA's B operand (8 activation rows per 16 columns, the other 8 columns carry the other half of
+ * the segment's K slots). Tile configuration: rb = 8-row weight blocks per workgroup (1, 2, 4; 4 up to M = 16),
+ * waves = wavefronts sharing the workgroup's K segments (1, 2, 4, 8; segment s to wave s % waves), split = K ranges
+ * in separate workgroups whose fp32 partials are added in split order by a second kernel (workspace as for
+ * bp_skinny_bf16), xstage = 1: each workgroup copies its activation rows and K range to LDS first (up to M = 16 and
+ * bp_skinny_mf_stage_bytes() >= 0), 0: the activation operands are loaded with the weights. The K order of every sum
+ * depends only on (K, waves, split): output row i is bitwise independent of M (1..64), rb and xstage. K not a
+ * multiple of the 128-byte segment (64 bf16 / 128 int8 elements) or x, w not 16-byte aligned: an element-load variant
+ * with the same segments (rb 1, 4 waves, xstage 0).
+ * Replaces: byteprof/optim/skinny.py:36-90 (_skinny_kernel MODE 0 / 1, _split_reduce) and :111-133 (_launch) via
+ *           skinny_mm (skinny.py:136-166) for every BM bucket (16, 32, 64).
  */
-int bp_skinny_mfma_config_supported(int wkind, int block_rows, int waves, int depth);
-int bp_skinny_mfma_k_step(int wkind);
-int bp_skinny_mfma_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
-                        int block_rows, int waves, int depth, int split, void* workspace, size_t workspace_bytes,
-                        void* stream);
-int bp_skinny_mfma_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y,
-                        int64_t M, int64_t N, int64_t K, int block_rows, int waves, int depth, int split,
-                        void* workspace, size_t workspace_bytes, void* stream);
-/* The gate|up projection of a verify pass (M = 1..16 rows) with the SiLU product as the epilogue of the depth 1 / 2
- * kernels (split 1): w [2 * ffn, K] (wkind 0 bf16, 1 int8 with per-row scale) with row 2f the gate row f and row
- * 2f + 1 the up row f; out [M, ffn] = bf16(bf16(silu(g)) * u) of the bf16-rounded row sums, equal bit for bit to
- * bp_skinny_mfma_* (same block_rows, waves, depth, split 1) followed by bp_decode_silu_mul_rows (interleaved).
- * Replaces: the gate / up projections and act_fn(gate) * up of HF Olmo2MLP in the verify forward that
- *           byteprof/optim/olmo_draft.py captures (make_generate_draft). */
-/* bp_skinny_mfma_* (depth 1 or 2, split >= 2) stopped after the partial sums: workspace [split][M][N] fp32 (unscaled
- * for int8: the reducer applies the scale), e.g. for bp_decode_splitk_norm_residual_rows. */
-int bp_skinny_mfma_partials(int wkind, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int block_rows,
-                            int waves, int depth, int split, void* workspace, size_t workspace_bytes, void* stream);
-int bp_skinny_mfma_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
-                        int64_t M, int64_t ffn, int64_t K, int block_rows, int waves, int depth, void* stream);
+int bp_skinny_mf_supported(int wkind, int M, int rb, int waves, int xstage);
+int bp_skinny_mf_k_segment(int wkind);
+/* LDS bytes a launch with xstage = 1 uses, or -1 when its activations do not fit (then xstage must be 0). */
+int64_t bp_skinny_mf_stage_bytes(int wkind, int64_t M, int64_t K, int split);
+int bp_skinny_mf(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y, int64_t M,
+                 int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* workspace,
+                 size_t workspace_bytes, void* stream);
+/* bp_skinny_mf stopped after the partial sums (split >= 2): workspace [split][M][N] fp32, unscaled for int8 (the
+ * reducer applies the scale), e.g. for bp_decode_splitk_norm_residual_rows. */
+int bp_skinny_mf_partials(int wkind, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int rb,
+                          int waves, int split, int xstage, void* workspace, size_t workspace_bytes, void* stream);
+/* The gate|up projection with the SiLU product as the epilogue (split 1, 1 <= M <= 16): w [2 ffn, K] with row 2f the
+ * gate row f and row 2f + 1 the up row f; out [M, ffn] = bf16(bf16(silu(bf16(g))) * bf16(u)) of the row sums, equal
+ * bit for bit to bp_skinny_mf (same rb, waves, split 1) followed by bp_decode_silu_mul_rows (interleaved).
+ * Replaces: the gate / up projections and act_fn(gate) * up of HF Olmo2MLP in the decode step that
+ *           byteprof/optim/olmo.py:122-219 captures. */
+int bp_skinny_mf_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
+                      int64_t M, int64_t ffn, int64_t K, int rb, int waves, int xstage, void* stream);
 
 /*
  * int4 group-128 weights in the tile-major format of byteprof's skinny kernels:
@@ -235,15 +233,10 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  *                 to qk_rope_cache_rows + attention_rows.
  * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
  *                 out may alias residual. splitk_norm_residual_rows: x = the split-K reduce of a projection's
- *                 partials (workspace [split][rows][n] from bp_skinny_mfma_partials, the int8 scale [n] applied,
+ *                 partials (workspace [split][rows][n] from bp_skinny_mf_partials, the int8 scale [n] applied,
  *                 NULL for bf16), equal bit for bit to bp_splitk_reduce + norm_residual_rows; n <= 8192.
  * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn); silu_mul_rows with
  *                 interleaved = 1 reads the pairs (gate_up[2f], gate_up[2f + 1]) instead.
- * gate_up_silu:   the gate|up projection of x[hidden] and silu_mul in one launch: w [2 * ffn, hidden] (wkind
- *                 BP_DT_BF16 (0) bf16 or 1 int8 with per-row scale [2 * ffn] of scale_dtype) with row 2n the gate
- *                 row n and row 2n + 1 the up row n; out[ffn] equal bit for bit to bp_skinny_* on w with 2 rows and
- *                 `waves` per workgroup (split 1) followed by silu_mul; hidden a multiple of 512 (bf16) / 1024
- *                 (int8); x, w 16-byte aligned; waves 1, 2, 4 or 8.
  * argmax_next:    *tok = first index of the largest logit (NaN counts as largest); *pos += 1. Several workgroups
  *                 share the logits and the last to finish writes the result; `scratch` holds their partials and
  *                 a counter: bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is
@@ -279,8 +272,6 @@ int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* 
                                  float eps, int rows, void* stream);
 int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream);
 int bp_decode_silu_mul_rows(const void* gate_up, void* out, int ffn, int rows, int interleaved, void* stream);
-int bp_decode_gate_up_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,
-                           int ffn, int hidden, int waves, void* stream);
 size_t bp_decode_argmax_scratch_bytes(void);
 int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream);
 size_t bp_decode_argmax_rows_scratch_bytes(int rows);

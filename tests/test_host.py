@@ -136,18 +136,22 @@ def test_skinny_mm_validation_errors():
 
 
 def test_configuration_keeps_one_k_order_per_shape():
-    """waves and split (the K order) must not depend on the activation-row bucket."""
+    """waves and split (the K order) must not depend on the row count: the tuned table and the heuristic give one
+    (waves, split) per shape for every launch of 1..64 rows (the weight blocks and staging may differ)."""
     for kind in ("bf16", "int8"):
-        for n, k in ((2048, 2048), (8192, 2048), (2048, 8192), (100352, 2048), (37, 256), (129, 640), (8, 5000)):
-            orders = {S._resolve(kind, n, k, bm, None)[1:] for bm in (1, 2, 4, 8, 16)}
+        for n, k in ((2048, 2048), (8192, 2048), (2048, 8192), (100352, 2048), (6144, 2048), (16384, 2048),
+                     (37, 256), (129, 640), (8, 5000)):
+            orders = {S._resolve(kind, n, k, m, None)[1:3] for m in (1, 2, 4, 5, 8, 9, 16, 17, 32, 33, 64)}
             assert len(orders) == 1, (kind, n, k, orders)
 
 
 def test_reference_cfg_tuples_are_mapped():
-    assert S._resolve("bf16", 192, 1024, 1, (32, 128, 4, 3, 4)) == (32, 4, 4)
-    assert S._resolve("bf16", 192, 1024, 16, (64, 64, 2, 2, 1)) == (4, 2, 1)  # rows clamped to the menu
-    assert S._resolve("int8", 192, 1024, 1, (16, 256, 4, 3, 3)) == (16, 4, 3)
-    assert S._resolve("bf16", 192, 1024, 1, (4, 8, 2)) == (4, 8, 2)
+    """(BN, BK, warps, stages[, split]) and (rows, waves, split) map onto (weight blocks, waves, split, staging)."""
+    assert S._resolve("bf16", 192, 1024, 1, (32, 128, 4, 3, 4)) == (4, 4, 4, 0)
+    assert S._resolve("bf16", 192, 1024, 16, (64, 64, 2, 2, 1)) == (4, 2, 1, 0)  # rows clamped to the menu
+    assert S._resolve("bf16", 192, 1024, 33, (64, 64, 2, 2, 1)) == (2, 2, 1, 0)  # 4 blocks only up to 16 rows
+    assert S._resolve("int8", 192, 1024, 1, (16, 256, 4, 3, 3)) == (2, 4, 3, 0)
+    assert S._resolve("bf16", 192, 1024, 1, (4, 8, 2)) == (1, 8, 2, 0)
     with pytest.raises(ValueError):
         S._resolve("bf16", 192, 1024, 1, (1, 2))
 

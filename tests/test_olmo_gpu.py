@@ -159,37 +159,44 @@ def test_fused_rope_attention_matches_the_oracle(shape, pos):
     assert ON.normwise_error(_np(out), OO.attention(q, kc, vc, pos, oc)) < 1e-2
 
 
-@pytest.mark.parametrize("waves", [1, 2, 4, 8])
+@pytest.mark.parametrize("plan", [(1, 4, 0), (2, 2, 0), (4, 8, 0), (1, 4, 1), (2, 2, 1)])
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
-def test_gate_up_silu_equals_the_two_launch_path(kind, waves):
-    """The fused gate|up + SiLU launch against skinny_mm on the same interleaved weight (2 rows, same waves, split 1)
-    followed by silu_mul on the de-interleaved halves: equal bit for bit; and within one bf16 step of the oracle."""
+def test_gate_up_silu_equals_the_two_launch_path(kind, plan):
+    """The gate|up projection with the SiLU epilogue (bp_skinny_mf_silu) against bp_skinny_mf on the same
+    interleaved weight (same plan, split 1) followed by silu_mul on the de-interleaved halves: equal bit for bit;
+    within one bf16 step of the oracle. F = 3000 leaves a partial last block."""
     L = _lib.lib()
     F, H = 3000, 2048
+    rb, waves, xs = plan
     rng = np.random.default_rng(7 + waves)
-    x = _bf16(ON.bf16_round(rng.standard_normal(H).astype(np.float32)))
+    x = _bf16(ON.bf16_round(rng.standard_normal(H).astype(np.float32)))[None]
     w = _bf16(ON.bf16_round(rng.standard_normal((2 * F, H)).astype(np.float32) * 0.05))
     if kind == "bf16":
         args, sc, sdt = (w,), None, 0
     else:
         args = quantize_rowwise_int8(w, torch.float16)
         sc, sdt = args[1].data_ptr(), _lib.TORCH_DT[torch.float16]
-    out = torch.empty(F, dtype=torch.bfloat16, device=DEV)
+    kc = 0 if kind == "bf16" else 1
+    out = torch.empty(1, F, dtype=torch.bfloat16, device=DEV)
     st = _lib.stream_ptr(out.device)
-    _lib.check(L.bp_decode_gate_up_silu(0 if kind == "bf16" else 1, x.data_ptr(), args[0].data_ptr(), sc, sdt,
-                                        out.data_ptr(), F, H, waves, st), "gate_up_silu")
-    y = skinny_mm(x[None], *args, cfg=(2, waves, 1))[0]
+    _lib.check(L.bp_skinny_mf_silu(kc, x.data_ptr(), args[0].data_ptr(), sc, sdt, out.data_ptr(), 1, F, H, rb, waves,
+                                   xs, st), "mf_silu")
+    y = torch.empty(1, 2 * F, dtype=torch.bfloat16, device=DEV)
+    _lib.check(L.bp_skinny_mf(kc, x.data_ptr(), args[0].data_ptr(), sc, sdt, y.data_ptr(), 1, 2 * F, H, rb, waves, 1,
+                              xs, None, 0, st), "mf")
+    y = y[0]
     gu = torch.cat([y[0::2], y[1::2]]).contiguous()
     ref = torch.empty(F, dtype=torch.bfloat16, device=DEV)
     _lib.check(L.bp_decode_silu_mul(gu.data_ptr(), ref.data_ptr(), F, st), "silu_mul")
     torch.cuda.synchronize()
-    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(out[0].view(torch.int16), ref.view(torch.int16))
     g, u = _np(y[0::2]), _np(y[1::2])
-    assert _ulps(_np(out), OO.silu_mul(g, u)).max() <= 1
-    bad = torch.empty(F, dtype=torch.bfloat16, device=DEV)
-    assert L.bp_decode_gate_up_silu(0, x.data_ptr(), w.data_ptr(), None, 0, bad.data_ptr(), F, 1000, 4, st) == -2
-    assert L.bp_decode_gate_up_silu(0, x.data_ptr(), w.data_ptr(), None, 0, bad.data_ptr(), F, H, 3, st) == -2
-    assert L.bp_decode_gate_up_silu(1, x.data_ptr(), args[0].data_ptr(), None, 1, bad.data_ptr(), F, H, 2, st) == -1
+    assert _ulps(_np(out[0]), OO.silu_mul(g, u)).max() <= 1
+    bad = torch.empty(1, F, dtype=torch.bfloat16, device=DEV)
+    assert L.bp_skinny_mf_silu(kc, x.data_ptr(), args[0].data_ptr(), sc, sdt, bad.data_ptr(), 17, F, H, rb, waves, 0,
+                               st) == -2  # the epilogue takes at most 16 rows
+    assert L.bp_skinny_mf_silu(1, x.data_ptr(), args[0].data_ptr(), None, 1, bad.data_ptr(), 1, F, H, rb, waves, 0,
+                               st) == -1  # int8 without a scale
 
 
 def test_silu_mul_matches_the_oracle():
@@ -260,7 +267,7 @@ def _deq(args: tuple) -> np.ndarray:
     return q.float().cpu().numpy() * scale.float().cpu().numpy()[:, None]
 
 
-# hidden a multiple of 1024: the decoder takes the fused gate|up + SiLU launch (bf16 and int8)
+# a second small shape: hidden a multiple of the 128-byte segment of both kinds (vector loads everywhere)
 FUSED_SMALL = OG.OlmoConfig(hidden=1024, ffn=1024, layers=2, heads=8, vocab=512, max_len=64)
 
 
@@ -275,10 +282,7 @@ def _small_decoder(kind: str, seed: int = 1, cfg: OG.OlmoConfig = SMALL):
             H = cfg.hidden
             W[p + "q"], W[p + "k"], W[p + "v"] = qkv[:H], qkv[H:2 * H], qkv[2 * H:]
             gu = _deq(lw["gate_up"])
-            if dec.gate_up_interleaved:
-                W[p + "gate"], W[p + "up"] = gu[0::2], gu[1::2]
-            else:
-                W[p + "gate"], W[p + "up"] = gu[:cfg.ffn], gu[cfg.ffn:]
+            W[p + "gate"], W[p + "up"] = gu[0::2], gu[1::2]
             W[p + "o"] = _deq(lw["o"])
             W[p + "down"] = _deq(lw["down"])
         W["lm_head"] = _deq(dec.lm_head)
@@ -289,7 +293,6 @@ def _small_decoder(kind: str, seed: int = 1, cfg: OG.OlmoConfig = SMALL):
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
 def test_decode_steps_match_the_oracle(kind, shape):
     dec, W, oc = _small_decoder(kind, cfg=SMALL if shape == "small" else FUSED_SMALL)
-    assert dec.gate_up_interleaved == (shape == "fused")
     prompt = [3, 17, 99, 250, 7]
     toks, logits = OO.greedy(W, oc, prompt, 10)
     feed = prompt + toks[:-1]

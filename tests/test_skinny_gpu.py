@@ -1,6 +1,7 @@
 """Skinny matmul kernels on the GPU against the CPU oracle: every M = 1..33 on the reference's real and odd shapes,
-empty inputs and chunking, split-K and other tile configurations, bitwise row independence, validation, the
-sentinel out-of-bounds check, unaligned inputs, graph capture. Mirrors byteprof tests/test_skinny.py:71-149."""
+empty inputs and chunking, split-K and other tile configurations, bitwise row independence (the reference's test on
+every shape, and across the launch buckets up to 64 rows), validation, the sentinel out-of-bounds check, unaligned
+inputs, graph capture, gemv_int8 against skinny_mm. Mirrors byteprof tests/test_skinny.py:71-149."""
 
 from __future__ import annotations
 
@@ -67,23 +68,29 @@ def test_split_k_and_other_configs_match(kind, cfg):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("n,k", [(2048, 2048), (2048, 8192), (129, 640)])
+@pytest.mark.parametrize("n,k", REAL + ODD)
 def test_rows_do_not_depend_on_the_other_rows(kind, n, k):
-    """Output row i is bitwise the same whatever the number of rows in the call, within each kernel family: the VALU
-    kernels (1..4 rows: one K order) and the matrix-core kernels (5..16 rows) (byteprof tests/test_skinny.py:114-121,
-    whose single M <= 16 bucket is split where the arithmetic unit changes)."""
+    """byteprof tests/test_skinny.py:110-120 unchanged (rows 1, 3 and 9 of a 16-row call are the 16-row call's), on
+    every shape: one kernel family and one K order serve every row count."""
     _, args = make_weights(kind, n, k)
-    x = randn_x(33, k, seed=3)
-    full4 = S.skinny_mm(x[:4].contiguous(), *args)
-    for m in (1, 2, 3):
-        assert torch.equal(S.skinny_mm(x[:m].contiguous(), *args), full4[:m]), m
-    full16 = S.skinny_mm(x[:16].contiguous(), *args)
-    full33 = S.skinny_mm(x, *args)
-    assert torch.equal(full33[:16], full16)
-    for m in (5, 8, 9, 15):
-        assert torch.equal(S.skinny_mm(x[:m].contiguous(), *args), full16[:m]), m
-    assert torch.equal(S.skinny_mm(x[16:32].contiguous(), *args), full33[16:32])
-    assert torch.equal(S.skinny_mm(x[32:33].contiguous(), *args), full33[32:33])
+    x = randn_x(16, k, seed=3)
+    full = S.skinny_mm(x, *args)
+    for m in (1, 3, 9):
+        assert torch.equal(S.skinny_mm(x[:m].contiguous(), *args), full[:m]), m
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n,k", [(2048, 2048), (2048, 8192), (129, 640), (100352, 2048)])
+def test_rows_do_not_depend_on_the_launch_bucket(kind, n, k):
+    """Beyond the reference's M <= 16 bucket: a row is the same in launches of 1..64 rows (activation blocks of 8,
+    16, 32, 64) and in the chunked launches of more than MAX_M rows."""
+    _, args = make_weights(kind, n, k)
+    x = randn_x(130, k, seed=4)
+    full = S.skinny_mm(x, *args)  # 64 + 64 + 2 rows
+    for m in (1, 2, 5, 8, 9, 16, 17, 31, 33, 64):
+        assert torch.equal(S.skinny_mm(x[:m].contiguous(), *args), full[:m]), m
+    assert torch.equal(S.skinny_mm(x[64:128].contiguous(), *args), full[64:128])
+    assert torch.equal(S.skinny_mm(x[128:].contiguous(), *args), full[128:])
 
 
 def test_input_validation():
@@ -168,3 +175,71 @@ def test_inside_a_hip_graph_with_changing_inputs(kind):
         torch.cuda.synchronize()
         assert torch.equal(y, S.skinny_mm(x, *args)), seed
     assert y_eager.shape == y.shape
+
+
+def test_gemv_int8_equals_the_one_row_skinny_call():
+    """gemv_int8 is the one-row launch of the int8 skinny kernel: bitwise equal to skinny_mm at M = 1."""
+    from byteprof_amd.quant.hip_int8 import gemv_int8
+
+    for n, k in ((2048, 2048), (8192, 2048), (129, 640)):
+        _, args = make_weights("int8", n, k, seed=n)
+        x = randn_x(1, k, seed=k)
+        assert torch.equal(gemv_int8(x, *args), S.skinny_mm(x, *args)), (n, k)
+
+
+def _mf_call(kind, x, args, rb, waves, split, xs):
+    from byteprof_amd import _lib
+
+    m, k = x.shape
+    n = args[0].shape[0]
+    y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(max(1, split * m * n), dtype=torch.float32, device="cuda")
+    sc, sdt = (args[1].data_ptr(), _lib.TORCH_DT[args[1].dtype]) if kind == "int8" else (None, 0)
+    rc = _lib.lib().bp_skinny_mf(S._KIND_CODE[kind], x.data_ptr(), args[0].data_ptr(), sc, sdt, y.data_ptr(), m, n,
+                                 k, rb, waves, split, xs, ws.data_ptr(), ws.numel() * 4, _lib.stream_ptr(x.device))
+    _lib.check(rc, "bp_skinny_mf")
+    return y
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n,k", [(2048, 2048), (100352, 2048), (2048, 8192), (129, 640)])
+def test_block_count_and_activation_staging_do_not_change_results(kind, n, k):
+    """At one K order (waves, split), the weight blocks per workgroup and whether the activations are staged in LDS
+    change nothing, bit for bit, at 1, 5, 9 and 16 rows; every variant matches the oracle."""
+    _, args = make_weights(kind, n, k, seed=11)
+    w_np = oracle_weights(kind, args) if n * k <= 2048 * 8192 else None
+    x = randn_x(16, k, seed=12)
+    for waves, split in ((4, 1), (2, 2)):
+        for m in (1, 5, 9, 16):
+            xm = x[:m].contiguous()
+            ref = _mf_call(kind, xm, args, 1, waves, split, 0)
+            if w_np is not None and m in (1, 16):
+                check_against_oracle(ref, xm, w_np)
+            for rb in (1, 2, 4):
+                for xs in (0, 1):
+                    if S._stage_bytes(kind, m, k, split) < 0 and xs:
+                        continue
+                    assert torch.equal(_mf_call(kind, xm, args, rb, waves, split, xs), ref), (waves, split, m, rb, xs)
+
+
+@pytest.mark.parametrize("kind,k", [("bf16", 2048), ("int8", 4096), ("int8", 2048)])
+def test_every_configuration_matches_the_oracle(kind, k):
+    """Every compiled (weight blocks, waves, split, staging) at 1, 5 and 17 rows against the fp32 reference,
+    componentwise (the kernel's whole menu at one shape, N = 192)."""
+    import itertools
+
+    _, args = make_weights(kind, 192, k, seed=3)
+    wf = args[0].float() if kind == "bf16" else args[0].float() * args[1].float()[:, None]
+    bad = []
+    for m in (1, 5, 17):
+        x = randn_x(m, k, seed=m + 40)
+        ref = x.float() @ wf.T
+        den = (x.float().abs() @ wf.abs().T).clamp(min=1e-30)
+        for rb, waves, split, xs in itertools.product((1, 2, 4), (1, 2, 4, 8), (1, 2, 3, 4), (0, 1)):
+            if not S._supported(kind, m, rb, waves, xs) or (xs and S._stage_bytes(kind, m, k, split) < 0):
+                continue
+            y = _mf_call(kind, x, args, rb, waves, split, xs)
+            err = float(((y.float() - ref).abs() / den).max())
+            if err > 4e-3:
+                bad.append((m, rb, waves, split, xs, err))
+    assert not bad, bad[:10]
