@@ -50,7 +50,8 @@ def units() -> list[tuple[Path, list[str], Path]]:
            (CSRC / "draft.hip", [], BUILD_DIR / "draft.o"),
            (CSRC / "decode.hip", [], BUILD_DIR / "decode.o"),
            (CSRC / "skinny_group.hip", [], BUILD_DIR / "skinny_group.o"),
-           (CSRC / "skinny_mf.hip", [], BUILD_DIR / "skinny_mf.o")]
+           (CSRC / "skinny_mf.hip", [], BUILD_DIR / "skinny_mf.o"),
+           (CSRC / "skinny_chain.hip", [], BUILD_DIR / "skinny_chain.o")]
     for kind in KINDS:
         for mt in ROW_BUCKETS:
             out.append((CSRC / "skinny_inst.hip", [f"-DBP_KIND={kind}", f"-DBP_MT={mt}"],

@@ -37,10 +37,24 @@ __device__ __forceinline__ uint32_t i8pair_to_bf16x2(uint32_t d, int sh) {
 }
 
 // Load a scale element of the given dtype code as fp32 (0 = bf16, 1 = fp16, 2 = fp32).
+// Global-memory views of generic pointers. Pointers read from memory (not kernel arguments) are otherwise
+// accessed with flat instructions, which also count against the LDS wait counter, so every LDS access would wait
+// for all outstanding memory loads.
+template <class T>
+using gptr = __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ gptr<const T> as_global(const T* p) {
+  return (gptr<const T>)(p);
+}
+template <class T>
+__device__ __forceinline__ gptr<T> as_global_mut(T* p) {
+  return (gptr<T>)(p);
+}
+
 __device__ __forceinline__ float load_scale(const void* p, int64_t i, int dt) {
-  if (dt == 0) return bf16_bits_to_float(static_cast<const uint16_t*>(p)[i]);
-  if (dt == 1) return static_cast<float>(static_cast<const _Float16*>(p)[i]);
-  return static_cast<const float*>(p)[i];
+  if (dt == 0) return bf16_bits_to_float(as_global(static_cast<const uint16_t*>(p))[i]);
+  if (dt == 1) return static_cast<float>(as_global(static_cast<const _Float16*>(p))[i]);
+  return as_global(static_cast<const float*>(p))[i];
 }
 
 // Sum of v over the 64 lanes of the wave, for P values at once (P a power of two). Butterfly stages pair lanes

@@ -198,7 +198,7 @@ struct MfMain {
       for (int rb = 0; rb < RB; ++rb) {
         if constexpr (VEC) {
           const uint8_t* p = live ? wrow[rb] + s * 128 : static_cast<const uint8_t*>(ph);
-          sl.w[rb] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+          sl.w[rb] = __builtin_nontemporal_load(as_global(reinterpret_cast<const u32x4*>(p)));
         } else {
           sl.w[rb] = live ? mf_load_w16<KIND, false>(wrow[rb], s * G::kSeg + kl, K) : u32x4{0u, 0u, 0u, 0u};
         }

@@ -6,10 +6,10 @@ Infinity Cache, so nothing is served from cache across replays). Weights ~ N(0, 
 ~ N(0, 1) renormalised to unit RMS. The reference measures the same linears one call each inside a CUDA graph
 (byteprof tools/skinny_bench.py:45-71; FINDINGS "OLMo-2 16-block linear set").
 
-The same independent linears also run as one grouped launch (`group_of`, optim/skinny_group.py): one grid over the
-row blocks of all 113 linears, every output bitwise equal to its own skinny_mm call.
+The same independent linears also run as one launch (`group_of`, optim/linear_chain.py): one grid over the row
+blocks of all 113 linears, every output bitwise equal to its own skinny_mm call with the same plan.
 
-The same linears also run as one persistent launch (`build_chain`, optim/linear_set.py): stages q|k|v, o,
+The same linears also run as one dependent launch (`build_chain`, optim/linear_chain.py): stages q|k|v, o,
 gate|up, down per layer and the head, each stage's input the unit-RMS renormalisation of the output it depends on
 in a decode step (o <- v: attention over one cached position returns v; gate|up <- o; down <- up; the next
 layer's q|k|v and the head <- down), or, in the independent variant, a fresh unit-RMS vector per stage with no
@@ -26,12 +26,12 @@ from dataclasses import dataclass
 import torch
 
 from .optim import skinny as S
-from .optim.linear_set import LinearSet, Stage
-from .optim.skinny_group import GroupItem, SkinnyGroup
+from .optim.linear_chain import ChainStage, LinearChain
 from .quant.accounting import Linear, call_bytes
 from .quant.hip_int8 import quantize_rowwise_int8
 
 LAYERS = 16
+CHAIN_RB, CHAIN_WAVES = 0, 8  # one-launch set: 8-row blocks per workgroup (0: per linear) and waves per workgroup
 HIDDEN, FFN, VOCAB = 2048, 8192, 100352
 LAYER_LINEARS = (("q", HIDDEN, HIDDEN), ("k", HIDDEN, HIDDEN), ("v", HIDDEN, HIDDEN), ("o", HIDDEN, HIDDEN),
                  ("gate", FFN, HIDDEN), ("up", FFN, HIDDEN), ("down", HIDDEN, FFN))
@@ -80,10 +80,10 @@ def build(kind: str = "bf16", m: int = 1, device="cuda:0", seed: int = 0, scale_
     return ops
 
 
-def group_of(ops: list[Op], cfg: tuple[int, int] | None = None) -> SkinnyGroup:
-    """The ops (each on its own input, M = 1) as one grouped launch writing the ops' own outputs."""
-    return SkinnyGroup([GroupItem(o.x[0], o.args[0], o.y[0], o.args[1] if len(o.args) > 1 else None) for o in ops],
-                       cfg=cfg)
+def group_of(ops: list[Op], rb: int = CHAIN_RB, waves: int = CHAIN_WAVES) -> LinearChain:
+    """The ops (each on its own input, M = 1) as one launch of independent stages writing the ops' own outputs."""
+    stages = [ChainStage([o.args if len(o.args) > 1 else o.args[0]], o.x[0], o.y[0]) for o in ops]
+    return LinearChain(stages, rb=rb, waves=waves)
 
 
 def algorithmic_bytes(ops: list[Op], kind: str, m: int) -> int:
@@ -145,11 +145,11 @@ LAYER_STAGES = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gateup", ("gate", "up
 
 @dataclass
 class Chain:
-    """The decode-step set as stages of one persistent launch."""
+    """The decode-step set as the stages of one launch."""
 
     kind: str
     stages: list
-    lset: LinearSet
+    lset: LinearChain
     weights: dict  # linear name -> (w,) or (q, scale)
 
 
@@ -164,8 +164,7 @@ def make_weights(kind: str = "bf16", device="cuda:0", seed: int = 0, scale_dtype
     return out
 
 
-def chain_stages(weights: dict, dependent: bool = True, device="cuda:0", seed: int = 1,
-                 record_inputs: bool = False) -> list:
+def chain_stages(weights: dict, dependent: bool = True, device="cuda:0", seed: int = 1) -> list:
     """Stages of the set in decode order over `weights` (make_weights). dependent: each stage reads (renormalised)
     the output it depends on in a decode step; otherwise each stage has its own unit-RMS input and no wait."""
     g = torch.Generator(device=device).manual_seed(seed)
@@ -173,19 +172,13 @@ def chain_stages(weights: dict, dependent: bool = True, device="cuda:0", seed: i
     def fresh(k):
         return unit_rms(torch.randn(1, k, generator=g, device=device))[0].contiguous()
 
-    kind = "bf16" if len(next(iter(weights.values()))) == 1 else "int8"
     stages: list = []
-    prev = None  # (stage index, slice of its out) feeding the next qkv / head
+    prev = None  # stage index feeding the next qkv / head
 
-    def add(names, src, wait, renorm):
-        args = [weights[nm] for nm in names]
-        ws = [a[0] for a in args]
-        scales = [a[1] for a in args] if kind == "int8" else None
-        n = sum(int(w.shape[0]) for w in ws)
-        k = int(ws[0].shape[1])
-        out = torch.empty(n, dtype=torch.bfloat16, device=device)
-        xu = torch.empty(k, dtype=torch.bfloat16, device=device) if record_inputs else None
-        stages.append(Stage(ws, src, out, scales=scales, wait=wait, renorm=renorm, x_used=xu))
+    def add(names, src, renorm):
+        ws = [weights[nm] if len(weights[nm]) > 1 else weights[nm][0] for nm in names]
+        n = sum(int((w[0] if isinstance(w, tuple) else w).shape[0]) for w in ws)
+        stages.append(ChainStage(ws, src, torch.empty(n, dtype=torch.bfloat16, device=device), renorm))
         return len(stages) - 1
 
     for layer in range(LAYERS):
@@ -193,26 +186,42 @@ def chain_stages(weights: dict, dependent: bool = True, device="cuda:0", seed: i
         if not dependent:
             for _, names in LAYER_STAGES:
                 k = int(weights[pre + names[0]][0].shape[1])
-                add([pre + nm for nm in names], fresh(k), -1, False)
+                add([pre + nm for nm in names], fresh(k), False)
             continue
-        src, wait = (fresh(HIDDEN), -1) if prev is None else (stages[prev].out, prev)
-        i_qkv = add([pre + "q", pre + "k", pre + "v"], src, wait, True)
-        i_o = add([pre + "o"], stages[i_qkv].out[2 * HIDDEN:3 * HIDDEN], i_qkv, True)
-        i_gu = add([pre + "gate", pre + "up"], stages[i_o].out, i_o, True)
-        prev = add([pre + "down"], stages[i_gu].out[FFN:2 * FFN], i_gu, True)
+        i_qkv = add([pre + "q", pre + "k", pre + "v"], fresh(HIDDEN) if prev is None else (prev, 0), True)
+        i_o = add([pre + "o"], (i_qkv, 2 * HIDDEN), True)
+        i_gu = add([pre + "gate", pre + "up"], (i_o, 0), True)
+        prev = add([pre + "down"], (i_gu, FFN), True)
     if dependent:
-        add(["lm_head"], stages[prev].out, prev, True)
+        add(["lm_head"], (prev, 0), True)
     else:
-        add(["lm_head"], fresh(HIDDEN), -1, False)
+        add(["lm_head"], fresh(HIDDEN), False)
     return stages
 
 
 def build_chain(kind: str = "bf16", device="cuda:0", seed: int = 0, scale_dtype=torch.float16,
-                dependent: bool = True, record_inputs: bool = False, weights: dict | None = None) -> Chain:
-    """The set as one persistent launch (weights from make_weights unless given)."""
+                dependent: bool = True, weights: dict | None = None, rb: int = CHAIN_RB,
+                waves: int = CHAIN_WAVES) -> Chain:
+    """The set as one launch (weights from make_weights unless given)."""
     weights = weights if weights is not None else make_weights(kind, device, seed, scale_dtype)
-    stages = chain_stages(weights, dependent, device, seed + 1, record_inputs)
-    return Chain(kind, stages, LinearSet(stages), weights)
+    stages = chain_stages(weights, dependent, device, seed + 1)
+    return Chain(kind, stages, LinearChain(stages, rb=rb, waves=waves), weights)
+
+
+def stage_launches(chain: Chain, rb: int = CHAIN_RB, waves: int = CHAIN_WAVES) -> list[LinearChain]:
+    """The dependent set as one launch per stage (65 stream-ordered launches): stage s is a launch of its own linears
+    on the renormalised slice of stage s-1's output, read as an ordinary input once the launch before it has
+    finished. Same weights and outputs as `chain` (whose stages must be dependent)."""
+    out = []
+    for st in chain.stages:
+        if isinstance(st.src, tuple):
+            dep, start = st.src
+            k = int((st.weights[0][0] if isinstance(st.weights[0], tuple) else st.weights[0]).shape[1])
+            src = chain.stages[dep].out[start:start + k]
+        else:
+            src = st.src
+        out.append(LinearChain([ChainStage(st.weights, src, st.out, st.renorm)], rb=rb, waves=waves))
+    return out
 
 
 def chain_bytes(kind: str) -> int:

@@ -114,6 +114,54 @@ int bp_skinny_mf_silu(int wkind, const void* x, const void* w, const void* scale
                       int64_t M, int64_t ffn, int64_t K, int rb, int waves, int xstage, void* stream);
 
 /*
+ * The decode-step linear set in one launch of the skinny matrix-core kernel (M = 1): a grid over row blocks of a
+ * list of linears ("items", in stage order), each workgroup owning 8 rb rows of one item.
+ *   independent (dependent = 0): each item reads its own input x[K] -- the reference's set benchmark, where every
+ *   linear is a separate skinny call (tools/skinny_bench.py:45-71);
+ *   dependent (dependent = 1): an item may read a slice of an earlier stage's output instead (tag_in), optionally
+ *   renormalised to unit RMS (bf16(v / sqrt(mean(v^2)))), as a decode step's linears wait for each other
+ *   (byteprof/optim/olmo.py:122-219). A workgroup's weight loads (its whole tile when it fits 16 segments per wave)
+ *   are issued before it waits, so the weights stream across stage boundaries. Outputs travel as 32-bit
+ *   [generation tag : bf16] words (tag_out).
+ * Every wait is bounded; a wait that gives up, or a tag_in item in an independent launch, sets scratch word 2 (the
+ * launch still finishes; its results are invalid).
+ * Every output equals bp_skinny_mf's at M = 1 with the same waves (split 1), bit for bit. K a multiple of the
+ * 128-byte segment and at most 8192; weights 16-byte aligned. waves 2, 4 or 8.
+ * bp_chain_plan checks the items and fills rb (rb_req 1, 2 or 4 for every item, or 0: per item, the most 8-row
+ * blocks whose whole tile is in flight at once), first_wg and dep_wgs, and the lookup table
+ * [ceil(workgroups / 256)] when given; it returns the workgroup count or a negative BP_E_* code.
+ * bp_chain_run launches the planned items (device copies of the items and the table); dependent launches first
+ * advance the generation in the scratch with a one-thread kernel. The scratch (bp_chain_scratch_bytes(stages),
+ * zeroed once, kept between launches, not shared by overlapping launches) holds the generation, the per-stage
+ * counters (they only grow) and the error word, so graph replays need no reset.
+ * Replaces: the 113 stream-ordered skinny_mm calls of the set (independent: skinny_bench.py:45-71; dependent: the
+ *           linears of one captured decode step, olmo.py:164-215).
+ */
+#define BP_CHAIN_RENORM 1
+typedef struct BpChainItem {
+  const void* x;           /* external input [K] bf16, 8-byte aligned, or NULL when the input is tag_in */
+  const void* w;           /* weights [n, K], bf16 or int8 */
+  const void* scale;       /* int8: per-row scale [n] (the launch's scale dtype) */
+  void* y;                 /* plain output [n] bf16, or NULL */
+  uint32_t* tag_out;       /* the output as tagged words [n] (dependent launches), or NULL */
+  const uint32_t* tag_in;  /* the producer's tagged words from the input's first element (8-byte aligned), or NULL */
+  int64_t n;
+  int64_t K;
+  int32_t first_wg;        /* set by bp_chain_plan */
+  int32_t flags;           /* BP_CHAIN_RENORM */
+  int32_t stage;           /* non-decreasing over the items */
+  int32_t dep_stage;       /* the stage whose output tag_in points into */
+  int32_t dep_wgs;         /* set by bp_chain_plan: workgroups of dep_stage (its counter's step per launch) */
+  int32_t rb;              /* set by bp_chain_plan: 8-row blocks per workgroup */
+} BpChainItem;
+int bp_chain_supported(int wkind, int rb_req, int waves);
+size_t bp_chain_scratch_bytes(int num_stages);
+int bp_chain_plan(BpChainItem* items, int num_items, int wkind, int rb_req, int waves, int32_t* lut,
+                  int lut_capacity);
+int bp_chain_run(int wkind, int scale_dtype, const void* dev_items, const void* dev_lut, int num_items,
+                 int total_wgs, int waves, void* scratch, int dependent, void* stream);
+
+/*
  * int4 group-128 weights in the tile-major format of byteprof's skinny kernels:
  *   packed uint8 [ceil(N / R), K / 128, R, 64]: the R rows (tile_rows: 16, 32 or 64) of one row tile and one group of
  *   128 inputs form a contiguous R x 64-byte block; byte j of a row's group holds code j (low nibble) and code

@@ -252,3 +252,119 @@ def test_group_plan_and_run_reject_bad_items_before_any_launch(L):
     empty = _group_items([(0, 512)])
     assert plan(empty) == 0
     assert run(empty, blocks=0) == 0                             # nothing to launch
+
+
+# ---- the one-launch linear chain (bp_chain_*) ---------------------------------------------------------------------
+
+
+def test_chain_item_layout_matches_the_header():
+    from byteprof_amd.optim.linear_chain import BpChainItem
+
+    text = HEADER.read_text()
+    body = text[text.index("typedef struct BpChainItem"):text.index("} BpChainItem;")]
+    fields = re.findall(r"\b(\w+);", body)
+    assert [f[0] for f in BpChainItem._fields_] == fields
+    assert ctypes.sizeof(BpChainItem) == 88
+
+
+def _chain_item(**kw):
+    from byteprof_amd.optim.linear_chain import BpChainItem
+
+    it = BpChainItem()
+    it.x, it.w, it.n, it.K, it.stage, it.dep_stage = 0x1000, 0x2000, 64, 2048, 0, -1
+    for key, v in kw.items():
+        setattr(it, key, v)
+    return it
+
+
+def _chain_plan(L, *items, rb=2, waves=8, kind=0, lut=None):
+    from byteprof_amd.optim.linear_chain import BpChainItem
+
+    arr = (BpChainItem * len(items))(*items)
+    rc = L.bp_chain_plan(arr, len(items), kind, rb, waves, lut, len(lut) if lut is not None else 0)
+    return rc, arr
+
+
+def test_chain_plan_rejects_bad_items(L):
+    assert _chain_plan(L, _chain_item())[0] == 4
+    assert _chain_plan(L, _chain_item(K=1000))[0] == -1                    # K not a multiple of the segment
+    assert _chain_plan(L, _chain_item(K=1024 + 64), kind=1)[0] == -1       # int8 segment is 128 elements
+    assert _chain_plan(L, _chain_item(K=16384))[0] == -1                   # K above the LDS stage
+    assert _chain_plan(L, _chain_item(tag_in=0x1000))[0] == -1             # two input sources
+    assert _chain_plan(L, _chain_item(x=None))[0] == -1                    # no input source
+    assert _chain_plan(L, _chain_item(w=0x2004))[0] == -1                  # weights not 16-byte aligned
+    assert _chain_plan(L, _chain_item(x=0x1004))[0] == -1                  # external input not 8-byte aligned
+    assert _chain_plan(L, _chain_item(), rb=3)[0] == -1                    # rb not 0, 1, 2, 4
+    assert _chain_plan(L, _chain_item(), waves=16)[0] == -1                # waves not 2, 4, 8
+    assert _chain_plan(L, _chain_item(stage=1), _chain_item(stage=0))[0] == -1          # stages out of order
+    dep = dict(x=None, tag_in=0x1000, stage=1)
+    assert _chain_plan(L, _chain_item(), _chain_item(dep_stage=1, **dep))[0] == -1      # depends on itself
+    assert _chain_plan(L, _chain_item(stage=2), _chain_item(dep_stage=1, x=None, tag_in=0x1000, stage=3))[0] == -1
+    assert _chain_plan(L, _chain_item(), _chain_item(x=None, tag_in=0x1004, stage=1, dep_stage=0))[0] == -1
+    rc, arr = _chain_plan(L, _chain_item(n=100), _chain_item(n=64, stage=1), _chain_item(dep_stage=0, **dep))
+    assert rc == 7 + 4 + 4 and arr[2].dep_wgs == 7 and arr[0].dep_wgs == 0
+    p = ctypes.c_void_p(16)
+    assert L.bp_chain_run(0, 0, None, None, 1, 1, 8, p, 0, None) == -1
+    assert L.bp_chain_run(0, 0, p, p, 1, 1, 8, None, 1, None) == -3       # no scratch
+    assert L.bp_chain_run(0, 0, p, p, 1, 1, 3, p, 1, None) == -2          # no kernel for 3 waves
+    assert L.bp_chain_run(1, 9, p, p, 1, 1, 8, p, 1, None) == -1          # bad scale dtype
+
+
+@pytest.mark.parametrize("waves", [2, 4, 8])
+def test_chain_plan_sizes_tiles_to_the_slots_in_flight(L, waves):
+    """rb = 0: per item, 4 blocks when a wave holds at most 4 segments, 2 up to 8, else 1 (16 in flight)."""
+    for kind, seg in ((0, 64), (1, 128)):
+        for k in (128, 1024, 2048, 4096, 8192):
+            per_wave = -(-(k // seg) // waves)
+            want = 4 if per_wave <= 4 else 2 if per_wave <= 8 else 1
+            rc, arr = _chain_plan(L, _chain_item(K=k, n=1000), rb=0, waves=waves, kind=kind)
+            assert arr[0].rb == want and rc == -(-1000 // (8 * want)), (kind, k, waves)
+
+
+@pytest.mark.parametrize("rb", [1, 2, 4])
+def test_chain_plan_places_items_in_order_with_a_lookup_table(L, rb):
+    """first_wg is the running sum of ceil(n / 8 rb); lut[c] is the item holding workgroup 256 c."""
+    ns = [1, 300, 5000, 8, 17, 100352, 9, 2048]
+    items = [_chain_item(n=n, stage=i) for i, n in enumerate(ns)]
+    total, arr = _chain_plan(L, *items, rb=rb)
+    per = [-(-n // (8 * rb)) for n in ns]
+    assert total == sum(per) and all(it.rb == rb for it in arr)
+    starts = [sum(per[:i]) for i in range(len(ns))]
+    assert [it.first_wg for it in arr] == starts
+    lut = (ctypes.c_int32 * (-(-total // 256)))()
+    assert _chain_plan(L, *items, rb=rb, lut=lut)[0] == total
+    for c, v in enumerate(lut):
+        owner = max(i for i in range(len(ns)) if starts[i] <= 256 * c)
+        assert v == owner, (c, v, owner)
+    short = (ctypes.c_int32 * (len(lut) - 1))()
+    assert _chain_plan(L, *items, rb=rb, lut=short)[0] == -1
+
+
+def test_linear_chain_builds_on_host_tensors():
+    """The stage list of a decode step (CPU tensors: nothing is launched) plans into items with the right inputs,
+    tagged outputs only for the stages that are read, and wait counts equal to the producer's workgroups."""
+    import torch
+
+    from byteprof_amd import decode_set as D
+    from byteprof_amd.optim.linear_chain import BpChainItem, LinearChain
+
+    weights = {name: (torch.zeros(n, k, dtype=torch.bfloat16),) for name, n, k in D.shapes()}
+    for dep in (True, False):
+        stages = D.chain_stages(weights, dependent=dep, device="cpu")
+        ch = LinearChain(stages, rb=0, waves=8)
+        assert ch.dependent == dep and ch.n_items == 113
+        items = (BpChainItem * ch.n_items).from_buffer_copy(ch.items.numpy().tobytes())
+        rbs = {k: 4 if k == 2048 else 1 for _, _, k in D.shapes()}  # 4 segments per wave at K = 2048, 16 at 8192
+        assert [it.rb for it in items] == [rbs[k] for _, _, k in D.shapes()]
+        assert ch.total_wgs == sum(-(-n // (8 * rbs[k])) for _, n, k in D.shapes())
+        assert sorted(ch.tagged) == (list(range(64)) if dep else [])
+        for it in items:
+            st = stages[it.stage]
+            if dep and it.stage > 0:
+                d, start = st.src
+                assert it.x is None and it.dep_stage == d and it.dep_wgs == ch.stage_wgs[d]
+                assert it.tag_in == ch.tagged[d].data_ptr() + 4 * start
+                assert it.flags == 1
+            else:
+                assert it.tag_in is None and it.x == st.src.data_ptr() and it.dep_stage == -1
+            assert (it.tag_out is not None) == (it.stage in ch.tagged)

@@ -292,16 +292,18 @@ def test_decode_chain_structure():
     weights = {name: (torch.zeros(n, k, dtype=torch.bfloat16),) for name, n, k in D.shapes()}
     stages = D.chain_stages(weights, dependent=True, device="cpu")
     assert len(stages) == 65
-    assert stages[0].wait == -1
+    assert isinstance(stages[0].src, torch.Tensor)
     for i, st in enumerate(stages[1:], start=1):
-        assert st.wait == i - 1 and st.renorm
-    o = stages[1]  # o reads v: rows 4096..6143 of q|k|v
-    assert o.src.data_ptr() == stages[0].out.data_ptr() + 2 * 2 * 2048
-    down = stages[3]  # down reads up: rows 8192..16383 of gate|up
-    assert down.src.data_ptr() == stages[2].out.data_ptr() + 2 * 8192 and down.k == 8192
-    assert stages[-1].n == 100352 and stages[-1].src.data_ptr() == stages[-2].out.data_ptr()
+        assert isinstance(st.src, tuple) and st.renorm
+    assert [len(st.weights) for st in stages[:4]] == [3, 1, 2, 1]
+    assert stages[1].src == (0, 2 * 2048)      # o reads v: rows 4096..6143 of q|k|v
+    assert stages[2].src == (1, 0)             # gate|up reads o
+    assert stages[3].src == (2, 8192)          # down reads up: rows 8192..16383 of gate|up
+    assert stages[3].weights[0].shape == (2048, 8192)
+    assert stages[4].src == (3, 0)             # the next layer's q|k|v reads down
+    assert stages[-1].out.numel() == 100352 and stages[-1].src == (63, 0)
     ind = D.chain_stages(weights, dependent=False, device="cpu")
-    assert len(ind) == 65 and all(st.wait == -1 for st in ind)
+    assert len(ind) == 65 and all(isinstance(st.src, torch.Tensor) and not st.renorm for st in ind)
     assert D.chain_bytes("bf16") == 2_560_237_568 and D.chain_bytes("int8") == 1_282_027_520
 
 
