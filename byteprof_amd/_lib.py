@@ -30,12 +30,7 @@ _c_i64, _c_int, _c_size, _c_vp, _c_float = ctypes.c_int64, ctypes.c_int, ctypes.
 SIGNATURES: dict[str, tuple] = {
     "bp_version": (_c_int, []),
     "bp_status_string": (ctypes.c_char_p, [_c_int]),
-    "bp_skinny_config_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "bp_skinny_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_int]),
-    "bp_skinny_bf16": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_size,
-                                _c_vp]),
-    "bp_skinny_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
-                                _c_vp, _c_size, _c_vp]),
     "bp_skinny_mf_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "bp_skinny_mf_k_segment": (_c_int, [_c_int]),
     "bp_skinny_mf_stage_bytes": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
@@ -52,7 +47,6 @@ SIGNATURES: dict[str, tuple] = {
     "bp_skinny_int4_config_supported": (_c_int, [_c_int, _c_int, _c_int]),
     "bp_skinny_int4": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                 _c_int, _c_vp, _c_size, _c_vp]),
-    "bp_gemv_int8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
     "bp_splitk_reduce": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_int, _c_vp]),
     "bp_mlstm_multistep": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                     _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
@@ -87,13 +81,6 @@ SIGNATURES: dict[str, tuple] = {
     "bp_decode_argmax_rows_scratch_bytes": (_c_size, [_c_int]),
     "bp_decode_argmax_rows": (_c_int, [_c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
     "bp_draft_verify_next": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
-    "bp_linear_set_scratch_bytes": (_c_size, [_c_vp, _c_int, _c_int]),
-    "bp_linear_set_workgroups": (_c_int, [_c_int]),
-    "bp_linear_set_validate": (_c_int, [_c_vp, _c_int, _c_int, _c_int]),
-    "bp_linear_set_run": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_size, _c_int, _c_vp]),
-    "bp_skinny_group_config_supported": (_c_int, [_c_int, _c_int, _c_int]),
-    "bp_skinny_group_plan": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_vp, _c_int]),
-    "bp_skinny_group_run": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -1,6 +1,5 @@
-"""Build recipe of libbyteprof_amd.so: hipcc for gfx950, one object per source (the skinny kernel menu is compiled in
-ten slices, one per weight kind x activation-row bucket), objects compiled in parallel, then linked into the shared
-library next to this file. `python -m byteprof_amd.build` runs it."""
+"""Build recipe of libbyteprof_amd.so: hipcc for gfx950, one object per source, objects compiled in parallel, then
+linked into the shared library next to this file. `python -m byteprof_amd.build` runs it."""
 
 from __future__ import annotations
 
@@ -20,9 +19,6 @@ LIB_NAME = "libbyteprof_amd.so"
 LIB_PATH = PKG / LIB_NAME
 ARCH = "gfx950"
 
-KINDS = (0, 1)  # bf16, int8 weights
-ROW_BUCKETS = (1, 2, 4, 8, 16)
-
 
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -41,22 +37,13 @@ def common_flags() -> list[str]:
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+SOURCES = ("skinny.hip", "skinny_mf.hip", "skinny_chain.hip", "skinny_int4.hip", "mlstm.hip", "draft.hip",
+           "decode.hip")
+
+
 def units() -> list[tuple[Path, list[str], Path]]:
     """(source, extra flags, object) for every translation unit."""
-    out = [(CSRC / "skinny.hip", [], BUILD_DIR / "skinny.o"),
-           (CSRC / "mlstm.hip", [], BUILD_DIR / "mlstm.o"),
-           (CSRC / "linear_set.hip", [], BUILD_DIR / "linear_set.o"),
-           (CSRC / "skinny_int4.hip", [], BUILD_DIR / "skinny_int4.o"),
-           (CSRC / "draft.hip", [], BUILD_DIR / "draft.o"),
-           (CSRC / "decode.hip", [], BUILD_DIR / "decode.o"),
-           (CSRC / "skinny_group.hip", [], BUILD_DIR / "skinny_group.o"),
-           (CSRC / "skinny_mf.hip", [], BUILD_DIR / "skinny_mf.o"),
-           (CSRC / "skinny_chain.hip", [], BUILD_DIR / "skinny_chain.o")]
-    for kind in KINDS:
-        for mt in ROW_BUCKETS:
-            out.append((CSRC / "skinny_inst.hip", [f"-DBP_KIND={kind}", f"-DBP_MT={mt}"],
-                        BUILD_DIR / f"skinny_inst_k{kind}_m{mt}.o"))
-    return out
+    return [(CSRC / name, [], BUILD_DIR / name.replace(".hip", ".o")) for name in SOURCES]
 
 
 def _run(cmd: list[str]) -> None:

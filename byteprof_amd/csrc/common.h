@@ -7,6 +7,10 @@
 
 namespace bp {
 
+// Weight kinds of the skinny kernels.
+constexpr int kBf16 = 0;
+constexpr int kInt8 = 1;
+
 constexpr int kWave = 64;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

@@ -20,7 +20,7 @@
 
 #include "byteprof_amd.h"
 #include "common.h"
-#include "skinny_kernel.h"
+#include "common.h"
 
 namespace bp {
 namespace {

@@ -1,25 +1,13 @@
-// C ABI of the skinny weight-only matmul (bf16 and int8 weights), the one-row int8 product and the split-K
-// reduction; dispatch over the compiled kernel menu of skinny_kernel.h.
+// C ABI of the library's common entry points (version, status strings, split-K workspace size, the split-K
+// reduction) and of the int4 group-128 skinny launch (kernels in skinny_int4.hip). The bf16 / int8 skinny launch
+// is skinny_mf.hip.
 //
-// Reference semantics: byteprof/optim/skinny.py:84-90 (_split_reduce), :111-166 (_launch, skinny_mm);
-// byteprof/quant/triton_int8.py:40-47 (gemv_int8).
+// Reference semantics: byteprof/optim/skinny.py:84-90 (_split_reduce).
 
 #include "byteprof_amd.h"
-#include "skinny_kernel.h"
+#include "common.h"
 
 namespace bp {
-
-// Explicit instantiations live in skinny_inst.hip (one object per slice).
-extern template SkinnyFn skinny_pick<kBf16, 1>(int, int, bool);
-extern template SkinnyFn skinny_pick<kBf16, 2>(int, int, bool);
-extern template SkinnyFn skinny_pick<kBf16, 4>(int, int, bool);
-extern template SkinnyFn skinny_pick<kBf16, 8>(int, int, bool);
-extern template SkinnyFn skinny_pick<kBf16, 16>(int, int, bool);
-extern template SkinnyFn skinny_pick<kInt8, 1>(int, int, bool);
-extern template SkinnyFn skinny_pick<kInt8, 2>(int, int, bool);
-extern template SkinnyFn skinny_pick<kInt8, 4>(int, int, bool);
-extern template SkinnyFn skinny_pick<kInt8, 8>(int, int, bool);
-extern template SkinnyFn skinny_pick<kInt8, 16>(int, int, bool);
 
 // int4 group-128 kernels (skinny_int4.hip).
 using Int4Fn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
@@ -48,30 +36,6 @@ __global__ void fill_zero_bf16_kernel(uint16_t* __restrict__ y, int64_t count) {
     y[idx] = 0;
 }
 
-SkinnyFn pick(int wkind, int mt, int rows, int waves, bool vec) {
-  if (wkind == kBf16) {
-    switch (mt) {
-      case 1: return skinny_pick<kBf16, 1>(rows, waves, vec);
-      case 2: return skinny_pick<kBf16, 2>(rows, waves, vec);
-      case 4: return skinny_pick<kBf16, 4>(rows, waves, vec);
-      case 8: return skinny_pick<kBf16, 8>(rows, waves, vec);
-      case 16: return skinny_pick<kBf16, 16>(rows, waves, vec);
-      default: return nullptr;
-    }
-  }
-  if (wkind == kInt8) {
-    switch (mt) {
-      case 1: return skinny_pick<kInt8, 1>(rows, waves, vec);
-      case 2: return skinny_pick<kInt8, 2>(rows, waves, vec);
-      case 4: return skinny_pick<kInt8, 4>(rows, waves, vec);
-      case 8: return skinny_pick<kInt8, 8>(rows, waves, vec);
-      case 16: return skinny_pick<kInt8, 16>(rows, waves, vec);
-      default: return nullptr;
-    }
-  }
-  return nullptr;
-}
-
 int row_bucket(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
 int launch_status() {
@@ -82,44 +46,6 @@ int launch_status() {
 int grid_for(int64_t count) {
   const int64_t b = (count + 255) / 256;
   return static_cast<int>(b < 2048 ? (b < 1 ? 1 : b) : 2048);
-}
-
-int skinny_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y, int64_t M,
-                  int64_t N, int64_t K, int rows, int waves, int split, void* ws, size_t ws_bytes, void* stream) {
-  if (M < 0 || N < 0 || K < 0 || M > 16) return BP_E_INVALID_ARG;
-  if (M == 0 || N == 0) return BP_OK;
-  if (x == nullptr || w == nullptr || y == nullptr) return BP_E_INVALID_ARG;
-  if (wkind == kInt8 && (scale == nullptr || scale_dt < BP_DT_BF16 || scale_dt > BP_DT_F32)) return BP_E_INVALID_ARG;
-  if (split < 1 || split > 1024) return BP_E_UNSUPPORTED;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (K == 0) {
-    fill_zero_bf16_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<uint16_t*>(y), M * N);
-    return launch_status();
-  }
-  const int epl = wkind == kBf16 ? 8 : 16;
-  const bool vec = (K % epl == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
-                   (reinterpret_cast<uintptr_t>(w) % 16 == 0);
-  SkinnyFn fn = pick(wkind, row_bucket(M), rows, waves, vec);
-  if (fn == nullptr) return BP_E_UNSUPPORTED;
-  if (!vec) {
-    rows = kGenericRows;
-    waves = kGenericWaves;
-  }
-  const int64_t nch = (K + 64 * epl - 1) / (64 * epl);
-  if (split > nch) split = static_cast<int>(nch);
-  if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
-    return BP_E_WORKSPACE;
-  const int64_t tiles = (N + rows - 1) / rows;
-  if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
-  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(split));
-  fn<<<grid, waves * kWave, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale,
-                                     scale_dt, static_cast<uint16_t*>(y), static_cast<float*>(ws),
-                                     static_cast<int>(M), N, K, split);
-  const int rc = launch_status();
-  if (rc != BP_OK || split == 1) return rc;
-  splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
-                                                       wkind == kInt8 ? scale : nullptr, scale_dt, M, N, split);
-  return launch_status();
 }
 
 int skinny_int4_launch(const void* x, const void* packed, const void* scale, int scale_dt, const void* zero, void* y,
@@ -193,31 +119,9 @@ const char* bp_status_string(int status) {
   }
 }
 
-int bp_skinny_config_supported(int wkind, int mt, int rows, int waves) {
-  return bp::pick(wkind, mt, rows, waves, true) != nullptr ? 1 : 0;
-}
-
 size_t bp_skinny_workspace_bytes(int64_t M, int64_t N, int split) {
   if (split <= 1 || M <= 0 || N <= 0) return 0;
   return static_cast<size_t>(split) * static_cast<size_t>(M) * static_cast<size_t>(N) * sizeof(float);
-}
-
-int bp_skinny_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int rows, int waves,
-                   int split, void* workspace, size_t workspace_bytes, void* stream) {
-  return bp::skinny_launch(bp::kBf16, x, w, nullptr, 0, y, M, N, K, rows, waves, split, workspace,
-                           workspace_bytes, stream);
-}
-
-int bp_skinny_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y, int64_t M, int64_t N,
-                   int64_t K, int rows, int waves, int split, void* workspace, size_t workspace_bytes,
-                   void* stream) {
-  return bp::skinny_launch(bp::kInt8, x, q, scale, scale_dtype, y, M, N, K, rows, waves, split, workspace,
-                           workspace_bytes, stream);
-}
-
-int bp_gemv_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y, int64_t N, int64_t K,
-                 int rows, int waves, void* stream) {
-  return bp::skinny_launch(bp::kInt8, x, q, scale, scale_dtype, y, 1, N, K, rows, waves, 1, nullptr, 0, stream);
 }
 
 int bp_splitk_reduce(const void* workspace, void* y, const void* scale, int scale_dtype, int64_t M, int64_t N,

@@ -285,7 +285,7 @@ __device__ __forceinline__ void chain_body(const BpChainItem& it, int b, int sca
 
 // Two workgroups of 8 waves per CU (at most 128 VGPRs): the weight tiles of both are in flight at once.
 template <int KIND, int WAVES>
-__global__ __launch_bounds__(WAVES * kWave, 16 / WAVES) void chain_kernel(const BpChainItem* __restrict__ items,
+__global__ __launch_bounds__(WAVES * kWave, WAVES == 8 ? 2 : 1) void chain_kernel(const BpChainItem* __restrict__ items,
                                                               const int32_t* __restrict__ lut, int n_items,
                                                               int scale_dt, uint32_t* __restrict__ hdr, int dependent) {
   __shared__ __attribute__((aligned(16))) ChainShared sh;

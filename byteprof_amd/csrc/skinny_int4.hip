@@ -27,7 +27,7 @@
 // (skinny_linear.py:39-44).
 
 #include "byteprof_amd.h"
-#include "skinny_kernel.h"
+#include "common.h"
 
 namespace bp {
 

@@ -25,7 +25,7 @@
 // skinny_mm (skinny.py:136-166) for every activation row count up to MAX_M = 64 (skinny.py:32).
 #pragma once
 
-#include "skinny_kernel.h"
+#include "common.h"
 
 namespace bp {
 

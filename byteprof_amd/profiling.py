@@ -2,9 +2,11 @@
 
   python -m byteprof_amd.profiling set  [--kind bf16|int8] [--replays R]   the decode-step set graph, R replays
   python -m byteprof_amd.profiling chain [--kind bf16|int8] [--dependent] [--replays R]
-                                                                         the set as one persistent launch, R launches
-  python -m byteprof_amd.profiling group [--kind bf16|int8] [--replays R]
-                                                                         the set as one grouped launch, R launches
+                                                                         the set as one launch (independent linears,
+                                                                         or the dependent stages), R launches
+  python -m byteprof_amd.profiling stages [--kind bf16|int8] [--replays R]
+                                                                         the dependent set as 65 stream-ordered
+                                                                         launches (one per stage), R passes
   python -m byteprof_amd.profiling decode [--kind bf16|int8] [--tokens N] [--draft]
                                                                          the graph-captured greedy decode loop
                                                                          of the OLMo-2-1B shape, 8 prompt + N tokens;
@@ -108,7 +110,7 @@ def summarize(a) -> int:
         traffic = (fv * f_scale + wv * w_scale) * 1024 / 1e6
         print(f"{_short(name)[:48]:<48} {grid:>12} {k:>10} {fv:>11.1f} {wv:>10.1f} {traffic:>11.3f}")
     if a.chain_tag:
-        kernel = "skinny_group_kernel" if a.chain_tag.startswith("group") else "linear_set_kernel"
+        kernel = "chain_kernel"
         print()
         print(f"## traffic per launch of the {kernel}, {a.chain_tag} (bytes; read by bench.py)")
         for key in sorted(fetch):
@@ -141,7 +143,7 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=("set", "chain", "group", "decode", "skinny", "copy", "summarize"))
+    ap.add_argument("what", choices=("set", "chain", "stages", "decode", "skinny", "copy", "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
     ap.add_argument("--write", help="summarize: WRITE_SIZE database of the workload")
@@ -151,8 +153,7 @@ def main(argv=None) -> int:
     ap.add_argument("--pmc", action="append", help="summarize: any --pmc database, counters per dispatch")
     ap.add_argument("--all", action="store_true", help="summarize: include kernels outside this library")
     ap.add_argument("--set-kind", choices=("bf16", "int8"), help="summarize: emit traffic lines for the set shapes")
-    ap.add_argument("--chain-tag", help="summarize: emit traffic lines for the set kernel under this tag (a tag "
-                    "starting with 'group': for the grouped kernel)")
+    ap.add_argument("--chain-tag", help="summarize: emit traffic lines for the one-launch set kernel under this tag")
     ap.add_argument("--kind", default="bf16", choices=("bf16", "int8"))
     ap.add_argument("--dependent", action="store_true", help="chain: stages read the outputs they depend on")
     ap.add_argument("--replays", type=int, default=5)
@@ -207,8 +208,16 @@ def main(argv=None) -> int:
         if ch.lset.timed_out():
             print("a launch gave up waiting for another workgroup", file=sys.stderr)
             return 1
-        print(f"ran the {a.kind} decode-step set as one persistent launch {a.replays} times "
+        print(f"ran the {a.kind} decode-step set as one launch {a.replays} times "
               f"({len(ch.stages)} stages, {'dependent' if a.dependent else 'independent'})", flush=True)
+        return 0
+    if a.what == "stages":
+        ch = D.build_chain(a.kind, device, dependent=True)
+        g = D.capture([lc.run for lc in D.stage_launches(ch)])
+        for _ in range(a.replays):
+            g.replay()
+        torch.cuda.synchronize()
+        print(f"replayed the {a.kind} dependent set as {len(ch.stages)} stage launches {a.replays} times", flush=True)
         return 0
     if a.what == "decode":
         from .optim import olmo as OG
@@ -231,15 +240,6 @@ def main(argv=None) -> int:
                 truth[key] = res[0, prompt.shape[1]:].tolist()
             torch.cuda.synchronize()
             print(f"drafting loop: {stats.dump()}", flush=True)
-        return 0
-    if a.what == "group":
-        ops = D.build(a.kind, 1, device)
-        grp = D.group_of(ops)
-        for _ in range(a.replays):
-            grp.run()
-        torch.cuda.synchronize()
-        print(f"ran the {a.kind} decode-step set as one grouped launch {a.replays} times ({len(ops)} linears, "
-              f"{grp.blocks} workgroups of {grp.rows} rows x {grp.waves} waves)", flush=True)
         return 0
     ops = D.build(a.kind, 1, device)
     g = D.capture(ops)

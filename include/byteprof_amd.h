@@ -43,38 +43,8 @@ int bp_version(void);
 /* Short static description of a status code returned by any bp_* function (BP_* and hipError_t codes). */
 const char* bp_status_string(int status);
 
-/*
- * Tile configuration menu of the skinny kernels. A call chooses
- *   rows  : weight rows (output channels) per workgroup, one of {2, 4, 8, 16, 32};
- *   waves : wavefronts per workgroup; the K dimension is dealt out to them in chunks of 512 (bf16) / 1024 (int8)
- *           elements and their partial sums are added in LDS, one of {1, 2, 4, 8, 16};
- *   split : K ranges computed by separate workgroups (1..1024); with split > 1 the partial sums go to an fp32
- *           workspace and a second kernel adds them in split order (deterministic).
- * bp_skinny_config_supported() tells whether a (kind, mt, rows, waves) combination is compiled; mt is the row
- * bucket of the activations (1, 2, 4, 8 or 16; M is rounded up to it).
- */
-int bp_skinny_config_supported(int wkind, int mt, int rows, int waves);
-
 /* Bytes of fp32 workspace a skinny call with this split needs: split * M * N * 4 when split > 1, else 0. */
 size_t bp_skinny_workspace_bytes(int64_t M, int64_t N, int split);
-
-/*
- * y[M, N] (bf16) = x[M, K] (bf16) . w[N, K]^T (bf16), fp32 accumulation. 1 <= M <= 16 per call (the Python layer
- * chunks larger M). M = 0 or N = 0 is a no-op; K = 0 writes zeros.
- * Replaces: byteprof/optim/skinny.py:111-129 (_launch, kind "bf16") + :36-45,64-72,76-80 (_skinny_kernel MODE 0)
- *           + :84-90 (_split_reduce), called from skinny_mm (skinny.py:136-166).
- */
-int bp_skinny_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
-                   int rows, int waves, int split, void* workspace, size_t workspace_bytes, void* stream);
-
-/*
- * y[M, N] (bf16) = (x[M, K] (bf16) . q[N, K]^T (int8)) * scale[N], the int8 -> float conversion fused into the
- * weight stream and the scale applied to the fp32 sum. scale_dtype: BP_DT_BF16, BP_DT_F16 or BP_DT_F32.
- * Replaces: byteprof/optim/skinny.py:64-75 (_skinny_kernel MODE 1) via skinny_mm with an int8 weight.
- */
-int bp_skinny_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y,
-                   int64_t M, int64_t N, int64_t K, int rows, int waves, int split,
-                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * The skinny matmul of every row count on the matrix cores (v_mfma_f32_16x16x32_bf16), the path skinny_mm takes for
@@ -86,13 +56,14 @@ int bp_skinny_int8(const void* x, const void* q, const void* scale, int scale_dt
  * the segment's K slots). Tile configuration: rb = 8-row weight blocks per workgroup (1, 2, 4; 4 up to M = 16),
  * waves = wavefronts sharing the workgroup's K segments (1, 2, 4, 8; segment s to wave s % waves), split = K ranges
  * in separate workgroups whose fp32 partials are added in split order by a second kernel (workspace as for
- * bp_skinny_bf16), xstage = 1: each workgroup copies its activation rows and K range to LDS first (up to M = 16 and
+ * bp_skinny_workspace_bytes), xstage = 1: each workgroup copies its activation rows and K range to LDS first (up to M = 16 and
  * bp_skinny_mf_stage_bytes() >= 0), 0: the activation operands are loaded with the weights. The K order of every sum
  * depends only on (K, waves, split): output row i is bitwise independent of M (1..64), rb and xstage. K not a
  * multiple of the 128-byte segment (64 bf16 / 128 int8 elements) or x, w not 16-byte aligned: an element-load variant
  * with the same segments (rb 1, 4 waves, xstage 0).
  * Replaces: byteprof/optim/skinny.py:36-90 (_skinny_kernel MODE 0 / 1, _split_reduce) and :111-133 (_launch) via
- *           skinny_mm (skinny.py:136-166) for every BM bucket (16, 32, 64).
+ *           skinny_mm (skinny.py:136-166) for every BM bucket (16, 32, 64); at M = 1 with int8 weights, the one-row
+ *           int8 product byteprof/quant/triton_int8.py:16-47 (_gemv_int8, gemv_int8).
  */
 int bp_skinny_mf_supported(int wkind, int M, int rb, int waves, int xstage);
 int bp_skinny_mf_k_segment(int wkind);
@@ -179,16 +150,9 @@ int bp_skinny_int4(const void* x, const void* packed, const void* scale, int sca
                    size_t workspace_bytes, void* stream);
 
 /*
- * One-row int8 product: y[1, N] (bf16) = scale[n] * sum_k float(q[n, k]) * float(x[k]).
- * Replaces: byteprof/quant/triton_int8.py:40-47 (gemv_int8) and :16-28 (_gemv_int8).
- */
-int bp_gemv_int8(const void* x, const void* q, const void* scale, int scale_dtype, void* y,
-                 int64_t N, int64_t K, int rows, int waves, void* stream);
-
-/*
  * Fixed-order reduction of split-K partial sums: y[M, N] = bf16(scale[n] * sum_{s < split} ws[s, M, N]);
- * scale may be null (bf16 weights). bp_skinny_* call it themselves when split > 1; it is exported for callers
- * that produce partial sums of their own.
+ * scale may be null (bf16 weights). bp_skinny_mf and bp_skinny_int4 call it themselves when split > 1; it is
+ * exported for callers that produce partial sums of their own (bp_skinny_mf_partials).
  * Replaces: byteprof/optim/skinny.py:84-90 (_split_reduce).
  */
 int bp_splitk_reduce(const void* workspace, void* y, const void* scale, int scale_dtype,
@@ -324,100 +288,6 @@ size_t bp_decode_argmax_scratch_bytes(void);
 int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream);
 size_t bp_decode_argmax_rows_scratch_bytes(int rows);
 int bp_decode_argmax_rows(const void* logits, int vocab, int rows, int64_t* tok, void* scratch, void* stream);
-
-/*
- * Decode-step linear set: a chain of skinny linears at one activation row run by one persistent launch.
- *
- * A stage is one or more linears sharing one input vector (q|k|v, gate|up, or a single linear). Its rows are the
- * concatenation of its weight segments; its output y is the concatenation of their outputs. A stage may read its
- * input from an earlier stage's output (wait_stage >= 0: it reads each of those rows once the workgroup that
- * computes it has published it), optionally renormalised to unit RMS: x = bf16(src * (1 / sqrt(mean(src^2)))), with fp32
- * arithmetic (an all-zero src is used unscaled). Each row is computed as the skinny kernels compute it (fp32
- * accumulation of bf16 or exact int8 -> bf16 pairs, int8 scale on the fp32 sum, bf16 round to nearest even).
- *
- * Layout (128 bytes, 8-byte aligned pointers): the array lives in device memory for the kernel, and a host copy
- * with the same contents is passed for validation.
- */
-typedef struct BpSetStage {
-  const void* src;      /* bf16 [K], 16-byte aligned: the input (external, or a slice of an earlier stage's y) */
-  void* y;              /* bf16 [N], 16-byte aligned: the stage's outputs */
-  void* x_used;         /* bf16 [K] or NULL: receives the input vector the stage used (after renormalisation) */
-  int32_t K;            /* input length: a multiple of 512 (bf16 weights) or 1024 (int8), at most 8192 */
-  int32_t N;            /* rows: at most (512 - 1) * workgroups */
-  int32_t wait_stage;   /* -1, or the index (< this stage's) of the stage whose outputs src reads (src must then
-                           lie inside that stage's y) */
-  int32_t renorm;       /* 1: renormalise the input to unit RMS; 0: use it as is */
-  int32_t nseg;         /* weight segments, 1..4 */
-  int32_t seg_end[4];   /* cumulative row ends of the segments; seg_end[nseg - 1] == N */
-  int32_t reserved;
-  const void* w[4];     /* segment weights [rows, K] row-major, 16-byte aligned (bf16 or int8) */
-  const void* scale[4]; /* int8: per-row scales of each segment (dtype given to bp_linear_set_run) */
-} BpSetStage;
-
-/* Bytes of scratch a launch of these stages needs: a launch counter, an error flag and every stage's rows tagged
- * with the launch (4 bytes per row, rows rounded up to 8); num_workgroups is the grid the launches use. The scratch
- * must be zero before its first launch and is then reused as is by every later launch (no reset between launches
- * or graph replays). The 32-bit word at index 32 becomes non-zero if a launch gave up waiting for another
- * workgroup (that launch's later results are invalid); the host clears it. */
-size_t bp_linear_set_scratch_bytes(const BpSetStage* stages, int num_stages, int num_workgroups);
-
-/* Workgroups the set kernel is launched with on `device`: one per compute unit (0 on error). */
-int bp_linear_set_workgroups(int device);
-
-/* Checks a host array of stages against the kernel's limits; BP_OK or a BP_E_* code. */
-int bp_linear_set_validate(const BpSetStage* stages, int num_stages, int wkind, int num_workgroups);
-
-/*
- * Runs the set: one launch of num_workgroups workgroups (use bp_linear_set_workgroups) on `stream`.
- * wkind: BP_DT_BF16 (0) bf16 weights or 1 int8 weights (scale_dtype BP_DT_BF16 / BP_DT_F16 / BP_DT_F32).
- * host_stages is validated; dev_stages must hold the same array in device memory. Calls on one scratch must not
- * overlap (they are ordered on one stream or a captured graph).
- * Replaces: per-token replays of the decode-step linears, each a skinny_mm / SkinnyLinear.forward call
- *           (byteprof/optim/skinny_linear.py:56-69 -> byteprof/optim/skinny.py:136-166) captured in the decode
- *           graph (byteprof/optim/olmo.py:164-174); the per-row arithmetic is skinny.py:36-90's.
- */
-int bp_linear_set_run(int wkind, int scale_dtype, const BpSetStage* host_stages, const void* dev_stages,
-                      int num_stages, void* scratch, size_t scratch_bytes, int num_workgroups, void* stream);
-
-/*
- * Grouped skinny launch: G independent linears at one activation row, y_i = x_i . W_i^T, in one non-persistent
- * launch. Workgroup b computes `rows` consecutive output rows of the item whose workgroup range holds b; every
- * output is bitwise equal to bp_skinny_bf16 / bp_skinny_int8 at M = 1 with the same rows and waves and split 1.
- *
- * Layout (48 bytes, 8-byte aligned pointers): the array lives in device memory for the kernel, and a host copy with
- * the same contents is passed for validation.
- */
-typedef struct BpGroupItem {
-  const void* x;      /* bf16 [K], 16-byte aligned: the item's activation row */
-  const void* w;      /* [N, K] row-major, 16-byte aligned: bf16 or int8 weights (one kind for the whole group) */
-  const void* scale;  /* int8: [N] per-row scales (dtype given to bp_skinny_group_run); bf16: ignored */
-  void* y;            /* bf16 [N]: the outputs */
-  int64_t N;          /* rows, >= 0 (an item of 0 rows takes no workgroup) */
-  int32_t K;          /* a positive multiple of 512 (bf16 weights) or 1024 (int8) */
-  int32_t block0;     /* first workgroup of the item: written by bp_skinny_group_plan */
-} BpGroupItem;
-
-/* Workgroups per entry of the lookup table: lut[j] is the item that holds workgroup j * BP_GROUP_LUT_SPAN. */
-#define BP_GROUP_LUT_SPAN 256
-
-/* 1 if a grouped kernel with `rows` output rows and `waves` wavefronts per workgroup is compiled for wkind. */
-int bp_skinny_group_config_supported(int wkind, int rows, int waves);
-
-/* Host-side plan: checks every item, writes items[i].block0 (workgroups of `rows` rows, items in order) and, when
- * lut is not NULL, fills lut[0 .. ceil(blocks / BP_GROUP_LUT_SPAN)) (lut_capacity entries available). Returns the
- * number of workgroups (>= 0) or a BP_E_* code. No device access. */
-int bp_skinny_group_plan(BpGroupItem* items, int num_items, int wkind, int rows, int32_t* lut, int lut_capacity);
-
-/*
- * Runs the group: one launch of `blocks` workgroups on `stream`. host_items must be the planned array (checked:
- * operands and every block0), dev_items and dev_lut its device copies. wkind BP_DT_BF16 (0) or 1 (int8 weights, with
- * scale_dtype BP_DT_BF16 / BP_DT_F16 / BP_DT_F32).
- * Replaces: the set benchmark's independent skinny_mm calls, one per linear (tools/skinny_bench.py:45-71 ->
- *           byteprof/optim/skinny.py:136-166), captured in one CUDA graph; the per-row arithmetic is
- *           skinny.py:36-90's at split 1.
- */
-int bp_skinny_group_run(int wkind, int scale_dtype, const BpGroupItem* host_items, const void* dev_items,
-                        const void* dev_lut, int num_items, int blocks, int rows, int waves, void* stream);
 
 #ifdef __cplusplus
 }

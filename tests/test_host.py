@@ -253,35 +253,32 @@ def test_bf16_of_torch_matches_the_oracle_rounding():
     assert np.array_equal(x.to(torch.bfloat16).float().numpy(), ON.bf16_round(x.numpy()))
 
 
-def test_linear_set_host_validation():
-    """LinearSet checks shapes, dtypes and dependencies before touching the GPU (CPU tensors here)."""
-    from byteprof_amd.optim.linear_set import LinearSet, Stage
+def test_linear_chain_host_validation():
+    """LinearChain checks kinds, shapes, inputs and dependencies before touching the GPU (CPU tensors here)."""
+    from byteprof_amd.optim.linear_chain import ChainStage, LinearChain
 
-    w = torch.zeros(8, 512, dtype=torch.bfloat16)
-    x = torch.zeros(512, dtype=torch.bfloat16)
-    out = torch.zeros(8, dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="at least one stage"):
-        LinearSet([])
-    with pytest.raises(ValueError, match="unsupported weight dtype"):
-        LinearSet([Stage([w.float()], x, out)])
-    with pytest.raises(ValueError, match="multiple of 512"):
-        LinearSet([Stage([torch.zeros(8, 100, dtype=torch.bfloat16)], torch.zeros(100, dtype=torch.bfloat16), out)])
-    with pytest.raises(ValueError, match="multiple of 1024"):
-        LinearSet([Stage([torch.zeros(8, 512, dtype=torch.int8)], x, out, scales=[torch.ones(8)])])
-    with pytest.raises(ValueError, match="need one scale"):
-        LinearSet([Stage([torch.zeros(8, 1024, dtype=torch.int8)], torch.zeros(1024, dtype=torch.bfloat16), out)])
-    with pytest.raises(ValueError, match="src must be"):
-        LinearSet([Stage([w], x[:100], out)])
-    with pytest.raises(ValueError, match="out must be"):
-        LinearSet([Stage([w], x, out[:4])])
-    with pytest.raises(ValueError, match="earlier stage"):
-        LinearSet([Stage([w], x, out, wait=0)])
-    with pytest.raises(ValueError, match="inside stage 0"):
-        LinearSet([Stage([w], x, out), Stage([torch.zeros(4, 512, dtype=torch.bfloat16)], x, out[:4], wait=0)])
-    with pytest.raises(ValueError, match="1..4 weights"):
-        LinearSet([Stage([w] * 5, x, torch.zeros(40, dtype=torch.bfloat16))])
-    with pytest.raises(ValueError, match="runs on a GPU"):
-        LinearSet([Stage([w], x, out)])
+    w = torch.zeros(64, 1024, dtype=torch.bfloat16)
+    x = torch.zeros(1024, dtype=torch.bfloat16)
+    out = torch.empty(64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        LinearChain([])
+    with pytest.raises(ValueError):  # no kernel for 3 waves
+        LinearChain([ChainStage([w], x, out)], waves=3)
+    with pytest.raises(ValueError):  # reads a later stage
+        LinearChain([ChainStage([w], (1, 0), out), ChainStage([w], x, torch.empty(64, dtype=torch.bfloat16))])
+    with pytest.raises(ValueError):  # the slice runs past the producer's output
+        LinearChain([ChainStage([w], x, out), ChainStage([w], (0, 0), torch.empty(64, dtype=torch.bfloat16))])
+    with pytest.raises(ValueError):  # the input is not bf16
+        LinearChain([ChainStage([w], x.float(), out)])
+    with pytest.raises(ValueError):  # mixed weight kinds
+        q, sc = quantize_rowwise_int8(w)
+        LinearChain([ChainStage([w], x, out), ChainStage([(q, sc)], x, torch.empty(64, dtype=torch.bfloat16))])
+    with pytest.raises(ValueError):  # out holds fewer rows than the weights
+        LinearChain([ChainStage([w, w], x, out)])
+    from byteprof_amd._lib import NativeError
+    with pytest.raises(NativeError):  # K not a multiple of the 64-element segment: refused by the plan
+        LinearChain([ChainStage([torch.zeros(8, 100, dtype=torch.bfloat16)], torch.zeros(100, dtype=torch.bfloat16),
+                                torch.empty(8, dtype=torch.bfloat16))])
 
 
 def test_decode_chain_structure():
