@@ -6,20 +6,23 @@ One step = one pass over the OLMo-2-1B-shaped decode-step linear set at M = 1 in
 113 linears, every weight distinct (2.56 GB, ten times the 256 MB Infinity Cache), all operands resident in HBM
 before the timed region.
 
-`value` is the dependency-respecting figure: the 113 linears as stream-ordered skinny_mm launches in one HIP graph,
-each launch starting after the one before it has finished, as a decode step orders them (the reference's execution
-model: one skinny call per linear in a CUDA graph, byteprof/optim/olmo.py:164-215; its set benchmark times the same
-calls, tools/skinny_bench.py:45-71). Every linear reads its own seeded unit-RMS input.
+`value` is the sequential figure: the set as the 65 stream-ordered skinny launches a decode step makes (q|k|v and
+gate|up each one launch over adjacent weight rows; o, down and the head one each), in one HIP graph, each launch
+starting after the one before it has finished, every stage reading its own seeded unit-RMS input. The reference's
+execution model is the same sequence with one skinny call per linear (byteprof/optim/olmo.py:164-215; its set
+benchmark times those calls, tools/skinny_bench.py:45-71): that 113-launch graph is reported beside it.
 
 Printed (one JSON line): GB/s of the step (algorithmic bytes = weights + activations + outputs, each once:
 2,560,237,568 B per step), us per set and % of the 8 TB/s peak; `roofline` for the kernel instantiation with the
 largest time per step (its launches' algorithmic bytes over their average duration from HIP events, HBM traffic per
 launch from the committed rocprofv3 counter summary); `cpu_baseline`: torch F.linear over the set on the host cores
 (the reference's CPU path); secondary figures:
+  - graph_113: the 113 linears as one skinny launch each (the reference's sequence);
   - one_launch_set: the same 113 independent linears as one grid (csrc/skinny_chain.hip), with its own roofline;
   - dependent: the set with real data dependencies (each stage reads the unit-RMS renormalisation of the output it
-    depends on in a decode step) as one launch (in-kernel hand-off) and as 65 stream-ordered stage launches (the two
-    give bitwise equal outputs, checked here);
+    depends on in a decode step) as 65 stream-ordered skinny launches (the renormalisation inside each launch), as
+    one launch of the chain kernel (in-kernel hand-off) and as 65 launches of the chain kernel (those two give
+    bitwise equal outputs, checked here);
   - int8_set: the int8 weight-only set (fp16 scales) in the same execution models, and as 113-launch graphs at
     M = 4 and 16; bf16 / int8 time ratios;
   - int4: the group-128 int4 kernel on the set's shapes;
@@ -187,13 +190,18 @@ def one_launch(kind: str, weights, nbytes: int, device, waves: int, tag: str) ->
 
 
 def dependent_figures(kind: str, weights, nbytes: int, device) -> dict:
-    """The set with a decode step's data dependencies: one launch (in-kernel hand-off between stages) and 65
-    stream-ordered stage launches in one HIP graph; their outputs must be equal bit for bit."""
+    """The set with a decode step's data dependencies: 65 stream-ordered skinny launches (renormalisation inside
+    each launch); one launch of the chain kernel (in-kernel hand-off between stages) and 65 stream-ordered launches
+    of it, whose outputs must be equal bit for bit."""
     import torch
 
     from byteprof_amd import decode_set as D
 
     ch = D.build_chain(kind, device, weights=weights, dependent=True)
+    gs = graph_of(D.stage_graph_calls(ch))
+    evs, _ = time_runs(gs.replay, 50)
+    del gs
+    skinny_stages = {**figures(evs, nbytes), "launches": len(ch.stages)}
     ev_ms, wall_ms = time_runs(ch.lset.run, 50)
     if ch.lset.timed_out():
         raise RuntimeError("a dependent launch gave up waiting: its results are invalid")
@@ -205,8 +213,8 @@ def dependent_figures(kind: str, weights, nbytes: int, device) -> dict:
     g.replay()
     _sync()
     same = all(torch.equal(a, st.out) for a, st in zip(ref, ch.stages))
-    out = {"one_launch": one, "stage_graph": {**figures(ev2, nbytes), "launches": len(stages)},
-           "outputs_equal": bool(same)}
+    out = {"skinny_stage_graph": skinny_stages, "chain_one_launch": one,
+           "chain_stage_graph": {**figures(ev2, nbytes), "launches": len(stages)}, "chain_outputs_equal": bool(same)}
     del g, stages, ch, ref
     return out
 
@@ -582,31 +590,41 @@ def main() -> int:
     _lib.lib()
     log("[bench] building the bf16 decode-step set (2.56 GB of weights)")
     weights = D.make_weights("bf16", device, seed=0)
-    ops = D.build("bf16", 1, device, seed=0, weights=weights)
+    stages = D.build_stages(weights, 1, device, seed=0)
     nbytes = D.chain_bytes("bf16")
-    g = graph_of(ops)
-    log(f"[bench] 113-launch graph: warm-up {WARM_S} s + {a.warmup} replays, timing {a.steps} replays")
+    g = graph_of(stages)
+    log(f"[bench] 65-launch stage graph: warm-up {WARM_S} s + {a.warmup} replays, timing {a.steps} replays")
     ev_ms, wall_ms = time_runs(g.replay, a.steps, a.warmup)
     del g
     ms = max(ev_ms, wall_ms)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] {ms * 1e3:.1f} us per set, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
     log("[bench] per-shape launch times (roofline)")
-    shapes = per_shape(ops, "bf16", 1)
+    shapes = per_shape(stages, "bf16", 1)
+    ops = D.build("bf16", 1, device, seed=0, weights=weights)
     result = {
         "metric": METRIC, "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0, 0.02^2) bf16 weights, unit-RMS N(0,1) activations)",
         "config": {"workload": ("OLMo-2-1B-shaped decode-step linear set at M=1, bf16: 16 x (q,k,v,o 2048->2048; "
-                                "gate,up 2048->8192; down 8192->2048) + LM head 2048->100352, 113 stream-ordered "
-                                "skinny_mm launches in one HIP graph"),
-                   "M": 1, "linears": len(D.shapes()), "bytes_per_step": nbytes, "us_per_set": ms * 1e3,
+                                "gate,up 2048->8192; down 8192->2048) + LM head 2048->100352 (113 linears), as 65 "
+                                "stream-ordered skinny launches in one HIP graph (q|k|v and gate|up one launch each)"),
+                   "M": 1, "linears": len(D.shapes()), "launches": len(stages), "bytes_per_step": nbytes,
+                   "us_per_set": ms * 1e3,
                    "pct_of_hbm_peak": gbs / HBM_PEAK_GBS * 100, "event_ms": ev_ms, "wall_ms": wall_ms,
                    "empty_launch_us": D.dispatch_gap_us()},
         "roofline": roofline_of_graph(shapes),
         "kernels": shapes,
     }
+    del stages
     if not a.no_extras:
+        def graph_113():
+            g113 = graph_of(ops)
+            e113, _ = time_runs(g113.replay, 50)
+            del g113
+            return {**figures(e113, nbytes), "launches": len(ops), "kernels": per_shape(ops, "bf16", 1)}
+
+        extra(result, "graph_113", graph_113)
         extra(result, "one_launch_set", one_launch, "bf16", weights, nbytes, device, 4, "one-launch-bf16")
         extra(result, "dependent", dependent_figures, "bf16", weights, nbytes, device)
     del ops
@@ -620,24 +638,31 @@ def main() -> int:
         nb8 = D.chain_bytes("int8")
 
         def int8_set():
+            st8 = D.build_stages(w8, 1, device, seed=0)
+            gs8 = graph_of(st8)
+            es8, _ = time_runs(gs8.replay, 50)
+            del gs8
             ops8 = D.build("int8", 1, device, seed=0, weights=w8)
             g8 = graph_of(ops8)
             e8, _ = time_runs(g8.replay, 50)
             del g8
             out = {"bytes_per_step": nb8, "scales": "fp16 per output row",
+                   "stage_graph": {**figures(es8, nb8), "launches": len(st8), "kernels": per_shape(st8, "int8", 1)},
                    "graph_113": {**figures(e8, nb8), "kernels": per_shape(ops8, "int8", 1)},
                    "graph_113_m4": graph_set("int8", w8, 4, device), "graph_113_m16": graph_set("int8", w8, 16, device),
                    "one_launch_set": one_launch("int8", w8, nb8, device, 2, "one-launch-int8"),
                    "dependent": dependent_figures("int8", w8, nb8, device)}
-            del ops8
             bf = result
             out["bf16_over_int8_time"] = {
-                "graph_113": bf["config"]["us_per_set"] / out["graph_113"]["us_per_set"],
+                "stage_graph": bf["config"]["us_per_set"] / out["stage_graph"]["us_per_set"],
+                "graph_113": (bf["graph_113"]["us_per_set"] / out["graph_113"]["us_per_set"]
+                              if "us_per_set" in bf.get("graph_113", {}) else None),
                 "one_launch_set": (bf["one_launch_set"]["us_per_set"] / out["one_launch_set"]["us_per_set"]
                                    if "us_per_set" in bf.get("one_launch_set", {}) else None),
-                "dependent_stage_graph": (bf["dependent"]["stage_graph"]["us_per_set"]
-                                          / out["dependent"]["stage_graph"]["us_per_set"]
-                                          if "stage_graph" in bf.get("dependent", {}) else None)}
+                "dependent_skinny_stage_graph": (bf["dependent"]["skinny_stage_graph"]["us_per_set"]
+                                                 / out["dependent"]["skinny_stage_graph"]["us_per_set"]
+                                                 if "skinny_stage_graph" in bf.get("dependent", {}) else None)}
+            del st8, ops8
             return out
 
         extra(result, "int8_set", int8_set)

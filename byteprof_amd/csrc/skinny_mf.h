@@ -164,6 +164,15 @@ struct MfStage {
   }
 };
 
+// s_waitcnt for at most N outstanding vector-memory loads of the wave, no wait on the other counters (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt in 6:4, lgkmcnt in 11:8). Loads complete in issue order, so after
+// mf_wait_vm<N>() every load but the last N issued has completed.
+template <int N>
+__device__ __forceinline__ void mf_wait_vm() {
+  constexpr int n = N > 63 ? 63 : N;
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // No-op hook of MfMain::run.
 struct MfNoHook {
   __device__ __forceinline__ void operator()() const {}

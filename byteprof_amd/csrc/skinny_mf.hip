@@ -18,18 +18,97 @@ int splitk_reduce_launch(const float* ws, uint16_t* y, const void* scale, int sc
 
 namespace {
 
+// Transform of the LDS-staged activation rows before the matmul (split 1: the workgroup holds whole rows).
+struct MfPro {
+  int kind;                  // 0 none, BP_PRO_UNIT_RMS, BP_PRO_NORM
+  float eps;                 // BP_PRO_NORM: inside the root
+  const uint16_t* gamma;     // BP_PRO_NORM: [K]
+  const uint16_t* residual;  // BP_PRO_NORM: [M, K] or null
+  uint16_t* xout;            // [M, K] or null: the transformed rows, written by workgroup (0, 0)
+};
+
+constexpr int kProThreads = 1024;  // the norm kernel's workgroup, whose summation order the prologue reproduces
+constexpr int kProWaves = kProThreads / kWave;
+
+// In place, row by row:
+//   BP_PRO_UNIT_RMS: x <- bf16(x * (1 / sqrt(mean(x^2)))) (an all-zero row is left as is);
+//   BP_PRO_NORM:     x <- bf16(residual + bf16(gamma * (x * (1 / sqrt(mean(x^2) + eps))))) (no residual: the plain
+//                    norm), and workgroup (0, 0) writes the rows to xout.
+// The sum of squares is added in the order of the decode norm kernel (decode.hip, norm_residual_kernel): 1024
+// threads, thread t summing x[t]^2, x[t + 1024]^2, ... in order, each 64-lane wave by an xor butterfly (lane
+// distance 32, 16, ..., 1), the 16 wave totals in order from 0. Here 1024 "virtual threads" do that with any
+// workgroup size, so a fused norm equals the separate norm launch bit for bit.
+// gl (BP_PRO_NORM over one row, else null): LDS copies of gamma [K] and the residual row [K], loaded ahead of the
+// weights.
+template <int NT>
+__device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, float* vals, float* parts,
+                            bool writer, const uint16_t* gl) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  for (int m = 0; m < rows; ++m) {
+    uint16_t* row = xs + m * K;
+    for (int v = threadIdx.x; v < kProThreads; v += NT) {
+      float s = 0.f;
+      for (int i = v; i < K; i += kProThreads) {
+        const float f = bf16_bits_to_float(row[i]);
+        s += f * f;
+      }
+      vals[v] = s;
+    }
+    __syncthreads();
+    for (int vw = wave; vw < kProWaves; vw += NT / kWave) {
+      float s = vals[vw * kWave + lane];
+      for (int o = kWave / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
+      if (lane == 0) parts[vw] = s;
+    }
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < kProWaves; ++i) t += parts[i];
+    if (pro.kind == BP_PRO_UNIT_RMS) {
+      const float ms = t / static_cast<float>(K);
+      const float inv = ms > 0.f ? 1.f / sqrtf(ms) : 1.f;
+      for (int i = threadIdx.x; i < K; i += NT) {
+        const uint16_t v = float_to_bf16_bits(bf16_bits_to_float(row[i]) * inv);
+        row[i] = v;
+        if (writer && pro.xout != nullptr) as_global_mut(pro.xout)[static_cast<int64_t>(m) * K + i] = v;
+      }
+    } else {
+      const float r = 1.f / sqrtf(t / static_cast<float>(K) + pro.eps);
+      const bool has_res = pro.residual != nullptr;
+      auto put = [&](int i, float g, float rv) {
+        const float yv = round_to_bf16(g * (bf16_bits_to_float(row[i]) * r));
+        const uint16_t v = float_to_bf16_bits(has_res ? rv + yv : yv);
+        row[i] = v;
+        if (writer && pro.xout != nullptr) as_global_mut(pro.xout)[static_cast<int64_t>(m) * K + i] = v;
+      };
+      if (gl != nullptr) {  // one row, gamma and the residual in LDS
+        for (int i = threadIdx.x; i < K; i += NT)
+          put(i, bf16_bits_to_float(gl[i]), has_res ? bf16_bits_to_float(gl[K + i]) : 0.f);
+      } else {
+        gptr<const uint16_t> gam = as_global(pro.gamma);
+        gptr<const uint16_t> res = has_res ? as_global(pro.residual + static_cast<int64_t>(m) * K) : nullptr;
+        for (int i = threadIdx.x; i < K; i += NT)
+          put(i, bf16_bits_to_float(gam[i]), has_res ? bf16_bits_to_float(res[i]) : 0.f);
+      }
+    }
+  }
+  __syncthreads();
+}
+
 // EPI: 0 = y[m][n] (split 1) or fp32 partials ws[split][m][n]; 1 = the SiLU product of interleaved gate|up rows
 // (rows 2f / 2f + 1 the gate / up rows of output f): y[m][f] = bf16(bf16(silu(bf16(g))) * bf16(u)).
 // XL: the workgroup's activation rows and K range are staged in LDS (dynamic shared memory of
 // min(M, 8 MB) x K-range x 2 bytes), their loads issued before the first weight loads; otherwise every segment's
 // activation operand is loaded from memory with its weights. Same operands either way: the results are equal bit
-// for bit.
-template <int KIND, int MB, int RB, int WAVES, bool VEC, int EPI, bool XL>
+// for bit. PRO (XL, split 1 only): a transform of the staged rows before the matmul (mf_prologue); for
+// BP_PRO_NORM over one row, gamma and the residual row are loaded into LDS ahead of the weights too (the launch
+// then adds 4 K bytes of dynamic LDS).
+template <int KIND, int MB, int RB, int WAVES, bool VEC, int EPI, bool XL, bool PRO>
 __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t* __restrict__ x,
                                                                   const uint8_t* __restrict__ w,
                                                                   const void* __restrict__ scale, int scale_dt,
                                                                   uint16_t* __restrict__ y, float* __restrict__ ws,
-                                                                  int M, int64_t N, int64_t K, int split) {
+                                                                  int M, int64_t N, int64_t K, int split, MfPro pro) {
   using G = MfGeom<KIND>;
   constexpr int D = VEC ? mf_depth<KIND, MB, RB, !XL>() : 1;
   __shared__ MfRed<WAVES, RB, MB> red;
@@ -74,13 +153,45 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
     stage.issue(x, mrows, K, k_lo, kn, 0);  // ahead of the weight loads: the commit waits for these only
     MfXLds<KIND, MB> xs;
     xs.init(xs_lds, mrows, kn, k_lo, ln);
-    auto commit = [&]() {
-      stage.commit(xs_lds, mrows, kn, 0);
-      for (int pass = 1; pass < passes; ++pass) {
-        stage.issue(x, mrows, K, k_lo, kn, pass);
-        stage.commit(xs_lds, mrows, kn, pass);
+    __shared__ float pro_vals[PRO ? kProThreads : 1];
+    __shared__ float pro_parts[PRO ? kProWaves : 1];
+    // BP_PRO_NORM over one row: gamma and the residual row straight into LDS after the staged row (64 lanes x 16
+    // bytes per load, no registers held), ahead of the weight loads
+    const uint16_t* gl = nullptr;
+    if constexpr (PRO) {
+      if (pro.kind == BP_PRO_NORM && mrows == 1) {
+        uint16_t* dst = xs_lds + kn;
+        gl = dst;
+        for (int j = wave; j * 512 < kn; j += WAVES) {
+          const int e = j * 512 + 8 * lane;
+          if (e < kn) {
+            __builtin_amdgcn_global_load_lds(as_global(pro.gamma + e),
+                                             (__attribute__((address_space(3))) void*)(dst + j * 512), 16, 0, 0);
+            if (pro.residual != nullptr)
+              __builtin_amdgcn_global_load_lds(as_global(pro.residual + e),
+                                               (__attribute__((address_space(3))) void*)(dst + kn + j * 512), 16, 0,
+                                               0);
+          }
+        }
       }
-      __syncthreads();
+    }
+    // The staged rows (and the prologue's operands) were loaded before the D x RB weight loads: waiting for them
+    // leaves the weights in flight. The prologue variants stage in one pass (the launch checks it) and have no
+    // other path, so the transform runs while the weights stream in.
+    auto commit = [&]() {
+      mf_wait_vm<D * RB>();
+      stage.commit(xs_lds, mrows, kn, 0);
+      if constexpr (PRO) {
+        __syncthreads();
+        if (pro.kind != 0)
+          mf_prologue<kNT>(xs_lds, mrows, kn, pro, pro_vals, pro_parts, blockIdx.x == 0 && blockIdx.y == 0, gl);
+      } else {
+        for (int pass = 1; pass < passes; ++pass) {
+          stage.issue(x, mrows, K, k_lo, kn, pass);
+          stage.commit(xs_lds, mrows, kn, pass);
+        }
+        __syncthreads();
+      }
     };
     MfMain<KIND, MB, RB, D, true, false, MfXLds<KIND, MB>>::run(wrow, xs, x, K, kl, s_first, WAVES, nseg, acc,
                                                                commit);
@@ -137,29 +248,29 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
 }
 
 using MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, uint16_t*, float*, int, int64_t, int64_t,
-                      int);
+                      int, MfPro);
 
 // Compiled menu: activation blocks MB in {1, 2, 4, 8} (M <= 8, 16, 32, 64) x row blocks RB in {1, 2, 4} (RB 4 up
 // to MB 2) x waves in {1, 2, 4, 8}; the SiLU epilogue and the LDS-staged activations up to MB 2; the element-load
 // variant at RB 1, 4 waves.
-template <int KIND, int MB, int RB, int EPI, bool XL>
+template <int KIND, int MB, int RB, int EPI, bool XL, bool PRO>
 MfFn pick_waves(int waves) {
   switch (waves) {
-    case 1: return &skinny_mf_kernel<KIND, MB, RB, 1, true, EPI, XL>;
-    case 2: return &skinny_mf_kernel<KIND, MB, RB, 2, true, EPI, XL>;
-    case 4: return &skinny_mf_kernel<KIND, MB, RB, 4, true, EPI, XL>;
-    case 8: return &skinny_mf_kernel<KIND, MB, RB, 8, true, EPI, XL>;
+    case 1: return &skinny_mf_kernel<KIND, MB, RB, 1, true, EPI, XL, PRO>;
+    case 2: return &skinny_mf_kernel<KIND, MB, RB, 2, true, EPI, XL, PRO>;
+    case 4: return &skinny_mf_kernel<KIND, MB, RB, 4, true, EPI, XL, PRO>;
+    case 8: return &skinny_mf_kernel<KIND, MB, RB, 8, true, EPI, XL, PRO>;
     default: return nullptr;
   }
 }
 
-template <int KIND, int MB, int EPI, bool XL>
+template <int KIND, int MB, int EPI, bool XL, bool PRO = false>
 MfFn pick_rb(int rb, int waves) {
   switch (rb) {
-    case 1: return pick_waves<KIND, MB, 1, EPI, XL>(waves);
-    case 2: return pick_waves<KIND, MB, 2, EPI, XL>(waves);
+    case 1: return pick_waves<KIND, MB, 1, EPI, XL, PRO>(waves);
+    case 2: return pick_waves<KIND, MB, 2, EPI, XL, PRO>(waves);
     case 4:
-      if constexpr (MB <= 2) return pick_waves<KIND, MB, 4, EPI, XL>(waves);
+      if constexpr (MB <= 2) return pick_waves<KIND, MB, 4, EPI, XL, PRO>(waves);
       return nullptr;
     default: return nullptr;
   }
@@ -171,10 +282,10 @@ MfFn pick_mb(int mb, int rb, int waves, bool vec) {
     if constexpr (EPI == 0 && !XL) {
       if (waves != 4) return nullptr;
       switch (mb) {
-        case 1: return &skinny_mf_kernel<KIND, 1, 1, 4, false, 0, false>;
-        case 2: return &skinny_mf_kernel<KIND, 2, 1, 4, false, 0, false>;
-        case 4: return &skinny_mf_kernel<KIND, 4, 1, 4, false, 0, false>;
-        case 8: return &skinny_mf_kernel<KIND, 8, 1, 4, false, 0, false>;
+        case 1: return &skinny_mf_kernel<KIND, 1, 1, 4, false, 0, false, false>;
+        case 2: return &skinny_mf_kernel<KIND, 2, 1, 4, false, 0, false, false>;
+        case 4: return &skinny_mf_kernel<KIND, 4, 1, 4, false, 0, false, false>;
+        case 8: return &skinny_mf_kernel<KIND, 8, 1, 4, false, 0, false, false>;
         default: return nullptr;
       }
     }
@@ -193,15 +304,26 @@ MfFn pick_mb(int mb, int rb, int waves, bool vec) {
   }
 }
 
+// The prologue variants: staged activations, up to 16 rows, both epilogues.
+template <int KIND, int EPI>
+MfFn pick_pro(int mb, int rb, int waves) {
+  switch (mb) {
+    case 1: return pick_rb<KIND, 1, EPI, true, true>(rb, waves);
+    case 2: return pick_rb<KIND, 2, EPI, true, true>(rb, waves);
+    default: return nullptr;
+  }
+}
+
 template <int KIND>
-MfFn mf_pick_kind(int mb, int rb, int waves, bool vec, int epi, bool xl) {
+MfFn mf_pick_kind(int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro) {
+  if (pro) return vec && xl ? (epi == 0 ? pick_pro<KIND, 0>(mb, rb, waves) : pick_pro<KIND, 1>(mb, rb, waves)) : nullptr;
   if (epi == 0) return xl ? pick_mb<KIND, 0, true>(mb, rb, waves, vec) : pick_mb<KIND, 0, false>(mb, rb, waves, vec);
   return xl ? pick_mb<KIND, 1, true>(mb, rb, waves, vec) : pick_mb<KIND, 1, false>(mb, rb, waves, vec);
 }
 
-MfFn mf_pick(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl) {
-  if (wkind == kBf16) return mf_pick_kind<kBf16>(mb, rb, waves, vec, epi, xl);
-  if (wkind == kInt8) return mf_pick_kind<kInt8>(mb, rb, waves, vec, epi, xl);
+MfFn mf_pick(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro = false) {
+  if (wkind == kBf16) return mf_pick_kind<kBf16>(mb, rb, waves, vec, epi, xl, pro);
+  if (wkind == kInt8) return mf_pick_kind<kInt8>(mb, rb, waves, vec, epi, xl, pro);
   return nullptr;
 }
 
@@ -233,7 +355,7 @@ int64_t mf_stage_bytes(int wkind, int64_t M, int64_t K, int split) {
 // mode 0: y (split > 1: partials then the reduce); 1: partials only (split >= 2, y unused); 2: SiLU epilogue.
 int mf_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y, int64_t M,
               int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* ws, size_t ws_bytes, void* stream,
-              int mode) {
+              int mode, const BpPrologue* prologue = nullptr) {
   if (wkind != kBf16 && wkind != kInt8) return BP_E_UNSUPPORTED;
   if (M < 0 || N < 0 || K < 0 || M > 64) return BP_E_INVALID_ARG;
   if (M == 0 || N == 0) return BP_OK;
@@ -263,12 +385,30 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   const int64_t nseg = (K + seg - 1) / seg;
   if (split > nseg) split = static_cast<int>(nseg);
   if (mode == 1 && split < 2) return BP_E_UNSUPPORTED;
+  MfPro pro{0, 0.f, nullptr, nullptr, nullptr};
+  if (prologue != nullptr && prologue->kind != 0) {
+    // whole rows staged in LDS: split 1, vector loads, at most 16 rows
+    if (prologue->kind != BP_PRO_UNIT_RMS && prologue->kind != BP_PRO_NORM) return BP_E_INVALID_ARG;
+    if (prologue->kind == BP_PRO_NORM && prologue->gamma == nullptr) return BP_E_INVALID_ARG;
+    // gamma, the residual and xout are read / written in 16-byte pieces
+    if (reinterpret_cast<uintptr_t>(prologue->gamma) % 16 != 0 || reinterpret_cast<uintptr_t>(prologue->residual) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(prologue->xout) % 16 != 0)
+      return BP_E_INVALID_ARG;
+    if (!vec || split != 1 || M > 16 || mode == 1) return BP_E_UNSUPPORTED;
+    // the rows in one staging pass: 4 pieces of 8 elements per thread
+    if (((M < 8 * mf_blocks(M) ? M : 8 * mf_blocks(M)) * (K / 8) + 4 * waves * kWave - 1) / (4 * waves * kWave) != 1)
+      return BP_E_UNSUPPORTED;
+    xstage = 1;
+    pro = MfPro{prologue->kind, prologue->eps, static_cast<const uint16_t*>(prologue->gamma),
+                static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout)};
+  }
   int64_t lds = 0;
   if (xstage) {
     lds = mf_stage_bytes(wkind, M, K, split);
     if (lds < 0) return BP_E_UNSUPPORTED;
   }
-  MfFn fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0);
+  if (pro.kind == BP_PRO_NORM && M == 1) lds += 4 * K;  // gamma and the residual row (mf_prologue)
+  MfFn fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0, pro.kind != 0);
   if (fn == nullptr) return BP_E_UNSUPPORTED;
   if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
     return BP_E_WORKSPACE;
@@ -276,7 +416,7 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
   fn<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(split)), waves * kWave, static_cast<size_t>(lds),
        st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale, scale_dt,
-             static_cast<uint16_t*>(y), static_cast<float*>(ws), static_cast<int>(M), N, K, split);
+             static_cast<uint16_t*>(y), static_cast<float*>(ws), static_cast<int>(M), N, K, split, pro);
   const int rc = mf_status();
   if (rc != BP_OK || split == 1 || mode == 1) return rc;
   return splitk_reduce_launch(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
@@ -312,6 +452,14 @@ int bp_skinny_mf_partials(int wkind, const void* x, const void* w, int64_t M, in
   if (workspace == nullptr) return BP_E_WORKSPACE;
   return bp::mf_launch(wkind, x, w, nullptr, 0, nullptr, M, N, K, rb, waves, split, xstage, workspace,
                        workspace_bytes, stream, 1);
+}
+
+int bp_skinny_mf_pro(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y, int64_t M,
+                     int64_t N, int64_t K, int rb, int waves, int epilogue, const BpPrologue* prologue, void* stream) {
+  if (prologue == nullptr || (epilogue != 0 && epilogue != 1)) return BP_E_INVALID_ARG;
+  if (epilogue == 1 && N < 0) return BP_E_INVALID_ARG;
+  return bp::mf_launch(wkind, x, w, scale, scale_dtype, y, M, epilogue == 1 ? 2 * N : N, K, rb, waves, 1, 1, nullptr,
+                       0, stream, epilogue == 1 ? 2 : 0, prologue);
 }
 
 int bp_skinny_mf_silu(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* out,

@@ -1,4 +1,4 @@
-"""The OLMo-2-1B-shaped decode-step linear set at M activation rows, as a captured HIP graph of skinny launches.
+"""The OLMo-2-1B-shaped decode-step linear set at M activation rows, as captured HIP graphs of skinny launches.
 
 Per layer (16): q, k, v, o 2048 -> 2048; gate, up 2048 -> 8192; down 8192 -> 2048; then the LM head
 2048 -> 100352: 113 linears in decode order, every weight distinct (2.56 GB in bf16, ten times MI355X's 256 MB
@@ -6,14 +6,19 @@ Infinity Cache, so nothing is served from cache across replays). Weights ~ N(0, 
 ~ N(0, 1) renormalised to unit RMS. The reference measures the same linears one call each inside a CUDA graph
 (byteprof tools/skinny_bench.py:45-71; FINDINGS "OLMo-2 16-block linear set").
 
+The linears of a stage (q|k|v, gate|up) are adjacent rows of one weight allocation, so the set also runs as the 65
+launches a decode step makes (`build_stages`: one skinny launch per stage, each on its own input), with the same
+bytes.
+
 The same independent linears also run as one launch (`group_of`, optim/linear_chain.py): one grid over the row
-blocks of all 113 linears, every output bitwise equal to its own skinny_mm call with the same plan.
+blocks of all 113 linears, every output bitwise equal to its own skinny_mm call with the same waves.
 
 The same linears also run as one dependent launch (`build_chain`, optim/linear_chain.py): stages q|k|v, o,
 gate|up, down per layer and the head, each stage's input the unit-RMS renormalisation of the output it depends on
 in a decode step (o <- v: attention over one cached position returns v; gate|up <- o; down <- up; the next
 layer's q|k|v and the head <- down), or, in the independent variant, a fresh unit-RMS vector per stage with no
-waits.
+waits; and as 65 stream-ordered skinny launches with the same dependencies (`stage_graph_calls`: each launch
+renormalises its producer's output inside the launch).
 
 Used by bench.py and by `python -m byteprof_amd.profiling`.
 """
@@ -154,14 +159,58 @@ class Chain:
 
 
 def make_weights(kind: str = "bf16", device="cuda:0", seed: int = 0, scale_dtype=torch.float16) -> dict:
-    """Seeded weights of the 113 linears, keyed by name (l{layer}.{q,k,v,o,gate,up,down}, lm_head)."""
+    """Seeded weights of the 113 linears, keyed by name (l{layer}.{q,k,v,o,gate,up,down}, lm_head). The linears of
+    one stage are adjacent rows of one allocation, also keyed by the stage (l{layer}.qkv = q|k|v, l{layer}.gateup =
+    gate|up), so a stage can run as one launch; per-row int8 scales make the two views quantise alike."""
     g = torch.Generator(device=device).manual_seed(seed)
     out = {}
-    for name, n, k in shapes():
-        w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
-        out[name] = (w,) if kind == "bf16" else quantize_rowwise_int8(w, scale_dtype)
+
+    def add(key, names_rows, k):
+        w = (torch.randn(sum(n for _, n in names_rows), k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+        full = (w,) if kind == "bf16" else quantize_rowwise_int8(w, scale_dtype)
         del w
+        out[key] = full
+        r = 0
+        for name, n in names_rows:
+            out[name] = tuple(t[r:r + n] for t in full)
+            r += n
+
+    for layer in range(LAYERS):
+        pre = f"l{layer}."
+        for stage, names in LAYER_STAGES:
+            dims = {nm: (n, k) for nm, n, k in LAYER_LINEARS}
+            add(pre + stage, [(pre + nm, dims[nm][0]) for nm in names], dims[names[0]][1])
+    add("lm_head", [("lm_head", VOCAB)], HIDDEN)
     return out
+
+
+def stage_keys() -> list[str]:
+    """Keys of the 65 stages' weights in decode order (make_weights)."""
+    return [f"l{layer}.{stage}" for layer in range(LAYERS) for stage, _ in LAYER_STAGES] + ["lm_head"]
+
+
+def stage_shapes() -> list[tuple[str, int, int]]:
+    """(key, N, K) of the 65 stages in decode order: q|k|v 6144 x 2048, o 2048 x 2048, gate|up 16384 x 2048, down
+    2048 x 8192 per layer, then the LM head."""
+    dims = {nm: (n, k) for nm, n, k in LAYER_LINEARS}
+    out = []
+    for layer in range(LAYERS):
+        for stage, names in LAYER_STAGES:
+            out.append((f"l{layer}.{stage}", sum(dims[nm][0] for nm in names), dims[names[0]][1]))
+    out.append(("lm_head", VOCAB, HIDDEN))
+    return out
+
+
+def build_stages(weights: dict, m: int = 1, device="cuda:0", seed: int = 0) -> list[Op]:
+    """The set as 65 skinny launches, one per stage over the stage's adjacent weight rows (make_weights), each on
+    its own seeded unit-RMS input of m rows: the launches a decode step makes (q|k|v and gate|up share their
+    inputs), with the same bytes as the 113 separate linears."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    ops = []
+    for key, n, k in stage_shapes():
+        x = unit_rms(torch.randn(m, k, generator=g, device=device))
+        ops.append(Op(key, n, k, weights[key], x, torch.empty(m, n, dtype=torch.bfloat16, device=device)))
+    return ops
 
 
 def chain_stages(weights: dict, dependent: bool = True, device="cuda:0", seed: int = 1) -> list:
@@ -222,6 +271,29 @@ def stage_launches(chain: Chain, rb: int = CHAIN_RB, waves: int = CHAIN_WAVES) -
             src = st.src
         out.append(LinearChain([ChainStage(st.weights, src, st.out, st.renorm)], rb=rb, waves=waves))
     return out
+
+
+def stage_graph_calls(chain: Chain) -> list:
+    """The set as 65 stream-ordered launches of the matrix-core skinny kernel, one per stage over the stage's weight
+    rows (q|k|v, o, gate|up, down, the head), each reading its input as `chain` defines it: a dependent stage reads
+    the slice of its producer's output and renormalises it to unit RMS inside the launch (BP_PRO_UNIT_RMS), so the
+    data dependencies of a decode step hold; an independent stage reads its own vector."""
+    calls = []
+    for key, st in zip(stage_keys(), chain.stages):
+        w = chain.weights[key]
+        q, scale = (w[0], None) if len(w) == 1 else w
+        k = int(q.shape[1])
+        if isinstance(st.src, tuple):
+            dep, start = st.src
+            src = chain.stages[dep].out[start:start + k]
+        else:
+            src = st.src
+        x, y = src.view(1, k), st.out.view(1, -1)
+        if st.renorm:
+            calls.append(lambda x=x, q=q, scale=scale, y=y: S.prologue_mm(x, q, scale, y, S.PRO_UNIT_RMS))
+        else:
+            calls.append(lambda x=x, w=w, y=y: S.skinny_mm(x, *w, out=y))
+    return calls
 
 
 def chain_bytes(kind: str) -> int:

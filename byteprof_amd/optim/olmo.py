@@ -1,6 +1,7 @@
-"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 116
-launches for the 16-layer model) captured in one HIP graph, greedy generation with one replay, one pinned
-device-to-host read and one event synchronize per token.
+"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 84
+launches for the 16-layer model: each sublayer norm and residual add runs inside the next linear's launch) captured
+in one HIP graph, greedy generation with one replay, one pinned device-to-host read and one event synchronize per
+token.
 
 Drop-in for the loops of byteprof/optim/olmo.py: `make_generate_graph` (olmo.py:122-219, the manually captured
 graph of the eager forward incl. argmax and next-step inputs) and `make_generate` (olmo.py:51-119, the minimal
@@ -133,6 +134,9 @@ class OlmoDecoder:
         z = lambda *shape, dtype=bf: torch.zeros(*shape, dtype=dtype, device=dev)  # noqa: E731
         self.tok, self.pos = z(1, dtype=torch.int64), z(1, dtype=torch.int64)
         self.x, self.xn, self.attn, self.o, self.dn = z(1, H), z(1, H), z(1, H), z(1, H), z(1, H)
+        self.h = z(1, H)  # the residual stream after the attention half of a layer (fused-norm step)
+        # the sublayer norms run inside the next linear's launch when its plan keeps whole rows (split 1)
+        self.fuse_norms = all(self._plan(n, H, 1)[2] == 1 for n in (3 * H, 2 * F, V))
         self.qkv, self.gu, self.act, self.logits = z(1, 3 * H), z(1, 2 * F), z(1, F), z(1, V)
         # the argmax's partials and counter: zeroed once, left at zero by every launch
         self.argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_scratch_bytes() // 4), dtype=torch.int32)
@@ -145,6 +149,51 @@ class OlmoDecoder:
 
     def step(self) -> None:
         """Logits of token tok at position pos; then tok <- argmax, pos <- pos + 1 (all on the device)."""
+        if self.fuse_norms:
+            self._step_fused()
+        else:
+            self._step_separate()
+
+    def _step_fused(self) -> None:
+        """The step with each sublayer norm and residual add inside the next linear's launch (bp_skinny_mf_pro,
+        BP_PRO_NORM: the norm kernel's arithmetic, so the tokens are those of the separate-norm step): q|k|v of
+        layer l > 0 reads down_{l-1} and writes the residual stream x_l; gate|up reads o and writes h_l = x_l +
+        norm(o); the last layer's post-feed-forward norm is one launch, and the final norm runs inside the LM head.
+        x and h alternate, so no launch reads what it writes."""
+        cfg, L = self.cfg, _lib.lib()
+        H, D = cfg.hidden, cfg.head_dim
+        st = _lib.stream_ptr(self.device)
+        c = _lib.check
+        c(L.bp_decode_embed(self.tok.data_ptr(), self.embed.data_ptr(), self.x.data_ptr(), H, cfg.vocab, st),
+          "bp_decode_embed")
+        for i, w in enumerate(self.layers):
+            kc, vc = self.k_cache[i], self.v_cache[i]
+            if i == 0:
+                self._mm(self.x, w["qkv"], self.qkv)
+            else:
+                self._pro_mm(self.dn, w["qkv"], self.qkv, self.layers[i - 1]["post_ff"], self.h, self.x)
+            c(L.bp_decode_rope_attention(self.qkv.data_ptr(), w["q_norm"].data_ptr(), w["k_norm"].data_ptr(),
+                                         self.inv_freq.data_ptr(), self.pos.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                         self.attn.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, self.scale, st),
+              "bp_decode_rope_attention")
+            self._mm(self.attn, w["o"], self.o)
+            self._pro_mm(self.o, w["gate_up"], self.act, w["post_attn"], self.x, self.h, silu=True)
+            self._mm(self.act, w["down"], self.dn)
+        c(L.bp_decode_norm_residual(self.dn.data_ptr(), self.layers[-1]["post_ff"].data_ptr(), self.h.data_ptr(),
+                                    self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")
+        self._pro_mm(self.x, self.lm_head, self.logits, self.norm, None, None)
+        c(L.bp_decode_argmax_next(self.logits.data_ptr(), cfg.vocab, self.tok.data_ptr(), self.pos.data_ptr(),
+                                  self.argmax_scratch.data_ptr(), st), "bp_decode_argmax_next")
+
+    def _pro_mm(self, x: torch.Tensor, args: tuple, out: torch.Tensor, gamma: torch.Tensor,
+                residual: torch.Tensor | None, xout: torch.Tensor | None, silu: bool = False) -> None:
+        """out = linear(bf16(residual + bf16(gamma * rmsnorm(x)))) in one launch; xout receives the normalised
+        rows (the new residual stream)."""
+        S.prologue_mm(x, args[0], args[1] if len(args) > 1 else None, out, S.PRO_NORM, gamma=gamma,
+                      residual=residual, xout=xout, eps=self.cfg.eps, silu=silu)
+
+    def _step_separate(self) -> None:
+        """The step with a norm launch after o and after down (plans that split K)."""
         cfg, L = self.cfg, _lib.lib()
         H, D = cfg.hidden, cfg.head_dim
         st = _lib.stream_ptr(self.device)
@@ -192,9 +241,13 @@ class OlmoDecoder:
 
     @property
     def launches_per_step(self) -> int:
-        """Kernel launches of one step: embed, 7 per layer (+1 per split-K linear), final norm, LM head, argmax."""
+        """Kernel launches of one step. Fused norms: embed, 5 per layer (q|k|v, RoPE + attention, o, gate|up,
+        down; + 1 per split-K o or down), the last layer's norm, the LM head, argmax. Separate norms: embed, 7 per
+        layer (+1 per split-K linear), final norm, LM head, argmax."""
         H, F, V = self.cfg.hidden, self.cfg.ffn, self.cfg.vocab
         extra = lambda n, k: int(self._plan(n, k, 1)[2] > 1)  # noqa: E731  (the split reduce)
+        if self.fuse_norms:
+            return 4 + (5 + extra(H, H) + extra(H, F)) * self.cfg.layers
         per_layer = 7 + extra(3 * H, H) + extra(H, H) + extra(H, F) + 2 * extra(2 * F, H)
         return 4 + per_layer * self.cfg.layers + extra(V, H)
 

@@ -1,6 +1,8 @@
 """Short GPU programs to run under rocprofv3 (kernel trace, HBM counters).
 
-  python -m byteprof_amd.profiling set  [--kind bf16|int8] [--replays R]   the decode-step set graph, R replays
+  python -m byteprof_amd.profiling set  [--kind bf16|int8] [--replays R]   the decode-step set as its 65 stage
+                                                                         launches in one graph, R replays
+  python -m byteprof_amd.profiling set113 [--kind bf16|int8] [--replays R] the same as 113 launches (one per linear)
   python -m byteprof_amd.profiling chain [--kind bf16|int8] [--dependent] [--replays R]
                                                                          the set as one launch (independent linears,
                                                                          or the dependent stages), R launches
@@ -129,12 +131,13 @@ def summarize(a) -> int:
 
 
 def _set_launches(kind: str) -> dict[tuple[str, str], int]:
-    """(kernel instantiation, 'NxK') -> grid threads of the decode-step set's launches at M = 1."""
+    """(kernel instantiation, 'NxK') -> grid threads of the decode-step set's launches at M = 1 (the 65 stage
+    launches and the 113 per-linear launches)."""
     from . import decode_set as D
     from .optim import skinny as S
 
     out = {}
-    for _, n, k in D.shapes():
+    for _, n, k in D.shapes() + D.stage_shapes():
         rb, waves, split, _ = S._resolve(kind, n, k, 1, None)
         grid = -(-n // (8 * rb)) * waves * 64 * split
         out[(D.kernel_key(kind, n, k, 1), f"{n}x{k}")] = grid
@@ -143,7 +146,7 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=("set", "chain", "stages", "decode", "skinny", "copy", "summarize"))
+    ap.add_argument("what", choices=("set", "set113", "chain", "stages", "decode", "skinny", "copy", "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
     ap.add_argument("--write", help="summarize: WRITE_SIZE database of the workload")
@@ -241,7 +244,8 @@ def main(argv=None) -> int:
             torch.cuda.synchronize()
             print(f"drafting loop: {stats.dump()}", flush=True)
         return 0
-    ops = D.build(a.kind, 1, device)
+    weights = D.make_weights(a.kind, device)
+    ops = D.build_stages(weights, 1, device) if a.what == "set" else D.build(a.kind, 1, device, weights=weights)
     g = D.capture(ops)
     for _ in range(a.replays):
         g.replay()

@@ -85,6 +85,33 @@ int bp_skinny_mf_silu(int wkind, const void* x, const void* w, const void* scale
                       int64_t M, int64_t ffn, int64_t K, int rb, int waves, int xstage, void* stream);
 
 /*
+ * bp_skinny_mf with a transform of the activation rows first (split 1, K a multiple of the segment, 16-byte aligned
+ * x and w, and the rows staged in LDS in one pass: M x K <= 32 x 64 x waves elements, e.g. one row of 2048 at any
+ * waves, one row of 8192 at 4 or 8 waves): the matmul reads
+ *   BP_PRO_UNIT_RMS: bf16(x * (1 / sqrt(mean(x^2)))) per row (an all-zero row as is): a decode step's renormalised
+ *                    input of the next linear;
+ *   BP_PRO_NORM:     bf16(residual + bf16(gamma * (x * (1 / sqrt(mean(x^2) + eps))))) per row (residual NULL: the
+ *                    plain norm), bit for bit bp_decode_norm_residual's output (its summation order), so that the
+ *                    norm of a sublayer's output and the residual add run inside the next linear;
+ * and when xout is not NULL the transformed rows [M, K] are written there (by one workgroup; xout must not overlap
+ * x or residual). gamma, residual and xout 16-byte aligned. epilogue 0: y [M, N] = the plain product; 1: the gate|up SiLU product of bp_skinny_mf_silu, y
+ * [M, N] with w [2 N, K] interleaved.
+ * Replaces: RMSNorm / residual add before the next linear in the decode step (HF Olmo2DecoderLayer, post-attention
+ *           and post-feed-forward norms) followed by the linear's skinny_mm call (byteprof/optim/olmo.py:164-215).
+ */
+#define BP_PRO_UNIT_RMS 1
+#define BP_PRO_NORM 2
+typedef struct BpPrologue {
+  int32_t kind;          /* BP_PRO_UNIT_RMS or BP_PRO_NORM */
+  float eps;             /* BP_PRO_NORM: added to the mean square inside the root */
+  const void* gamma;     /* BP_PRO_NORM: bf16 [K] */
+  const void* residual;  /* BP_PRO_NORM: bf16 [M, K], or NULL */
+  void* xout;            /* bf16 [M, K], or NULL */
+} BpPrologue;
+int bp_skinny_mf_pro(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y, int64_t M,
+                     int64_t N, int64_t K, int rb, int waves, int epilogue, const BpPrologue* prologue, void* stream);
+
+/*
  * The decode-step linear set in one launch of the skinny matrix-core kernel (M = 1): a grid over row blocks of a
  * list of linears ("items", in stage order), each workgroup owning 8 rb rows of one item.
  *   independent (dependent = 0): each item reads its own input x[K] -- the reference's set benchmark, where every

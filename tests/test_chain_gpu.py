@@ -166,16 +166,9 @@ def test_graph_replays_match_eager_and_new_inputs_reach_every_stage():
     assert not ch.timed_out()
 
 
-@pytest.mark.parametrize("kind", ["bf16", "int8"])
-@pytest.mark.parametrize("dependent", [True, False])
-def test_full_decode_step_set(kind, dependent):
-    print(f"\n[chain] decode-step set {kind} dependent={dependent}", flush=True)
-    weights = D.make_weights(kind, DEV, seed=0)
-    chain = D.build_chain(kind, DEV, weights=weights, dependent=dependent)
-    for _ in range(2):
-        chain.lset.run()
-    torch.cuda.synchronize()
-    assert not chain.lset.timed_out()
+def _check_decode_stages(chain):
+    """Every stage's outputs against the fp32 product of its input as the chain defines it (the renormalised slice
+    of its producer's actual output, or its own vector)."""
     for i, st in enumerate(chain.stages):
         k = int((st.weights[0][0] if isinstance(st.weights[0], tuple) else st.weights[0]).shape[1])
         if isinstance(st.src, tuple):
@@ -192,3 +185,40 @@ def test_full_decode_step_set(kind, dependent):
         norm = float((st.out[None].float() - ref).abs().max() / ref.abs().max())
         assert comp < 4e-3 and norm < 1e-2, (i, comp, norm)
         del w32
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("dependent", [True, False])
+def test_full_decode_step_set(kind, dependent):
+    print(f"\n[chain] decode-step set {kind} dependent={dependent}", flush=True)
+    weights = D.make_weights(kind, DEV, seed=0)
+    chain = D.build_chain(kind, DEV, weights=weights, dependent=dependent)
+    for _ in range(2):
+        chain.lset.run()
+    torch.cuda.synchronize()
+    assert not chain.lset.timed_out()
+    _check_decode_stages(chain)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_stage_graph_of_skinny_launches(kind):
+    """The dependent set as 65 stream-ordered skinny launches (one per stage over its adjacent weight rows, the
+    renormalisation inside the launch), eager and replayed from a HIP graph: every stage within the gates of its
+    input; replays equal the eager pass."""
+    print(f"\n[chain] stage graph of skinny launches {kind}", flush=True)
+    weights = D.make_weights(kind, DEV, seed=0)
+    chain = D.build_chain(kind, DEV, weights=weights, dependent=True)
+    calls = D.stage_graph_calls(chain)
+    assert len(calls) == 65
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    _check_decode_stages(chain)
+    eager = [st.out.clone() for st in chain.stages]
+    g = D.capture(calls)
+    for _ in range(3):
+        for st in chain.stages:
+            st.out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, st.out) for a, st in zip(eager, chain.stages))

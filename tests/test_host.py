@@ -366,3 +366,20 @@ def test_drafting_host_logic_matches_the_reference_definitions():
     with pytest.raises(ValueError):
         OD.OracleDrafter().reset([1], None)
     assert OD.NullDrafter().propose(4) == []
+
+
+def test_decode_stages_cover_the_linears():
+    """The 65 stages are the 113 linears grouped by shared input (q|k|v, o, gate|up, down per layer, the head), in
+    decode order, with the same bytes."""
+    from byteprof_amd import decode_set as D
+
+    stages = D.stage_shapes()
+    assert len(stages) == 65 and [key for key, _, _ in stages] == D.stage_keys()
+    assert stages[:4] == [("l0.qkv", 6144, 2048), ("l0.o", 2048, 2048), ("l0.gateup", 16384, 2048),
+                          ("l0.down", 2048, 8192)]
+    assert stages[-1] == ("lm_head", 100352, 2048)
+    assert sum(n * k for _, n, k in stages) == sum(n * k for _, n, k in D.shapes())
+    # algorithmic bytes of the 65 launches: weights (+ scales) once, inputs once per stage, outputs once
+    stage_bytes = sum(A.call_bytes(A.Linear(n, k), None, 1) for _, n, k in stages)
+    fewer_inputs = 2 * (2 * 2048 + 2048) * 16  # q|k|v read one input instead of three, gate|up one instead of two
+    assert stage_bytes == D.chain_bytes("bf16") - fewer_inputs

@@ -359,3 +359,27 @@ def test_graph_loop_equals_the_eager_loop_olmo2_1b(kind):
     assert len(set(a[0, 8:].tolist())) > 1
     del dec
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_fused_norm_step_equals_the_separate_norm_step(kind):
+    """The step with the sublayer norms inside the next linears (84 launches) gives the logits and tokens of the
+    step with separate norm launches (116 launches), bit for bit, step after step."""
+    cfg = OG.OLMO2_1B
+    print(f"\n[olmo] fused norms {kind}", flush=True)
+    dec = OG.OlmoDecoder(cfg, OG.random_weights(cfg, DEV, seed=4), kind)
+    assert dec.fuse_norms and dec.launches_per_step == 84
+    runs = {}
+    for fused in (True, False):
+        dec.fuse_norms = fused
+        dec.pos.zero_()
+        out = []
+        for t in (11, 2027, 5, 99999, 42, 3, 3, 1000):
+            dec.tok.fill_(t)
+            dec.step()
+            out.append((dec.logits.clone(), int(dec.tok)))
+        runs[fused] = out
+    for (la, ta), (lb, tb) in zip(runs[True], runs[False]):
+        assert ta == tb and torch.equal(la, lb)
+    del dec
+    torch.cuda.empty_cache()

@@ -1,0 +1,142 @@
+"""GPU parity of the activation prologue of the matrix-core skinny kernel (bp_skinny_mf_pro, skinny.prologue_mm).
+
+  - BP_PRO_NORM equals the separate decode norm launch (bp_decode_norm_residual[_rows]: bf16(residual + bf16(gamma *
+    rmsnorm(x)))) followed by the plain skinny launch, bit for bit, for the transformed rows (xout) and for the
+    products, with and without a residual, at 1, 2 and 3 rows, bf16 and int8 weights, plain and SiLU epilogues;
+  - BP_PRO_UNIT_RMS: the transformed rows are the oracle's unit-RMS renormalisation (oracle.linear_set.unit_rms,
+    float64) within one bf16 rounding, and the products equal skinny_mm of those rows bit for bit and the oracle
+    within the skinny gates;
+  - launches that cannot stage their whole rows in one pass (more than 16 rows, more rows than 4 x 8 elements per
+    thread, K not a multiple of the segment, unaligned rows) are refused before anything runs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from byteprof_amd import _lib
+from byteprof_amd.optim import skinny as S
+from byteprof_amd.quant.hip_int8 import quantize_rowwise_int8
+from oracle import linear_set as OL
+from tests.helpers import check_against_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _gen(seed):
+    return torch.Generator(device=DEV).manual_seed(seed)
+
+
+def _norm_rows(x, gamma, residual, eps):
+    """The separate decode norm launch over the rows of x."""
+    L = _lib.lib()
+    out = torch.empty_like(x)
+    rows, n = x.shape
+    rc = L.bp_decode_norm_residual_rows(x.data_ptr(), gamma.data_ptr(), _lib.ptr(residual), out.data_ptr(), n, eps,
+                                        rows, _lib.stream_ptr(x.device))
+    _lib.check(rc, "bp_decode_norm_residual_rows")
+    return out
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_norm_prologue_equals_norm_launch_then_skinny(kind, m, with_residual):
+    g = _gen(10 + m)
+    n, k, eps = 2048, 2048, 1e-6
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    args = (w, None) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
+    x = (torch.randn(m, k, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
+    gamma = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    res = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16) if with_residual else None
+    xn = _norm_rows(x, gamma, res, eps)
+    want = S.skinny_mm(xn, *[a for a in args if a is not None])
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    xout = torch.empty(m, k, dtype=torch.bfloat16, device=DEV)
+    S.prologue_mm(x, args[0], args[1], out, S.PRO_NORM, gamma=gamma, residual=res, xout=xout, eps=eps)
+    torch.cuda.synchronize()
+    assert torch.equal(xout, xn)
+    assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_norm_prologue_with_the_silu_epilogue(kind):
+    """The fused norm before the interleaved gate|up projection equals norm launch + bp_skinny_mf_silu."""
+    g = _gen(20)
+    f, k, eps = 8192, 2048, 1e-6
+    w = (torch.randn(2 * f, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    args = (w, None) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
+    x = torch.randn(1, k, generator=g, device=DEV).to(torch.bfloat16)
+    gamma = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    res = torch.randn(1, k, generator=g, device=DEV).to(torch.bfloat16)
+    xn = _norm_rows(x, gamma, res, eps)
+    rb, waves, split, xs = S._resolve(kind, 2 * f, k, 1, None)
+    assert split == 1
+    want = torch.empty(1, f, dtype=torch.bfloat16, device=DEV)
+    L = _lib.lib()
+    sc, sdt = (args[1].data_ptr(), _lib.TORCH_DT[args[1].dtype]) if kind == "int8" else (None, 0)
+    _lib.check(L.bp_skinny_mf_silu(S._KIND_CODE[kind], xn.data_ptr(), args[0].data_ptr(), sc, sdt, want.data_ptr(), 1,
+                                   f, k, rb, waves, xs, _lib.stream_ptr(x.device)), "bp_skinny_mf_silu")
+    out = torch.empty(1, f, dtype=torch.bfloat16, device=DEV)
+    S.prologue_mm(x, args[0], args[1], out, S.PRO_NORM, gamma=gamma, residual=res, eps=eps, silu=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("n,k", [(2048, 2048), (6144, 2048), (2048, 8192), (100352, 2048)])
+def test_unit_rms_prologue_matches_the_oracle(kind, n, k):
+    g = _gen(30)
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    args = (w, None) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
+    x = (torch.randn(1, k, generator=g, device=DEV) * 7.0).to(torch.bfloat16)
+    out = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    xout = torch.empty(1, k, dtype=torch.bfloat16, device=DEV)
+    S.prologue_mm(x, args[0], args[1], out, S.PRO_UNIT_RMS, xout=xout)
+    torch.cuda.synchronize()
+    want_x = OL.unit_rms(x.float().cpu().numpy()[0])
+    got_x = xout.float().cpu().numpy()[0]
+    # within one bf16 rounding of the float64 renormalisation
+    assert np.all(np.abs(got_x - want_x) <= np.abs(want_x) * 2.0 ** -7 + 1e-30)
+    assert torch.equal(out, S.skinny_mm(xout, *[a for a in args if a is not None]))
+    wo = w.float().cpu().numpy() if kind == "bf16" else (args[0].float() * args[1].float()[:, None]).cpu().numpy()
+    check_against_oracle(out, xout, wo)
+
+
+def test_unit_rms_of_a_zero_row_is_the_row():
+    w = torch.ones(2048, 2048, dtype=torch.bfloat16, device=DEV)
+    x = torch.zeros(1, 2048, dtype=torch.bfloat16, device=DEV)
+    out = torch.full((1, 2048), 5.0, dtype=torch.bfloat16, device=DEV)
+    S.prologue_mm(x, w, None, out, S.PRO_UNIT_RMS)
+    torch.cuda.synchronize()
+    assert not out.any()
+    with pytest.raises(ValueError):  # a plan that splits K cannot renormalise whole rows
+        S.prologue_mm(x, w[:64], None, out[:, :64], S.PRO_UNIT_RMS, cfg=(8, 4, 2))
+
+
+def test_prologue_refusals():
+    L = _lib.lib()
+    w = torch.zeros(64, 2048, dtype=torch.bfloat16, device=DEV)
+    x = torch.zeros(17, 2048, dtype=torch.bfloat16, device=DEV)
+    y = torch.empty(17, 64, dtype=torch.bfloat16, device=DEV)
+    st = _lib.stream_ptr(x.device)
+
+    def call(pro, m=1, k=2048, xp=None):
+        return L.bp_skinny_mf_pro(0, xp or x.data_ptr(), w.data_ptr(), None, 0, y.data_ptr(), m, 64, k, 1, 4, 0, pro, st)
+
+    import ctypes
+    assert call(None) == -1
+    assert call(ctypes.byref(S.BpPrologue(3, 0.0, None, None, None))) == -1       # unknown kind
+    assert call(ctypes.byref(S.BpPrologue(2, 0.0, None, None, None))) == -1       # norm without gamma
+    unit = ctypes.byref(S.BpPrologue(1, 0.0, None, None, None))
+    assert call(unit, m=17) == -2                                                   # more than 16 rows
+    assert call(unit, m=16) == -2                                                   # 16 x 2048 rows: 64 KiB of LDS
+    assert call(unit, m=8) == -2                                                    # 8 x 2048: two staging passes
+    assert call(unit, k=2000) == -2                                                 # K not a multiple of the segment
+    assert call(unit, xp=x.data_ptr() + 2) == -2                                    # unaligned rows
+    g = torch.ones(2050, dtype=torch.bfloat16, device=DEV)
+    assert call(ctypes.byref(S.BpPrologue(2, 1e-6, g.data_ptr() + 2, None, None))) == -1  # unaligned gamma
+    torch.cuda.synchronize()
