@@ -55,6 +55,52 @@ __device__ __forceinline__ gptr<T> as_global_mut(T* p) {
   return (gptr<T>)(p);
 }
 
+// Sum of squares of n values (read through at(i)) in a fixed order that one 64-lane wave computes alone: lane l adds,
+// in order, the squares of elements 256 j + 4 l + e (j = 0, 1, ...; e = 0 .. 3; elements past n left out), then
+// the lanes are added by an xor butterfly (lane distance 32, 16, ..., 1). Every lane of every wave that runs it
+// gets the same total, so the RMS norms of the decode step (separate or inside a linear's launch) and the
+// renormalisations of the linear set agree bit for bit whatever their workgroup shapes.
+template <class At>
+__device__ __forceinline__ float wave_sumsq(const At& at, int n) {
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  float s = 0.f;
+  for (int base = 4 * lane; base < n; base += 256) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (base + e < n) {
+        const float f = at(base + e);
+        s += f * f;
+      }
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  return s;
+}
+
+// wave_sumsq of a bf16 row in LDS (8-byte aligned), four elements per read: the same additions in the same order.
+__device__ __forceinline__ float wave_sumsq_lds(const uint16_t* row, int n) {
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  float s = 0.f;
+  for (int base = 4 * lane; base < n; base += 256) {
+    if (base + 4 <= n) {
+      const uint2 q = *reinterpret_cast<const uint2*>(row + base);
+      const float f0 = __uint_as_float(q.x << 16), f1 = __uint_as_float(q.x & 0xffff0000u);
+      const float f2 = __uint_as_float(q.y << 16), f3 = __uint_as_float(q.y & 0xffff0000u);
+      s += f0 * f0;
+      s += f1 * f1;
+      s += f2 * f2;
+      s += f3 * f3;
+    } else {
+      for (int e = 0; base + e < n; ++e) {
+        const float f = bf16_bits_to_float(row[base + e]);
+        s += f * f;
+      }
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  return s;
+}
+
 __device__ __forceinline__ float load_scale(const void* p, int64_t i, int dt) {
   if (dt == 0) return bf16_bits_to_float(as_global(static_cast<const uint16_t*>(p))[i]);
   if (dt == 1) return static_cast<float>(as_global(static_cast<const _Float16*>(p))[i]);

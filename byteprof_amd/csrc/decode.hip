@@ -8,7 +8,8 @@
 //   rope_attention  qk_rope_cache and attention fused, one workgroup per head (the decode loop's path)
 //   attention       per head: s_t = bf16(bf16(q . k_t) * scale) for t <= pos, p = bf16(softmax_fp32(s)),
 //                   out = bf16(sum_t p_t v_t)
-//   norm_residual   out <- bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))) (no residual: the plain norm)
+//   norm_residual   out <- bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))) (no residual: the plain norm;
+//                   the mean square in wave_sumsq's order, common.h)
 //   silu_mul        out <- bf16(bf16(silu(g)) * u), g and u the two halves of the fused gate|up projection
 //   argmax_next     tok <- first index of the largest logit (NaN counts as largest); pos <- pos + 1
 //
@@ -621,96 +622,52 @@ void launch_rope_attention(const void* qkv, const void* qw, const void* kw, cons
   }
 }
 
-constexpr int kNormPer = 8;  // elements per thread kept in registers by norm_residual (n <= kBlock * kNormPer)
+constexpr int kNormMax = 16384;  // elements of one norm row (its bf16 copy in LDS: 32 KiB)
 
-// grid = rows, one workgroup per row of x / residual / out [rows, n]. For n <= kBlock * kNormPer, x, the weight
-// and the residual are loaded once, together, before the reduction (one round trip to memory); longer vectors take
-// a second pass over memory.
-__global__ __launch_bounds__(kBlock) void norm_residual_kernel(const uint16_t* __restrict__ x,
-                                                               const uint16_t* __restrict__ w,
-                                                               const uint16_t* residual, uint16_t* out, int n,
-                                                               float eps) {
-  __shared__ float red[kBlock / kWave];
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * n;
-  x += row;
-  out += row;
-  if (residual != nullptr) residual += row;
-  if (n <= static_cast<int>(blockDim.x) * kNormPer) {
-    float xv[kNormPer], wv[kNormPer], rv[kNormPer];
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < kNormPer; ++e) {
-      const int i = threadIdx.x + e * blockDim.x;
-      xv[e] = wv[e] = rv[e] = 0.f;
-      if (i < n) {
-        xv[e] = ld_bf16(x, i);
-        wv[e] = ld_bf16(w, i);
-        if (residual != nullptr) rv[e] = ld_bf16(residual, i);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < kNormPer; ++e) ss += xv[e] * xv[e];
-    const float r = 1.f / sqrtf(block_sum(ss, red) / static_cast<float>(n) + eps);
-#pragma unroll
-    for (int e = 0; e < kNormPer; ++e) {
-      const int i = threadIdx.x + e * blockDim.x;
-      if (i < n) {
-        const float y = round_to_bf16(wv[e] * (xv[e] * r));
-        out[i] = float_to_bf16_bits(residual != nullptr ? rv[e] + y : y);
-      }
-    }
-    return;
-  }
-  float ss = 0.f;
+// The row x (bf16 values in LDS) normalised: out = bf16(residual + bf16(w * (x * r))), r = 1 / sqrt(mean(x^2) +
+// eps), the mean square in wave_sumsq's order (every wave computes it).
+__device__ __forceinline__ void norm_row_out(const uint16_t* xs, const uint16_t* __restrict__ w,
+                                             const uint16_t* residual, uint16_t* out, int n, float eps) {
+  const float ss = wave_sumsq_lds(xs, n);
+  const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float v = ld_bf16(x, i);
-    ss += v * v;
-  }
-  const float r = 1.f / sqrtf(block_sum(ss, red) / static_cast<float>(n) + eps);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float y = round_to_bf16(ld_bf16(w, i) * (ld_bf16(x, i) * r));
+    const float y = round_to_bf16(ld_bf16(w, i) * (bf16_bits_to_float(xs[i]) * r));
     out[i] = float_to_bf16_bits(residual != nullptr ? ld_bf16(residual, i) + y : y);
   }
 }
 
+// grid = rows, one workgroup per row of x / residual / out [rows, n], n <= kNormMax; out may alias residual.
+__global__ __launch_bounds__(kBlock) void norm_residual_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ w,
+                                                               const uint16_t* residual, uint16_t* out, int n,
+                                                               float eps) {
+  extern __shared__ uint16_t norm_xs[];
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * n;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) norm_xs[i] = x[row + i];
+  __syncthreads();
+  norm_row_out(norm_xs, w, residual != nullptr ? residual + row : nullptr, out + row, n, eps);
+}
+
 // The split-K reduce of a projection's partials (ws [split][rows][n], added in split order, the int8 scale applied
-// to the sum, rounded to bf16: splitk_reduce_kernel's arithmetic) feeding norm_residual_kernel's register path in the
-// same workgroup (grid = rows, n <= kBlock * kNormPer): out = bf16(residual + bf16(w * y * rsqrt(mean(y^2) + eps))),
-// equal bit for bit to the two launches; out may alias residual.
+// to the sum, rounded to bf16: splitk_reduce_kernel's arithmetic) feeding norm_residual_kernel's arithmetic in the
+// same workgroup (grid = rows, n <= kNormMax): out = bf16(residual + bf16(w * y * rsqrt(mean(y^2) + eps))), equal
+// bit for bit to the two launches; out may alias residual.
 __global__ __launch_bounds__(kBlock) void splitk_norm_residual_kernel(const float* __restrict__ ws, int split,
                                                                       const void* __restrict__ scale, int scale_dt,
                                                                       const uint16_t* __restrict__ w,
                                                                       const uint16_t* residual, uint16_t* out, int n,
                                                                       float eps) {
-  __shared__ float red[kBlock / kWave];
+  extern __shared__ uint16_t norm_xs[];
   const int64_t total = static_cast<int64_t>(gridDim.x) * n;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * n;
-  float xv[kNormPer], wv[kNormPer], rv[kNormPer];
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < kNormPer; ++e) {
-    const int i = threadIdx.x + e * blockDim.x;
-    xv[e] = wv[e] = rv[e] = 0.f;
-    if (i < n) {
-      float t = ws[row + i];
-      for (int s = 1; s < split; ++s) t += ws[s * total + row + i];
-      if (scale != nullptr) t *= load_scale(scale, i, scale_dt);
-      xv[e] = round_to_bf16(t);
-      wv[e] = ld_bf16(w, i);
-      if (residual != nullptr) rv[e] = ld_bf16(residual, row + i);
-    }
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    float t = ws[row + i];
+    for (int s = 1; s < split; ++s) t += ws[s * total + row + i];
+    if (scale != nullptr) t *= load_scale(scale, i, scale_dt);
+    norm_xs[i] = float_to_bf16_bits(t);
   }
-#pragma unroll
-  for (int e = 0; e < kNormPer; ++e) ss += xv[e] * xv[e];
-  const float r = 1.f / sqrtf(block_sum(ss, red) / static_cast<float>(n) + eps);
-#pragma unroll
-  for (int e = 0; e < kNormPer; ++e) {
-    const int i = threadIdx.x + e * blockDim.x;
-    if (i < n) {
-      const float y = round_to_bf16(wv[e] * (xv[e] * r));
-      out[row + i] = float_to_bf16_bits(residual != nullptr ? rv[e] + y : y);
-    }
-  }
+  __syncthreads();
+  norm_row_out(norm_xs, w, residual != nullptr ? residual + row : nullptr, out + row, n, eps);
 }
 
 // out[r, f] = bf16(bf16(silu(g)) * u) for rows r of gu [rows, 2F]: g = gu[r, f], u = gu[r, F + f] (concatenated
@@ -953,7 +910,8 @@ int bp_decode_rope_attention_rows(const void* qkv, const void* q_norm_w, const v
 int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* residual, void* out, int n,
                                  float eps, int rows, void* stream) {
   if (x == nullptr || weight == nullptr || out == nullptr || n <= 0 || rows <= 0) return BP_E_INVALID_ARG;
-  bp::norm_residual_kernel<<<rows, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+  if (n > bp::kNormMax) return BP_E_UNSUPPORTED;
+  bp::norm_residual_kernel<<<rows, bp::kBlock, static_cast<size_t>(n) * 2, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight),
       static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), n, eps);
   return bp::status();
@@ -965,8 +923,9 @@ int bp_decode_splitk_norm_residual_rows(const float* workspace, int split, const
   if (workspace == nullptr || weight == nullptr || out == nullptr || n <= 0 || rows <= 0 || split < 1)
     return BP_E_INVALID_ARG;
   if (scale != nullptr && (scale_dtype < BP_DT_BF16 || scale_dtype > BP_DT_F32)) return BP_E_INVALID_ARG;
-  if (n > bp::kBlock * bp::kNormPer) return BP_E_UNSUPPORTED;
-  bp::splitk_norm_residual_kernel<<<rows, bp::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+  if (n > bp::kNormMax) return BP_E_UNSUPPORTED;
+  bp::splitk_norm_residual_kernel<<<rows, bp::kBlock, static_cast<size_t>(n) * 2,
+                                    static_cast<hipStream_t>(stream)>>>(
       workspace, split, scale, scale_dtype, static_cast<const uint16_t*>(weight),
       static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), n, eps);
   return bp::status();

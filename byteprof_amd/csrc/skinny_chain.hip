@@ -135,7 +135,6 @@ __device__ __forceinline__ void chain_body(const BpChainItem& it, int b, int sca
   }
 
   auto finish = [&]() {
-    float ss = 0.f;
     uint32_t* xs2 = reinterpret_cast<uint32_t*>(sh.xs);
     if (external) {
       for (int64_t j0 = 0; j0 < units; j0 += kGatherLoads * kT) {
@@ -146,11 +145,6 @@ __device__ __forceinline__ void chain_body(const BpChainItem& it, int b, int sca
           const uint64_t v = j0 == 0 ? pre[u] : src64[j];  // later batches: plain loads (after the weights)
           xs2[2 * j] = static_cast<uint32_t>(v);
           xs2[2 * j + 1] = static_cast<uint32_t>(v >> 32);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float f = bf16_bits_to_float(static_cast<uint32_t>(v >> (16 * e)) & 0xffffu);
-            ss += f * f;
-          }
         }
       }
     } else {
@@ -238,21 +232,14 @@ __device__ __forceinline__ void chain_body(const BpChainItem& it, int b, int sca
             }
           }
           xs2[j] = (w2[0] & 0xffffu) | (w2[1] << 16);
-          const float lo = bf16_bits_to_float(w2[0] & 0xffffu), hi = bf16_bits_to_float(w2[1] & 0xffffu);
-          ss += lo * lo;
-          ss += hi * hi;
         }
       }
     }
     if (it.flags & BP_CHAIN_RENORM) {
-      // fixed order: per thread in index order, the wave by a butterfly, the waves in order
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-      if (lane == 0) sh.ss[wave] = ss;
+      // the mean square in wave_sumsq's order (common.h): the renormalisation of the skinny kernel's prologue
       __syncthreads();
-      float tot = sh.ss[0];
-#pragma unroll
-      for (int v = 1; v < WAVES; ++v) tot += sh.ss[v];
+      const float tot = wave_sumsq_lds(sh.xs, static_cast<int>(K));
+      __syncthreads();  // every wave has read the row before it is rewritten
       const float ms = tot / static_cast<float>(K);
       const float inv = ms > 0.f ? 1.f / sqrtf(ms) : 1.f;
       for (int64_t j = threadIdx.x; j < K; j += kT) sh.xs[j] = float_to_bf16_bits(bf16_bits_to_float(sh.xs[j]) * inv);

@@ -27,50 +27,33 @@ struct MfPro {
   uint16_t* xout;            // [M, K] or null: the transformed rows, written by workgroup (0, 0)
 };
 
-constexpr int kProThreads = 1024;  // the norm kernel's workgroup, whose summation order the prologue reproduces
-constexpr int kProWaves = kProThreads / kWave;
-
 // In place, row by row:
 //   BP_PRO_UNIT_RMS: x <- bf16(x * (1 / sqrt(mean(x^2)))) (an all-zero row is left as is);
 //   BP_PRO_NORM:     x <- bf16(residual + bf16(gamma * (x * (1 / sqrt(mean(x^2) + eps))))) (no residual: the plain
 //                    norm), and workgroup (0, 0) writes the rows to xout.
-// The sum of squares is added in the order of the decode norm kernel (decode.hip, norm_residual_kernel): 1024
-// threads, thread t summing x[t]^2, x[t + 1024]^2, ... in order, each 64-lane wave by an xor butterfly (lane
-// distance 32, 16, ..., 1), the 16 wave totals in order from 0. Here 1024 "virtual threads" do that with any
-// workgroup size, so a fused norm equals the separate norm launch bit for bit.
-// gl (BP_PRO_NORM over one row, else null): LDS copies of gamma [K] and the residual row [K], loaded ahead of the
-// weights.
+// The mean square is wave_sumsq's (common.h), which every wave computes from the staged row, so the fused norm
+// equals the separate norm launch (decode.hip, norm_residual_kernel) bit for bit. gl (BP_PRO_NORM over one row,
+// else null): LDS copies of gamma [K] and the residual row [K], loaded ahead of the weights.
 template <int NT>
-__device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, float* vals, float* parts,
-                            bool writer, const uint16_t* gl) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+__device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, bool writer, const uint16_t* gl) {
   for (int m = 0; m < rows; ++m) {
     uint16_t* row = xs + m * K;
-    for (int v = threadIdx.x; v < kProThreads; v += NT) {
-      float s = 0.f;
-      for (int i = v; i < K; i += kProThreads) {
-        const float f = bf16_bits_to_float(row[i]);
-        s += f * f;
-      }
-      vals[v] = s;
-    }
-    __syncthreads();
-    for (int vw = wave; vw < kProWaves; vw += NT / kWave) {
-      float s = vals[vw * kWave + lane];
-      for (int o = kWave / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
-      if (lane == 0) parts[vw] = s;
-    }
-    __syncthreads();
-    float t = 0.f;
-    for (int i = 0; i < kProWaves; ++i) t += parts[i];
+    const float t = wave_sumsq_lds(row, K);
+    __syncthreads();  // every wave has read the row before it is rewritten
     if (pro.kind == BP_PRO_UNIT_RMS) {
       const float ms = t / static_cast<float>(K);
       const float inv = ms > 0.f ? 1.f / sqrtf(ms) : 1.f;
-      for (int i = threadIdx.x; i < K; i += NT) {
-        const uint16_t v = float_to_bf16_bits(bf16_bits_to_float(row[i]) * inv);
-        row[i] = v;
-        if (writer && pro.xout != nullptr) as_global_mut(pro.xout)[static_cast<int64_t>(m) * K + i] = v;
+      for (int i = 4 * static_cast<int>(threadIdx.x); i < K; i += 4 * NT) {  // K is a multiple of 64
+        const uint2 xq = *reinterpret_cast<const uint2*>(row + i);
+        const uint32_t xw[4] = {xq.x << 16, xq.x & 0xffff0000u, xq.y << 16, xq.y & 0xffff0000u};
+        uint32_t ov[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = float_to_bf16_bits(__uint_as_float(xw[e]) * inv);
+        const uint2 o2{ov[0] | (ov[1] << 16), ov[2] | (ov[3] << 16)};
+        *reinterpret_cast<uint2*>(row + i) = o2;
+        if (writer && pro.xout != nullptr)
+          *as_global_mut(reinterpret_cast<uint64_t*>(pro.xout + static_cast<int64_t>(m) * K + i)) =
+              static_cast<uint64_t>(o2.x) | (static_cast<uint64_t>(o2.y) << 32);
       }
     } else {
       const float r = 1.f / sqrtf(t / static_cast<float>(K) + pro.eps);
@@ -81,9 +64,26 @@ __device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, flo
         row[i] = v;
         if (writer && pro.xout != nullptr) as_global_mut(pro.xout)[static_cast<int64_t>(m) * K + i] = v;
       };
-      if (gl != nullptr) {  // one row, gamma and the residual in LDS
-        for (int i = threadIdx.x; i < K; i += NT)
-          put(i, bf16_bits_to_float(gl[i]), has_res ? bf16_bits_to_float(gl[K + i]) : 0.f);
+      if (gl != nullptr) {  // one row, gamma and the residual in LDS: four elements per thread and step
+        for (int i = 4 * static_cast<int>(threadIdx.x); i < K; i += 4 * NT) {
+          const uint2 xq = *reinterpret_cast<const uint2*>(row + i);
+          const uint2 gq = *reinterpret_cast<const uint2*>(gl + i);
+          const uint2 rq = has_res ? *reinterpret_cast<const uint2*>(gl + K + i) : uint2{0u, 0u};
+          const uint32_t xw[4] = {xq.x << 16, xq.x & 0xffff0000u, xq.y << 16, xq.y & 0xffff0000u};
+          const uint32_t gw[4] = {gq.x << 16, gq.x & 0xffff0000u, gq.y << 16, gq.y & 0xffff0000u};
+          const uint32_t rw[4] = {rq.x << 16, rq.x & 0xffff0000u, rq.y << 16, rq.y & 0xffff0000u};
+          uint32_t ov[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float yv = round_to_bf16(__uint_as_float(gw[e]) * (__uint_as_float(xw[e]) * r));
+            ov[e] = float_to_bf16_bits(has_res ? __uint_as_float(rw[e]) + yv : yv);
+          }
+          const uint2 o2{ov[0] | (ov[1] << 16), ov[2] | (ov[3] << 16)};
+          *reinterpret_cast<uint2*>(row + i) = o2;
+          if (writer && pro.xout != nullptr)
+            *as_global_mut(reinterpret_cast<uint64_t*>(pro.xout + i)) =
+                static_cast<uint64_t>(o2.x) | (static_cast<uint64_t>(o2.y) << 32);
+        }
       } else {
         gptr<const uint16_t> gam = as_global(pro.gamma);
         gptr<const uint16_t> res = has_res ? as_global(pro.residual + static_cast<int64_t>(m) * K) : nullptr;
@@ -153,8 +153,6 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
     stage.issue(x, mrows, K, k_lo, kn, 0);  // ahead of the weight loads: the commit waits for these only
     MfXLds<KIND, MB> xs;
     xs.init(xs_lds, mrows, kn, k_lo, ln);
-    __shared__ float pro_vals[PRO ? kProThreads : 1];
-    __shared__ float pro_parts[PRO ? kProWaves : 1];
     // BP_PRO_NORM over one row: gamma and the residual row straight into LDS after the staged row (64 lanes x 16
     // bytes per load, no registers held), ahead of the weight loads
     const uint16_t* gl = nullptr;
@@ -184,7 +182,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
       if constexpr (PRO) {
         __syncthreads();
         if (pro.kind != 0)
-          mf_prologue<kNT>(xs_lds, mrows, kn, pro, pro_vals, pro_parts, blockIdx.x == 0 && blockIdx.y == 0, gl);
+          mf_prologue<kNT>(xs_lds, mrows, kn, pro, blockIdx.x == 0 && blockIdx.y == 0, gl);
       } else {
         for (int pass = 1; pass < passes; ++pass) {
           stage.issue(x, mrows, K, k_lo, kn, pass);

@@ -270,10 +270,12 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  *                 two launches; qkv 16-byte aligned. rope_attention_rows: rows (<= 16) consecutive positions
  *                 *pos .. *pos + rows - 1 (>= 0) in one launch (one workgroup per head and row), equal bit for bit
  *                 to qk_rope_cache_rows + attention_rows.
- * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))); residual NULL: the plain norm;
+ * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))), the mean square summed in one fixed
+ *                 order (lane l of a 64-lane wave adds the squares of elements 256 j + 4 l + e in order, then an xor
+ *                 butterfly over the lanes; bp_skinny_mf_pro uses the same); residual NULL: the plain norm;
  *                 out may alias residual. splitk_norm_residual_rows: x = the split-K reduce of a projection's
  *                 partials (workspace [split][rows][n] from bp_skinny_mf_partials, the int8 scale [n] applied,
- *                 NULL for bf16), equal bit for bit to bp_splitk_reduce + norm_residual_rows; n <= 8192.
+ *                 NULL for bf16), equal bit for bit to bp_splitk_reduce + norm_residual_rows; n <= 16384.
  * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn); silu_mul_rows with
  *                 interleaved = 1 reads the pairs (gate_up[2f], gate_up[2f + 1]) instead.
  * argmax_next:    *tok = first index of the largest logit (NaN counts as largest); *pos += 1. Several workgroups
