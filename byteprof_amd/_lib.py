@@ -40,6 +40,9 @@ SIGNATURES: dict[str, tuple] = {
                                        _c_vp, _c_size, _c_vp]),
     "bp_skinny_mf_silu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                    _c_int, _c_vp]),
+    "bp_skinny_mf_static_bytes": (_c_size, []),
+    "bp_skinny_mf_static": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                     _c_int, _c_int, _c_vp]),
     "bp_skinny_mf_pro": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                   _c_int, _c_vp, _c_vp]),
     "bp_chain_supported": (_c_int, [_c_int, _c_int, _c_int]),

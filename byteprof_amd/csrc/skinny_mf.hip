@@ -6,6 +6,7 @@
 // (skinny.py:136-166).
 
 #include <algorithm>
+#include <mutex>
 
 #include "byteprof_amd.h"
 #include "skinny_mf.h"
@@ -421,10 +422,51 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
                               wkind == kInt8 ? scale : nullptr, scale_dt, M, N, split, st);
 }
 
+// The split-K partials of bp_skinny_mf_static: a fixed device array instead of a caller's workspace. Each GPU the
+// library runs on holds its own copy until the process ends; host code uses the per-device address from
+// hipGetSymbolAddress (static_scratch), never the array's name.
+constexpr size_t kStaticScratchBytes = size_t{8} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device (resolved once per device), or null on error.
+void* static_scratch() {
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
 }  // namespace
 }  // namespace bp
 
 extern "C" {
+
+size_t bp_skinny_mf_static_bytes(void) { return bp::kStaticScratchBytes; }
+
+int bp_skinny_mf_static(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y,
+                        int64_t M, int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* stream) {
+  if (M < 0 || N < 0 || split < 1) return BP_E_INVALID_ARG;
+  if (split > 1 && M > 0 && N > 0 &&
+      static_cast<double>(split) * static_cast<double>(M) * static_cast<double>(N) * sizeof(float) >
+          static_cast<double>(bp::kStaticScratchBytes))
+    return BP_E_WORKSPACE;
+  void* ws = nullptr;
+  if (split > 1) {
+    ws = bp::static_scratch();
+    if (ws == nullptr) return static_cast<int>(hipErrorInvalidSymbol);
+  }
+  return bp::mf_launch(wkind, x, w, scale, scale_dtype, y, M, N, K, rb, waves, split, xstage, ws,
+                       split > 1 ? bp::kStaticScratchBytes : 0, stream, 0);
+}
 
 int bp_skinny_mf_supported(int wkind, int M, int rb, int waves, int xstage) {
   if (M < 1 || M > 64) return 0;

@@ -85,6 +85,18 @@ int bp_skinny_mf_silu(int wkind, const void* x, const void* w, const void* scale
                       int64_t M, int64_t ffn, int64_t K, int rb, int waves, int xstage, void* stream);
 
 /*
+ * bp_skinny_mf without a caller workspace and without allocating: the split-K partials go to a fixed device array
+ * of bp_skinny_mf_static_bytes() bytes (8 MiB) inside the library, one per GPU, held until the process ends.
+ * split x M x N x 4 must fit it (else BP_E_WORKSPACE before anything runs); calls that overlap on one GPU share the
+ * array and race (order them on one stream). No counterpart in the reference (whose skinny_mm allocates the
+ * workspace per call): for callers that cannot allocate device memory, such as code under HIP graph capture or
+ * tight serving loops. Same outputs as bp_skinny_mf with the same plan, bit for bit.
+ */
+size_t bp_skinny_mf_static_bytes(void);
+int bp_skinny_mf_static(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y,
+                        int64_t M, int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* stream);
+
+/*
  * bp_skinny_mf with a transform of the activation rows first (split 1, K a multiple of the segment, 16-byte aligned
  * x and w, and the rows staged in LDS in one pass: M x K <= 32 x 64 x waves elements, e.g. one row of 2048 at any
  * waves, one row of 8192 at 4 or 8 waves): the matmul reads
