@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple] = {
     "bp_mlstm_multistep": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                     _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                     _c_float, _c_float, _c_int, _c_vp]),
+    "bp_mlstm_step": (_c_int, [_c_vp] * 12 + [_c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int,
+                                                _c_vp]),
     "bp_mlstm_lazy_commit": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                       _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                       _c_int, _c_vp]),

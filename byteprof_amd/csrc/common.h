@@ -114,18 +114,37 @@ __device__ __forceinline__ float load_scale(const void* p, int64_t i, int dt) {
 //   P <  64: v[0] of lane l holds the total of index l / (64 / P) (all 64/P lanes of a group hold the same).
 // The addition tree of every index is the same for every P (pairs by lane bit 5, then 4, ..., then 0), so a total
 // does not depend on how many other values were reduced with it.
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float x, float old = 0.0f) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), CTRL, ROW_MASK, BANK_MASK, false));
+}
+
+// One stage pairs, for j < P/2, lane l's v[j] (bit d of l clear) or v[j + P/2] (bit d set) with the same index at
+// lane l ^ d. Every exchange stays in the VALU: d = 32 and d = 16 are one v_permlane{32,16}_swap per pair (the swap
+// leaves lane l's kept value in one register and its partner's in the other), d = 8 is a row rotation by 8, d = 4
+// a row shift by 4 in each direction under bank masks (lanes with bit 2 clear are banks 0 and 2 of their row),
+// d = 2 and d = 1 are quad permutations. Each sum is kept + received, as a shuffle would give it.
 template <int P, int D>
 __device__ __forceinline__ void reduce_stage(float* v, int lane) {
-  if constexpr (P > 1) {
-    const bool hi = (lane & D) != 0;
+  constexpr int H = P > 1 ? P / 2 : 1;
+  const bool hi = (lane & D) != 0;
 #pragma unroll
-    for (int j = 0; j < P / 2; ++j) {
-      const float keep = hi ? v[j + P / 2] : v[j];
-      const float send = hi ? v[j] : v[j + P / 2];
-      v[j] = keep + __shfl_xor(send, D);
+  for (int j = 0; j < H; ++j) {
+    const float a = v[j];
+    const float b = P > 1 ? v[j + P / 2] : v[j];
+    if constexpr (D == 32 || D == 16) {
+      const auto r = D == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false)
+                             : __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+      v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else if constexpr (D == 4) {
+      const float lo_recv = dpp_f32<0x104, 0xF, 0x5>(a);           // row_shl:4 into lanes with bit 2 clear
+      const float recv = dpp_f32<0x114, 0xF, 0xA>(b, lo_recv);     // row_shr:4 into lanes with bit 2 set
+      v[j] = (hi ? b : a) + recv;
+    } else {
+      constexpr int ctrl = D == 8 ? 0x128 : D == 2 ? 0x4E : 0xB1;  // row_ror:8, quad_perm [2,3,0,1], [1,0,3,2]
+      v[j] = (hi ? b : a) + dpp_f32<ctrl>(hi ? a : b);
     }
-  } else {
-    v[0] += __shfl_xor(v[0], D);
   }
 }
 
@@ -144,11 +163,6 @@ __device__ __forceinline__ void wave_transpose_reduce(float* v, int lane) {
 // half-rows within rows of 16 (after which every lane of a row holds the row's sum), then rows 0..3 accumulated
 // into row 3 through row broadcasts. The order is fixed, so the result is deterministic; it is returned to every
 // lane (the value of lane 63).
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_f32(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
-}
-
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp_f32<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
   v += dpp_f32<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]

@@ -14,12 +14,17 @@
 // dot products are then added across the wave in one transposing butterfly (wave_transpose_reduce<64>) and across
 // waves in LDS, so the dependent chain per position is a handful of FMAs and one reduction serves G positions.
 // The scalar gate chain (m_t) runs across lanes: lane g computes the activations of position t0 + g.
+// Latency: every load of a group is unconditional and issued in the order of use (start state, gates, v, q, k),
+// so each wait is an exact count; v reaches the lanes by readlane, the butterflies run in the VALU (permlane swaps
+// and DPP), and full groups are compiled without per-position checks.
 //
 // Reference semantics: byteprof/optim/mlstm_multistep.py:21-30 (_gates), :34-86 (multistep_fw_kernel);
 // byteprof/optim/draft_fused.py:27-40 (multistep_fw).
 
 #include "byteprof_amd.h"
 #include "common.h"
+
+#include <type_traits>
 
 namespace bp {
 namespace {
@@ -45,10 +50,43 @@ __device__ __forceinline__ void store_io(void* p, int64_t i, float f) {
   else static_cast<float*>(p)[i] = f;
 }
 
+// The raw bits of an io_dtype element (loaded without converting, so a batch of loads stays in flight) and their
+// value.
+template <int IO>
+__device__ __forceinline__ uint32_t load_raw(const void* p, int64_t i) {
+  if constexpr (IO == BP_DT_F32) return static_cast<const uint32_t*>(p)[i];
+  else return static_cast<const uint16_t*>(p)[i];
+}
+
+template <int IO>
+__device__ __forceinline__ float raw_value(uint32_t r) {
+  if constexpr (IO == BP_DT_BF16) return bf16_bits_to_float(r);
+  else if constexpr (IO == BP_DT_F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
+  else return __uint_as_float(r);
+}
+
 __device__ __forceinline__ float load_gate(const void* p, int64_t i, int dt) {
   if (dt == BP_DT_BF16) return bf16_bits_to_float(static_cast<const uint16_t*>(p)[i]);
   if (dt == BP_DT_F16) return static_cast<float>(static_cast<const _Float16*>(p)[i]);
   return static_cast<const float*>(p)[i];
+}
+
+// A gate element as two raw 16-bit halves: a 4-byte gate is read as its two halves, a 2-byte gate twice, so the
+// loads are the same two instructions for every gate dtype (no branch between loads that would force a full wait).
+struct GateRaw {
+  uint32_t lo, hi;
+};
+
+__device__ __forceinline__ GateRaw load_gate_raw(const void* p, int64_t i, int dt) {
+  const auto b = as_global(static_cast<const uint16_t*>(p));
+  const int64_t e = dt == BP_DT_F32 ? 2 * i : i;
+  return {b[e], b[e + (dt == BP_DT_F32 ? 1 : 0)]};
+}
+
+__device__ __forceinline__ float gate_value(GateRaw r, int dt) {
+  if (dt == BP_DT_F32) return __uint_as_float(r.lo | (r.hi << 16));
+  if (dt == BP_DT_BF16) return bf16_bits_to_float(r.lo);
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.lo)));
 }
 
 constexpr int kMaxWaves = 4;
@@ -58,8 +96,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
     const float* __restrict__ c, const float* __restrict__ n, const float* __restrict__ m,
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const void* __restrict__ ig, const void* __restrict__ fg, void* __restrict__ h, float* __restrict__ nstart,
-    float* __restrict__ mstart, int T, int DQ, int DV, int64_t str_qk, int64_t str_v, int64_t str_if,
-    int64_t str_h, int gate_dt, float qk_scale, float eps) {
+    float* __restrict__ mstart, float* __restrict__ c_out, float* __restrict__ n_out, float* __restrict__ m_out,
+    int T, int DQ, int DV, int64_t str_qk, int64_t str_v, int64_t str_if, int64_t str_h, int gate_dt,
+    float qk_scale, float eps) {
   constexpr int G = kWave / BV;  // positions per reduction group
   __shared__ float red_h[kMaxWaves][kWave];
   __shared__ float red_q[kMaxWaves][G];
@@ -72,81 +111,115 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
   const int nthreads = blockDim.x;
   const int nwaves = nthreads / kWave;
 
+  // This thread's block of the start state, loaded first (the loop keeps a copy of the start n, whose wait then
+  // covers only these loads).
   float C[DPT][BV];
-  float nn[DPT];
+  float nn[DPT], n_start[DPT];
 #pragma unroll
   for (int j = 0; j < DPT; ++j) {
     const int dq = tid + j * nthreads;
     const float* crow = c + (static_cast<int64_t>(hd) * DQ + dq) * DV + v0;
 #pragma unroll
     for (int b = 0; b < BV; ++b) C[j][b] = crow[b];
-    nn[j] = n[static_cast<int64_t>(hd) * DQ + dq];
-    if (blockIdx.x == 0) nstart[static_cast<int64_t>(hd) * DQ + dq] = nn[j];
+    nn[j] = n_start[j] = n[static_cast<int64_t>(hd) * DQ + dq];
   }
   float m_prev = m[hd];
-  if (blockIdx.x == 0 && tid == 0) mstart[hd] = m_prev;
+  const float m_start = m_prev;
+
+  // Everything a group of G positions reads, as raw bits, issued in the order it is needed: lane g's gate
+  // pre-activations of position t0 + g (they head the longest dependent chain), lane l's v element (position
+  // t0 + l / BV, column v0 + l % BV), then this thread's q and k rows. Positions past T read the group's last
+  // position, unused; every load is unconditional, so the waits for them are exact counts.
+  GateRaw fr, ir;
+  uint32_t vr;
+  uint32_t qv[G][DPT], kv[G][DPT];
+  auto issue_group = [&](int t0) {
+    const int last = (T - t0 < G ? T - t0 : G) - 1;
+    const int64_t goff = static_cast<int64_t>(t0 + (lane < last ? lane : last)) * str_if + hd;
+    fr = load_gate_raw(fg, goff, gate_dt);
+    ir = load_gate_raw(ig, goff, gate_dt);
+    const int vg = lane / BV < last ? lane / BV : last;
+    vr = load_raw<IO>(v, static_cast<int64_t>(t0 + vg) * str_v + static_cast<int64_t>(hd) * DV + v0 + lane % BV);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < DPT; ++j) {
+        const int64_t qk_off = static_cast<int64_t>(t0 + (g < last ? g : last)) * str_qk +
+                               static_cast<int64_t>(hd) * DQ + tid + j * nthreads;
+        qv[g][j] = load_raw<IO>(q, qk_off);
+        kv[g][j] = load_raw<IO>(k, qk_off);
+      }
+  };
+  __builtin_assume(T >= 1);  // the host handles T = 0 without a launch
+  issue_group(0);
 
   for (int t0 = 0; t0 < T; t0 += G) {
     const int gcount = T - t0 < G ? T - t0 : G;
 
-    // Gate activations: lane g < gcount handles position t0 + g; the max-plus chain of m runs through the lanes.
-    float fl = 0.f, iv = 0.f;
-    if (lane < gcount) {
-      const int64_t off = static_cast<int64_t>(t0 + lane) * str_if + hd;
-      const float fv = load_gate(fg, off, gate_dt);
-      iv = load_gate(ig, off, gate_dt);
-      fl = logf(1.f / (1.f + expf(-fv)));
-    }
-    float m_old_l = 0.f, m_new_l = 0.f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (g < gcount) {
-        const float fg_g = __shfl(fl, g);
-        const float ig_g = __shfl(iv, g);
-        const float mn = fmaxf(fg_g + m_prev, ig_g);
-        if (lane == g) {
-          m_old_l = m_prev;
-          m_new_l = mn;
-        }
-        m_prev = mn;
-      }
-    }
-    const float fa_l = round_io<IO>(expf(fl + m_old_l - m_new_l));
-    const float ia_l = round_io<IO>(expf(iv - m_new_l));
-    const float mv_l = round_io<IO>(expf(-m_new_l));
-
-    // Advance the state over the group's positions, keeping the per-thread partial dot products.
+    // The gate chain and the state advance over the group's positions; a full group (every group but a last,
+    // partial one) is compiled without the per-position checks.
     float hp[G * BV];
     float qp[G];
+    float mv_l;
+    auto advance = [&](auto full) {
+      constexpr bool FULL = decltype(full)::value;
+      // Gate activations: lane g < gcount handles position t0 + g; the max-plus chain of m runs through the lanes.
+      const float fv = gate_value(fr, gate_dt);
+      const float iv = gate_value(ir, gate_dt);
+      const float fl = logf(1.f / (1.f + expf(-fv)));
+      float m_old_l = 0.f, m_new_l = 0.f;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      qp[g] = 0.f;
-#pragma unroll
-      for (int b = 0; b < BV; ++b) hp[g * BV + b] = 0.f;
-      if (g < gcount) {
-        const int t = t0 + g;
-        const float fa = __shfl(fa_l, g);
-        const float ia = __shfl(ia_l, g);
-        float vv[BV];
-#pragma unroll
-        for (int b = 0; b < BV; ++b) vv[b] = load_io<IO>(v, static_cast<int64_t>(t) * str_v + static_cast<int64_t>(hd) * DV + v0 + b);
-#pragma unroll
-        for (int j = 0; j < DPT; ++j) {
-          const int dq = tid + j * nthreads;
-          const int64_t qk_off = static_cast<int64_t>(t) * str_qk + static_cast<int64_t>(hd) * DQ + dq;
-          const float kk = load_io<IO>(k, qk_off);
-          const float qs = load_io<IO>(q, qk_off) * qk_scale;
-          const float ik = ia * kk;
-#pragma unroll
-          for (int b = 0; b < BV; ++b) {
-            C[j][b] = fmaf(ik, vv[b], fa * C[j][b]);
-            hp[g * BV + b] = fmaf(qs, round_io<IO>(C[j][b]), hp[g * BV + b]);
+      for (int g = 0; g < G; ++g) {
+        if (FULL || g < gcount) {
+          // lane g's values, broadcast through a scalar register (g is a constant of the unrolled loop)
+          const float fg_g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fl), g));
+          const float ig_g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(iv), g));
+          const float mn = fmaxf(fg_g + m_prev, ig_g);
+          if (lane == g) {
+            m_old_l = m_prev;
+            m_new_l = mn;
           }
-          nn[j] = fmaf(fa, nn[j], ik);
-          qp[g] = fmaf(qs, round_io<IO>(nn[j]), qp[g]);
+          m_prev = mn;
         }
       }
-    }
+      const float fa_l = round_io<IO>(expf(fl + m_old_l - m_new_l));
+      const float ia_l = round_io<IO>(expf(iv - m_new_l));
+      mv_l = round_io<IO>(expf(-m_new_l));
+      const float v_l = raw_value<IO>(vr);
+
+      // Advance the state over the group's positions, keeping the per-thread partial dot products.
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        qp[g] = 0.f;
+#pragma unroll
+        for (int b = 0; b < BV; ++b) hp[g * BV + b] = 0.f;
+        if (FULL || g < gcount) {
+          const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa_l), g));
+          const float ia = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ia_l), g));
+          float vv[BV];
+#pragma unroll
+          for (int b = 0; b < BV; ++b)
+            vv[b] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_l), g * BV + b));
+#pragma unroll
+          for (int j = 0; j < DPT; ++j) {
+            const float kk = raw_value<IO>(kv[g][j]);
+            const float qs = raw_value<IO>(qv[g][j]) * qk_scale;
+            const float ik = ia * kk;
+#pragma unroll
+            for (int b = 0; b < BV; ++b) {
+              C[j][b] = fmaf(ik, vv[b], fa * C[j][b]);
+              hp[g * BV + b] = fmaf(qs, round_io<IO>(C[j][b]), hp[g * BV + b]);
+            }
+            nn[j] = fmaf(fa, nn[j], ik);
+            qp[g] = fmaf(qs, round_io<IO>(nn[j]), qp[g]);
+          }
+        }
+      }
+    };
+    if (gcount == G) advance(std::true_type{});
+    else advance(std::false_type{});
+
+    if (t0 + G < T) issue_group(t0 + G);  // the next group's loads, in flight during the reductions
 
     wave_transpose_reduce<G * BV>(hp, lane);  // lane l: wave total of index l = g * BV + b
     wave_transpose_reduce<G>(qp, lane);       // lane l: wave total of position l / (64 / G)
@@ -169,6 +242,24 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
       }
     }
     __syncthreads();
+  }
+  // copies of the start n and m (stored last, so no wait for their loads delays the gate chain)
+  if (blockIdx.x == 0 && nstart != nullptr) {
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) nstart[static_cast<int64_t>(hd) * DQ + tid + j * nthreads] = n_start[j];
+    if (tid == 0 && mstart != nullptr) mstart[hd] = m_start;
+  }
+  // the state after the last position, into the caller's buffers (a step writing its new state)
+  if (c_out != nullptr) {
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) {
+      const int dq = tid + j * nthreads;
+      float* crow = c_out + (static_cast<int64_t>(hd) * DQ + dq) * DV + v0;
+#pragma unroll
+      for (int b = 0; b < BV; ++b) crow[b] = C[j][b];
+      if (blockIdx.x == 0) n_out[static_cast<int64_t>(hd) * DQ + dq] = nn[j];
+    }
+    if (blockIdx.x == 0 && tid == 0) m_out[hd] = m_prev;
   }
 }
 
@@ -263,8 +354,8 @@ CommitFn pick_commit(int io, int bv, int dpt) {
 }
 
 using MlstmFn = void (*)(const float*, const float*, const float*, const void*, const void*, const void*,
-                         const void*, const void*, void*, float*, float*, int, int, int, int64_t, int64_t, int64_t,
-                         int64_t, int, float, float);
+                         const void*, const void*, void*, float*, float*, float*, float*, float*, int, int, int,
+                         int64_t, int64_t, int64_t, int64_t, int, float, float);
 
 template <int IO, int BV>
 MlstmFn pick_dpt(int dpt) {
@@ -293,30 +384,71 @@ MlstmFn pick(int io, int bv, int dpt) {
 }  // namespace
 }  // namespace bp
 
+namespace bp {
+namespace {
+
+// Workgroups of DQ / dpt threads (dpt = 1 up to 256, else 2): whole waves only, so DQ a multiple of 64 up to 256,
+// or 384 / 512.
+int mlstm_dpt(int DQ) {
+  if (DQ <= 0 || DQ % kWave != 0 || DQ > 2 * kMaxWaves * kWave) return 0;
+  const int dpt = DQ <= kMaxWaves * kWave ? 1 : 2;
+  return (DQ / dpt) % kWave == 0 ? dpt : 0;
+}
+
+int mlstm_launch(const void* c, const void* n, const void* m, const void* q, const void* k, const void* v,
+                 const void* i, const void* f, void* h, void* nstart, void* mstart, void* c_out, void* n_out,
+                 void* m_out, int T, int NH, int DQ, int DV, int64_t str_t_qk, int64_t str_t_v, int64_t str_t_if,
+                 int64_t str_t_h, int io_dtype, int gate_dtype, float qk_scale, float eps, int bv, void* stream) {
+  if (T < 0 || NH < 0 || DQ <= 0 || DV <= 0) return BP_E_INVALID_ARG;
+  if (NH == 0) return BP_OK;
+  if (c == nullptr || n == nullptr || m == nullptr) return BP_E_INVALID_ARG;
+  if (T > 0 && (q == nullptr || k == nullptr || v == nullptr || i == nullptr || f == nullptr || h == nullptr))
+    return BP_E_INVALID_ARG;
+  const int dpt = mlstm_dpt(DQ);
+  if (dpt == 0) return BP_E_UNSUPPORTED;
+  if (gate_dtype < BP_DT_BF16 || gate_dtype > BP_DT_F32) return BP_E_UNSUPPORTED;
+  if (bv != 4 && bv != 8 && bv != 16) return BP_E_UNSUPPORTED;
+  if (DV % bv != 0) return BP_E_UNSUPPORTED;
+  MlstmFn fn = pick(io_dtype, bv, dpt);
+  if (fn == nullptr) return BP_E_UNSUPPORTED;
+  const auto st = static_cast<hipStream_t>(stream);
+  if (T == 0) {  // no positions: the start-state copies are the whole result
+    if (nstart == nullptr) return BP_OK;
+    hipError_t e = hipMemcpyAsync(nstart, n, sizeof(float) * NH * DQ, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(mstart, m, sizeof(float) * NH, hipMemcpyDeviceToDevice, st);
+    return e == hipSuccess ? BP_OK : static_cast<int>(e);
+  }
+  dim3 grid(static_cast<unsigned>(DV / bv), static_cast<unsigned>(NH));
+  fn<<<grid, DQ / dpt, 0, st>>>(
+      static_cast<const float*>(c), static_cast<const float*>(n), static_cast<const float*>(m), q, k, v, i, f, h,
+      static_cast<float*>(nstart), static_cast<float*>(mstart), static_cast<float*>(c_out),
+      static_cast<float*>(n_out), static_cast<float*>(m_out), T, DQ, DV, str_t_qk, str_t_v, str_t_if, str_t_h,
+      gate_dtype, qk_scale, eps);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? BP_OK : static_cast<int>(e);
+}
+
+}  // namespace
+}  // namespace bp
+
+extern "C" int bp_mlstm_step(const void* c, const void* n, const void* m, const void* q, const void* k, const void* v,
+                             const void* i, const void* f, void* h, void* c_new, void* n_new, void* m_new, int NH,
+                             int DQ, int DV, int io_dtype, int gate_dtype, float qk_scale, float eps, int bv,
+                             void* stream) {
+  if (c_new == nullptr || n_new == nullptr || m_new == nullptr) return BP_E_INVALID_ARG;
+  return bp::mlstm_launch(c, n, m, q, k, v, i, f, h, nullptr, nullptr, c_new, n_new, m_new, 1, NH, DQ, DV,
+                          static_cast<int64_t>(NH) * DQ, static_cast<int64_t>(NH) * DV, NH,
+                          static_cast<int64_t>(NH) * DV, io_dtype, gate_dtype, qk_scale, eps, bv, stream);
+}
+
 extern "C" int bp_mlstm_multistep(const void* c, const void* n, const void* m, const void* q, const void* k,
                                   const void* v, const void* i, const void* f, void* h, void* nstart, void* mstart,
                                   int T, int NH, int DQ, int DV, int64_t str_t_qk, int64_t str_t_v,
                                   int64_t str_t_if, int64_t str_t_h, int io_dtype, int gate_dtype, float qk_scale,
                                   float eps, int bv, void* stream) {
-  if (T < 0 || NH < 0 || DQ <= 0 || DV <= 0) return BP_E_INVALID_ARG;
-  if (NH == 0) return BP_OK;
-  if (c == nullptr || n == nullptr || m == nullptr || nstart == nullptr || mstart == nullptr) return BP_E_INVALID_ARG;
-  if (T > 0 && (q == nullptr || k == nullptr || v == nullptr || i == nullptr || f == nullptr || h == nullptr))
-    return BP_E_INVALID_ARG;
-  if (DQ % bp::kWave != 0 || DQ > 2 * bp::kMaxWaves * bp::kWave) return BP_E_UNSUPPORTED;
-  if (gate_dtype < BP_DT_BF16 || gate_dtype > BP_DT_F32) return BP_E_UNSUPPORTED;
-  if (bv != 4 && bv != 8 && bv != 16) return BP_E_UNSUPPORTED;
-  if (DV % bv != 0) return BP_E_UNSUPPORTED;
-  const int dpt = DQ <= bp::kMaxWaves * bp::kWave ? 1 : 2;
-  bp::MlstmFn fn = bp::pick(io_dtype, bv, dpt);
-  if (fn == nullptr) return BP_E_UNSUPPORTED;
-  dim3 grid(static_cast<unsigned>(DV / bv), static_cast<unsigned>(NH));
-  fn<<<grid, DQ / dpt, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const float*>(c), static_cast<const float*>(n), static_cast<const float*>(m), q, k, v, i, f, h,
-      static_cast<float*>(nstart), static_cast<float*>(mstart), T, DQ, DV, str_t_qk, str_t_v, str_t_if, str_t_h,
-      gate_dtype, qk_scale, eps);
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? BP_OK : static_cast<int>(e);
+  if (nstart == nullptr || mstart == nullptr) return BP_E_INVALID_ARG;
+  return bp::mlstm_launch(c, n, m, q, k, v, i, f, h, nstart, mstart, nullptr, nullptr, nullptr, T, NH, DQ, DV,
+                          str_t_qk, str_t_v, str_t_if, str_t_h, io_dtype, gate_dtype, qk_scale, eps, bv, stream);
 }
 
 extern "C" int bp_mlstm_lazy_commit(void* c, void* n, void* m, const void* nstart, const void* mstart, const void* k,
@@ -328,11 +460,11 @@ extern "C" int bp_mlstm_lazy_commit(void* c, void* n, void* m, const void* nstar
   if (c == nullptr || n == nullptr || m == nullptr || nstart == nullptr || mstart == nullptr || length == nullptr)
     return BP_E_INVALID_ARG;
   if (T > 0 && (k == nullptr || v == nullptr || i == nullptr || f == nullptr)) return BP_E_INVALID_ARG;
-  if (DQ % bp::kWave != 0 || DQ > 2 * bp::kMaxWaves * bp::kWave) return BP_E_UNSUPPORTED;
+  const int dpt = bp::mlstm_dpt(DQ);
+  if (dpt == 0) return BP_E_UNSUPPORTED;
   if (gate_dtype < BP_DT_BF16 || gate_dtype > BP_DT_F32) return BP_E_UNSUPPORTED;
   if (bv != 4 && bv != 8 && bv != 16) return BP_E_UNSUPPORTED;
   if (DV % bv != 0) return BP_E_UNSUPPORTED;
-  const int dpt = DQ <= bp::kMaxWaves * bp::kWave ? 1 : 2;
   bp::CommitFn fn = bp::pick_commit(io_dtype, bv, dpt);
   if (fn == nullptr) return BP_E_UNSUPPORTED;
   dim3 grid(static_cast<unsigned>(DV / bv), static_cast<unsigned>(NH));

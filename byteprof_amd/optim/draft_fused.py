@@ -7,8 +7,8 @@ mstart [NH]. The arithmetic is that of byteprof/optim/mlstm_multistep.py:21-86 (
 stabiliser m, gate activations rounded to the input dtype, fp32 state, state rounded to the input dtype before the
 q products, h = q.C / (max(|q.n|, exp(-m)) + eps), qk_scale = DQ ** -0.5).
 
-Geometry: the reference accepts DQ of one or two 64-wide blocks (draft_fused.py:14-24); this kernel takes any DQ
-that is a multiple of 64 up to 512 (so also the 256-wide heads of the 4-head configuration) and any DV that is a
+Geometry: the reference accepts DQ of one or two 64-wide blocks (draft_fused.py:14-24); this kernel takes DQ a
+multiple of 64 up to 256 (so also the 256-wide heads of the 4-head configuration) or 384 / 512, and any DV that is a
 multiple of the value block BV (4, 8 or 16). Unsupported geometry raises NotImplementedError, as the reference does.
 
 `lazy_commit` (draft_fused.py:43-56) recomputes the state after the accepted positions 0 .. L from the start state
@@ -22,14 +22,21 @@ import torch
 
 from .. import _lib
 
-BV = 8  # value columns per workgroup (4, 8 or 16)
+BV = 4  # value columns per workgroup (4, 8 or 16): 4 gives NH x DV / 4 workgroups (256 at 4 heads of 256)
+
+
+def supported_dq(dq: int) -> bool:
+    """Head dims the fused kernel takes: one row of q per thread up to 256 (a multiple of 64), two rows per thread
+    at 384 and 512 (workgroups of whole 64-lane waves)."""
+    return dq > 0 and dq % 64 == 0 and (dq <= 256 or dq in (384, 512))
 
 
 def _geometry(q: torch.Tensor, v: torch.Tensor, bv: int) -> tuple[int, int, int]:
     _, nh, dq = q.shape
     dv = v.shape[-1]
-    if dq % 64 or dq > 512:
-        raise NotImplementedError(f"the fused kernel needs head_dim_qk a multiple of 64 up to 512 (got {dq})")
+    if not supported_dq(dq):
+        raise NotImplementedError(f"the fused kernel needs head_dim_qk a multiple of 64 up to 256, or 384 / 512 "
+                                  f"(got {dq})")
     if dv % bv:
         raise NotImplementedError(f"head_dim_v {dv} is not a multiple of the value block {bv}")
     return nh, dq, dv

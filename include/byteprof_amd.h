@@ -208,7 +208,8 @@ int bp_splitk_reduce(const void* workspace, void* y, const void* scale, int scal
  *   m' = max(logsigmoid(f) + m, i); fa = exp(logsigmoid(f) + m - m'); ia = exp(i - m'); mv = exp(-m'),
  *   the three rounded to io_dtype; C <- fa C + ia k v^T; n <- fa n + ia k (fp32 state);
  *   h = (qs . io(C)) / (max(|qs . io(n)|, mv) + eps) with qs = q * qk_scale, stored as io_dtype.
- * bv: value columns per workgroup (4, 8 or 16); dq must be a multiple of 64, at most 512.
+ * bv: value columns per workgroup (4, 8 or 16); DQ a multiple of 64 up to 256, or 384 / 512 (workgroups of DQ or
+ * DQ / 2 threads, whole 64-lane waves); other DQ: BP_E_UNSUPPORTED.
  * Replaces: byteprof/optim/draft_fused.py:27-40 (multistep_fw) and byteprof/optim/mlstm_multistep.py:21-86
  *           (_gates, multistep_fw_kernel).
  */
@@ -218,6 +219,19 @@ int bp_mlstm_multistep(const void* c, const void* n, const void* m,
                        int T, int NH, int DQ, int DV,
                        int64_t str_t_qk, int64_t str_t_v, int64_t str_t_if, int64_t str_t_h,
                        int io_dtype, int gate_dtype, float qk_scale, float eps, int bv, void* stream);
+
+/*
+ * One step from the state (c [NH, DQ, DV], n [NH, DQ], m [NH], fp32, read only) into the caller's buffers: h [NH, DV]
+ * (io_dtype) and the next state c_new, n_new, m_new (fp32, same shapes; must not overlap c, n, m), so each
+ * position's state can go to a history slot. q, k [NH, DQ], v [NH, DV]: io_dtype; i, f [NH]: gate_dtype; the
+ * arithmetic of one bp_mlstm_multistep position, and the state bp_mlstm_lazy_commit computes for L = 0; the same
+ * DQ and bv rules.
+ * Replaces: byteprof/optim/draft_core.py:114-141 (mlstm_step_into: the library's recurrent step kernel writing into
+ *           given buffers).
+ */
+int bp_mlstm_step(const void* c, const void* n, const void* m, const void* q, const void* k, const void* v,
+                  const void* i, const void* f, void* h, void* c_new, void* n_new, void* m_new, int NH, int DQ,
+                  int DV, int io_dtype, int gate_dtype, float qk_scale, float eps, int bv, void* stream);
 
 /*
  * Lazy commit of a verify round: the state after positions 0 .. L, with L = *length (an int64 in device memory, so

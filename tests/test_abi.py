@@ -98,6 +98,12 @@ def test_invalid_arguments_are_rejected_before_any_launch(L):
     assert L.bp_mlstm_multistep(*args, 4, 2, 64, 16, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 5, None) == -2
     assert L.bp_mlstm_multistep(*args, 4, 2, 64, 12, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 8, None) == -2
     assert L.bp_mlstm_multistep(*args, 4, 0, 64, 16, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 8, None) == 0  # NH = 0: no-op
+    # DQ whose workgroup would not be whole waves (320 -> 160 threads, 448 -> 224), or beyond 512
+    for dq in (320, 448, 576):
+        assert L.bp_mlstm_multistep(*args, 4, 2, dq, 16, 1, 1, 1, 1, 0, 2, 0.1, 1e-6, 8, None) == -2, dq
+        assert L.bp_mlstm_lazy_commit(*[p] * 10, 4, 2, dq, 16, 1, 1, 1, 0, 2, 8, None) == -2, dq
+    assert L.bp_mlstm_step(*[p] * 12, 2, 320, 16, 0, 2, 0.1, 1e-6, 8, None) == -2
+    assert L.bp_mlstm_step(*[p] * 9, None, p, p, 2, 64, 16, 0, 2, 0.1, 1e-6, 8, None) == -1  # no new state
 
 
 # ---- the one-launch linear chain (bp_chain_*) ---------------------------------------------------------------------

@@ -383,3 +383,14 @@ def test_decode_stages_cover_the_linears():
     stage_bytes = sum(A.call_bytes(A.Linear(n, k), None, 1) for _, n, k in stages)
     fewer_inputs = 2 * (2 * 2048 + 2048) * 16  # q|k|v read one input instead of three, gate|up one instead of two
     assert stage_bytes == D.chain_bytes("bf16") - fewer_inputs
+
+
+def test_mlstm_head_dims_are_whole_waves():
+    """DQ the fused mLSTM kernels take: multiples of 64 up to 256 (one row per thread) and 384 / 512 (two); 320 and
+    448 would give workgroups of partial waves and are refused before any launch."""
+    from byteprof_amd.optim import draft_fused as F
+
+    assert [d for d in range(64, 640, 64) if F.supported_dq(d)] == [64, 128, 192, 256, 384, 512]
+    q = torch.zeros(1, 2, 320)
+    with pytest.raises(NotImplementedError):
+        F._geometry(q, torch.zeros(1, 2, 16), 4)

@@ -148,3 +148,59 @@ def test_zero_positions_only_saves_the_start_state():
     torch.cuda.synchronize()
     assert torch.equal(ns, state[1][0]) and torch.equal(ms, state[2].reshape(-1)) and (h == 0).all()
     assert np.isfinite(ns.cpu().numpy()).all()
+
+
+def _step(state, q, k, v, i, f, eps=1e-6, bv=None):
+    from byteprof_amd.optim import draft_core as DC
+
+    nh, dv = q.shape[1], v.shape[-1]
+    new = tuple(torch.full_like(x, float("nan")) for x in state)
+    h = torch.zeros(1, nh, dv, dtype=q.dtype, device="cuda")
+    DC.mlstm_step_into(state, new, q, k, v, i, f, h, eps, bv=bv)
+    return h, new
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("nh,dq,dv", [(4, 256, 256), (16, 128, 128), (2, 512, 64)])
+def test_step_matches_the_oracle(dtype, nh, dq, dv):
+    """mlstm_step_into (bp_mlstm_step): h and the new state of one position against the oracle at T = 1; the
+    previous state is left as it was."""
+    print(f"\n[mlstm step] dtype={dtype} nh={nh} dq={dq} dv={dv}", flush=True)
+    q, k, v, i, f, state = rand_inputs(1, nh, dq, dv, dtype, seed=11, f_mean=3.0)
+    start = tuple(x.clone() for x in state)
+    h, new = _step(state, q, k, v, i, f)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(state, start))
+    h_ref, (c_ref, n_ref, m_ref) = oracle(state, q, k, v, i, f, 1e-6, IO[dtype])
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert ON.normwise_error(h.float().cpu().numpy(), h_ref) < tol
+    assert ON.normwise_error(new[0].cpu().numpy().reshape(c_ref.shape), c_ref) < 1e-5
+    assert ON.normwise_error(new[1].cpu().numpy().reshape(n_ref.shape), n_ref) < 1e-5
+    assert np.allclose(new[2].cpu().numpy().reshape(-1), m_ref, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("bv", [4, 8, 16])
+def test_step_equals_multistep_then_lazy_commit(dtype, bv):
+    """One step equals the fused multistep over one position (h) followed by the lazy commit of L = 0 (the state),
+    bit for bit."""
+    q, k, v, i, f, state = rand_inputs(1, 4, 256, 256, dtype, seed=12)
+    h, new = _step(state, q, k, v, i, f, bv=bv)
+    cur = tuple(x.clone() for x in state)
+    h1 = torch.zeros_like(h)
+    ns, ms = torch.zeros(4, 256, device="cuda"), torch.zeros(4, device="cuda")
+    F.multistep_fw(cur, q, k, v, i, f, h1, ns, ms, eps=1e-6, bv=bv)
+    F.lazy_commit(cur, k, v, i, f, torch.tensor(0, device="cuda"), ns, ms, bv=bv)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h1)
+    for a, b in zip(new, cur):
+        assert torch.equal(a.reshape(-1), b.reshape(-1))
+
+
+def test_step_refuses_overlapping_state():
+    from byteprof_amd.optim import draft_core as DC
+
+    q, k, v, i, f, state = rand_inputs(1, 2, 64, 16, torch.bfloat16, seed=13)
+    h = torch.zeros(1, 2, 16, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        DC.mlstm_step_into(state, state, q, k, v, i, f, h, 1e-6)
