@@ -37,8 +37,8 @@ def common_flags() -> list[str]:
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-SOURCES = ("skinny.hip", "skinny_mf.hip", "skinny_chain.hip", "skinny_int4.hip", "mlstm.hip", "draft.hip",
-           "decode.hip")
+SOURCES = ("skinny.hip", "skinny_mf.hip", "skinny_mf_n4.hip", "skinny_mf_n8.hip", "skinny_mf_n16.hip",
+           "skinny_chain.hip", "skinny_int4.hip", "mlstm.hip", "draft.hip", "decode.hip")
 
 
 def units() -> list[tuple[Path, list[str], Path]]:

@@ -193,6 +193,47 @@ struct MfMain {
     u32x4 x[kXP];
   };
 
+  // The loads of segment s into a slot (vector loads; wrow[rb] advanced to the lane's bytes of a segment).
+  __device__ __forceinline__ static void load_slot(Slot& sl, const uint8_t* const (&wrow)[RB], const XS& xs,
+                                                   int64_t s) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      sl.w[rb] = __builtin_nontemporal_load(as_global(reinterpret_cast<const u32x4*>(wrow[rb] + s * 128)));
+    if constexpr (XMEM) {
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int p = 0; p < G::kParts; ++p) sl.x[b * G::kParts + p] = xs.load(s, b, p);
+    }
+  }
+
+  // The MFMAs of segment s (its weights in the slot) into the wave's tiles.
+  __device__ __forceinline__ static void compute_slot(const Slot& sl, const XS& xs, int64_t s,
+                                                      floatx4 (&acc)[RB][MB]) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      u32x4 a[G::kParts];
+      if constexpr (KIND == kBf16) {
+        a[0] = sl.w[rb];
+      } else {
+        a[0] = mf_i8x8(sl.w[rb].x, sl.w[rb].y);
+        a[1] = mf_i8x8(sl.w[rb].z, sl.w[rb].w);
+      }
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int p = 0; p < G::kParts; ++p) {
+          u32x4 bx;
+          if constexpr (XMEM) {
+            bx = sl.x[b * G::kParts + p];
+          } else {
+            bx = xs.load(s, b, p);
+          }
+          acc[rb][b] = mf_mfma(a[p], bx, acc[rb][b]);
+        }
+    }
+  }
+
   // wrow[rb]: the lane's weight row of block rb, advanced to the lane's byte offset in a segment.
   // (VEC = false: wrow[rb] is the row start and kl the lane's K offset in a segment, for bounded element loads.)
   template <class Hook = MfNoHook>
@@ -219,40 +260,39 @@ struct MfMain {
           for (int p = 0; p < G::kParts; ++p) sl.x[b * G::kParts + p] = xs.load(s, b, p);
       }
     };
-    auto compute = [&](const Slot& sl, int64_t idx) {
-      const int64_t s = s_first + idx * stride;
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        u32x4 a[G::kParts];
-        if constexpr (KIND == kBf16) {
-          a[0] = sl.w[rb];
-        } else {
-          a[0] = mf_i8x8(sl.w[rb].x, sl.w[rb].y);
-          a[1] = mf_i8x8(sl.w[rb].z, sl.w[rb].w);
-        }
-#pragma unroll
-        for (int b = 0; b < MB; ++b)
-#pragma unroll
-          for (int p = 0; p < G::kParts; ++p) {
-            u32x4 bx;
-            if constexpr (XMEM) {
-              bx = sl.x[b * G::kParts + p];
-            } else {
-              bx = xs.load(s, b, p);
-            }
-            acc[rb][b] = mf_mfma(a[p], bx, acc[rb][b]);
-          }
-      }
-    };
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(buf[d], d);
     hook();
     for (int64_t base = 0; base < nseg; base += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        if (base + d < nseg) compute(buf[d], base + d);
+        if (base + d < nseg) compute_slot(buf[d], xs, s_first + (base + d) * stride, acc);
         issue(buf[d], base + d + D);
       }
+    }
+  }
+};
+
+// The segments of one wave when their count NSEG is a compile-time constant (every wave of the launch has exactly
+// NSEG): straight-line code, D in flight, no load past the wave's last segment, so the compiler's wait counts are
+// exact and the wave ends as soon as its last MFMA is issued. Same segments, same order and same MFMA chain as
+// MfMain::run (bitwise equal results). `hook` runs after the first min(D, NSEG) segments' loads are issued.
+template <int KIND, int MB, int RB, int D, int NSEG, bool XMEM, class XS>
+struct MfFixed {
+  using Ops = MfMain<KIND, MB, RB, 1, true, XMEM, XS>;
+  static constexpr int kD = D < NSEG ? D : NSEG;  // segments in flight
+
+  template <class Hook = MfNoHook>
+  __device__ __forceinline__ static void run(const uint8_t* const (&wrow)[RB], const XS& xs, int64_t s_first,
+                                             int64_t stride, floatx4 (&acc)[RB][MB], const Hook& hook = Hook()) {
+    typename Ops::Slot buf[kD];
+#pragma unroll
+    for (int i = 0; i < kD; ++i) Ops::load_slot(buf[i], wrow, xs, s_first + i * stride);
+    hook();
+#pragma unroll
+    for (int i = 0; i < NSEG; ++i) {
+      Ops::compute_slot(buf[i % kD], xs, s_first + i * stride, acc);
+      if (i + kD < NSEG) Ops::load_slot(buf[i % kD], wrow, xs, s_first + (i + kD) * stride);
     }
   }
 };

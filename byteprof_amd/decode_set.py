@@ -136,12 +136,8 @@ def dispatch_gap_us(launches: int = 100) -> float:
 
 
 def kernel_key(kind: str, n: int, k: int, m: int) -> str:
-    """Name of the kernel instantiation a launch uses, as the profiler reports it (template arguments: kind,
-    activation blocks, weight blocks, waves, vector loads, epilogue, staged activations)."""
-    rb, waves, _, xs = S._resolve(kind, n, k, m, None)
-    mb = 1 if m <= 8 else 2 if m <= 16 else 4 if m <= 32 else 8
-    return (f"skinny_mf_kernel<{0 if kind == 'bf16' else 1}, {mb}, {rb}, {waves}, true, 0, "
-            f"{'true' if xs else 'false'}>")
+    """Name of the kernel instantiation a launch uses, as the profiler reports it."""
+    return S.kernel_name(kind, n, k, m)
 
 
 # stages of one layer: (stage name, linears sharing its input)

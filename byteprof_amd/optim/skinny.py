@@ -34,6 +34,7 @@ MAX_M = 64  # activation rows per launch; more rows are processed in chunks of M
 ROWS_PER_LAUNCH = MAX_M
 
 _KIND_CODE = {"bf16": 0, "int8": 1}
+XS_STAGE, XS_GENERAL = 1, 2  # BP_XS_STAGE, BP_XS_GENERAL: activations staged in LDS; the general segment loop
 _RB_MENU = (1, 2, 4)        # 8-row weight blocks per workgroup
 _WAVES_MENU = (1, 2, 4, 8)
 _BUCKETS = (1, 8, 16, 32, 64)  # row buckets of the tuned plans (8-row activation blocks per launch: 1, 1, 2, 4, 8)
@@ -101,7 +102,7 @@ def get_cfg(kind: str, n: int, k: int, bm: int) -> tuple[int, int, int]:
 
 
 def _table_plan(kind: str, n: int, k: int, m: int) -> tuple[int, int, int, int]:
-    """(weight blocks per workgroup, waves, split, staged activations) from the table, else the heuristic."""
+    """(weight blocks per workgroup, waves, split, xstage flags) from the table, else the heuristic."""
     bucket = _bucket(m)
     entry = _TABLE.get((kind, n, k))
     if entry is not None:
@@ -113,8 +114,8 @@ def _table_plan(kind: str, n: int, k: int, m: int) -> tuple[int, int, int, int]:
 
 
 def _resolve(kind: str, n: int, k: int, m: int, cfg) -> tuple[int, int, int, int]:
-    """(weight blocks per workgroup, waves, split, staged activations) of a launch from a user / table
-    configuration, mapped onto the compiled menu (largest supported value at or below the request)."""
+    """(weight blocks per workgroup, waves, split, xstage flags) of a launch from a user / table configuration,
+    mapped onto the compiled menu (largest supported value at or below the request)."""
     xs = 0
     if cfg is None:
         rb, waves, split, xs = _table_plan(kind, n, k, m)
@@ -128,13 +129,36 @@ def _resolve(kind: str, n: int, k: int, m: int, cfg) -> tuple[int, int, int, int
     rb = max(r for r in _RB_MENU if r <= max(rows // 8, 1))
     waves = max(w for w in _WAVES_MENU if w <= max(waves, 1))
     split = max(1, min(int(split), -(-k // k_segment(kind))))
-    if xs and (m > 16 or _stage_bytes(kind, m, k, split) < 0):
-        xs = 0
-    while rb > 1 and not _supported(kind, m, rb, waves, xs):
+    if xs & XS_STAGE and (m > 16 or _stage_bytes(kind, m, k, split) < 0):
+        xs &= ~XS_STAGE
+    while rb > 1 and not _supported(kind, m, rb, waves, xs & XS_STAGE):
         rb //= 2
-    if not _supported(kind, m, rb, waves, xs):
+    if not _supported(kind, m, rb, waves, xs & XS_STAGE):
         raise ValueError(f"no compiled kernel for {kind} at {m} rows, {8 * rb} weight rows, {waves} waves")
     return rb, waves, split, xs
+
+
+def segments_per_wave(kind: str, k: int, waves: int, split: int, xs: int = 0) -> int:
+    """K segments every wave of a launch handles when the launch runs the straight-line kernel of that count (4, 8
+    or 16: the split ranges and the waves divide K's segments evenly, and XS_GENERAL is not set), else 0."""
+    seg = k_segment(kind)
+    if k % seg or xs & XS_GENERAL:
+        return 0
+    nseg = k // seg
+    if nseg % split or (nseg // split) % waves:
+        return 0
+    n = nseg // split // waves
+    return n if n in (4, 8, 16) else 0
+
+
+def kernel_name(kind: str, n: int, k: int, m: int, cfg=None) -> str:
+    """Name of the kernel instantiation a skinny_mm launch of m rows runs, as the profiler reports it (template
+    arguments: kind, activation blocks, weight blocks, waves, vector loads, epilogue, staged activations, prologue,
+    segments per wave)."""
+    rb, waves, split, xs = _resolve(kind, n, k, m, cfg)
+    mb = 1 if m <= 8 else 2 if m <= 16 else 4 if m <= 32 else 8
+    return (f"skinny_mf_kernel<{_KIND_CODE[kind]}, {mb}, {rb}, {waves}, true, 0, "
+            f"{'true' if xs & XS_STAGE else 'false'}, false, {segments_per_wave(kind, k, waves, split, xs)}>")
 
 
 @functools.lru_cache(maxsize=None)

@@ -3,7 +3,7 @@
   python -m byteprof_amd.profiling set  [--kind bf16|int8] [--replays R]   the decode-step set as its 65 stage
                                                                          launches in one graph, R replays
   python -m byteprof_amd.profiling set113 [--kind bf16|int8] [--replays R] the same as 113 launches (one per linear)
-  python -m byteprof_amd.profiling chain [--kind bf16|int8] [--dependent] [--replays R]
+  python -m byteprof_amd.profiling chain [--kind bf16|int8] [--dependent] [--waves W] [--replays R]
                                                                          the set as one launch (independent linears,
                                                                          or the dependent stages), R launches
   python -m byteprof_amd.profiling stages [--kind bf16|int8] [--replays R]
@@ -14,8 +14,10 @@
                                                                          of the OLMo-2-1B shape, 8 prompt + N tokens;
                                                                          --draft: then the drafting loop with the
                                                                          oracle drafter (K up to 8)
-  python -m byteprof_amd.profiling skinny [--kind bf16|int8] [--n N] [--k K] [--m M] [--replays R]
+  python -m byteprof_amd.profiling skinny [--kind bf16|int8|int4] [--n N] [--k K] [--m M] [--replays R]
                                                                          skinny_mm over a ring of distinct weights
+  python -m byteprof_amd.profiling mlstm [--replays R]                    the fused mLSTM multistep (4 heads,
+                                                                         256 x 256, 16 steps), R launches
   python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
   python -m byteprof_amd.profiling summarize TRACE_DB [--fetch DB --write DB --fetch-copy DB --write-copy DB
                                              --copy-mib 256]               text summary of rocprofv3 databases
@@ -146,7 +148,8 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=("set", "set113", "chain", "stages", "decode", "skinny", "copy", "summarize"))
+    ap.add_argument("what", choices=("set", "set113", "chain", "stages", "decode", "skinny", "mlstm", "copy",
+                                     "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
     ap.add_argument("--write", help="summarize: WRITE_SIZE database of the workload")
@@ -157,8 +160,9 @@ def main(argv=None) -> int:
     ap.add_argument("--all", action="store_true", help="summarize: include kernels outside this library")
     ap.add_argument("--set-kind", choices=("bf16", "int8"), help="summarize: emit traffic lines for the set shapes")
     ap.add_argument("--chain-tag", help="summarize: emit traffic lines for the one-launch set kernel under this tag")
-    ap.add_argument("--kind", default="bf16", choices=("bf16", "int8"))
+    ap.add_argument("--kind", default="bf16", choices=("bf16", "int8", "int4"))
     ap.add_argument("--dependent", action="store_true", help="chain: stages read the outputs they depend on")
+    ap.add_argument("--waves", type=int, default=0, help="chain: waves per workgroup (0: the set's default)")
     ap.add_argument("--replays", type=int, default=5)
     ap.add_argument("--n", type=int, default=100352, help="skinny: output rows")
     ap.add_argument("--k", type=int, default=2048, help="skinny: input length")
@@ -187,11 +191,16 @@ def main(argv=None) -> int:
         from .optim import skinny as S
         from .quant.hip_int8 import quantize_rowwise_int8
 
-        per = a.n * a.k * (2 if a.kind == "bf16" else 1)
+        per = a.n * a.k * {"bf16": 2, "int8": 1, "int4": 0.5}[a.kind]
         ring = []
-        for r in range(max(2, (1 << 30) // per)):  # >= 1 GiB of distinct weights: streamed from HBM every call
+        for r in range(max(2, int((1 << 30) // per))):  # >= 1 GiB of distinct weights: streamed from HBM every call
             w = (torch.randn(a.n, a.k, device=device) * 0.02).to(torch.bfloat16)
-            ring.append((w,) if a.kind == "bf16" else quantize_rowwise_int8(w, torch.float16))
+            if a.kind == "bf16":
+                ring.append((w,))
+            elif a.kind == "int8":
+                ring.append(quantize_rowwise_int8(w, torch.float16))
+            else:
+                ring.append(S.quantize_int4(w))
             del w
         x = torch.randn(a.m, a.k, device=device).to(torch.bfloat16)
         y = torch.empty(a.m, a.n, dtype=torch.bfloat16, device=device)
@@ -203,8 +212,24 @@ def main(argv=None) -> int:
         print(f"skinny_mm {a.kind} {a.n}x{a.k} at M={a.m} (tuned plan): {a.replays} passes "
               f"over {len(ring)} weights", flush=True)
         return 0
+    if a.what == "mlstm":
+        from .optim import draft_fused
+
+        g = torch.Generator(device=device).manual_seed(0)
+        t, nh, dq, dv = 16, 4, 256, 256
+        r = lambda *shape: torch.randn(*shape, generator=g, device=device)  # noqa: E731
+        q, k, v = (r(t, nh, d).to(torch.bfloat16) for d in (dq, dq, dv))
+        i, f = r(t, nh, 1), r(t, nh, 1) + 3.0
+        state = (r(1, nh, dq, dv) * 0.1, r(1, nh, dq) * 0.1, r(1, nh, 1))
+        h = torch.empty(t, nh, dv, dtype=torch.bfloat16, device=device)
+        ns, ms = torch.empty(nh, dq, device=device), torch.empty(nh, device=device)
+        for _ in range(a.replays):
+            draft_fused.multistep_fw(state, q, k, v, i, f, h, ns, ms, eps=1e-6)
+        torch.cuda.synchronize()
+        print(f"mLSTM multistep (NH {nh}, {dq} x {dv}, T {t}): {a.replays} launches", flush=True)
+        return 0
     if a.what == "chain":
-        ch = D.build_chain(a.kind, device, dependent=a.dependent)
+        ch = D.build_chain(a.kind, device, dependent=a.dependent, waves=a.waves or D.CHAIN_WAVES)
         for _ in range(a.replays):
             ch.lset.run()
         torch.cuda.synchronize()

@@ -8,9 +8,10 @@ MI355X's 256 MB Infinity Cache (at least 1 GiB of weights per cell) instead of a
 bf16 / int8 (the matrix-core kernel of every row count): per (kind, N, K) the tuner keeps ONE K order -- (waves,
 split) -- for every activation-row bucket, so an output row stays bitwise independent of M. It times every
 (waves, split) at one row (the decode metric) and at 16 rows (the verify widths), each with its best weight blocks
-per workgroup and activation staging, and keeps the fastest one-row order unless another is within 2% at one row
-and faster at 16 rows; like the reference, a split > 1 must win by more than 3%. Then, at that K order, it picks
-the weight blocks per workgroup and the staging for each bucket (1; 8: four and eight rows together; 16, 32, 64).
+per workgroup and xstage flags (activation staging; the straight-line kernel of the segment count or the general
+loop), and keeps the fastest one-row order unless another is within 2% at one row and faster at 16 rows; like the
+reference, a split > 1 must win by more than 3%. Then, at that K order, it picks the weight blocks per workgroup and
+the flags for each bucket (1; 8: four and eight rows together; 16, 32, 64).
 
 Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8,int4] [--out path]
 """
@@ -94,11 +95,16 @@ def _launcher(kind: str, ring, x, y, rb: int, waves: int, split: int, xs: int):
 
 
 def _plans(kind: str, m: int, k: int, waves: int, split: int):
+    """(rb, xstage flags) of every compiled plan at this K order: staged activations or not, and where the
+    straight-line kernel of the segment count applies, that kernel or the general loop (XS_GENERAL)."""
+    fixed = S.segments_per_wave(kind, k, waves, split) > 0
     for rb in RBS:
-        for xs in (0, 1):
-            if xs and (m > 16 or S._stage_bytes(kind, m, k, split) < 0):
+        for xs in (0, S.XS_STAGE, S.XS_GENERAL, S.XS_STAGE | S.XS_GENERAL):
+            if xs & S.XS_STAGE and (m > 16 or S._stage_bytes(kind, m, k, split) < 0):
                 continue
-            if S._supported(kind, m, rb, waves, xs):
+            if xs & S.XS_GENERAL and not fixed:
+                continue
+            if S._supported(kind, m, rb, waves, xs & S.XS_STAGE):
                 yield rb, xs
 
 
@@ -202,9 +208,11 @@ def main(argv=None) -> int:
     table = json.loads(out.read_text()) if out.exists() else {}
     table["_about"] = ("skinny kernel configurations for gfx950, tuned by python -m byteprof_amd.tune. kind|N|K "
                        "(bf16, int8): waves and split of the matrix-core kernel (they fix the K order for every row "
-                       "count), rb = 8-row weight blocks per workgroup and xs = activations staged in LDS, per "
-                       "row bucket (1, 8, 16, 32, 64), us = measured time per call by row count (ring of "
-                       "distinct weights, HIP graph); int4|N|K: waves and split of the int4 kernel (tile rows 32).")
+                       "count), rb = 8-row weight blocks per workgroup and xs = xstage flags (1: activations "
+                       "staged in LDS, 2: the general segment loop instead of the straight-line kernel of the "
+                       "segment count), per row bucket (1, 8, 16, 32, 64), us = measured time per call by row count "
+                       "(ring of distinct weights, HIP graph); int4|N|K: waves and split of the int4 kernel (tile "
+                       "rows 32).")
     log = lambda m: print(m, flush=True)  # noqa: E731
     for kind in a.kinds.split(","):
         for n, k in shapes:

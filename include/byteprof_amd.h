@@ -56,18 +56,22 @@ size_t bp_skinny_workspace_bytes(int64_t M, int64_t N, int split);
  * the segment's K slots). Tile configuration: rb = 8-row weight blocks per workgroup (1, 2, 4; 4 up to M = 16),
  * waves = wavefronts sharing the workgroup's K segments (1, 2, 4, 8; segment s to wave s % waves), split = K ranges
  * in separate workgroups whose fp32 partials are added in split order by a second kernel (workspace as for
- * bp_skinny_workspace_bytes), xstage = 1: each workgroup copies its activation rows and K range to LDS first (up to M = 16 and
- * bp_skinny_mf_stage_bytes() >= 0), 0: the activation operands are loaded with the weights. The K order of every sum
- * depends only on (K, waves, split): output row i is bitwise independent of M (1..64), rb and xstage. K not a
- * multiple of the 128-byte segment (64 bf16 / 128 int8 elements) or x, w not 16-byte aligned: an element-load variant
- * with the same segments (rb 1, 4 waves, xstage 0).
+ * bp_skinny_workspace_bytes), xstage: flags BP_XS_STAGE (each workgroup copies its activation rows and K range to
+ * LDS first; up to M = 16 and bp_skinny_mf_stage_bytes() >= 0; else the activation operands are loaded with the
+ * weights) and BP_XS_GENERAL (the general segment loop; without it, a launch whose waves have exactly 4, 8 or 16
+ * segments each runs a straight-line kernel for that count). The K order of every sum depends only on (K, waves,
+ * split): output row i is bitwise independent of M (1..64), rb and xstage. K not a multiple of the 128-byte segment
+ * (64 bf16 / 128 int8 elements) or x, w not 16-byte aligned: an element-load variant with the same segments (rb 1,
+ * 4 waves, xstage 0).
  * Replaces: byteprof/optim/skinny.py:36-90 (_skinny_kernel MODE 0 / 1, _split_reduce) and :111-133 (_launch) via
  *           skinny_mm (skinny.py:136-166) for every BM bucket (16, 32, 64); at M = 1 with int8 weights, the one-row
  *           int8 product byteprof/quant/triton_int8.py:16-47 (_gemv_int8, gemv_int8).
  */
+#define BP_XS_STAGE 1
+#define BP_XS_GENERAL 2
 int bp_skinny_mf_supported(int wkind, int M, int rb, int waves, int xstage);
 int bp_skinny_mf_k_segment(int wkind);
-/* LDS bytes a launch with xstage = 1 uses, or -1 when its activations do not fit (then xstage must be 0). */
+/* LDS bytes a launch with BP_XS_STAGE uses, or -1 when its activations do not fit (then the flag must be off). */
 int64_t bp_skinny_mf_stage_bytes(int wkind, int64_t M, int64_t K, int split);
 int bp_skinny_mf(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y, int64_t M,
                  int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* workspace,

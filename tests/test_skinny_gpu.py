@@ -243,3 +243,46 @@ def test_every_configuration_matches_the_oracle(kind, k):
             if err > 4e-3:
                 bad.append((m, rb, waves, split, xs, err))
     assert not bad, bad[:10]
+
+
+# (N, K, rows, waves, split): launches whose waves have exactly 4, 8 or 16 K segments (the straight-line kernels),
+# with full and partial last row blocks
+FIXED_PLANS = [(2048, 2048, 8, 4, 1), (6144, 2048, 8, 2, 1), (2050, 2048, 16, 8, 1), (1000, 8192, 8, 8, 1),
+               (1000, 8192, 32, 4, 2), (300, 4096, 8, 2, 4), (520, 2048, 8, 1, 1)]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n,k,rows,waves,split", FIXED_PLANS)
+def test_straight_line_kernel_equals_the_general_loop(kind, n, k, rows, waves, split):
+    """A launch whose waves all have 4, 8 or 16 segments runs the straight-line kernel of that count; with
+    BP_XS_GENERAL the same plan runs the general segment loop. Same segments in the same order: equal bit for bit,
+    with and without the LDS-staged activations, at 1..33 rows; and within the oracle's tolerance."""
+    from byteprof_amd import _lib
+
+    L = _lib.lib()
+    _, args = make_weights(kind, n, k, seed=n + k + waves)
+    w_np = oracle_weights(kind, args)
+    x = randn_x(33, k, seed=3)
+    kc = S._KIND_CODE[kind]
+    sc, sdt = (args[1].data_ptr(), _lib.TORCH_DT[args[1].dtype]) if kind == "int8" else (None, 0)
+    rb = rows // 8
+    fixed_seen = False
+    for m in (1, 2, 5, 9, 16, 33):
+        xm = x[:m].contiguous()
+        ws = torch.empty(max(1, split * m * n), dtype=torch.float32, device="cuda")
+        outs = []
+        for xs in (0, S.XS_GENERAL, S.XS_STAGE, S.XS_STAGE | S.XS_GENERAL):
+            if xs & S.XS_STAGE and (m > 16 or S._stage_bytes(kind, m, k, split) < 0):
+                continue
+            r = rb if m <= 16 else min(rb, 2)
+            y = torch.full((m, n), 7.0, dtype=torch.bfloat16, device="cuda")
+            _lib.check(L.bp_skinny_mf(kc, xm.data_ptr(), args[0].data_ptr(), sc, sdt, y.data_ptr(), m, n, k, r, waves,
+                                      split, xs, ws.data_ptr(), ws.numel() * 4, _lib.stream_ptr(xm.device)), "mf")
+            outs.append(y)
+            fixed_seen |= S.segments_per_wave(kind, k, waves, split, xs) > 0
+        torch.cuda.synchronize()
+        for y in outs[1:]:
+            assert torch.equal(y.view(torch.int16), outs[0].view(torch.int16)), (m, kind, n, k)
+        check_against_oracle(outs[0], xm, w_np)
+    # bf16 covers 4 / 8 / 16 segments per wave over these plans, int8 4 / 8 / 16 (the others run the general loop)
+    assert fixed_seen == (S.segments_per_wave(kind, k, waves, split) > 0)
