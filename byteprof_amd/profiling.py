@@ -80,10 +80,10 @@ def _short(name: str) -> str:
 
 def summarize(a) -> int:
     print("## kernel trace (rocprofv3 --kernel-trace --stats)")
-    print(f"{'kernel':<48} {'grid threads':>12} {'calls':>7} {'total us':>11} {'avg us':>9} {'median us':>10}")
+    print(f"{'kernel':<72} {'grid threads':>12} {'calls':>7} {'total us':>11} {'avg us':>9} {'median us':>10}")
     for name, grid, calls, tot, avg, med in _kernel_stats(a.db):
         if a.all or "bp::" in name:
-            print(f"{_short(name)[:48]:<48} {grid:>12} {calls:>7} {tot:>11.1f} {avg:>9.3f} {med:>10.3f}")
+            print(f"{_short(name)[:72]:<72} {grid:>12} {calls:>7} {tot:>11.1f} {avg:>9.3f} {med:>10.3f}")
     for db in a.pmc or []:
         print()
         print(f"## counters per dispatch ({db.split('/')[-2] if '/' in db else db})")
@@ -103,7 +103,7 @@ def summarize(a) -> int:
     print(f"copy: FETCH_SIZE {fetch_copy:.1f} KiB -> scale {f_scale:.4f}; WRITE_SIZE {write_copy:.1f} KiB "
           f"-> scale {w_scale:.4f}")
     fetch, write = _counter_avgs(a.fetch), _counter_avgs(a.write)
-    print(f"{'kernel':<48} {'grid threads':>12} {'dispatches':>10} {'FETCH KiB':>11} {'WRITE KiB':>10} "
+    print(f"{'kernel':<72} {'grid threads':>12} {'dispatches':>10} {'FETCH KiB':>11} {'WRITE KiB':>10} "
           f"{'traffic MB':>11}")
     for key in sorted(fetch):
         name, grid = key
@@ -112,7 +112,7 @@ def summarize(a) -> int:
         _, k, fv = fetch[key]
         wv = write.get(key, ("", 0, 0.0))[2]
         traffic = (fv * f_scale + wv * w_scale) * 1024 / 1e6
-        print(f"{_short(name)[:48]:<48} {grid:>12} {k:>10} {fv:>11.1f} {wv:>10.1f} {traffic:>11.3f}")
+        print(f"{_short(name)[:72]:<72} {grid:>12} {k:>10} {fv:>11.1f} {wv:>10.1f} {traffic:>11.3f}")
     if a.chain_tag:
         kernel = "chain_kernel"
         print()
