@@ -40,7 +40,6 @@ __device__ __forceinline__ uint32_t i8pair_to_bf16x2(uint32_t d, int sh) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-// Load a scale element of the given dtype code as fp32 (0 = bf16, 1 = fp16, 2 = fp32).
 // Global-memory views of generic pointers. Pointers read from memory (not kernel arguments) are otherwise
 // accessed with flat instructions, which also count against the LDS wait counter, so every LDS access would wait
 // for all outstanding memory loads.
@@ -55,52 +54,7 @@ __device__ __forceinline__ gptr<T> as_global_mut(T* p) {
   return (gptr<T>)(p);
 }
 
-// Sum of squares of n values (read through at(i)) in a fixed order that one 64-lane wave computes alone: lane l adds,
-// in order, the squares of elements 256 j + 4 l + e (j = 0, 1, ...; e = 0 .. 3; elements past n left out), then
-// the lanes are added by an xor butterfly (lane distance 32, 16, ..., 1). Every lane of every wave that runs it
-// gets the same total, so the RMS norms of the decode step (separate or inside a linear's launch) and the
-// renormalisations of the linear set agree bit for bit whatever their workgroup shapes.
-template <class At>
-__device__ __forceinline__ float wave_sumsq(const At& at, int n) {
-  const int lane = static_cast<int>(threadIdx.x) & 63;
-  float s = 0.f;
-  for (int base = 4 * lane; base < n; base += 256) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (base + e < n) {
-        const float f = at(base + e);
-        s += f * f;
-      }
-    }
-  }
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-  return s;
-}
-
-// wave_sumsq of a bf16 row in LDS (8-byte aligned), four elements per read: the same additions in the same order.
-__device__ __forceinline__ float wave_sumsq_lds(const uint16_t* row, int n) {
-  const int lane = static_cast<int>(threadIdx.x) & 63;
-  float s = 0.f;
-  for (int base = 4 * lane; base < n; base += 256) {
-    if (base + 4 <= n) {
-      const uint2 q = *reinterpret_cast<const uint2*>(row + base);
-      const float f0 = __uint_as_float(q.x << 16), f1 = __uint_as_float(q.x & 0xffff0000u);
-      const float f2 = __uint_as_float(q.y << 16), f3 = __uint_as_float(q.y & 0xffff0000u);
-      s += f0 * f0;
-      s += f1 * f1;
-      s += f2 * f2;
-      s += f3 * f3;
-    } else {
-      for (int e = 0; base + e < n; ++e) {
-        const float f = bf16_bits_to_float(row[base + e]);
-        s += f * f;
-      }
-    }
-  }
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-  return s;
-}
-
+// Load a scale element of the given dtype code as fp32 (0 = bf16, 1 = fp16, 2 = fp32).
 __device__ __forceinline__ float load_scale(const void* p, int64_t i, int dt) {
   if (dt == 0) return bf16_bits_to_float(as_global(static_cast<const uint16_t*>(p))[i]);
   if (dt == 1) return static_cast<float>(as_global(static_cast<const _Float16*>(p))[i]);
@@ -157,6 +111,99 @@ __device__ __forceinline__ void wave_transpose_reduce(float* v, int lane) {
   reduce_stage<(P > 8 ? P / 8 : 1), 4>(v, lane);
   reduce_stage<(P > 16 ? P / 16 : 1), 2>(v, lane);
   reduce_stage<(P > 32 ? P / 32 : 1), 1>(v, lane);
+}
+
+// One stage of an xor butterfly without LDS traffic: op(v, v of lane l ^ D) for a commutative op, so every lane
+// gets exactly what `op(v, __shfl_xor(v, D))` gives. D = 32, 16: a v_permlane{32,16}_swap of two copies of v
+// (one result register holds the lane's own value, the other its partner's); D = 8: row_ror:8; D = 4: row_shl:4
+// into the lanes with bit 2 clear and row_shr:4 into the others (bank masks); D = 2, 1: quad permutations.
+template <int D, class Op>
+__device__ __forceinline__ float xor_stage(float v, Op op) {
+  if constexpr (D == 32 || D == 16) {
+    const auto r = D == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                           : __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else if constexpr (D == 4) {
+    const float lo_recv = dpp_f32<0x104, 0xF, 0x5>(v);
+    return op(v, dpp_f32<0x114, 0xF, 0xA>(v, lo_recv));
+  } else {
+    static_assert(D == 8 || D == 2 || D == 1, "xor distance");
+    return op(v, dpp_f32<D == 8 ? 0x128 : D == 2 ? 0x4E : 0xB1>(v));
+  }
+}
+
+struct AddOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// Butterfly over the lane bits D_LO .. 32 (D_LO a power of two): the stages of `for (o = D_LO; o < 64; o <<= 1)
+// v = op(v, __shfl_xor(v, o))` in that order, and D_LO = 1 in the order 32, 16, ..., 1 when DOWN (the usual
+// whole-wave reduction, every lane ends with the total).
+template <bool DOWN, int D_LO = 1, class Op>
+__device__ __forceinline__ float xor_butterfly(float v, Op op) {
+  if constexpr (DOWN) {
+    v = xor_stage<32>(v, op);
+    v = xor_stage<16>(v, op);
+    v = xor_stage<8>(v, op);
+    v = xor_stage<4>(v, op);
+    v = xor_stage<2>(v, op);
+    return xor_stage<1>(v, op);
+  } else {
+    if constexpr (D_LO <= 1) v = xor_stage<1>(v, op);
+    if constexpr (D_LO <= 2) v = xor_stage<2>(v, op);
+    if constexpr (D_LO <= 4) v = xor_stage<4>(v, op);
+    if constexpr (D_LO <= 8) v = xor_stage<8>(v, op);
+    if constexpr (D_LO <= 16) v = xor_stage<16>(v, op);
+    return xor_stage<32>(v, op);
+  }
+}
+
+// Sum of squares of a bf16 row of n elements in LDS (8-byte aligned), in a fixed order that one 64-lane wave
+// computes alone: lane l adds, in order, the squares of elements 256 j + 4 l + e (j = 0, 1, ...; e = 0 .. 3;
+// elements past n left out), then the lanes are added by a butterfly pairing lane l with lane l ^ d for d = 32,
+// 16, ..., 1 (wave_transpose_reduce: permlane swaps and DPP, no LDS round trips). Every lane of every wave that runs
+// it gets the same total, so the RMS norms of the decode step (separate or inside a linear's launch) and the
+// renormalisations of the linear set agree bit for bit whatever their workgroup shapes. The reads of eight steps
+// are issued before their squares are added (the additions stay in order).
+__device__ __forceinline__ float wave_sumsq_lds(const uint16_t* row, int n) {
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  float s = 0.f;
+  int base = 4 * lane;
+  for (; base + 7 * 256 + 4 <= n; base += 8 * 256) {
+    uint2 q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = *reinterpret_cast<const uint2*>(row + base + 256 * j);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f0 = __uint_as_float(q[j].x << 16), f1 = __uint_as_float(q[j].x & 0xffff0000u);
+      const float f2 = __uint_as_float(q[j].y << 16), f3 = __uint_as_float(q[j].y & 0xffff0000u);
+      s += f0 * f0;
+      s += f1 * f1;
+      s += f2 * f2;
+      s += f3 * f3;
+    }
+  }
+  for (; base < n; base += 256) {
+    if (base + 4 <= n) {
+      const uint2 q = *reinterpret_cast<const uint2*>(row + base);
+      const float f0 = __uint_as_float(q.x << 16), f1 = __uint_as_float(q.x & 0xffff0000u);
+      const float f2 = __uint_as_float(q.y << 16), f3 = __uint_as_float(q.y & 0xffff0000u);
+      s += f0 * f0;
+      s += f1 * f1;
+      s += f2 * f2;
+      s += f3 * f3;
+    } else {
+      for (int e = 0; base + e < n; ++e) {
+        const float f = bf16_bits_to_float(row[base + e]);
+        s += f * f;
+      }
+    }
+  }
+  wave_transpose_reduce<1>(&s, lane);
+  return s;
 }
 
 // Sum of v over the 64 lanes with DPP moves only (no LDS traffic): pairs within quads, quads within half-rows,

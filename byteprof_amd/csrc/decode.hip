@@ -32,7 +32,7 @@ constexpr int kAttnMaxLen = 4096;  // positions a cache may hold (scores in LDS)
 
 // Sum of v over the workgroup (blockDim.x a multiple of 64, at most kBlock); every thread gets the total.
 __device__ float block_sum(float v, float* red) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  v = xor_butterfly<true>(v, AddOp{});
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, waves = blockDim.x / kWave;
   __syncthreads();  // red may still be read by a previous call
   if (lane == 0) red[wave] = v;
@@ -43,7 +43,7 @@ __device__ float block_sum(float v, float* red) {
 }
 
 __device__ float block_max(float v, float* red) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  v = xor_butterfly<true>(v, MaxOp{});
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, waves = blockDim.x / kWave;
   __syncthreads();
   if (lane == 0) red[wave] = v;
@@ -88,19 +88,13 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (LPR >= 4) v += dpp_f32<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
   if constexpr (LPR >= 8) v += dpp_f32<0x141, 0xF>(v);  // row_half_mirror
   if constexpr (LPR >= 16) v += dpp_f32<0x140, 0xF>(v); // row_mirror
-  if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
+  if constexpr (LPR >= 32) v = xor_stage<16>(v, AddOp{});
   return v;
 }
 
-// Sum (or maximum) of v over the wave, returned to every lane.
-__device__ __forceinline__ float wave_sum(float v) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
+// Sum (or maximum) of v over the wave, returned to every lane (an xor butterfly, distances 32 .. 1).
+__device__ __forceinline__ float wave_sum(float v) { return xor_butterfly<true>(v, AddOp{}); }
+__device__ __forceinline__ float wave_max(float v) { return xor_butterfly<true>(v, MaxOp{}); }
 
 constexpr int kAttnWaves = kAttnThreads / kWave;
 
@@ -231,10 +225,7 @@ struct HeadAttention {
     }
     // the wave's row groups (lanes s, s + LPR, s + 2 LPR, ...) added by butterflies over the group bits
 #pragma unroll
-    for (int o = LPR; o < kWave; o <<= 1) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
-    }
+    for (int e = 0; e < 8; ++e) acc[e] = xor_butterfly<false, LPR>(acc[e], AddOp{});
     if (lane < LPR) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) part[wave * D + 8 * s + e] = acc[e];

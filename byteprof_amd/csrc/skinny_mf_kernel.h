@@ -37,15 +37,23 @@ namespace {
 //   BP_PRO_UNIT_RMS: x <- bf16(x * (1 / sqrt(mean(x^2)))) (an all-zero row is left as is);
 //   BP_PRO_NORM:     x <- bf16(residual + bf16(gamma * (x * (1 / sqrt(mean(x^2) + eps))))) (no residual: the plain
 //                    norm), and workgroup (0, 0) writes the rows to xout.
-// The mean square is wave_sumsq's (common.h), which every wave computes from the staged row, so the fused norm
-// equals the separate norm launch (decode.hip, norm_residual_kernel) bit for bit. gl (BP_PRO_NORM over one row,
-// else null): LDS copies of gamma [K] and the residual row [K], loaded ahead of the weights.
+// The mean square is wave_sumsq's (common.h), the same bits whichever wave computes it, so the fused norm equals
+// the separate norm launch (decode.hip, norm_residual_kernel) bit for bit. Wave w sums rows w, w + waves, ... into
+// sums[] (LDS, one float per row); one barrier later every row is rewritten. gl (BP_PRO_NORM over one row, else
+// null): LDS copies of gamma [K] and the residual row [K], loaded ahead of the weights.
 template <int NT>
-__device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, bool writer, const uint16_t* gl) {
+__device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, bool writer, const uint16_t* gl,
+                            float* sums) {
+  constexpr int kWaves = NT / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  for (int m = wave; m < rows; m += kWaves) {
+    const float t = wave_sumsq_lds(xs + m * K, K);
+    if ((threadIdx.x & (kWave - 1)) == 0) sums[m] = t;
+  }
+  __syncthreads();  // every row's sum is in sums[] before any row is rewritten
   for (int m = 0; m < rows; ++m) {
     uint16_t* row = xs + m * K;
-    const float t = wave_sumsq_lds(row, K);
-    __syncthreads();  // every wave has read the row before it is rewritten
+    const float t = sums[m];
     if (pro.kind == BP_PRO_UNIT_RMS) {
       const float ms = t / static_cast<float>(K);
       const float inv = ms > 0.f ? 1.f / sqrtf(ms) : 1.f;
@@ -121,6 +129,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
   constexpr int D = VEC ? mf_depth<KIND, MB, RB, !XL>() : 1;
   constexpr int kInFlight = NSEG > 0 && NSEG < D ? NSEG : D;  // weight segments issued before the staging commit
   __shared__ MfRed<WAVES, RB, MB> red;
+  __shared__ float pro_sums[PRO ? 8 * MB : 1];  // the prologue's per-row sums of squares
   extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -192,7 +201,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
       if constexpr (PRO) {
         __syncthreads();
         if (pro.kind != 0)
-          mf_prologue<kNT>(xs_lds, mrows, kn, pro, blockIdx.x == 0 && blockIdx.y == 0, gl);
+          mf_prologue<kNT>(xs_lds, mrows, kn, pro, blockIdx.x == 0 && blockIdx.y == 0, gl, pro_sums);
       } else {
         for (int pass = 1; pass < passes; ++pass) {
           stage.issue(x, mrows, K, k_lo, kn, pass);
