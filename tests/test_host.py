@@ -394,3 +394,45 @@ def test_mlstm_head_dims_are_whole_waves():
     q = torch.zeros(1, 2, 320)
     with pytest.raises(NotImplementedError):
         F._geometry(q, torch.zeros(1, 2, 16), 4)
+
+
+# ---- the tuner's plan menu and table (byteprof_amd/tune.py) ------------------------------------------------------
+
+
+def test_tuner_plans_cover_the_compiled_menu_and_skip_duplicates():
+    """The tuner times (rb, xstage flags) plans that the library compiles: staging only where the rows fit the LDS
+    stage, the general-loop flag only where a straight-line kernel of the segment count exists (elsewhere both
+    flags run the same kernel)."""
+    from byteprof_amd import tune as T
+
+    fixed = list(T._plans("bf16", 1, 2048, 4, 1))    # 32 segments / 4 waves = 8 per wave: straight-line kernel
+    assert {xs for _, xs in fixed} == {0, S.XS_STAGE, S.XS_GENERAL, S.XS_STAGE | S.XS_GENERAL}
+    assert {rb for rb, _ in fixed} == {1, 2, 4}
+    general = list(T._plans("bf16", 1, 2048, 1, 1))  # 32 segments per wave: the general loop only
+    assert {xs for _, xs in general} == {0, S.XS_STAGE}
+    big = list(T._plans("bf16", 33, 2048, 4, 1))      # more than 16 rows: no staging, 4 blocks only up to 16 rows
+    assert {xs for _, xs in big} == {0, S.XS_GENERAL} and {rb for rb, _ in big} == {1, 2}
+    assert all(S._supported("bf16", m, rb, w, xs & S.XS_STAGE)
+               for m, w in ((1, 4), (1, 1), (33, 4)) for rb, xs in T._plans("bf16", m, 2048, w, 1))
+
+
+def test_tuned_table_entries_resolve_to_compiled_plans():
+    """Every bf16 / int8 entry of the committed table names one K order (waves, split) and, per row bucket, a
+    weight-block count and flags that the launch maps onto a compiled kernel; every int4 entry a valid plan."""
+    table = json.loads(S._CFG_FILE.read_text())
+    for key, e in table.items():
+        if key.startswith("_"):
+            continue
+        kind, n, k = key.split("|")
+        n, k = int(n), int(k)
+        if kind == "int4":
+            waves, split = S.int4_cfg(n, k, 32)
+            assert (waves, split) == (e["waves"], e["split"]) and waves in (1, 2, 4, 8) and 1 <= split <= k // 128
+            continue
+        assert e["waves"] in (1, 2, 4, 8) and e["split"] >= 1
+        for bucket in ("1", "8", "16", "32", "64"):
+            assert int(e["rb"][bucket]) in (1, 2, 4) and int(e["xs"][bucket]) in (0, 1, 2, 3)
+        for m in (1, 5, 8, 9, 16, 17, 33, 64):
+            rb, waves, split, xs = S._resolve(kind, n, k, m, None)
+            assert (waves, split) == (e["waves"], e["split"])
+            assert S._supported(kind, m, rb, waves, xs & S.XS_STAGE)
