@@ -121,6 +121,45 @@ def test_fused_rope_attention_rows_equal_the_two_launch_rows(shape, rows, base):
                                                     cfg.heads, D, 17, cfg.max_len, cfg.eps, D ** -0.5, _st()) != 0
 
 
+@pytest.mark.parametrize("shape,rows,base", [("d128", 2, 0), ("d128", 4, 8), ("d128", 4, 125), ("d128", 9, 126),
+                                             ("d128", 16, 250), ("d64", 3, 5), ("d256", 5, 120), ("d8", 4, 61)])
+def test_fused_rows_equal_the_fused_one_row_steps(shape, rows, base):
+    """rope_attention_rows over rows at base against rope_attention called at base, base + 1, ... in turn (the
+    drafting loop against the one-token loop, directly): outputs and caches equal bit for bit, and a second
+    one-row pass over the same inputs gives the same bits (no race in the launch)."""
+    cfg = ROWS_CFGS[shape]
+    oc = _ocfg(cfg)
+    L = _lib.lib()
+    H, D = cfg.hidden, cfg.head_dim
+    rng = np.random.default_rng(rows * 7 + base)
+    qkv = _bf16(ON.bf16_round(rng.standard_normal((rows, 3 * H)).astype(np.float32)))
+    qw, kw = (_bf16(ON.bf16_round(1 + 0.1 * rng.standard_normal(H).astype(np.float32))) for _ in range(2))
+    cache0 = ON.bf16_round(rng.standard_normal((cfg.heads, cfg.max_len, D)).astype(np.float32))
+    inv = torch.from_numpy(OO.inv_freq(oc)).to(DEV)
+    kc_a, vc_a = _bf16(cache0), _bf16(cache0)
+    o_a = torch.empty(rows, H, dtype=torch.bfloat16, device=DEV)
+    pos = torch.tensor([base], dtype=torch.int64, device=DEV)
+    _lib.check(L.bp_decode_rope_attention_rows(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), inv.data_ptr(),
+                                               pos.data_ptr(), kc_a.data_ptr(), vc_a.data_ptr(), o_a.data_ptr(),
+                                               cfg.heads, D, rows, cfg.max_len, cfg.eps, D ** -0.5, _st()), "rows")
+    outs = []
+    for _ in range(2):
+        kc_b, vc_b = _bf16(cache0), _bf16(cache0)
+        o_b = torch.empty(rows, H, dtype=torch.bfloat16, device=DEV)
+        for r in range(rows):
+            p = torch.tensor([base + r], dtype=torch.int64, device=DEV)
+            _lib.check(L.bp_decode_rope_attention(qkv[r].data_ptr(), qw.data_ptr(), kw.data_ptr(), inv.data_ptr(),
+                                                  p.data_ptr(), kc_b.data_ptr(), vc_b.data_ptr(), o_b[r].data_ptr(),
+                                                  cfg.heads, D, cfg.max_len, cfg.eps, D ** -0.5, _st()), "one")
+        outs.append((o_b, kc_b, vc_b))
+    torch.cuda.synchronize()
+    for o_b, kc_b, vc_b in outs:
+        for r in range(rows):
+            assert torch.equal(o_a[r].view(torch.int16), o_b[r].view(torch.int16)), f"row {r}"
+        assert torch.equal(kc_a.view(torch.int16), kc_b.view(torch.int16))
+        assert torch.equal(vc_a.view(torch.int16), vc_b.view(torch.int16))
+
+
 @pytest.mark.parametrize("plan", [(1, 4, 0), (2, 2, 0), (4, 8, 0), (1, 4, 1)])
 @pytest.mark.parametrize("m", [1, 5, 9, 16])
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
