@@ -33,6 +33,9 @@ def hipcc() -> str:
 
 def common_flags() -> list[str]:
     return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", f"-I{INCLUDE}", f"-I{CSRC}",
+            # a multiply and an add fuse only where one expression writes them (a * b + c), never across
+            # statements or inlined calls: kernels that share arithmetic and must agree bit for bit round alike
+            "-ffp-contract=on",
             # no packed-fp32 VALU instructions in device code
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 

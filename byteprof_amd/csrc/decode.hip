@@ -123,22 +123,19 @@ struct HeadAttention {
     slot = wave * RPW + lane / LPR;  // this lane's row within a batch
   }
 
-  // Rows at or past limit load row limit - 1 (in bounds, not used): the loads are not conditional, so that the
-  // waits for loads issued before them count exactly.
-  __device__ __forceinline__ void load_batch(const uint16_t* base, int t0, int limit,
-                                             u32x4 (&out)[kAttnUnroll]) const {
+  __device__ __forceinline__ void load_batch(const uint16_t* base, int t0, u32x4 (&out)[kAttnUnroll]) const {
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
       const int t = t0 + u * STEP + slot;
-      out[u] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(t < limit ? t : limit - 1) * D + 8 * s);
+      out[u] = u32x4{0u, 0u, 0u, 0u};
+      if (t < T) out[u] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(t) * D + 8 * s);
     }
   }
 
-  // Issues the loads of the first batch of K and V rows: rows below T, or below limit (>= T, e.g. the cache
-  // length, before T is known: the rows past T are loaded and not used).
-  __device__ __forceinline__ void prefetch(int limit = 0) {
-    load_batch(K, 0, limit > 0 ? limit : T, k0);
-    load_batch(V, 0, limit > 0 ? limit : T, v0);
+  // Issues the loads of the first batch of K and V rows.
+  __device__ __forceinline__ void prefetch() {
+    load_batch(K, 0, k0);
+    load_batch(V, 0, v0);
   }
 
   __device__ __forceinline__ void scores(const u32x4 (&kv)[kAttnUnroll], int t0, const float (&qv)[8],
@@ -197,7 +194,7 @@ struct HeadAttention {
     scores(k0, 0, qv, ksub, sub_lo, scale, sc, m);
     for (int t0 = BATCH; t0 < T; t0 += BATCH) {
       u32x4 kv[kAttnUnroll];
-      load_batch(K, t0, T, kv);
+      load_batch(K, t0, kv);
       scores(kv, t0, qv, ksub, sub_lo, scale, sc, m);
     }
     m = wave_max(m);
@@ -223,7 +220,7 @@ struct HeadAttention {
     values(v0, 0, vsub, sub_lo, sc, inv, acc);
     for (int t0 = BATCH; t0 < T; t0 += BATCH) {
       u32x4 vv[kAttnUnroll];
-      load_batch(V, t0, T, vv);
+      load_batch(V, t0, vv);
       values(vv, t0, vsub, sub_lo, sc, inv, acc);
     }
     // the wave's row groups (lanes s, s + LPR, s + 2 LPR, ...) added by butterflies over the group bits
@@ -244,111 +241,68 @@ struct HeadAttention {
 
 constexpr int kAttnPart = kAttnWaves * 256;  // floats of the value partials: waves x D (D <= 256)
 
-// Sum of squares of 8 bf16 values added to acc in order.
-__device__ __forceinline__ float sumsq8(const u32x4& a, float acc) {
-  const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+// 1 / rms of q[0 .. H) and of k[0 .. H) (+ eps inside the root), by a kAttnThreads-thread workgroup: thread t sums
+// the squares of elements 8t .. 8t + 7 (then + 8 * kAttnThreads ...) in order, each wave by a butterfly, the waves in
+// order. Both attention paths use it, so their q and k are equal bit for bit.
+__device__ __forceinline__ void qk_rms(const uint16_t* q, const uint16_t* k, int H, float eps, float* red_q,
+                                       float* red_k, float& rq, float& rk) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  float sq = 0.f, sk = 0.f;
+  for (int i = 8 * threadIdx.x; i < H; i += 8 * kAttnThreads) {
+    const u32x4 qa = *reinterpret_cast<const u32x4*>(q + i);
+    const u32x4 ka = *reinterpret_cast<const u32x4*>(k + i);
+    const uint32_t qd[4] = {qa.x, qa.y, qa.z, qa.w}, kd[4] = {ka.x, ka.y, ka.z, ka.w};
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float x0 = bf16_bits_to_float(d[e] & 0xffffu), x1 = bf16_bits_to_float(d[e] >> 16);
-    acc += x0 * x0;
-    acc += x1 * x1;
-  }
-  return acc;
-}
-
-// 1 / rms of q[0 .. H) and of k[0 .. H) (+ eps inside the root), by a kAttnThreads-thread workgroup, in this order:
-// thread t adds the squares of elements 8t .. 8t + 7 (then + 8 * kAttnThreads ...) in order, each wave's threads
-// are added by a butterfly, then the waves in order. With SPLIT (H <= 4 * kAttnThreads: at most one chunk per
-// thread in half the workgroup) waves 0 .. 3 take q's chunks and waves 4 .. 7 k's, which gives the same sums (the
-// waves left without chunks only added zeros) with one load and one reduction per thread; load() then issues that
-// load unconditionally (a thread without a chunk loads chunk 0 and adds nothing), so that nothing waits for it
-// early. finish() reduces (one barrier), and loads the chunks itself without SPLIT. Every attention path uses it,
-// so their q and k agree bit for bit.
-template <bool SPLIT>
-struct QkNorm {
-  static constexpr int kHalf = kAttnThreads / 2;
-  u32x4 chunk;
-  bool has;
-
-  __device__ __forceinline__ void load(const uint16_t* q, const uint16_t* k, int H) {
-    if constexpr (SPLIT) {
-      const int c = threadIdx.x % kHalf;
-      has = 8 * c < H;
-      chunk = *reinterpret_cast<const u32x4*>((threadIdx.x < kHalf ? q : k) + (has ? 8 * c : 0));
+    for (int e = 0; e < 4; ++e) {
+      const float q0 = bf16_bits_to_float(qd[e] & 0xffffu), q1 = bf16_bits_to_float(qd[e] >> 16);
+      const float k0 = bf16_bits_to_float(kd[e] & 0xffffu), k1 = bf16_bits_to_float(kd[e] >> 16);
+      sq += q0 * q0;
+      sq += q1 * q1;
+      sk += k0 * k0;
+      sk += k1 * k1;
     }
   }
-
-  __device__ __forceinline__ void finish(const uint16_t* q, const uint16_t* k, int H, float eps, float* red_q,
-                                         float* red_k, float& rq, float& rk) const {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    float a, b;
-    if constexpr (SPLIT) {
-      const float t = wave_sum(has ? sumsq8(chunk, 0.f) : 0.f);
-      if (lane == 0) red_q[wave] = t;
-      __syncthreads();
-      constexpr int kW = kAttnWaves / 2;
-      a = red_q[0];
-      b = red_q[kW];
-      for (int w = 1; w < kW; ++w) {
-        a += red_q[w];
-        b += red_q[kW + w];
-      }
-    } else {
-      float sq = 0.f, sk = 0.f;
-      for (int i = 8 * threadIdx.x; i < H; i += 8 * kAttnThreads) {
-        sq = sumsq8(*reinterpret_cast<const u32x4*>(q + i), sq);
-        sk = sumsq8(*reinterpret_cast<const u32x4*>(k + i), sk);
-      }
-      const float tq = wave_sum(sq), tk = wave_sum(sk);
-      if (lane == 0) {
-        red_q[wave] = tq;
-        red_k[wave] = tk;
-      }
-      __syncthreads();
-      a = red_q[0];
-      b = red_k[0];
-      for (int w = 1; w < kAttnWaves; ++w) {
-        a += red_q[w];
-        b += red_k[w];
-      }
-    }
-    rq = 1.f / sqrtf(a / static_cast<float>(H) + eps);
-    rk = 1.f / sqrtf(b / static_cast<float>(H) + eps);
+  sq = wave_sum(sq);
+  sk = wave_sum(sk);
+  if (lane == 0) {
+    red_q[wave] = sq;
+    red_k[wave] = sk;
   }
-};
-
-// Whether QkNorm's SPLIT order applies to H = heads * head_dim.
-inline bool qk_split(int H) { return H <= 4 * kAttnThreads; }
-
-// cos and sin of the RoPE angle inv_freq * pos (fp32).
-__device__ __forceinline__ void rope_angle(float fr, int64_t pos, float& c, float& sn) {
-  sincosf(fr * static_cast<float>(pos), &sn, &c);
+  __syncthreads();
+  sq = red_q[0];
+  sk = red_k[0];
+  for (int w = 1; w < kAttnWaves; ++w) {
+    sq += red_q[w];
+    sk += red_k[w];
+  }
+  rq = 1.f / sqrtf(sq / static_cast<float>(H) + eps);
+  rk = 1.f / sqrtf(sk / static_cast<float>(H) + eps);
 }
 
-// The RoPE pair (a, a + D/2) of head h: q and k normalised (weights in fp32, bf16 rounding), rotated with the
-// pair's fp32 cos / sin (x c - y s and y c + x s as one fused multiply-add over a rounded product, spelled out so
-// that every kernel that inlines it rounds alike); returns the rotated q as bf16 values and k as bf16 bits.
+// The RoPE pair (a, a + D/2) of head h at position pos: q and k normalised (weights in fp32, bf16 rounding), rotated
+// with fp32 cos / sin; returns the rotated q as bf16 values and k as bf16 bits.
 struct RopePair {
   float qa, qb;
   uint16_t ka, kb;
 };
 __device__ __forceinline__ RopePair rope_pair(float fqa, float fqb, float fka, float fkb, float wqa, float wqb,
-                                              float wka, float wkb, float c, float sn, float rq, float rk) {
+                                              float wka, float wkb, float fr, int64_t pos, float rq, float rk) {
+  const float f = fr * static_cast<float>(pos);
+  const float c = cosf(f), sn = sinf(f);
   const float qa = round_to_bf16(wqa * (fqa * rq));
   const float qb = round_to_bf16(wqb * (fqb * rq));
   const float ka = round_to_bf16(wka * (fka * rk));
   const float kb = round_to_bf16(wkb * (fkb * rk));
   RopePair r;
-  r.qa = round_to_bf16(fmaf(qa, c, -(qb * sn)));
-  r.qb = round_to_bf16(fmaf(qb, c, qa * sn));
-  r.ka = float_to_bf16_bits(fmaf(ka, c, -(kb * sn)));
-  r.kb = float_to_bf16_bits(fmaf(kb, c, ka * sn));
+  r.qa = round_to_bf16(qa * c + (-qb) * sn);
+  r.qb = round_to_bf16(qb * c + qa * sn);
+  r.ka = float_to_bf16_bits(ka * c + (-kb) * sn);
+  r.kb = float_to_bf16_bits(kb * c + ka * sn);
   return r;
 }
 
-// grid = rows: row r of qkv [rows, 3H] at position *pos_p + r: q, k normalised over the whole projection (QkNorm)
+// grid = rows: row r of qkv [rows, 3H] at position *pos_p + r: q, k normalised over the whole projection (qk_rms)
 // and rotated (rope_pair) for every head; q -> q_out[r]; k, v -> the caches at that position (if inside them).
-template <bool SPLIT>
 __global__ __launch_bounds__(kAttnThreads) void qk_rope_cache_kernel(const uint16_t* __restrict__ qkv,
                                                                      const uint16_t* __restrict__ qw,
                                                                      const uint16_t* __restrict__ kw,
@@ -367,17 +321,13 @@ __global__ __launch_bounds__(kAttnThreads) void qk_rope_cache_kernel(const uint1
   const uint16_t* k = q + H;
   const uint16_t* v = q + 2 * H;
   uint16_t* qo = q_out + static_cast<int64_t>(r) * H;
-  QkNorm<SPLIT> norm;
-  norm.load(q, k, H);
   float rq, rk;
-  norm.finish(q, k, H, eps, red_q, red_k, rq, rk);
+  qk_rms(q, k, H, eps, red_q, red_k, rq, rk);
   for (int i = threadIdx.x; i < H / 2; i += kAttnThreads) {
     const int h = i / half, j = i % half;
     const int a = h * D + j, b = a + half;
-    float c, sn;
-    rope_angle(inv_freq[j], pos, c, sn);
     const RopePair rp = rope_pair(ld_bf16(q, a), ld_bf16(q, b), ld_bf16(k, a), ld_bf16(k, b), ld_bf16(qw, a),
-                                  ld_bf16(qw, b), ld_bf16(kw, a), ld_bf16(kw, b), c, sn, rq, rk);
+                                  ld_bf16(qw, b), ld_bf16(kw, a), ld_bf16(kw, b), inv_freq[j], pos, rq, rk);
     qo[a] = float_to_bf16_bits(rp.qa);
     qo[b] = float_to_bf16_bits(rp.qb);
     if (in_cache) {
@@ -417,14 +367,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const uint16_t*
 }
 
 // qk_rope_cache and attention in one launch: every workgroup h computes the q / k norms over the whole projections
-// (the same sums in every workgroup, QkNorm's order: the results are equal bit for bit to the two launches), rotates
-// its own head (the first D/2 threads, one pair each), writes its k and v at pos to the cache, and attends over
-// positions 0 .. pos with that row taken from LDS. Every load is unconditional (so the waits count exactly) and
-// issued in the order it is needed: the pairs' inv_freq, the head's RoPE operands (one 16-byte chunk per thread,
-// staged in LDS), the norms' chunks, then the first batch of cache rows, before the position has arrived (rows
-// up to the batch or the cache length; those past the position are not used); the pairs' cos / sin are computed
-// while those loads are in flight.
-template <int LPR, bool SPLIT>
+// (the same sums in every workgroup, in qk_rope_cache_kernel's order: the results are equal bit for bit to the two
+// launches), rotates its own head, writes its k and v at pos to the cache, and attends over positions
+// 0 .. pos with that row taken from LDS. Every load that does not depend on the norms (the projections, the RoPE
+// operands, the first batch of cache rows) is issued before the first reduction.
+template <int LPR>
 __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint16_t* __restrict__ qkv,
                                                                       const uint16_t* __restrict__ qw,
                                                                       const uint16_t* __restrict__ kw,
@@ -442,61 +389,57 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint
   __shared__ __align__(16) uint16_t vs[D];
   __shared__ float red_q[kAttnWaves], red_k[kAttnWaves], red_m[kAttnWaves], red_l[kAttnWaves];
   __shared__ float part[kAttnPart];
-  __shared__ u32x4 ops[6 * D / 8];
   const int h = blockIdx.x;
   const int H = heads * D;
-  const uint16_t* q = qkv;
-  const uint16_t* k = qkv + H;
-  const uint16_t* v = qkv + 2 * H;
-
-  // Head h's slices of q, k, v, the two norm weights and inv_freq, one 16-byte chunk per thread (kOps chunks;
-  // threads past them load chunk 0 and keep nothing), staged in LDS for the threads that rotate the pairs
-  // (j, j + D/2), j < D/2; the pair's inv_freq also straight into register for its cos / sin.
-  constexpr int kChunks = D / 8;  // 16-byte chunks of one D-element bf16 slice (and of the D/2 fp32 inv_freq)
-  constexpr int kOps = 6 * kChunks;
-  const int j = threadIdx.x;
-  const bool roper = j < half;
-  const float fr = inv_freq[roper ? j : 0];
-  const int op = threadIdx.x / kChunks, oc = threadIdx.x % kChunks;
-  const bool op_mine = threadIdx.x < kOps;
-  const void* op_src = op == 5 ? static_cast<const void*>(inv_freq + 4 * oc)
-                               : static_cast<const void*>((op == 0 ? q : op == 1 ? k : op == 2 ? v : op == 3 ? qw : kw) +
-                                                          h * D + 8 * oc);
-  const u32x4 op_val = *reinterpret_cast<const u32x4*>(op_mine ? op_src : static_cast<const void*>(q));
-  QkNorm<SPLIT> norm;
-  norm.load(q, k, H);
-  uint16_t* K = kc + static_cast<int64_t>(h) * max_len * D;
-  uint16_t* V = vc + static_cast<int64_t>(h) * max_len * D;
-  HeadAttention<LPR, true> att(K, V, 0);
-  att.prefetch(max_len);  // issued before the position arrives
-  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the arithmetic below
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int64_t pos_in = *pos_p;
   const bool in_cache = pos_in >= 0 && pos_in < max_len;
   const int64_t pos = pos_in < 0 ? 0 : (pos_in >= max_len ? max_len - 1 : pos_in);
-  att.T = static_cast<int>(pos) + 1;
-  float c = 0.f, sn = 0.f;
-  if (roper) rope_angle(fr, pos_in, c, sn);
-  asm volatile("" : "+v"(c), "+v"(sn));  // computed here, not sunk past the norms' barrier
-  if (op_mine) ops[threadIdx.x] = op_val;
+  const uint16_t* q = qkv;
+  const uint16_t* k = qkv + H;
+  const uint16_t* v = qkv + 2 * H;
+  uint16_t* K = kc + static_cast<int64_t>(h) * max_len * D;
+  uint16_t* V = vc + static_cast<int64_t>(h) * max_len * D;
 
-  float rq, rk;
-  norm.finish(q, k, H, eps, red_q, red_k, rq, rk);  // its barrier also makes ops visible
+  // RoPE operands of this thread's pair (j, j + D/2) of head h (threads j < D/2; D <= 256 <= threads)
+  const int j = threadIdx.x;
+  const bool roper = j < half;
+  const int a = h * D + j, b = a + half;
+  float f_qa = 0.f, f_qb = 0.f, f_ka = 0.f, f_kb = 0.f, w_qa = 0.f, w_qb = 0.f, w_ka = 0.f, w_kb = 0.f, fr = 0.f;
+  uint16_t v_a = 0, v_b = 0;
   if (roper) {
-    const uint16_t* o16 = reinterpret_cast<const uint16_t*>(ops);
-    auto val = [&](int which, int e) { return bf16_bits_to_float(o16[which * D + e]); };
-    const uint16_t v_a = o16[2 * D + j], v_b = o16[2 * D + j + half];
-    const RopePair rp = rope_pair(val(0, j), val(0, j + half), val(1, j), val(1, j + half), val(3, j),
-                                  val(3, j + half), val(4, j), val(4, j + half), c, sn, rq, rk);
+    f_qa = ld_bf16(q, a);
+    f_qb = ld_bf16(q, b);
+    f_ka = ld_bf16(k, a);
+    f_kb = ld_bf16(k, b);
+    w_qa = ld_bf16(qw, a);
+    w_qb = ld_bf16(qw, b);
+    w_ka = ld_bf16(kw, a);
+    w_kb = ld_bf16(kw, b);
+    v_a = v[a];
+    v_b = v[b];
+    fr = inv_freq[j];
+  }
+  HeadAttention<LPR, true> att(K, V, static_cast<int>(pos) + 1);
+  att.prefetch();
+
+  // the norms over the whole projections
+  float rq, rk;
+  qk_rms(q, k, H, eps, red_q, red_k, rq, rk);
+  if (roper) {
+    const RopePair rp = rope_pair(f_qa, f_qb, f_ka, f_kb, w_qa, w_qb, w_ka, w_kb, fr, pos_in, rq, rk);
     qs[j] = rp.qa;
     qs[j + half] = rp.qb;
-    ks[j] = rp.ka;
-    ks[j + half] = rp.kb;
+    const uint16_t k_lo = rp.ka;
+    const uint16_t k_hi = rp.kb;
+    ks[j] = k_lo;
+    ks[j + half] = k_hi;
     vs[j] = v_a;
     vs[j + half] = v_b;
     if (in_cache) {
       const int64_t r = pos_in * D;
-      K[r + j] = rp.ka;
-      K[r + j + half] = rp.kb;
+      K[r + j] = k_lo;
+      K[r + j + half] = k_hi;
       V[r + j] = v_a;
       V[r + j + half] = v_b;
     }
@@ -509,7 +452,7 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(const uint
 constexpr int kRowsMax = 16;  // rows of one fused verify launch
 
 // grid = (heads, rows): workgroup (h, r) attends for row r of qkv [rows, 3H], at position *pos_p + r, over positions
-// 0 .. *pos_p + r. The rows 0 .. r of the launch for its own head are normalised (QkNorm's order) and rotated
+// 0 .. *pos_p + r. The rows 0 .. r of the launch for its own head are normalised (qk_rms's order) and rotated
 // (rope_pair) in this workgroup and read from LDS, the positions before them from the cache; the workgroup writes
 // only its own row's k and v to the cache. Equal bit for bit to qk_rope_cache_kernel + attention_kernel on the same
 // rows (the same sums in the same order).
@@ -565,7 +508,7 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_rows_kernel(const
     v_b[p] = qj[2 * H + b];
   }
 
-  // sums of squares of q (row r) and k (rows 0 .. r), each in QkNorm's order
+  // sums of squares of q (row r) and k (rows 0 .. r), each in qk_rms's order
   float sq = 0.f;
   float sk[kRowsMax];
 #pragma unroll
@@ -614,9 +557,8 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_rows_kernel(const
       float skj = red_k[j][0];
       for (int w = 1; w < kAttnWaves; ++w) skj += red_k[j][w];
       const float rk = 1.f / sqrtf(skj / static_cast<float>(H) + eps);
-      float c, sn;
-      rope_angle(fr, pos0 + j, c, sn);
-      const RopePair rp = rope_pair(f_qa[p], f_qb[p], f_ka[p], f_kb[p], wqa, wqb, wka, wkb, c, sn, rq, rk);
+      const RopePair rp =
+          rope_pair(f_qa[p], f_qb[p], f_ka[p], f_kb[p], wqa, wqb, wka, wkb, fr, pos0 + j, rq, rk);
       ks[j * D + jp] = rp.ka;
       ks[j * D + jp + half] = rp.kb;
       vs[j * D + jp] = v_a[p];
@@ -659,8 +601,7 @@ void launch_rope_attention(const void* qkv, const void* qw, const void* kw, cons
                            void* kc, void* vc, void* out, int heads, int rows, int max_len, float eps, float scale,
                            hipStream_t st) {
   if (rows == 1) {
-    auto kernel = qk_split(heads * 8 * LPR) ? rope_attention_kernel<LPR, true> : rope_attention_kernel<LPR, false>;
-    kernel<<<heads, kAttnThreads, 0, st>>>(
+    rope_attention_kernel<LPR><<<heads, kAttnThreads, 0, st>>>(
         static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(qw), static_cast<const uint16_t*>(kw),
         inv_freq, pos, static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), static_cast<uint16_t*>(out), heads,
         max_len, eps, scale);
@@ -881,8 +822,7 @@ int bp_decode_qk_rope_cache_rows(const void* qkv, const void* q_norm_w, const vo
     return BP_E_INVALID_ARG;
   if (head_dim <= 0 || head_dim % 8 != 0) return BP_E_UNSUPPORTED;
   if (!bp::aligned16(qkv)) return BP_E_INVALID_ARG;
-  auto kernel = bp::qk_split(heads * head_dim) ? bp::qk_rope_cache_kernel<true> : bp::qk_rope_cache_kernel<false>;
-  kernel<<<rows, bp::kAttnThreads, 0, static_cast<hipStream_t>(stream)>>>(
+  bp::qk_rope_cache_kernel<<<rows, bp::kAttnThreads, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(q_norm_w),
       static_cast<const uint16_t*>(k_norm_w), inv_freq, pos, static_cast<uint16_t*>(q_out),
       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), heads, head_dim, max_len, eps);
