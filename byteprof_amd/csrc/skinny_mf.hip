@@ -50,6 +50,7 @@ __global__ void mf_fill_zero_kernel(uint16_t* __restrict__ y, int64_t count) {
 }
 
 constexpr int64_t kMaxStageBytes = 32 * 1024;  // LDS for staged activations (dynamic shared memory)
+constexpr int64_t kMaxProLdsBytes = 48 * 1024;  // with a norm prologue's gamma and residual rows as well
 
 // LDS bytes of the staged activations of a launch (the largest K range of a workgroup), or -1 when they do not fit.
 int64_t mf_stage_bytes(int wkind, int64_t M, int64_t K, int split) {
@@ -97,7 +98,7 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   const int64_t nseg = (K + seg - 1) / seg;
   if (split > nseg) split = static_cast<int>(nseg);
   if (mode == 1 && split < 2) return BP_E_UNSUPPORTED;
-  MfPro pro{0, 0.f, nullptr, nullptr, nullptr};
+  MfPro pro{0, 0.f, nullptr, nullptr, nullptr, 0};
   if (prologue != nullptr && prologue->kind != 0) {
     // whole rows staged in LDS: split 1, vector loads, at most 16 rows
     if (prologue->kind != BP_PRO_UNIT_RMS && prologue->kind != BP_PRO_NORM) return BP_E_INVALID_ARG;
@@ -112,14 +113,22 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
       return BP_E_UNSUPPORTED;
     xstage = 1;
     pro = MfPro{prologue->kind, prologue->eps, static_cast<const uint16_t*>(prologue->gamma),
-                static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout)};
+                static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout), 0};
   }
   int64_t lds = 0;
   if (xstage) {
     lds = mf_stage_bytes(wkind, M, K, split);
     if (lds < 0) return BP_E_UNSUPPORTED;
   }
-  if (pro.kind == BP_PRO_NORM && M == 1) lds += 4 * K;  // gamma and the residual row (mf_prologue)
+  if (pro.kind == BP_PRO_NORM) {
+    // gamma and the residual rows staged in LDS after the rows (mf_prologue reads them from there), when they fit;
+    // otherwise the prologue reads them from memory
+    const int64_t gl = 2 * K * (1 + (pro.residual != nullptr ? M : 0));
+    if (M == 1 || lds + gl <= kMaxProLdsBytes) {
+      pro.gl = 1;
+      lds += gl;
+    }
+  }
   // every wave has the same segment count when the split ranges and the waves divide the segments evenly
   const int nseg_wave = !general && nseg % split == 0 && (nseg / split) % waves == 0
                             ? static_cast<int>(nseg / split / waves)

@@ -21,6 +21,7 @@ struct MfPro {
   const uint16_t* gamma;     // BP_PRO_NORM: [K]
   const uint16_t* residual;  // BP_PRO_NORM: [M, K] or null
   uint16_t* xout;            // [M, K] or null: the transformed rows, written by workgroup (0, 0)
+  int gl;                    // BP_PRO_NORM: 1 when gamma and the residual rows are staged in LDS (the launch sized it)
 };
 
 using MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, uint16_t*, float*, int, int64_t, int64_t,
@@ -39,8 +40,8 @@ namespace {
 //                    norm), and workgroup (0, 0) writes the rows to xout.
 // The mean square is wave_sumsq's (common.h), the same bits whichever wave computes it, so the fused norm equals
 // the separate norm launch (decode.hip, norm_residual_kernel) bit for bit. Wave w sums rows w, w + waves, ... into
-// sums[] (LDS, one float per row); one barrier later every row is rewritten. gl (BP_PRO_NORM over one row, else
-// null): LDS copies of gamma [K] and the residual row [K], loaded ahead of the weights.
+// sums[] (LDS, one float per row); one barrier later every row is rewritten. gl (BP_PRO_NORM with pro.gl, else
+// null): LDS copies of gamma [K] and the residual rows [rows][K], loaded ahead of the weights.
 template <int NT>
 __device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, bool writer, const uint16_t* gl,
                             float* sums) {
@@ -78,11 +79,12 @@ __device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, boo
         row[i] = v;
         if (writer && pro.xout != nullptr) as_global_mut(pro.xout)[static_cast<int64_t>(m) * K + i] = v;
       };
-      if (gl != nullptr) {  // one row, gamma and the residual in LDS: four elements per thread and step
+      if (gl != nullptr) {  // gamma and the residual rows in LDS: four elements per thread and step
+        const uint16_t* gres = gl + (1 + m) * K;
         for (int i = 4 * static_cast<int>(threadIdx.x); i < K; i += 4 * NT) {
           const uint2 xq = *reinterpret_cast<const uint2*>(row + i);
           const uint2 gq = *reinterpret_cast<const uint2*>(gl + i);
-          const uint2 rq = has_res ? *reinterpret_cast<const uint2*>(gl + K + i) : uint2{0u, 0u};
+          const uint2 rq = has_res ? *reinterpret_cast<const uint2*>(gres + i) : uint2{0u, 0u};
           const uint32_t xw[4] = {xq.x << 16, xq.x & 0xffff0000u, xq.y << 16, xq.y & 0xffff0000u};
           const uint32_t gw[4] = {gq.x << 16, gq.x & 0xffff0000u, gq.y << 16, gq.y & 0xffff0000u};
           const uint32_t rw[4] = {rq.x << 16, rq.x & 0xffff0000u, rq.y << 16, rq.y & 0xffff0000u};
@@ -95,7 +97,7 @@ __device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, boo
           const uint2 o2{ov[0] | (ov[1] << 16), ov[2] | (ov[3] << 16)};
           *reinterpret_cast<uint2*>(row + i) = o2;
           if (writer && pro.xout != nullptr)
-            *as_global_mut(reinterpret_cast<uint64_t*>(pro.xout + i)) =
+            *as_global_mut(reinterpret_cast<uint64_t*>(pro.xout + static_cast<int64_t>(m) * K + i)) =
                 static_cast<uint64_t>(o2.x) | (static_cast<uint64_t>(o2.y) << 32);
         }
       } else {
@@ -172,22 +174,38 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
     stage.issue(x, mrows, K, k_lo, kn, 0);  // ahead of the weight loads: the commit waits for these only
     MfXLds<KIND, MB> xs;
     xs.init(xs_lds, mrows, kn, k_lo, ln);
-    // BP_PRO_NORM over one row: gamma and the residual row straight into LDS after the staged row (64 lanes x 16
+    // BP_PRO_NORM with pro.gl: gamma and the residual rows straight into LDS after the staged rows (64 lanes x 16
     // bytes per load, no registers held), ahead of the weight loads
     const uint16_t* gl = nullptr;
     if constexpr (PRO) {
-      if (pro.kind == BP_PRO_NORM && mrows == 1) {
-        uint16_t* dst = xs_lds + kn;
+      if (pro.kind == BP_PRO_NORM && pro.gl) {
+        uint16_t* dst = xs_lds + mrows * kn;
         gl = dst;
-        for (int j = wave; j * 512 < kn; j += WAVES) {
-          const int e = j * 512 + 8 * lane;
-          if (e < kn) {
-            __builtin_amdgcn_global_load_lds(as_global(pro.gamma + e),
-                                             (__attribute__((address_space(3))) void*)(dst + j * 512), 16, 0, 0);
-            if (pro.residual != nullptr)
-              __builtin_amdgcn_global_load_lds(as_global(pro.residual + e),
-                                               (__attribute__((address_space(3))) void*)(dst + kn + j * 512), 16, 0,
-                                               0);
+        // LDS: gamma [kn], then the residual rows [kn] each
+        if (mrows == 1) {
+          for (int j = wave; j * 512 < kn; j += WAVES) {
+            const int e = j * 512 + 8 * lane;
+            if (e < kn) {
+              __builtin_amdgcn_global_load_lds(as_global(pro.gamma + e),
+                                               (__attribute__((address_space(3))) void*)(dst + j * 512), 16, 0, 0);
+              if (pro.residual != nullptr)
+                __builtin_amdgcn_global_load_lds(as_global(pro.residual + e),
+                                                 (__attribute__((address_space(3))) void*)(dst + kn + j * 512), 16,
+                                                 0, 0);
+            }
+          }
+        } else {
+          const int nres = pro.residual != nullptr ? mrows : 0;
+          for (int j = wave; j * 512 < kn; j += WAVES) {
+            const int e = j * 512 + 8 * lane;
+            if (e < kn) {
+              __builtin_amdgcn_global_load_lds(as_global(pro.gamma + e),
+                                               (__attribute__((address_space(3))) void*)(dst + j * 512), 16, 0, 0);
+              for (int r = 0; r < nres; ++r)
+                __builtin_amdgcn_global_load_lds(
+                    as_global(pro.residual + static_cast<int64_t>(r) * K + e),
+                    (__attribute__((address_space(3))) void*)(dst + (1 + r) * kn + j * 512), 16, 0, 0);
+            }
           }
         }
       }

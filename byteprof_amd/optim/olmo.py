@@ -274,11 +274,23 @@ class OlmoDecoder:
         self.v_ids, self.v_tok, self.v_out = z(n, dtype=torch.int64), z(n, dtype=torch.int64), \
             z(n + 1, dtype=torch.int64)
         self.v_pos = z(1, dtype=torch.int64)
-        self.vx, self.vq, self.vattn, self.vo, self.vdn, self.vxn = (z(n, H) for _ in range(6))
+        self.vx, self.vh, self.vq, self.vattn, self.vo, self.vdn, self.vxn = (z(n, H) for _ in range(7))
         self.vqkv, self.vgu, self.vact, self.vlogits = z(n, 3 * H), z(n, 2 * F), z(n, F), z(n, V)
         self.v_argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_rows_scratch_bytes(n) // 4), dtype=torch.int32)
         split = max(p[2] for p in (self._plan(H, F, r) for r in range(1, n + 1)))
         self.vws = torch.empty(split * n * H, dtype=torch.float32, device=dev)  # the down launch's partials
+
+    def _pro_fits(self, n: int, k: int, rows: int) -> bool:
+        """Whether the launch of an n x k linear at rows rows takes a norm prologue: at most 4 rows, a plan that keeps
+        whole rows (split 1), the rows x k activations staged in LDS in one pass (rows x k <= 2048 x waves), and
+        gamma with the residual rows in LDS beside them (one row, or 48 KiB in all: the launch's limit; past it the
+        prologue would read them from memory element by element). Measured on the OLMo-2-1B shape, the prologue
+        wins over a separate norm launch at 1..4 rows and loses at 5 (the staged rows and norm operands then hold
+        44 KiB of LDS per workgroup)."""
+        _, waves, split, _ = self._plan(n, k, rows)
+        if split != 1 or rows > 4 or rows * k > 2048 * waves:
+            return False
+        return rows == 1 or S._stage_bytes(self.kind, rows, k, 1) + 2 * k * (1 + rows) <= 48 * 1024
 
     def verify(self, s: int) -> None:
         """One verify pass of s = 1 + drafts rows (the reference's captured draft step, olmo_draft.py
@@ -286,38 +298,56 @@ class OlmoDecoder:
         rows' k / v written first, row r attending over positions <= pos + r), the argmax of every row, the accepted
         length L (drafts ids[1 + j] equal to the prediction of row j) and the next round's inputs: ids[0] <- the
         token after the accepted prefix, pos += L + 1. Every row is computed as the one-token step at its position
-        computes it (the linears' rows do not depend on the row count)."""
+        computes it (the linears' rows do not depend on the row count). Each sublayer norm runs inside the next
+        linear's launch where that launch can stage the s rows in one pass (_pro_fits), else as its own launch (the
+        same bits either way); the residual stream alternates between vx and vh where a prologue writes it."""
         if not 1 <= s <= getattr(self, "smax", 0):
             raise ValueError(f"s must be in 1..{getattr(self, 'smax', 0)} (verify_buffers)")
         cfg, L = self.cfg, _lib.lib()
-        H, F, D = cfg.hidden, cfg.ffn, cfg.head_dim
+        H, F, V = cfg.hidden, cfg.ffn, cfg.vocab
         st = _lib.stream_ptr(self.device)
         c = _lib.check
         c(L.bp_decode_embed_rows(self.v_ids.data_ptr(), self.embed.data_ptr(), self.vx.data_ptr(), s, H, cfg.vocab,
                                  st), "bp_decode_embed_rows")
-        x = self.vx[:s]
+        res, spare = self.vx, self.vh  # the residual stream [s, H] and the buffer a prologue writes the next one to
+        pending = None  # the post-feed-forward norm weight still to apply to vdn (with the residual add)
+
+        def norm_into(src: torch.Tensor, gamma: torch.Tensor) -> None:  # res <- res + norm(src), in place
+            c(L.bp_decode_norm_residual_rows(src.data_ptr(), gamma.data_ptr(), res.data_ptr(), res.data_ptr(), H,
+                                             cfg.eps, s, st), "bp_decode_norm_residual_rows")
+
         for i, w in enumerate(self.layers):
             kc, vc = self.k_cache[i], self.v_cache[i]
-            self._mm(x, w["qkv"], self.vqkv[:s])
+            if pending is not None and self._pro_fits(3 * H, H, s):
+                self._pro_mm(self.vdn[:s], w["qkv"], self.vqkv[:s], pending, res[:s], spare[:s])
+                res, spare = spare, res
+            else:
+                if pending is not None:
+                    norm_into(self.vdn, pending)
+                self._mm(res[:s], w["qkv"], self.vqkv[:s])
+            pending = None
             if s <= ROPE_ATTENTION_ROWS:  # one fused launch (equal bit for bit to the two below)
                 c(L.bp_decode_rope_attention_rows(self.vqkv.data_ptr(), w["q_norm"].data_ptr(),
                                                   w["k_norm"].data_ptr(), self.inv_freq.data_ptr(),
                                                   self.v_pos.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                                  self.vattn.data_ptr(), cfg.heads, D, s, cfg.max_len, cfg.eps,
-                                                  self.scale, st), "bp_decode_rope_attention_rows")
+                                                  self.vattn.data_ptr(), cfg.heads, cfg.head_dim, s, cfg.max_len,
+                                                  cfg.eps, self.scale, st), "bp_decode_rope_attention_rows")
             else:
                 c(L.bp_decode_qk_rope_cache_rows(self.vqkv.data_ptr(), w["q_norm"].data_ptr(),
                                                  w["k_norm"].data_ptr(), self.inv_freq.data_ptr(),
                                                  self.v_pos.data_ptr(), self.vq.data_ptr(), kc.data_ptr(),
-                                                 vc.data_ptr(), cfg.heads, D, cfg.max_len, cfg.eps, s, st),
+                                                 vc.data_ptr(), cfg.heads, cfg.head_dim, cfg.max_len, cfg.eps, s, st),
                   "bp_decode_qk_rope_cache_rows")
                 c(L.bp_decode_attention_rows(self.vq.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.v_pos.data_ptr(),
-                                             self.vattn.data_ptr(), cfg.heads, D, cfg.max_len, self.scale, s, st),
-                  "bp_decode_attention_rows")
+                                             self.vattn.data_ptr(), cfg.heads, cfg.head_dim, cfg.max_len, self.scale,
+                                             s, st), "bp_decode_attention_rows")
             self._mm(self.vattn[:s], w["o"], self.vo[:s])
-            c(L.bp_decode_norm_residual_rows(self.vo.data_ptr(), w["post_attn"].data_ptr(), self.vx.data_ptr(),
-                                             self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
-            self._gate_up_silu(x, w["gate_up"], self.vact, self.vgu, s)
+            if self._pro_fits(2 * F, H, s):
+                self._pro_mm(self.vo[:s], w["gate_up"], self.vact[:s], w["post_attn"], res[:s], spare[:s], silu=True)
+                res, spare = spare, res
+            else:
+                norm_into(self.vo, w["post_attn"])
+                self._gate_up_silu(res[:s], w["gate_up"], self.vact, self.vgu, s)
             dc = self._down_splitk(s)
             if dc is not None:  # split-K partials; their reduce feeds the norm in one launch
                 dw = w["down"]
@@ -327,15 +357,19 @@ class OlmoDecoder:
                   "bp_skinny_mf_partials")
                 sc, sdt = (dw[1].data_ptr(), _lib.TORCH_DT[dw[1].dtype]) if self.kind == "int8" else (None, 0)
                 c(L.bp_decode_splitk_norm_residual_rows(self.vws.data_ptr(), split, sc, sdt, w["post_ff"].data_ptr(),
-                                                        self.vx.data_ptr(), self.vx.data_ptr(), H, cfg.eps, s, st),
+                                                        res.data_ptr(), res.data_ptr(), H, cfg.eps, s, st),
                   "bp_decode_splitk_norm_residual_rows")
             else:
                 self._mm(self.vact[:s], w["down"], self.vdn[:s])
-                c(L.bp_decode_norm_residual_rows(self.vdn.data_ptr(), w["post_ff"].data_ptr(), self.vx.data_ptr(),
-                                                 self.vx.data_ptr(), H, cfg.eps, s, st), "bp_decode_norm_residual_rows")
-        c(L.bp_decode_norm_residual_rows(self.vx.data_ptr(), self.norm.data_ptr(), None, self.vxn.data_ptr(), H,
-                                         cfg.eps, s, st), "bp_decode_norm_residual_rows")
-        self._mm(self.vxn[:s], self.lm_head, self.vlogits[:s])
+                pending = w["post_ff"]
+        if pending is not None:
+            norm_into(self.vdn, pending)
+        if self._pro_fits(V, H, s):
+            self._pro_mm(res[:s], self.lm_head, self.vlogits[:s], self.norm, None, None)
+        else:
+            c(L.bp_decode_norm_residual_rows(res.data_ptr(), self.norm.data_ptr(), None, self.vxn.data_ptr(), H,
+                                             cfg.eps, s, st), "bp_decode_norm_residual_rows")
+            self._mm(self.vxn[:s], self.lm_head, self.vlogits[:s])
         c(L.bp_decode_argmax_rows(self.vlogits.data_ptr(), cfg.vocab, s, self.v_tok.data_ptr(),
                                   self.v_argmax_scratch.data_ptr(), st), "bp_decode_argmax_rows")
         c(L.bp_draft_verify_next(self.v_ids.data_ptr(), self.v_tok.data_ptr(), self.v_out.data_ptr(),

@@ -42,7 +42,7 @@ def _norm_rows(x, gamma, residual, eps):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
-@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("with_residual", [True, False])
 def test_norm_prologue_equals_norm_launch_then_skinny(kind, m, with_residual):
     g = _gen(10 + m)
