@@ -101,24 +101,27 @@ def get_cfg(kind: str, n: int, k: int, bm: int) -> tuple[int, int, int]:
     return 8 * rb, waves, split
 
 
-def _table_plan(kind: str, n: int, k: int, m: int) -> tuple[int, int, int, int]:
-    """(weight blocks per workgroup, waves, split, xstage flags) from the table, else the heuristic."""
+def _table_plan(kind: str, n: int, k: int, m: int, pro: bool = False) -> tuple[int, int, int, int]:
+    """(weight blocks per workgroup, waves, split, xstage flags) from the table, else the heuristic. pro: a launch
+    with a norm prologue, whose weight blocks per workgroup the table may tune apart (rb_pro; same K order)."""
     bucket = _bucket(m)
     entry = _TABLE.get((kind, n, k))
     if entry is not None:
         rb = int(entry.get("rb", {}).get(str(bucket), _default_rb(n, bucket)))
+        if pro:
+            rb = int(entry.get("rb_pro", {}).get(str(bucket), rb))
         xs = int(entry.get("xs", {}).get(str(bucket), 0))
         return rb, int(entry["waves"]), int(entry.get("split", 1)), xs
     waves = _default_waves(kind, k)
     return _default_rb(n, bucket), waves, _default_split(kind, n, k, waves), int(n >= 16384)
 
 
-def _resolve(kind: str, n: int, k: int, m: int, cfg) -> tuple[int, int, int, int]:
+def _resolve(kind: str, n: int, k: int, m: int, cfg, pro: bool = False) -> tuple[int, int, int, int]:
     """(weight blocks per workgroup, waves, split, xstage flags) of a launch from a user / table configuration,
-    mapped onto the compiled menu (largest supported value at or below the request)."""
+    mapped onto the compiled menu (largest supported value at or below the request); pro: a norm-prologue launch."""
     xs = 0
     if cfg is None:
-        rb, waves, split, xs = _table_plan(kind, n, k, m)
+        rb, waves, split, xs = _table_plan(kind, n, k, m, pro)
         rows = 8 * rb
     elif len(cfg) == 3:
         rows, waves, split = (int(c) for c in cfg)
@@ -207,7 +210,7 @@ def prologue_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None, ou
     m, k = x.shape
     n = w.shape[0] // (2 if silu else 1)
     kind = "bf16" if scale is None else "int8"
-    rb, waves, split, _ = _resolve(kind, w.shape[0], k, m, cfg)
+    rb, waves, split, _ = _resolve(kind, w.shape[0], k, m, cfg, pro=True)
     if split != 1:
         raise ValueError(f"a prologue needs whole rows per workgroup: the {w.shape[0]}x{k} plan splits K {split} ways")
     for t in (x, w, out, gamma, residual, xout):

@@ -11,9 +11,11 @@ split) -- for every activation-row bucket, so an output row stays bitwise indepe
 per workgroup and xstage flags (activation staging; the straight-line kernel of the segment count or the general
 loop), and keeps the fastest one-row order unless another is within 2% at one row and faster at 16 rows; like the
 reference, a split > 1 must win by more than 3%. Then, at that K order, it picks the weight blocks per workgroup and
-the flags for each bucket (1; 8: four and eight rows together; 16, 32, 64).
+the flags for each bucket (1; 8: four and eight rows together; 16, 32, 64). Last, for launches with a norm
+prologue (bp_skinny_mf_pro: the decode loops' q|k|v, gate|up and LM head launches), the weight blocks per workgroup
+at the same K order, for buckets 1 and 8 (rb_pro; `--pro-only` retunes just those in an existing table).
 
-Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8,int4] [--out path]
+Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8,int4] [--out path] [--pro-only]
 """
 
 from __future__ import annotations
@@ -119,6 +121,48 @@ def _best_plan(kind, ring, x, y, waves, split, rows_list) -> tuple[float, int, i
     return best
 
 
+PRO_BUCKETS = {1: (1,), 8: (2, 4)}  # the row buckets (and row counts timed) where the decode loops run norm prologues
+
+
+def tune_pro(kind: str, n: int, k: int, entry: dict, device, log=print) -> dict:
+    """rb_pro: the weight blocks per workgroup of launches with a norm prologue (bp_skinny_mf_pro, BP_PRO_NORM with
+    a residual, as the decode step's q|k|v, gate|up and LM head launches run) at the table's K order, per row bucket
+    where the rows stage in one pass; {} where the order splits K (no prologue there)."""
+    waves, split = int(entry["waves"]), int(entry.get("split", 1))
+    if split != 1:
+        return {}
+    ring = _ring(kind, n, k, device)
+    g = torch.Generator(device=device).manual_seed(n + k)
+    x = torch.randn(4, k, generator=g, device=device).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(k, generator=g, device=device)).to(torch.bfloat16)
+    res = torch.randn(4, k, generator=g, device=device).to(torch.bfloat16)
+    xout = torch.empty(4, k, dtype=torch.bfloat16, device=device)
+    y = torch.empty(4, n, dtype=torch.bfloat16, device=device)
+    out = {}
+    for bucket, rows in PRO_BUCKETS.items():
+        if max(rows) * k > 2048 * waves:  # the rows must stage in one pass
+            continue
+        best = None
+        for rb in RBS:
+            if not S._supported(kind, max(rows), rb, waves, True):
+                continue
+            t = 0.0
+            for m in rows:
+                calls = [lambda a=a, m=m: S.prologue_mm(x[:m], a[0], a[1] if kind == "int8" else None, y[:m],
+                                                        S.PRO_NORM, gamma=gamma, residual=res[:m], xout=xout[:m],
+                                                        eps=1e-6, cfg=(8 * rb, waves, 1))
+                         for a in ring]
+                t += _time_calls(calls)
+            if best is None or t < best[0]:
+                best = (t, rb)
+        if best is not None:
+            out[str(bucket)] = best[1]
+    log(f"  {kind} {n}x{k}: rb_pro={out}")
+    del ring
+    torch.cuda.empty_cache()
+    return out
+
+
 def tune_shape(kind: str, n: int, k: int, device, log=print) -> dict:
     ring = _ring(kind, n, k, device)
     nseg = -(-k // S.k_segment(kind))
@@ -149,11 +193,13 @@ def tune_shape(kind: str, n: int, k: int, device, log=print) -> dict:
             us[str(m)] = round(_time_calls(_launcher(kind, ring, x[:m].contiguous(), y[:m], rb[str(bucket)], waves,
                                                      split, xs[str(bucket)])), 3)
     per = n * k * (2 if kind == "bf16" else 1)
+    entry = {"waves": waves, "split": split}
+    rb_pro = tune_pro(kind, n, k, entry, device, log)
     log(f"  {kind} {n}x{k}: waves={waves} split={split} rb={rb} xs={xs} us={us} "
         f"(M=1: {per / us['1'] / 1e3:.0f} GB/s of weights)")
     del ring
     torch.cuda.empty_cache()
-    return {"waves": waves, "split": split, "rb": rb, "xs": xs, "us": us}
+    return {"waves": waves, "split": split, "rb": rb, "xs": xs, "us": us, **({"rb_pro": rb_pro} if rb_pro else {})}
 
 
 def tune_int4(n: int, k: int, device, log=print) -> dict | None:
@@ -201,6 +247,8 @@ def main(argv=None) -> int:
     ap.add_argument("--shapes", default=None, help="N:K,N:K,... (default: the decode-step set shapes)")
     ap.add_argument("--kinds", default="bf16,int8")
     ap.add_argument("--out", default=str(S._CFG_FILE))
+    ap.add_argument("--pro-only", action="store_true",
+                    help="only (re)tune rb_pro of the table's existing bf16 / int8 entries (the K orders kept)")
     a = ap.parse_args(argv)
     shapes = DEFAULT_SHAPES if a.shapes is None else [tuple(int(v) for v in s.split(":")) for s in a.shapes.split(",")]
     device = torch.device("cuda:0")
@@ -210,10 +258,25 @@ def main(argv=None) -> int:
                        "(bf16, int8): waves and split of the matrix-core kernel (they fix the K order for every row "
                        "count), rb = 8-row weight blocks per workgroup and xs = xstage flags (1: activations "
                        "staged in LDS, 2: the general segment loop instead of the straight-line kernel of the "
-                       "segment count), per row bucket (1, 8, 16, 32, 64), us = measured time per call by row count "
-                       "(ring of distinct weights, HIP graph); int4|N|K: waves and split of the int4 kernel (tile "
-                       "rows 32).")
+                       "segment count), per row bucket (1, 8, 16, 32, 64), rb_pro = rb of launches with a norm "
+                       "prologue (buckets 1 and 8), us = measured time per call by row count (ring of distinct "
+                       "weights, HIP graph); int4|N|K: waves and split of the int4 kernel (tile rows 32).")
     log = lambda m: print(m, flush=True)  # noqa: E731
+    if a.pro_only:
+        for kind in a.kinds.split(","):
+            for n, k in shapes:
+                key = f"{kind}|{n}|{k}"
+                if kind == "int4" or key not in table:
+                    continue
+                print(f"[tune] {key} rb_pro", flush=True)
+                rb_pro = tune_pro(kind, n, k, table[key], device, log=log)
+                if rb_pro:
+                    table[key]["rb_pro"] = rb_pro
+                else:
+                    table[key].pop("rb_pro", None)
+                out.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
+        print(f"[tune] wrote {out}")
+        return 0
     for kind in a.kinds.split(","):
         for n, k in shapes:
             print(f"[tune] {kind} {n}x{k}", flush=True)

@@ -436,3 +436,11 @@ def test_tuned_table_entries_resolve_to_compiled_plans():
             rb, waves, split, xs = S._resolve(kind, n, k, m, None)
             assert (waves, split) == (e["waves"], e["split"])
             assert S._supported(kind, m, rb, waves, xs & S.XS_STAGE)
+        # rb_pro (norm-prologue launches): only where the order keeps whole rows, for buckets 1 and 8, compiled,
+        # and the one picked for those launches (same K order)
+        assert set(e.get("rb_pro", {})) <= {"1", "8"} and (not e.get("rb_pro") or e["split"] == 1)
+        for bucket, m in (("1", 1), ("8", 4)):
+            if bucket in e.get("rb_pro", {}):
+                rb, waves, split, _ = S._resolve(kind, n, k, m, None, pro=True)
+                assert rb == int(e["rb_pro"][bucket]) and (waves, split) == (e["waves"], e["split"])
+                assert S._supported(kind, m, rb, waves, True)

@@ -38,6 +38,20 @@ def test_tuned_plan_is_one_k_order_and_matches_the_oracle(kind):
                                   int(e["rb"][bucket]), e["waves"], split, int(e["xs"][bucket]), ws.data_ptr(),
                                   ws.numel() * 4, _lib.stream_ptr(DEV)), "bp_skinny_mf")
         check_against_oracle(y, x, w_np)
+    # the norm-prologue plans (rb_pro) at the same K order: equal bit for bit to the plain launch on the normed rows
+    assert set(e.get("rb_pro", {})) <= {"1", "8"}
+    gamma = (1 + 0.1 * torch.randn(k, generator=torch.Generator(device=DEV).manual_seed(5), device=DEV)).to(
+        torch.bfloat16)
+    for bucket, m in (("1", 1), ("8", 4)):
+        if bucket not in e.get("rb_pro", {}):
+            continue
+        x = randn_x(m, k, seed=10 + m)
+        xn = torch.empty(m, k, dtype=torch.bfloat16, device=DEV)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+        S.prologue_mm(x, args[0], args[1] if kind == "int8" else None, y, S.PRO_NORM, gamma=gamma, xout=xn, eps=1e-6,
+                      cfg=(8 * int(e["rb_pro"][bucket]), e["waves"], 1))
+        want = S.skinny_mm(xn, *args, cfg=(8 * int(e["rb"][bucket]), e["waves"], 1))
+        assert torch.equal(y, want)
 
 
 def test_int4_tuned_plan_matches_the_oracle():
