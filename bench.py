@@ -382,7 +382,7 @@ def draft_figures(dec, prompt, ref, new_tokens: int) -> dict:
 def decode_loop(device, new_tokens: int = 128) -> dict:
     """The graph-captured greedy decode loop (byteprof_amd/optim/olmo.py) on the OLMo-2-1B shape with synthetic
     weights: per kind, the GPU time of one captured decode step (replays timed with events), the loop's time per
-    token (one replay + one pinned read + one sync; a generate of 1 + N tokens minus one of 1, over N) and the
+    token (two-step graph replays kept one ahead of the host; a generate of 1 + N tokens minus one of 1, over N) and the
     eager loop's, with the weight bytes a step streams."""
     import torch
 

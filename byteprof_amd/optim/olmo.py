@@ -1,7 +1,7 @@
 """OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 84
 launches for the 16-layer model: each sublayer norm and residual add runs inside the next linear's launch) captured
-in one HIP graph, greedy generation with one replay, one pinned device-to-host read and one event synchronize per
-token.
+in HIP graphs of two steps, each step's token copied to pinned memory inside the graph; greedy generation replays
+them one replay ahead of the host (one event synchronize per two tokens).
 
 Drop-in for the loops of byteprof/optim/olmo.py: `make_generate_graph` (olmo.py:122-219, the manually captured
 graph of the eager forward incl. argmax and next-step inputs) and `make_generate` (olmo.py:51-119, the minimal
@@ -381,10 +381,17 @@ class OlmoDecoder:
         return sum(t.numel() * t.element_size() for args in lins for t in args)
 
 
-def _loop(dec: OlmoDecoder, replay: Callable[[], None] | None, prepare: Callable[[], None] | None):
-    pinned = torch.zeros(1, dtype=torch.long).pin_memory()
-    pinned_np = pinned.numpy()
-    done = torch.cuda.Event()
+def _loop(dec: OlmoDecoder, group: int, issue: Callable[[int, int], None], prepare: Callable[[], None] | None,
+          slots: torch.Tensor):
+    """The token loop. After the prompt, the steps run in groups of up to `group` steps; issue(g, n) enqueues group
+    g (n steps, each followed by a copy of its token into pinned slot 2 (g % 2) + j). Groups are enqueued one ahead
+    of the host: the host reads group g's tokens while the GPU runs group g + 1 (whose first step reads the last
+    token on the device), so the GPU does not wait for the host between groups. The tokens are those of one step
+    at a time; steps enqueued past the end (an EOS inside a group, or the group after it) compute tokens nobody
+    reads and leave cache rows past the end, which a later generate overwrites before reading them (it refills the
+    cache from position 0)."""
+    slots_np = slots.numpy()
+    done = [torch.cuda.Event(), torch.cuda.Event()]
 
     @torch.no_grad()
     def generate(inputs: torch.Tensor, generation_config=None, **kwargs) -> torch.Tensor:
@@ -406,39 +413,64 @@ def _loop(dec: OlmoDecoder, replay: Callable[[], None] | None, prepare: Callable
         for t in ids:  # prefill one position at a time; the last step leaves the first new token in tok
             dec.tok.fill_(t)
             dec.step()
-        pinned.copy_(dec.tok, non_blocking=True)
-        done.record()
-        done.synchronize()
-        new = [int(pinned_np[0])]
-        if prepare is not None and new[0] not in eos_ids and len(new) < max_new:
-            prepare()
-        while new[-1] not in eos_ids and len(new) < max_new:
-            if replay is not None:
-                replay()
-            else:
-                dec.step()
-            pinned.copy_(dec.tok, non_blocking=True)
-            done.record()
-            done.synchronize()  # the single sync of this token
-            new.append(int(pinned_np[0]))
+        slots[0].copy_(dec.tok[0], non_blocking=True)
+        done[0].record()
+        done[0].synchronize()
+        new = [int(slots_np[0])]
+        need = max_new - 1  # tokens still to come
+        if new[0] not in eos_ids and need > 0:
+            if prepare is not None:
+                prepare()
+            sizes = [min(group, need - s) for s in range(0, need, group)]
+
+            def launch(g: int) -> None:
+                issue(g, sizes[g])
+                done[g % 2].record()
+
+            launch(0)
+            for g, n in enumerate(sizes):
+                if g + 1 < len(sizes):
+                    launch(g + 1)  # one group ahead of the host
+                done[g % 2].synchronize()
+                stop = False
+                for j in range(n):
+                    new.append(int(slots_np[2 * (g % 2) + j]))
+                    if new[-1] in eos_ids:
+                        stop = True
+                        break
+                if stop:
+                    break
         return torch.cat([inputs[0].to(dev), torch.tensor(new, dtype=torch.long, device=dev)]).unsqueeze(0)
 
     return generate
 
 
 def make_generate(dec: OlmoDecoder):
-    """The minimal loop (olmo.py:51-119): the decode step run eagerly, one device-to-host read per token."""
-    return _loop(dec, None, None)
+    """The minimal loop (olmo.py:51-119): the decode step run eagerly, its token copied to pinned memory."""
+    slots = torch.zeros(4, dtype=torch.long).pin_memory()
+
+    def issue(g: int, n: int) -> None:
+        for j in range(n):
+            dec.step()
+            slots[2 * (g % 2) + j].copy_(dec.tok[0], non_blocking=True)
+
+    return _loop(dec, 1, issue, None, slots)
+
+
+GRAPH_STEPS = 2  # decode steps per graph replay (one graph launch per two tokens)
 
 
 def make_generate_graph(dec: OlmoDecoder):
     """The graph loop (olmo.py:122-219): the first decode captures the step (after three warm-up steps on a side
     stream, which run at positions L .. L + 2 and leave cache rows that the real steps overwrite before they are
-    read); each token is then one replay, one pinned read and one synchronize."""
+    read) into graphs of GRAPH_STEPS steps and of one step, each step followed by the copy of its token into its
+    pinned slot, one graph per slot pair; the tokens then come GRAPH_STEPS per replay, with one synchronize per
+    replay and the next replay already enqueued."""
     state: dict = {}
+    slots = torch.zeros(4, dtype=torch.long).pin_memory()
 
     def prepare() -> None:
-        if "graph" in state:
+        if "graphs" in state:
             return
         tok, pos = dec.tok.clone(), dec.pos.clone()
         s = torch.cuda.Stream(dec.device)
@@ -448,14 +480,20 @@ def make_generate_graph(dec: OlmoDecoder):
                 dec.step()
         torch.cuda.current_stream(dec.device).wait_stream(s)
         torch.cuda.synchronize(dec.device)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            dec.step()
-        state["graph"] = g
+        graphs = {}
+        for pair in (0, 1):
+            for n in sorted({1, GRAPH_STEPS}):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for j in range(n):
+                        dec.step()
+                        slots[2 * pair + j].copy_(dec.tok[0], non_blocking=True)
+                graphs[(pair, n)] = g
+        state["graphs"] = graphs
         dec.tok.copy_(tok)
         dec.pos.copy_(pos)
 
-    def replay() -> None:
-        state["graph"].replay()
+    def issue(g: int, n: int) -> None:
+        state["graphs"][(g % 2, n)].replay()
 
-    return _loop(dec, replay, prepare)
+    return _loop(dec, GRAPH_STEPS, issue, prepare, slots)
