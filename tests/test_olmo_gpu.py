@@ -339,10 +339,17 @@ def test_generate_contract():
     with pytest.raises(OG.OptimizeError):
         gen(torch.tensor([[1, SMALL.vocab]]), max_new_tokens=4)
     full = gen(torch.tensor([[7, 8, 9]]), max_new_tokens=12)
-    eos = int(full[0, 3 + 4])  # the fifth new token as the end-of-sequence id
-    first = [int(t) for t in full[0, 3:]].index(eos)
-    out = gen(torch.tensor([[7, 8, 9]]), max_new_tokens=12, eos_token_id=eos)
-    assert torch.equal(out.cpu(), full[:, :3 + first + 1].cpu())
+    eager = OG.make_generate(dec)
+    # an end-of-sequence id at every place of the two-step groups (the first new token comes from the prompt's last
+    # step, then pairs), and runs of every length: the same tokens as the run to 12, cut after the first EOS
+    for k in range(6):
+        eos = int(full[0, 3 + k])
+        first = [int(t) for t in full[0, 3:]].index(eos)
+        for g in (gen, eager):
+            out = g(torch.tensor([[7, 8, 9]]), max_new_tokens=12, eos_token_id=eos)
+            assert torch.equal(out.cpu(), full[:, :3 + first + 1].cpu()), (k, g is gen)
+    for n in range(1, 7):
+        assert torch.equal(gen(torch.tensor([[7, 8, 9]]), max_new_tokens=n).cpu(), full[:, :3 + n].cpu()), n
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
