@@ -117,8 +117,8 @@ __device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, boo
 // min(M, 8 MB) x K-range x 2 bytes), their loads issued before the first weight loads; otherwise every segment's
 // activation operand is loaded from memory with its weights. Same operands either way: the results are equal bit
 // for bit. PRO (XL, split 1 only): a transform of the staged rows before the matmul (mf_prologue); for
-// BP_PRO_NORM over one row, gamma and the residual row are loaded into LDS ahead of the weights too (the launch
-// then adds 4 K bytes of dynamic LDS). NSEG > 0 (VEC only): every wave of the launch has exactly NSEG segments (the
+// BP_PRO_NORM, gamma and the residual rows are loaded into LDS ahead of the weights too where the launch sized the
+// LDS for them (pro.gl: 2 K (1 + rows) more bytes, always at one row, else within 48 KiB in all). NSEG > 0 (VEC only): every wave of the launch has exactly NSEG segments (the
 // host checks K / (segment x split x waves) == NSEG), run as straight-line code (MfFixed); 0: any count (MfMain).
 template <int KIND, int MB, int RB, int WAVES, bool VEC, int EPI, bool XL, bool PRO, int NSEG>
 __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t* __restrict__ x,

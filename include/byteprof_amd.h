@@ -110,8 +110,10 @@ int bp_skinny_mf_static(int wkind, const void* x, const void* w, const void* sca
  *                    plain norm), bit for bit bp_decode_norm_residual's output (its summation order), so that the
  *                    norm of a sublayer's output and the residual add run inside the next linear;
  * and when xout is not NULL the transformed rows [M, K] are written there (by one workgroup; xout must not overlap
- * x or residual). gamma, residual and xout 16-byte aligned. epilogue 0: y [M, N] = the plain product; 1: the gate|up SiLU product of bp_skinny_mf_silu, y
- * [M, N] with w [2 N, K] interleaved.
+ * x or residual). gamma, residual and xout 16-byte aligned. BP_PRO_NORM keeps gamma and the residual rows in LDS
+ * beside the staged rows at one row, and at more rows while all of it fits 48 KiB (else it reads them from memory;
+ * the same result). epilogue 0: y [M, N] = the plain product; 1: the gate|up SiLU product of bp_skinny_mf_silu,
+ * y [M, N] with w [2 N, K] interleaved.
  * Replaces: RMSNorm / residual add before the next linear in the decode step (HF Olmo2DecoderLayer, post-attention
  *           and post-feed-forward norms) followed by the linear's skinny_mm call (byteprof/optim/olmo.py:164-215).
  */
