@@ -13,6 +13,7 @@ namespace bp {
 using Int4Fn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
                         int64_t, int64_t, int);
 Int4Fn int4_pick(int mt, int tile_rows, int waves);
+Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt);
 
 namespace {
 
@@ -65,7 +66,11 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(packed) % 16 != 0 ||
       reinterpret_cast<uintptr_t>(zero) % 2 != 0)
     return BP_E_UNSUPPORTED;
-  Int4Fn fn = int4_pick(row_bucket(M), tile_rows, waves);
+  // the matrix-core kernel where a lane's four rows can read their scale and zero as one vector each
+  const int64_t sc_align = scale_dt == BP_DT_F32 ? 16 : 8;
+  const bool mf = N % 4 == 0 && reinterpret_cast<uintptr_t>(zero) % 8 == 0 &&
+                  reinterpret_cast<uintptr_t>(scale) % sc_align == 0;
+  Int4Fn fn = mf ? int4_mf_pick(tile_rows, waves, scale_dt) : int4_pick(row_bucket(M), tile_rows, waves);
   if (fn == nullptr) return BP_E_UNSUPPORTED;
   const int64_t groups = K / 128;
   if (split > groups) split = static_cast<int>(groups);

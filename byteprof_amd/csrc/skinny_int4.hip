@@ -6,7 +6,11 @@
 // high nibble (codes 0..15); scale [G, N] (bf16, fp16 or fp32) and zero [G, N] (fp16) per group and row;
 // deq(W)[n, 128 g + j] = scale[g, n] * (code - zero[g, n]). Padding rows of the last tile are never stored.
 //
-// Work decomposition (every weight byte is read once):
+// Two kernels, each with one summation order per (K, WAVES, split): the matrix-core kernel (skinny_int4_mf_kernel,
+// below) wherever N % 4 == 0 and scale / zero are aligned to four elements, its cost nearly flat in M; else the
+// VALU kernel described next, whose work grows with every activation row.
+//
+// VALU kernel. Work decomposition (every weight byte is read once):
 //   - a workgroup owns one row tile (R = 16, 32 or 64 rows) and WAVES waves; the tile's groups are dealt to the waves
 //     (with split > 1, consecutive group ranges go to separate workgroups and a fixed-order reduce adds them);
 //   - a group of 16 rows is one fully coalesced 1 KiB load: lane (rr = lane / 4, q = lane % 4) reads 16 bytes of row
@@ -155,6 +159,207 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_kernel(const uint16
   }
 }
 
+// ---- matrix-core form -----------------------------------------------------------------------------------------
+// v_mfma_f32_16x16x32_bf16 with a block of 16 weight rows as A and the activation rows (up to 16, zero-padded) as
+// the B columns, so the work per group does not grow with M. A block's 1 KiB is loaded in lane order (lane l: bytes
+// 16 l .. 16 l + 15, row l / 4, quarter l % 4: consecutive lanes on consecutive bytes, the fast streaming order),
+// then passed across lanes (ds_bpermute) so that lane l (row / column i = l % 16, K block kb = l / 16) holds bytes
+// 16 kb .. 16 kb + 15 of row i, i.e. codes 16 kb + e (low nibbles) and 64 + 16 kb + e (high nibbles), e < 16; it
+// loads the activations at the same K indices; the four MFMAs of a group take K slots {16 kb + e}, {16 kb + 8 + e}, {64 + 16 kb + e},
+// {64 + 16 kb + 8 + e} (e < 8) of every kb, the same for A and B, so D[r][m] is the group's sum over all 128 codes.
+// Codes enter as bf16(128 + code) (v_perm_b32 under 0x43); per group, D (a fresh accumulator) becomes
+// scale (D - (128 + zero) X), X the group's sum of the activation row (four more MFMAs: an all-ones A against the
+// same B operands), and the lane adds it to its rows' sums in group order; the waves'
+// sums meet in LDS in wave order. The groups of a wave are loaded DEPTH ahead of their use. The order of every sum
+// depends on (K, WAVES, split) only: an output row does not depend on M (bitwise).
+// Needs N % 4 == 0 (a lane's four D rows read their scale and zero as one 8- or 16-byte load) and 16-byte aligned x,
+// 8-byte aligned zero, scale aligned to 4 of its elements.
+
+template <int RB>
+struct I4Slot {
+  u32x4 wv[RB];   // bytes 16 l .. 16 l + 15 of each 16-row block (lane order)
+  u32x4 xv[4];    // activations at K 16 kb + 0..7, + 8..15, 64 + 16 kb + 0..7, + 8..15 of the lane's column
+  u32x4 sc[RB];   // scale of the lane's four D rows (fp32 x 4, or 16-bit x 4 in .x, .y)
+  uint2 zr[RB];   // zero (fp16 x 4) of the same rows
+};
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+template <int RB, int WAVES, int DEPTH, int SDT>
+__global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uint16_t* __restrict__ x,
+                                                                       const uint8_t* __restrict__ w,
+                                                                       const void* __restrict__ scale, int scale_dt,
+                                                                       const uint16_t* __restrict__ zero,
+                                                                       uint16_t* __restrict__ y,
+                                                                       float* __restrict__ ws, int M, int64_t N,
+                                                                       int64_t K, int split) {
+  using floatx4 = float __attribute__((ext_vector_type(4)));
+  using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+  constexpr int R = 16 * RB;
+  __shared__ float red[WAVES][R][16];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int i = lane & 15, kb = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int64_t G = K / 128;
+  const int s = blockIdx.y;
+  const int64_t g_lo = s * G / split;
+  const int64_t g_hi = (s + 1) * G / split;
+  const int64_t first = g_lo + wave;
+  const int cnt = first < g_hi ? static_cast<int>((g_hi - first + WAVES - 1) / WAVES) : 0;
+  const uint8_t* tile = w + static_cast<int64_t>(blockIdx.x) * G * R * 64 + lane * 16;
+  const int perm = 4 * (4 * i + kb);  // ds_bpermute address of the lane that loaded row i, quarter kb
+  const uint16_t* xr = x + static_cast<int64_t>(i < M ? i : M - 1) * K + kb * 16;
+  // first of the lane's four D rows per block (n0 + 16 h + 4 kb + r); past N (all four, as N % 4 == 0): row N - 4,
+  // loaded and never stored
+  int64_t srow[RB];
+#pragma unroll
+  for (int h = 0; h < RB; ++h) {
+    const int64_t r0 = n0 + 16 * h + 4 * kb;
+    srow[h] = r0 < N ? r0 : N - 4;
+  }
+  constexpr bool f32 = SDT == BP_DT_F32;  // the scale's dtype (scale_dt == SDT)
+
+  auto load = [&](I4Slot<RB>& sl, int j) {
+    const int64_t g = first + static_cast<int64_t>(j) * WAVES;
+#pragma unroll
+    for (int h = 0; h < RB; ++h)
+      sl.wv[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + (g * R + 16 * h) * 64));
+    const uint16_t* xg = xr + g * 128;
+    sl.xv[0] = *reinterpret_cast<const u32x4*>(xg);
+    sl.xv[1] = *reinterpret_cast<const u32x4*>(xg + 8);
+    sl.xv[2] = *reinterpret_cast<const u32x4*>(xg + 64);
+    sl.xv[3] = *reinterpret_cast<const u32x4*>(xg + 72);
+#pragma unroll
+    for (int h = 0; h < RB; ++h) {
+      const int64_t e = g * N + srow[h];
+      sl.zr[h] = *reinterpret_cast<const uint2*>(zero + e);
+      if constexpr (f32) {
+        sl.sc[h] = *reinterpret_cast<const u32x4*>(static_cast<const float*>(scale) + e);
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(scale) + e);
+        sl.sc[h] = u32x4{v.x, v.y, 0u, 0u};
+      }
+    }
+  };
+
+  float acc[RB][4];
+#pragma unroll
+  for (int h = 0; h < RB; ++h)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[h][r] = 0.f;
+
+  auto compute = [&](const I4Slot<RB>& sl) {
+    // columns past M hold a copy of row M - 1: computed, never stored
+    const u32x4 ones = u32x4{kBf16OnePair, kBf16OnePair, kBf16OnePair, kBf16OnePair};
+    // X: the group's sum of each column's activations, as the product of an all-ones A with the same B operands
+    floatx4 X = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      X = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ones), __builtin_bit_cast(bf16x8, sl.xv[c]),
+                                                  X, 0, 0, 0);
+#pragma unroll
+    for (int h = 0; h < RB; ++h) {
+      const uint32_t d[4] = {static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm, static_cast<int>(sl.wv[h].x))),
+                             static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm, static_cast<int>(sl.wv[h].y))),
+                             static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm, static_cast<int>(sl.wv[h].z))),
+                             static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm, static_cast<int>(sl.wv[h].w)))};
+      // operand c: codes of dwords 2 (c % 2), 2 (c % 2) + 1, low nibbles for c < 2, high for c >= 2
+      u32x4 a[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int sh = c < 2 ? 0 : 4;
+        uint32_t p0, p1, p2, p3;
+        codes_to_bf16((d[2 * (c % 2)] >> sh) & 0x0F0F0F0Fu, p0, p1);
+        codes_to_bf16((d[2 * (c % 2) + 1] >> sh) & 0x0F0F0F0Fu, p2, p3);
+        a[c] = u32x4{p0, p1, p2, p3};
+      }
+      floatx4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[c]),
+                                                    __builtin_bit_cast(bf16x8, sl.xv[c]), D, 0, 0, 0);
+      const uint32_t zw[2] = {sl.zr[h].x, sl.zr[h].y};
+      const uint32_t sw[4] = {sl.sc[h].x, sl.sc[h].y, sl.sc[h].z, sl.sc[h].w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float z = half_bits_to_float(r % 2 == 0 ? zw[r / 2] & 0xffffu : zw[r / 2] >> 16);
+        const uint32_t s16 = r % 2 == 0 ? sw[r / 2] & 0xffffu : sw[r / 2] >> 16;
+        const float sc = f32 ? __uint_as_float(sw[r]) : (SDT == BP_DT_BF16 ? bf16_bits_to_float(s16)
+                                                                             : half_bits_to_float(s16));
+        acc[h][r] += sc * (D[r] - (128.f + z) * X[r]);
+      }
+    }
+  };
+
+  if (cnt > 0) {
+    // whole rounds of DEPTH groups with every load unconditional (so the waits count exactly), then the rest
+    I4Slot<RB> sl[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      load(sl[d], d < cnt ? d : cnt - 1);
+      __builtin_amdgcn_sched_barrier(0);  // the slots' loads in slot order
+    }
+    int j0 = 0;
+    for (; j0 + DEPTH <= cnt; j0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int j = j0 + d;
+        compute(sl[d]);
+        load(sl[d], j + DEPTH < cnt ? j + DEPTH : cnt - 1);  // past the last group: the last again (not used)
+        __builtin_amdgcn_sched_barrier(0);  // keeps the pipeline's order: group j's arithmetic before j + 1's
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+      if (j0 + d < cnt) compute(sl[d]);
+  }
+
+  // the waves' sums in wave order
+#pragma unroll
+  for (int h = 0; h < RB; ++h)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][16 * h + 4 * kb + r][i] = acc[h][r];
+  __syncthreads();
+  for (int e = threadIdx.x; e < R * 16; e += WAVES * kWave) {
+    const int row = e / 16;
+    const int m = e % 16;
+    const int64_t n = n0 + row;
+    if (m >= M || n >= N) continue;
+    float t = red[0][row][m];
+#pragma unroll
+    for (int v = 1; v < WAVES; ++v) t += red[v][row][m];
+    if (split == 1)
+      y[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);
+    else
+      ws[(static_cast<int64_t>(s) * M + m) * N + n] = t;
+  }
+}
+
+template <int RB, int DEPTH, int SDT>
+Int4Fn int4_mf_waves(int waves) {
+  switch (waves) {
+    case 1: return &skinny_int4_mf_kernel<RB, 1, DEPTH, SDT>;
+    case 2: return &skinny_int4_mf_kernel<RB, 2, DEPTH, SDT>;
+    case 4: return &skinny_int4_mf_kernel<RB, 4, DEPTH, SDT>;
+    case 8: return &skinny_int4_mf_kernel<RB, 8, DEPTH, SDT>;
+    default: return nullptr;
+  }
+}
+
+template <int RB, int DEPTH>
+Int4Fn int4_mf_dtype(int waves, int scale_dt) {
+  switch (scale_dt) {
+    case BP_DT_BF16: return int4_mf_waves<RB, DEPTH, BP_DT_BF16>(waves);
+    case BP_DT_F16: return int4_mf_waves<RB, DEPTH, BP_DT_F16>(waves);
+    case BP_DT_F32: return int4_mf_waves<RB, DEPTH, BP_DT_F32>(waves);
+    default: return nullptr;
+  }
+}
+
 template <int MT, int RB>
 Int4Fn int4_waves(int waves) {
   switch (waves) {
@@ -177,6 +382,17 @@ Int4Fn int4_rows(int rb, int waves) {
 }
 
 }  // namespace
+
+// Matrix-core kernel for (tile rows, waves, scale dtype), or null; groups in flight per wave: 4 at 16 and 32 tile
+// rows, 2 at 64.
+Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt) {
+  switch (tile_rows) {
+    case 16: return int4_mf_dtype<1, 4>(waves, scale_dt);
+    case 32: return int4_mf_dtype<2, 3>(waves, scale_dt);
+    case 64: return int4_mf_dtype<4, 2>(waves, scale_dt);
+    default: return nullptr;
+  }
+}
 
 // Kernel for (activation-row bucket, tile rows, waves), or null.
 Int4Fn int4_pick(int mt, int tile_rows, int waves) {
