@@ -186,7 +186,9 @@ int bp_chain_run(int wkind, int scale_dtype, const void* dev_items, const void* 
  * y[M, N] (bf16) = sum over groups g of scale[g, n] * sum_j (code - zero[g, n]) * x[m, 128 g + j], fp32; the codes,
  * zeros and activations enter the products exactly. 1 <= M <= 16; K a multiple of 128; x and packed 16-byte aligned.
  * waves: 1, 2, 4 or 8 (groups dealt to the waves); split: as for the other skinny kernels (the scale is applied per
- * group, so the reduce adds the partial sums as they are). The K order depends only on (K, waves, split).
+ * group, so the reduce adds the partial sums as they are). The K order depends only on (K, waves, split) and on
+ * which of two kernels runs: the matrix-core kernel (the activation rows as MFMA columns: nearly the same time at
+ * any M) when N % 4 == 0, zero is 8-byte aligned and scale aligned to four of its elements; else a VALU kernel.
  * Replaces: byteprof/optim/skinny.py:46-63 (_skinny_kernel MODE 3) via skinny_mm (skinny.py:136-166).
  */
 int bp_skinny_int4_config_supported(int mt, int tile_rows, int waves);
