@@ -9,8 +9,10 @@ bf16 / int8 (the matrix-core kernel of every row count): per (kind, N, K) the tu
 split) -- for every activation-row bucket, so an output row stays bitwise independent of M. It times every
 (waves, split) at one row (the decode metric) and at 16 rows (the verify widths), each with its best weight blocks
 per workgroup and xstage flags (activation staging; the straight-line kernel of the segment count or the general
-loop), and keeps the fastest one-row order unless another is within 2% at one row and faster at 16 rows; like the
-reference, a split > 1 must win by more than 3%. Then, at that K order, it picks the weight blocks per workgroup and
+loop), and at one row with a norm prologue (split 1). It keeps the fastest one-row order; like the reference, a
+split > 1 must win by more than 3%; when that order has no split, the split-1 order within 5% of it whose plain and
+prologue launches are fastest together (the decode step runs the prologue form); then, among the orders within 2%
+of that, the fastest at 16 rows. Then, at that K order, it picks the weight blocks per workgroup and
 the flags for each bucket (1; 8: four and eight rows together; 16, 32, 64). Last, for launches with a norm
 prologue (bp_skinny_mf_pro: the decode loops' q|k|v, gate|up and LM head launches), the weight blocks per workgroup
 at the same K order, for buckets 1 and 8 (rb_pro; `--pro-only` retunes just those in an existing table).
@@ -163,12 +165,34 @@ def tune_pro(kind: str, n: int, k: int, entry: dict, device, log=print) -> dict:
     return out
 
 
+def _pro_time(kind: str, ring, x, n: int, k: int, waves: int) -> float | None:
+    """us of the best norm-prologue launch (BP_PRO_NORM with a residual, M = 1) at (waves, split 1), or None where
+    the row does not stage in one pass."""
+    if k > 2048 * waves:
+        return None
+    g = torch.Generator(device=x.device).manual_seed(7)
+    gamma = (1 + 0.1 * torch.randn(k, generator=g, device=x.device)).to(torch.bfloat16)
+    res = torch.randn(1, k, generator=g, device=x.device).to(torch.bfloat16)
+    xout = torch.empty(1, k, dtype=torch.bfloat16, device=x.device)
+    y = torch.empty(1, n, dtype=torch.bfloat16, device=x.device)
+    x1 = x[:1].contiguous()
+    best = None
+    for rb in RBS:
+        if not S._supported(kind, 1, rb, waves, True):
+            continue
+        t = _time_calls([lambda a=a: S.prologue_mm(x1, a[0], a[1] if kind == "int8" else None, y, S.PRO_NORM,
+                                                   gamma=gamma, residual=res, xout=xout, eps=1e-6,
+                                                   cfg=(8 * rb, waves, 1)) for a in ring])
+        best = t if best is None or t < best else best
+    return best
+
+
 def tune_shape(kind: str, n: int, k: int, device, log=print) -> dict:
     ring = _ring(kind, n, k, device)
     nseg = -(-k // S.k_segment(kind))
     x = torch.randn(64, k, device=device).to(torch.bfloat16)
     y = torch.empty(64, n, dtype=torch.bfloat16, device=device)
-    orders = {}
+    orders, pro = {}, {}
     for waves in WAVES:
         for split in SPLITS:
             if waves * split > nseg:
@@ -176,14 +200,24 @@ def tune_shape(kind: str, n: int, k: int, device, log=print) -> dict:
             t1 = _best_plan(kind, ring, x, y, waves, split, [1])
             t16 = _best_plan(kind, ring, x, y, waves, split, [16])
             orders[(waves, split)] = (t1[0], t16[0])
+            if split == 1:
+                pro[(waves, split)] = _pro_time(kind, ring, x, n, k, waves)
+            tp = pro.get((waves, split))
             log(f"  {kind} {n}x{k} waves={waves} split={split}: M=1 {t1[0]:.2f} us (rb {t1[1]}, xs {t1[2]}), "
-                f"M=16 {t16[0]:.2f} us (rb {t16[1]}, xs {t16[2]})")
+                f"M=16 {t16[0]:.2f} us (rb {t16[1]}, xs {t16[2]})" + (f", with a norm prologue {tp:.2f} us" if tp else ""))
     best = min(orders, key=lambda o: orders[o][0])
     if best[1] > 1:
         no_split = min((o for o in orders if o[1] == 1), key=lambda o: orders[o][0])
         if orders[no_split][0] <= orders[best][0] * 1.03:
             best = no_split
-    near = [o for o in orders if orders[o][0] <= orders[best][0] * 1.02 and (o[1] == 1 or best[1] > 1)]
+    if best[1] == 1 and pro.get(best) is not None:
+        # among split-1 orders within 5% at one row, the one fastest as a plain launch and with a norm prologue
+        # together (the decode step runs the prologue form of its q|k|v, gate|up and head launches)
+        cand = [o for o in orders if o[1] == 1 and pro.get(o) is not None and orders[o][0] <= orders[best][0] * 1.05]
+        best = min(cand, key=lambda o: orders[o][0] + pro[o])
+    near = [o for o in orders if orders[o][0] <= orders[best][0] * 1.02 and (o[1] == 1 or best[1] > 1)
+            and (pro.get(best) is None or (pro.get(o) is not None and orders[o][0] + pro[o]
+                                            <= (orders[best][0] + pro[best]) * 1.02))]
     best = min(near, key=lambda o: orders[o][1])
     waves, split = best
     rb, xs, us = {}, {}, {}
