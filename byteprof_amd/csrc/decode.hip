@@ -686,6 +686,7 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
 }
 
 constexpr int kArgmaxBlocks = 64;    // workgroups of argmax_next
+constexpr long kArgmaxSpin = 1L << 16;  // re-reads of a stale partial word before the fold takes it as it is
 constexpr int kArgmaxThreads = 256;  // threads per workgroup
 
 // (best value, index) of this thread folded with (v, i).
@@ -705,14 +706,19 @@ __device__ __forceinline__ void wave_take(float& best, int& idx) {
   }
 }
 
-constexpr int kArgmaxRowWords = 2 * kArgmaxBlocks + 1;  // scratch words per row: values, indices, counter
+// scratch words (u32) per row: the partials [kArgmaxBlocks] as 64-bit words, then the launch generation and the
+// ticket counter
+constexpr int kArgmaxRowWords = 2 * kArgmaxBlocks + 2;
 
 // grid = (G, rows), G <= kArgmaxBlocks: for row r of logits [rows, V], G workgroups each take an even share
 // (vec: 16-byte aligned rows, 8 logits per load; the V % 8 tail and, when not vec, every element one at a time);
-// each writes its (value, index) to the row's scratch, and the last workgroup of the row to finish (a ticket
-// counter, reset by that workgroup) folds them and writes tok[r]; with pos (one row only), it also advances *pos.
-// better() is a total order, so the result does not depend on the split. Scratch per row: values [kArgmaxBlocks]
-// float, indices [kArgmaxBlocks] int, then the counter (zero before the first launch).
+// each stores its (value, index) to the row's scratch as one 64-bit word [tag 16 : bf16 value 16 : index 32] with
+// an agent-scope (device-coherent) store, no fence, then takes a ticket; the last workgroup of the row reads the
+// words (re-reading any whose tag is not the launch's), folds them and writes tok[r]; with pos (one row only), it
+// also advances *pos. The tag is the row's generation (advanced by that last workgroup, after every other
+// workgroup read it) mod 65535 + 1: never 0, so zeroed words are stale. The logits are bf16, so a partial's value
+// is exact in 16 bits. better() is a total order, so the result does not depend on the split. Scratch per row:
+// the words, the generation, the counter (all zero before the first launch; the counter is left at zero).
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint16_t* __restrict__ logits, int V,
                                                                      int vec, int64_t* __restrict__ tok,
                                                                      int64_t* __restrict__ pos,
@@ -723,10 +729,13 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint1
   const int row = blockIdx.y;
   logits += static_cast<int64_t>(row) * V;
   scratch += static_cast<int64_t>(row) * kArgmaxRowWords;
-  float* part_v = reinterpret_cast<float*>(scratch);
-  int* part_i = reinterpret_cast<int*>(scratch + kArgmaxBlocks);
-  uint32_t* counter = scratch + 2 * kArgmaxBlocks;
+  uint64_t* words = reinterpret_cast<uint64_t*>(scratch);
+  uint32_t* gen_p = scratch + 2 * kArgmaxBlocks;
+  uint32_t* counter = gen_p + 1;
   const int b = blockIdx.x, G = gridDim.x;
+  // the launch's generation, read before the ticket (only the last workgroup advances it, after every ticket)
+  const uint32_t gen = threadIdx.x == 0 ? __hip_atomic_load(as_global(gen_p), __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT) : 0u;
   float best = -INFINITY;
   int idx = 0x7fffffff;
   const int nvec = vec ? V / 8 : 0;
@@ -765,24 +774,34 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint1
     bi[wave] = idx;
   }
   __syncthreads();
+  __shared__ uint32_t tag_s;
   if (threadIdx.x == 0) {
     for (int w = 0; w < static_cast<int>(blockDim.x / kWave); ++w) take(best, idx, bv[w], bi[w]);
-    part_v[b] = best;
-    part_i[b] = idx;
-    __threadfence();  // the partial is visible device-wide before the ticket is taken
-    ticket = atomicAdd(counter, 1u);
+    const uint32_t tag = gen % 65535u + 1u;
+    tag_s = tag;
+    // best is -inf (no element) or a bf16 logit: its upper 16 bits hold it exactly
+    const uint64_t word = (static_cast<uint64_t>(tag) << 48) | (static_cast<uint64_t>(__float_as_uint(best) >> 16)
+                                                                 << 32) | static_cast<uint32_t>(idx);
+    __hip_atomic_store(as_global_mut(words + b), word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __hip_atomic_fetch_add(as_global_mut(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (ticket != static_cast<uint32_t>(G - 1) || threadIdx.x >= kWave) return;
-  __threadfence();  // every other workgroup's partial is visible to the loads below
+  const uint32_t tag = tag_s;
   best = -INFINITY;
   idx = 0x7fffffff;
-  for (int k = threadIdx.x; k < G; k += kWave) take(best, idx, part_v[k], part_i[k]);
+  for (int k = threadIdx.x; k < G; k += kWave) {
+    uint64_t w = __hip_atomic_load(as_global(words + k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (long spin = 0; static_cast<uint32_t>(w >> 48) != tag && spin < kArgmaxSpin; ++spin)
+      w = __hip_atomic_load(as_global(words + k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    take(best, idx, __uint_as_float(static_cast<uint32_t>(w >> 16) & 0xffff0000u), static_cast<int>(w));
+  }
   wave_take(best, idx);
   if (threadIdx.x == 0) {
     tok[row] = idx == 0x7fffffff ? 0 : idx;
     if (pos != nullptr) *pos += 1;
-    *counter = 0u;  // ready for the next launch
+    __hip_atomic_store(as_global_mut(counter), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(as_global_mut(gen_p), gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -947,7 +966,8 @@ size_t bp_decode_argmax_rows_scratch_bytes(int rows) {
 }
 
 int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream) {
-  if (logits == nullptr || tok == nullptr || pos == nullptr || scratch == nullptr || vocab <= 0)
+  if (logits == nullptr || tok == nullptr || pos == nullptr || scratch == nullptr || vocab <= 0 ||
+      reinterpret_cast<uintptr_t>(scratch) % 8 != 0)
     return BP_E_INVALID_ARG;
   bp::argmax_next_kernel<<<dim3(bp::kArgmaxBlocks, 1), bp::kArgmaxThreads, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(logits), vocab, bp::aligned16(logits) ? 1 : 0, tok, pos,
@@ -956,10 +976,12 @@ int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* 
 }
 
 int bp_decode_argmax_rows(const void* logits, int vocab, int rows, int64_t* tok, void* scratch, void* stream) {
-  if (logits == nullptr || tok == nullptr || scratch == nullptr || vocab <= 0 || rows <= 0) return BP_E_INVALID_ARG;
+  if (logits == nullptr || tok == nullptr || scratch == nullptr || vocab <= 0 || rows <= 0 ||
+      reinterpret_cast<uintptr_t>(scratch) % 8 != 0)
+    return BP_E_INVALID_ARG;
   const int vec = bp::aligned16(logits) && (rows == 1 || vocab % 8 == 0) ? 1 : 0;
-  // about kArgmaxBlocks workgroups in all: each ends with a device-scope release fence, whose cost grows with their
-  // number (the result does not depend on the split: the fold is exact)
+  // about kArgmaxBlocks workgroups in all: the last one of a row reads every partial (the result does not depend
+  // on the split: the fold is exact)
   const int per_row = bp::kArgmaxBlocks / rows > 4 ? bp::kArgmaxBlocks / rows : 4;
   bp::argmax_next_kernel<<<dim3(per_row, rows), bp::kArgmaxThreads, 0,
                            static_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t*>(logits), vocab, vec, tok,

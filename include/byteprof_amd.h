@@ -313,9 +313,10 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  * silu_mul:       out[ffn] = bf16(bf16(silu(g)) * u), gate_up = [g | u] (2 * ffn); silu_mul_rows with
  *                 interleaved = 1 reads the pairs (gate_up[2f], gate_up[2f + 1]) instead.
  * argmax_next:    *tok = first index of the largest logit (NaN counts as largest); *pos += 1. Several workgroups
- *                 share the logits and the last to finish writes the result; `scratch` holds their partials and
- *                 a counter: bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is
- *                 (each call leaves the counter at zero); calls sharing one scratch must not overlap.
+ *                 share the logits and the last to finish writes the result; `scratch` (8-byte aligned) holds
+ *                 their partials (tagged with the call's generation, no fences), the generation and a counter:
+ *                 bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is (each
+ *                 call leaves the counter at zero); calls sharing one scratch must not overlap.
  * argmax_rows:    tok[r] = argmax of row r of logits [rows, vocab] (as argmax_next; no position update), with
  *                 bp_decode_argmax_rows_scratch_bytes(rows) bytes of scratch (zero before the first call).
  */
