@@ -50,7 +50,7 @@ __global__ void mf_fill_zero_kernel(uint16_t* __restrict__ y, int64_t count) {
 }
 
 constexpr int64_t kMaxStageBytes = 32 * 1024;  // LDS for staged activations (dynamic shared memory)
-constexpr int64_t kMaxProLdsBytes = 48 * 1024;  // with a norm prologue's gamma and residual rows as well
+constexpr int64_t kMaxProLdsBytes = 80 * 1024;  // with a norm prologue's gamma and residual rows as well
 
 // LDS bytes of the staged activations of a launch (the largest K range of a workgroup), or -1 when they do not fit.
 int64_t mf_stage_bytes(int wkind, int64_t M, int64_t K, int split) {
@@ -108,9 +108,6 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
         reinterpret_cast<uintptr_t>(prologue->xout) % 16 != 0)
       return BP_E_INVALID_ARG;
     if (!vec || split != 1 || M > 16 || mode == 1) return BP_E_UNSUPPORTED;
-    // the rows in one staging pass: 4 pieces of 8 elements per thread
-    if (((M < 8 * mf_blocks(M) ? M : 8 * mf_blocks(M)) * (K / 8) + 4 * waves * kWave - 1) / (4 * waves * kWave) != 1)
-      return BP_E_UNSUPPORTED;
     xstage = 1;
     pro = MfPro{prologue->kind, prologue->eps, static_cast<const uint16_t*>(prologue->gamma),
                 static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout), 0};

@@ -118,7 +118,7 @@ __device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, boo
 // activation operand is loaded from memory with its weights. Same operands either way: the results are equal bit
 // for bit. PRO (XL, split 1 only): a transform of the staged rows before the matmul (mf_prologue); for
 // BP_PRO_NORM, gamma and the residual rows are loaded into LDS ahead of the weights too where the launch sized the
-// LDS for them (pro.gl: 2 K (1 + rows) more bytes, always at one row, else within 48 KiB in all). NSEG > 0 (VEC only): every wave of the launch has exactly NSEG segments (the
+// LDS for them (pro.gl: 2 K (1 + rows) more bytes, always at one row, else within 80 KiB in all). NSEG > 0 (VEC only): every wave of the launch has exactly NSEG segments (the
 // host checks K / (segment x split x waves) == NSEG), run as straight-line code (MfFixed); 0: any count (MfMain).
 template <int KIND, int MB, int RB, int WAVES, bool VEC, int EPI, bool XL, bool PRO, int NSEG>
 __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t* __restrict__ x,
@@ -178,6 +178,16 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
     // bytes per load, no registers held), ahead of the weight loads
     const uint16_t* gl = nullptr;
     if constexpr (PRO) {
+      // rows past the register pass (kPer pieces per thread): straight into LDS, 64 pieces of 16 bytes per load
+      // (piece e at element 8 e of the staged rows), ahead of the weight loads as well
+      const int pieces = mrows * (kn / 8);
+      for (int c = kPer * WAVES + wave; c * kWave < pieces; c += WAVES) {
+        const int e = c * kWave + lane;
+        if (e < pieces)
+          __builtin_amdgcn_global_load_lds(
+              as_global(x + static_cast<int64_t>(e / (kn / 8)) * K + k_lo + 8 * (e % (kn / 8))),
+              (__attribute__((address_space(3))) void*)(xs_lds + c * 512), 16, 0, 0);
+      }
       if (pro.kind == BP_PRO_NORM && pro.gl) {
         uint16_t* dst = xs_lds + mrows * kn;
         gl = dst;
@@ -211,8 +221,8 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
       }
     }
     // The staged rows (and the prologue's operands) were loaded before the kInFlight x RB weight loads: waiting for them
-    // leaves the weights in flight. The prologue variants stage in one pass (the launch checks it) and have no
-    // other path, so the transform runs while the weights stream in.
+    // leaves the weights in flight. The prologue variants stage their first pass through registers and the rest by
+    // the LDS loads above, all before the weights, so the transform runs while the weights stream in.
     auto commit = [&]() {
       mf_wait_vm<kInFlight * RB>();
       stage.commit(xs_lds, mrows, kn, 0);

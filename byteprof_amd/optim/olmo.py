@@ -34,6 +34,8 @@ from . import skinny as S
 MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
 ROPE_ATTENTION_ROWS = 16  # most rows of one fused q/k-norm + RoPE + cache + attention launch
 VERIFY_ROWS = 16  # rows of the verify-pass buffers (allocated once per decoder, never reallocated)
+PRO_MAX_ROWS = {"bf16": 5, "int8": 4}  # most rows of a linear launch with the sublayer norm as its prologue
+PRO_LDS_BYTES = 80 * 1024  # the launch keeps gamma and the residual rows in LDS while the staged rows and they fit
 
 
 class OptimizeError(RuntimeError):
@@ -281,16 +283,17 @@ class OlmoDecoder:
         self.vws = torch.empty(split * n * H, dtype=torch.float32, device=dev)  # the down launch's partials
 
     def _pro_fits(self, n: int, k: int, rows: int) -> bool:
-        """Whether the launch of an n x k linear at rows rows takes a norm prologue: at most 4 rows, a plan that keeps
-        whole rows (split 1), the rows x k activations staged in LDS in one pass (rows x k <= 2048 x waves), and
-        gamma with the residual rows in LDS beside them (one row, or 48 KiB in all: the launch's limit; past it the
-        prologue would read them from memory element by element). Measured on the OLMo-2-1B shape, the prologue
-        wins over a separate norm launch at 1..4 rows and loses at 5 (the staged rows and norm operands then hold
-        44 KiB of LDS per workgroup)."""
-        _, waves, split, _ = self._plan(n, k, rows)
-        if split != 1 or rows > 4 or rows * k > 2048 * waves:
+        """Whether the launch of an n x k linear at rows rows takes a norm prologue: a plan that keeps whole rows
+        (split 1), the rows x k activations staged in LDS (32 KiB), gamma with the residual rows in LDS beside them
+        (one row, or PRO_LDS_BYTES in all: past it the prologue would read them from memory element by element, which
+        made 7-row verify rounds 870 -> 1206 us), and at most PRO_MAX_ROWS rows: measured on the OLMo-2-1B shape, the
+        prologue beats a separate norm launch at 1..5 rows for bf16 (5-row round 838 -> 817 us; 7 rows: no gain) and
+        at 1..4 for int8 (5 rows: 685 -> 736 us, 7 rows: 724 -> 809 us)."""
+        _, _, split, _ = self._plan(n, k, rows)
+        if split != 1 or rows > PRO_MAX_ROWS[self.kind]:
             return False
-        return rows == 1 or S._stage_bytes(self.kind, rows, k, 1) + 2 * k * (1 + rows) <= 48 * 1024
+        st = S._stage_bytes(self.kind, rows, k, 1)
+        return st >= 0 and (rows == 1 or st + 2 * k * (1 + rows) <= PRO_LDS_BYTES)
 
     def verify(self, s: int) -> None:
         """One verify pass of s = 1 + drafts rows (the reference's captured draft step, olmo_draft.py
@@ -299,7 +302,7 @@ class OlmoDecoder:
         length L (drafts ids[1 + j] equal to the prediction of row j) and the next round's inputs: ids[0] <- the
         token after the accepted prefix, pos += L + 1. Every row is computed as the one-token step at its position
         computes it (the linears' rows do not depend on the row count). Each sublayer norm runs inside the next
-        linear's launch where that launch can stage the s rows in one pass (_pro_fits), else as its own launch (the
+        linear's launch where _pro_fits allows (up to 5 bf16 / 4 int8 rows), else as its own launch (the
         same bits either way); the residual stream alternates between vx and vh where a prologue writes it."""
         if not 1 <= s <= getattr(self, "smax", 0):
             raise ValueError(f"s must be in 1..{getattr(self, 'smax', 0)} (verify_buffers)")

@@ -129,7 +129,7 @@ PRO_BUCKETS = {1: (1,), 8: (2, 4)}  # the row buckets (and row counts timed) whe
 def tune_pro(kind: str, n: int, k: int, entry: dict, device, log=print) -> dict:
     """rb_pro: the weight blocks per workgroup of launches with a norm prologue (bp_skinny_mf_pro, BP_PRO_NORM with
     a residual, as the decode step's q|k|v, gate|up and LM head launches run) at the table's K order, per row bucket
-    where the rows stage in one pass; {} where the order splits K (no prologue there)."""
+    where the rows stage in LDS; {} where the order splits K (no prologue there)."""
     waves, split = int(entry["waves"]), int(entry.get("split", 1))
     if split != 1:
         return {}
@@ -142,7 +142,7 @@ def tune_pro(kind: str, n: int, k: int, entry: dict, device, log=print) -> dict:
     y = torch.empty(4, n, dtype=torch.bfloat16, device=device)
     out = {}
     for bucket, rows in PRO_BUCKETS.items():
-        if max(rows) * k > 2048 * waves:  # the rows must stage in one pass
+        if S._stage_bytes(kind, max(rows), k, 1) < 0:  # the rows must stage in LDS
             continue
         best = None
         for rb in RBS:
@@ -167,8 +167,8 @@ def tune_pro(kind: str, n: int, k: int, entry: dict, device, log=print) -> dict:
 
 def _pro_time(kind: str, ring, x, n: int, k: int, waves: int) -> float | None:
     """us of the best norm-prologue launch (BP_PRO_NORM with a residual, M = 1) at (waves, split 1), or None where
-    the row does not stage in one pass."""
-    if k > 2048 * waves:
+    the row does not stage in LDS."""
+    if S._stage_bytes(kind, 1, k, 1) < 0:
         return None
     g = torch.Generator(device=x.device).manual_seed(7)
     gamma = (1 + 0.1 * torch.randn(k, generator=g, device=x.device)).to(torch.bfloat16)

@@ -102,8 +102,8 @@ int bp_skinny_mf_static(int wkind, const void* x, const void* w, const void* sca
 
 /*
  * bp_skinny_mf with a transform of the activation rows first (split 1, K a multiple of the segment, 16-byte aligned
- * x and w, and the rows staged in LDS in one pass: M x K <= 32 x 64 x waves elements, e.g. one row of 2048 at any
- * waves, one row of 8192 at 4 or 8 waves): the matmul reads
+ * x and w, and the rows staged in LDS: M x K x 2 bytes <= 32 KiB, e.g. 8 rows of 2048 or one of 16384; the first
+ * 2048 x waves elements pass through registers, the rest are loaded into LDS directly): the matmul reads
  *   BP_PRO_UNIT_RMS: bf16(x * (1 / sqrt(mean(x^2)))) per row (an all-zero row as is): a decode step's renormalised
  *                    input of the next linear;
  *   BP_PRO_NORM:     bf16(residual + bf16(gamma * (x * (1 / sqrt(mean(x^2) + eps))))) per row (residual NULL: the
@@ -111,7 +111,7 @@ int bp_skinny_mf_static(int wkind, const void* x, const void* w, const void* sca
  *                    norm of a sublayer's output and the residual add run inside the next linear;
  * and when xout is not NULL the transformed rows [M, K] are written there (by one workgroup; xout must not overlap
  * x or residual). gamma, residual and xout 16-byte aligned. BP_PRO_NORM keeps gamma and the residual rows in LDS
- * beside the staged rows at one row, and at more rows while all of it fits 48 KiB (else it reads them from memory;
+ * beside the staged rows at one row, and at more rows while all of it fits 80 KiB (else it reads them from memory;
  * the same result). epilogue 0: y [M, N] = the plain product; 1: the gate|up SiLU product of bp_skinny_mf_silu,
  * y [M, N] with w [2 N, K] interleaved.
  * Replaces: RMSNorm / residual add before the next linear in the decode step (HF Olmo2DecoderLayer, post-attention

@@ -6,8 +6,8 @@
   - BP_PRO_UNIT_RMS: the transformed rows are the oracle's unit-RMS renormalisation (oracle.linear_set.unit_rms,
     float64) within one bf16 rounding, and the products equal skinny_mm of those rows bit for bit and the oracle
     within the skinny gates;
-  - launches that cannot stage their whole rows in one pass (more than 16 rows, more rows than 4 x 8 elements per
-    thread, K not a multiple of the segment, unaligned rows) are refused before anything runs.
+  - launches that cannot stage their whole rows (more than 16 rows, more than 32 KiB of rows, K not a multiple of
+    the segment, unaligned rows) are refused before anything runs.
 """
 
 from __future__ import annotations
@@ -42,9 +42,11 @@ def _norm_rows(x, gamma, residual, eps):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("with_residual", [True, False])
 def test_norm_prologue_equals_norm_launch_then_skinny(kind, m, with_residual):
+    """1..4 rows: the staged rows in one pass of registers; 5 and 8 (four waves): the rest by LDS loads; gamma and
+    the residual rows in LDS beside them (up to 80 KiB in all: 8 rows of 2048 take 68 KiB)."""
     g = _gen(10 + m)
     n, k, eps = 2048, 2048, 1e-6
     w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
@@ -134,7 +136,7 @@ def test_prologue_refusals():
     unit = ctypes.byref(S.BpPrologue(1, 0.0, None, None, None))
     assert call(unit, m=17) == -2                                                   # more than 16 rows
     assert call(unit, m=16) == -2                                                   # 16 x 2048 rows: 64 KiB of LDS
-    assert call(unit, m=8) == -2                                                    # 8 x 2048: two staging passes
+    assert call(unit, m=9) == -2                                                    # 9 x 2048 rows: 36 KiB of LDS
     assert call(unit, k=2000) == -2                                                 # K not a multiple of the segment
     assert call(unit, xp=x.data_ptr() + 2) == -2                                    # unaligned rows
     g = torch.ones(2050, dtype=torch.bfloat16, device=DEV)
