@@ -67,9 +67,10 @@ def test_scale_dtypes(scale_dtype):
     check_against_oracle(S.skinny_mm(x, *args), x, w_np)
 
 
-@pytest.mark.parametrize("n,k", [(2048, 2048), (129, 640)])
+@pytest.mark.parametrize("n,k", [(2048, 2048), (129, 640), (2048, 8192)])
 def test_rows_do_not_depend_on_the_other_rows(n, k):
-    """One int4 kernel serves 1..16 rows with one K order: row i is bitwise the same for every M."""
+    """One int4 kernel serves 1..16 rows with one K order: row i is bitwise the same for every M (2048 x 8192: the
+    activations staged in LDS up to 3 rows, loaded with the weights past that)."""
     args, _ = make_int4(n, k, seed=4)
     x = randn_x(33, k, seed=3)
     full16 = S.skinny_mm(x[:16].contiguous(), *args)
