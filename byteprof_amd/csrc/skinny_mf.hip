@@ -98,19 +98,21 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   const int64_t nseg = (K + seg - 1) / seg;
   if (split > nseg) split = static_cast<int>(nseg);
   if (mode == 1 && split < 2) return BP_E_UNSUPPORTED;
-  MfPro pro{0, 0.f, nullptr, nullptr, nullptr, 0};
+  MfPro pro{0, 0.f, nullptr, nullptr, nullptr, 0, nullptr};
   if (prologue != nullptr && prologue->kind != 0) {
     // whole rows staged in LDS: split 1, vector loads, at most 16 rows
     if (prologue->kind != BP_PRO_UNIT_RMS && prologue->kind != BP_PRO_NORM) return BP_E_INVALID_ARG;
     if (prologue->kind == BP_PRO_NORM && prologue->gamma == nullptr) return BP_E_INVALID_ARG;
     // gamma, the residual and xout are read / written in 16-byte pieces
     if (reinterpret_cast<uintptr_t>(prologue->gamma) % 16 != 0 || reinterpret_cast<uintptr_t>(prologue->residual) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(prologue->xout) % 16 != 0)
+        reinterpret_cast<uintptr_t>(prologue->xout) % 16 != 0 || reinterpret_cast<uintptr_t>(prologue->gamma2) % 16 != 0)
       return BP_E_INVALID_ARG;
+    if (prologue->gamma2 != nullptr && prologue->kind != BP_PRO_NORM) return BP_E_INVALID_ARG;
     if (!vec || split != 1 || M > 16 || mode == 1) return BP_E_UNSUPPORTED;
     xstage = 1;
     pro = MfPro{prologue->kind, prologue->eps, static_cast<const uint16_t*>(prologue->gamma),
-                static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout), 0};
+                static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout), 0,
+                static_cast<const uint16_t*>(prologue->gamma2)};
   }
   int64_t lds = 0;
   if (xstage) {
@@ -120,7 +122,7 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   if (pro.kind == BP_PRO_NORM) {
     // gamma and the residual rows staged in LDS after the rows (mf_prologue reads them from there), when they fit;
     // otherwise the prologue reads them from memory
-    const int64_t gl = 2 * K * (1 + (pro.residual != nullptr ? M : 0));
+    const int64_t gl = 2 * K * (1 + (pro.residual != nullptr ? M : 0) + (pro.gamma2 != nullptr ? 1 : 0));
     if (M == 1 || lds + gl <= kMaxProLdsBytes) {
       pro.gl = 1;
       lds += gl;

@@ -22,6 +22,7 @@ struct MfPro {
   const uint16_t* residual;  // BP_PRO_NORM: [M, K] or null
   uint16_t* xout;            // [M, K] or null: the transformed rows, written by workgroup (0, 0)
   int gl;                    // BP_PRO_NORM: 1 when gamma and the residual rows are staged in LDS (the launch sized it)
+  const uint16_t* gamma2;    // BP_PRO_NORM: [K] or null: a second norm (no residual) of the transformed rows
 };
 
 using MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, uint16_t*, float*, int, int64_t, int64_t,
@@ -37,13 +38,14 @@ namespace {
 // In place, row by row:
 //   BP_PRO_UNIT_RMS: x <- bf16(x * (1 / sqrt(mean(x^2)))) (an all-zero row is left as is);
 //   BP_PRO_NORM:     x <- bf16(residual + bf16(gamma * (x * (1 / sqrt(mean(x^2) + eps))))) (no residual: the plain
-//                    norm), and workgroup (0, 0) writes the rows to xout.
+//                    norm), and workgroup (0, 0) writes the rows to xout; with gamma2, then x <- bf16(gamma2 * (x *
+//                    (1 / sqrt(mean(x^2) + eps)))) (a decoder's last post-feed-forward norm, then its final norm).
 // The mean square is wave_sumsq's (common.h), the same bits whichever wave computes it, so the fused norm equals
 // the separate norm launch (decode.hip, norm_residual_kernel) bit for bit. Wave w sums rows w, w + waves, ... into
 // sums[] (LDS, one float per row); one barrier later every row is rewritten. gl (BP_PRO_NORM with pro.gl, else
-// null): LDS copies of gamma [K] and the residual rows [rows][K], loaded ahead of the weights.
+// null): LDS copies of gamma [K], the residual rows [rows][K] and gamma2 [K] (if any), loaded ahead of the weights.
 template <int NT>
-__device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, bool writer, const uint16_t* gl,
+__device__ void mf_prologue(uint16_t* xs, int rows, int K, MfPro pro, bool writer, const uint16_t* gl,
                             float* sums) {
   constexpr int kWaves = NT / kWave;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -105,6 +107,38 @@ __device__ void mf_prologue(uint16_t* xs, int rows, int K, const MfPro& pro, boo
         gptr<const uint16_t> res = has_res ? as_global(pro.residual + static_cast<int64_t>(m) * K) : nullptr;
         for (int i = threadIdx.x; i < K; i += NT)
           put(i, bf16_bits_to_float(gam[i]), has_res ? bf16_bits_to_float(res[i]) : 0.f);
+      }
+    }
+  }
+  if (pro.kind == BP_PRO_NORM && pro.gamma2 != nullptr) {
+    // the second norm: the same sums and roundings over the rewritten rows, gamma2 from LDS or memory
+    __syncthreads();
+    for (int m = wave; m < rows; m += kWaves) {
+      const float t = wave_sumsq_lds(xs + m * K, K);
+      if ((threadIdx.x & (kWave - 1)) == 0) sums[m] = t;
+    }
+    __syncthreads();
+    const int nres = pro.residual != nullptr ? rows : 0;
+    for (int m = 0; m < rows; ++m) {
+      uint16_t* row = xs + m * K;
+      const float r = 1.f / sqrtf(sums[m] / static_cast<float>(K) + pro.eps);
+      if (gl != nullptr) {
+        const uint16_t* g2 = gl + (1 + nres) * K;
+        for (int i = 4 * static_cast<int>(threadIdx.x); i < K; i += 4 * NT) {
+          const uint2 xq = *reinterpret_cast<const uint2*>(row + i);
+          const uint2 gq = *reinterpret_cast<const uint2*>(g2 + i);
+          const uint32_t xw[4] = {xq.x << 16, xq.x & 0xffff0000u, xq.y << 16, xq.y & 0xffff0000u};
+          const uint32_t gw[4] = {gq.x << 16, gq.x & 0xffff0000u, gq.y << 16, gq.y & 0xffff0000u};
+          uint32_t ov[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            ov[e] = float_to_bf16_bits(round_to_bf16(__uint_as_float(gw[e]) * (__uint_as_float(xw[e]) * r)));
+          *reinterpret_cast<uint2*>(row + i) = uint2{ov[0] | (ov[1] << 16), ov[2] | (ov[3] << 16)};
+        }
+      } else {
+        gptr<const uint16_t> g2 = as_global(pro.gamma2);
+        for (int i = threadIdx.x; i < K; i += NT)
+          row[i] = float_to_bf16_bits(round_to_bf16(bf16_bits_to_float(g2[i]) * (bf16_bits_to_float(row[i]) * r)));
       }
     }
   }
@@ -193,6 +227,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
         gl = dst;
         // LDS: gamma [kn], then the residual rows [kn] each
         if (mrows == 1) {
+          uint16_t* dst2 = dst + (pro.residual != nullptr ? 2 : 1) * kn;  // gamma2 after gamma and the residual
           for (int j = wave; j * 512 < kn; j += WAVES) {
             const int e = j * 512 + 8 * lane;
             if (e < kn) {
@@ -202,6 +237,9 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
                 __builtin_amdgcn_global_load_lds(as_global(pro.residual + e),
                                                  (__attribute__((address_space(3))) void*)(dst + kn + j * 512), 16,
                                                  0, 0);
+              if (pro.gamma2 != nullptr)
+                __builtin_amdgcn_global_load_lds(as_global(pro.gamma2 + e),
+                                                 (__attribute__((address_space(3))) void*)(dst2 + j * 512), 16, 0, 0);
             }
           }
         } else {
@@ -215,6 +253,11 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
                 __builtin_amdgcn_global_load_lds(
                     as_global(pro.residual + static_cast<int64_t>(r) * K + e),
                     (__attribute__((address_space(3))) void*)(dst + (1 + r) * kn + j * 512), 16, 0, 0);
+              if (pro.gamma2 != nullptr)
+                __builtin_amdgcn_global_load_lds(as_global(pro.gamma2 + e),
+                                                 (__attribute__((address_space(3))) void*)(dst + (1 + nres) * kn +
+                                                                                           j * 512),
+                                                 16, 0, 0);
             }
           }
         }

@@ -1,5 +1,6 @@
-"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 84
-launches for the 16-layer model: each sublayer norm and residual add runs inside the next linear's launch) captured
+"""OLMo-2 decode loop on gfx950: the whole decode step (skinny linears + the decode kernels of csrc/decode.hip, 83
+launches for the 16-layer model: each sublayer norm and residual add runs inside the next linear's launch, the
+last layer's and the final norm both inside the LM head's) captured
 in HIP graphs of two steps, each step's token copied to pinned memory inside the graph; greedy generation replays
 them one replay ahead of the host (one event synchronize per two tokens).
 
@@ -160,7 +161,7 @@ class OlmoDecoder:
         """The step with each sublayer norm and residual add inside the next linear's launch (bp_skinny_mf_pro,
         BP_PRO_NORM: the norm kernel's arithmetic, so the tokens are those of the separate-norm step): q|k|v of
         layer l > 0 reads down_{l-1} and writes the residual stream x_l; gate|up reads o and writes h_l = x_l +
-        norm(o); the last layer's post-feed-forward norm is one launch, and the final norm runs inside the LM head.
+        norm(o); the last layer's post-feed-forward norm and the final norm both run inside the LM head's launch.
         x and h alternate, so no launch reads what it writes."""
         cfg, L = self.cfg, _lib.lib()
         H, D = cfg.hidden, cfg.head_dim
@@ -181,18 +182,17 @@ class OlmoDecoder:
             self._mm(self.attn, w["o"], self.o)
             self._pro_mm(self.o, w["gate_up"], self.act, w["post_attn"], self.x, self.h, silu=True)
             self._mm(self.act, w["down"], self.dn)
-        c(L.bp_decode_norm_residual(self.dn.data_ptr(), self.layers[-1]["post_ff"].data_ptr(), self.h.data_ptr(),
-                                    self.x.data_ptr(), H, cfg.eps, st), "bp_decode_norm_residual")
-        self._pro_mm(self.x, self.lm_head, self.logits, self.norm, None, None)
+        self._pro_mm(self.dn, self.lm_head, self.logits, self.layers[-1]["post_ff"], self.h, self.x, gamma2=self.norm)
         c(L.bp_decode_argmax_next(self.logits.data_ptr(), cfg.vocab, self.tok.data_ptr(), self.pos.data_ptr(),
                                   self.argmax_scratch.data_ptr(), st), "bp_decode_argmax_next")
 
     def _pro_mm(self, x: torch.Tensor, args: tuple, out: torch.Tensor, gamma: torch.Tensor,
-                residual: torch.Tensor | None, xout: torch.Tensor | None, silu: bool = False) -> None:
-        """out = linear(bf16(residual + bf16(gamma * rmsnorm(x)))) in one launch; xout receives the normalised
-        rows (the new residual stream)."""
+                residual: torch.Tensor | None, xout: torch.Tensor | None, silu: bool = False,
+                gamma2: torch.Tensor | None = None) -> None:
+        """out = linear(bf16(residual + bf16(gamma * rmsnorm(x)))) in one launch (with gamma2: linear of the
+        gamma2-norm of that); xout receives the normalised rows (the new residual stream)."""
         S.prologue_mm(x, args[0], args[1] if len(args) > 1 else None, out, S.PRO_NORM, gamma=gamma,
-                      residual=residual, xout=xout, eps=self.cfg.eps, silu=silu)
+                      residual=residual, xout=xout, eps=self.cfg.eps, silu=silu, gamma2=gamma2)
 
     def _step_separate(self) -> None:
         """The step with a norm launch after o and after down (plans that split K)."""
@@ -244,12 +244,12 @@ class OlmoDecoder:
     @property
     def launches_per_step(self) -> int:
         """Kernel launches of one step. Fused norms: embed, 5 per layer (q|k|v, RoPE + attention, o, gate|up,
-        down; + 1 per split-K o or down), the last layer's norm, the LM head, argmax. Separate norms: embed, 7 per
+        down; + 1 per split-K o or down), the LM head with the last two norms, argmax. Separate norms: embed, 7 per
         layer (+1 per split-K linear), final norm, LM head, argmax."""
         H, F, V = self.cfg.hidden, self.cfg.ffn, self.cfg.vocab
         extra = lambda n, k: int(self._plan(n, k, 1)[2] > 1)  # noqa: E731  (the split reduce)
         if self.fuse_norms:
-            return 4 + (5 + extra(H, H) + extra(H, F)) * self.cfg.layers
+            return 3 + (5 + extra(H, H) + extra(H, F)) * self.cfg.layers
         per_layer = 7 + extra(3 * H, H) + extra(H, H) + extra(H, F) + 2 * extra(2 * F, H)
         return 4 + per_layer * self.cfg.layers + extra(V, H)
 
@@ -282,7 +282,7 @@ class OlmoDecoder:
         split = max(p[2] for p in (self._plan(H, F, r) for r in range(1, n + 1)))
         self.vws = torch.empty(split * n * H, dtype=torch.float32, device=dev)  # the down launch's partials
 
-    def _pro_fits(self, n: int, k: int, rows: int) -> bool:
+    def _pro_fits(self, n: int, k: int, rows: int, norms: int = 1) -> bool:
         """Whether the launch of an n x k linear at rows rows takes a norm prologue: a plan that keeps whole rows
         (split 1), the rows x k activations staged in LDS (32 KiB), gamma with the residual rows in LDS beside them
         (one row, or PRO_LDS_BYTES in all: past it the prologue would read them from memory element by element, which
@@ -293,7 +293,7 @@ class OlmoDecoder:
         if split != 1 or rows > PRO_MAX_ROWS[self.kind]:
             return False
         st = S._stage_bytes(self.kind, rows, k, 1)
-        return st >= 0 and (rows == 1 or st + 2 * k * (1 + rows) <= PRO_LDS_BYTES)
+        return st >= 0 and (rows == 1 or st + 2 * k * (norms + rows) <= PRO_LDS_BYTES)
 
     def verify(self, s: int) -> None:
         """One verify pass of s = 1 + drafts rows (the reference's captured draft step, olmo_draft.py
@@ -365,14 +365,17 @@ class OlmoDecoder:
             else:
                 self._mm(self.vact[:s], w["down"], self.vdn[:s])
                 pending = w["post_ff"]
-        if pending is not None:
-            norm_into(self.vdn, pending)
-        if self._pro_fits(V, H, s):
-            self._pro_mm(res[:s], self.lm_head, self.vlogits[:s], self.norm, None, None)
+        if pending is not None and self._pro_fits(V, H, s, norms=2):  # both norms inside the head's launch
+            self._pro_mm(self.vdn[:s], self.lm_head, self.vlogits[:s], pending, res[:s], spare[:s], gamma2=self.norm)
         else:
-            c(L.bp_decode_norm_residual_rows(res.data_ptr(), self.norm.data_ptr(), None, self.vxn.data_ptr(), H,
-                                             cfg.eps, s, st), "bp_decode_norm_residual_rows")
-            self._mm(self.vxn[:s], self.lm_head, self.vlogits[:s])
+            if pending is not None:
+                norm_into(self.vdn, pending)
+            if self._pro_fits(V, H, s):
+                self._pro_mm(res[:s], self.lm_head, self.vlogits[:s], self.norm, None, None)
+            else:
+                c(L.bp_decode_norm_residual_rows(res.data_ptr(), self.norm.data_ptr(), None, self.vxn.data_ptr(), H,
+                                                 cfg.eps, s, st), "bp_decode_norm_residual_rows")
+                self._mm(self.vxn[:s], self.lm_head, self.vlogits[:s])
         c(L.bp_decode_argmax_rows(self.vlogits.data_ptr(), cfg.vocab, s, self.v_tok.data_ptr(),
                                   self.v_argmax_scratch.data_ptr(), st), "bp_decode_argmax_rows")
         c(L.bp_draft_verify_next(self.v_ids.data_ptr(), self.v_tok.data_ptr(), self.v_out.data_ptr(),

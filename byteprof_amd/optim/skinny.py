@@ -191,10 +191,10 @@ def _launch(kind: str, x: torch.Tensor, w: torch.Tensor, scale, y: torch.Tensor,
 
 
 class BpPrologue(ctypes.Structure):
-    """Mirror of `BpPrologue` in include/byteprof_amd.h (32 bytes)."""
+    """Mirror of `BpPrologue` in include/byteprof_amd.h (40 bytes)."""
 
     _fields_ = [("kind", ctypes.c_int32), ("eps", ctypes.c_float), ("gamma", ctypes.c_void_p),
-                ("residual", ctypes.c_void_p), ("xout", ctypes.c_void_p)]
+                ("residual", ctypes.c_void_p), ("xout", ctypes.c_void_p), ("gamma2", ctypes.c_void_p)]
 
 
 PRO_UNIT_RMS, PRO_NORM = 1, 2  # BP_PRO_UNIT_RMS, BP_PRO_NORM
@@ -202,10 +202,12 @@ PRO_UNIT_RMS, PRO_NORM = 1, 2  # BP_PRO_UNIT_RMS, BP_PRO_NORM
 
 def prologue_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None, out: torch.Tensor, pro: int,
                 gamma: torch.Tensor | None = None, residual: torch.Tensor | None = None,
-                xout: torch.Tensor | None = None, eps: float = 0.0, silu: bool = False, cfg=None) -> None:
+                xout: torch.Tensor | None = None, eps: float = 0.0, silu: bool = False, cfg=None,
+                gamma2: torch.Tensor | None = None) -> None:
     """out = (transform of x) . W^T in one launch (bp_skinny_mf_pro): pro PRO_UNIT_RMS renormalises each row of x
-    to unit RMS, PRO_NORM takes bf16(residual + bf16(gamma * rmsnorm(x))) (the decode norm kernel's arithmetic);
-    xout, when given, receives the transformed rows. silu: w is the interleaved gate|up weight [2 F, K] and out [M,
+    to unit RMS, PRO_NORM takes bf16(residual + bf16(gamma * rmsnorm(x))) (the decode norm kernel's arithmetic),
+    then with gamma2 the plain norm of that with weight gamma2; xout, when given, receives the rows before the
+    second norm. silu: w is the interleaved gate|up weight [2 F, K] and out [M,
     F] the SiLU product. The shape's plan must have split 1 (rows x K of x are staged in LDS; M <= 16)."""
     m, k = x.shape
     n = w.shape[0] // (2 if silu else 1)
@@ -213,10 +215,10 @@ def prologue_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None, ou
     rb, waves, split, _ = _resolve(kind, w.shape[0], k, m, cfg, pro=True)
     if split != 1:
         raise ValueError(f"a prologue needs whole rows per workgroup: the {w.shape[0]}x{k} plan splits K {split} ways")
-    for t in (x, w, out, gamma, residual, xout):
+    for t in (x, w, out, gamma, residual, xout, gamma2):
         if t is not None and not t.is_contiguous():
             raise ValueError("prologue_mm operands must be contiguous")
-    p = BpPrologue(pro, eps, _lib.ptr(gamma), _lib.ptr(residual), _lib.ptr(xout))
+    p = BpPrologue(pro, eps, _lib.ptr(gamma), _lib.ptr(residual), _lib.ptr(xout), _lib.ptr(gamma2))
     sc, sdt = (scale.data_ptr(), _lib.TORCH_DT[scale.dtype]) if scale is not None else (None, 0)
     L = _lib.lib()
     rc = L.bp_skinny_mf_pro(_KIND_CODE[kind], x.data_ptr(), w.data_ptr(), sc, sdt, out.data_ptr(), m, n, k, rb, waves,

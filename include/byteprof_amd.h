@@ -110,7 +110,10 @@ int bp_skinny_mf_static(int wkind, const void* x, const void* w, const void* sca
  *                    plain norm), bit for bit bp_decode_norm_residual's output (its summation order), so that the
  *                    norm of a sublayer's output and the residual add run inside the next linear;
  * and when xout is not NULL the transformed rows [M, K] are written there (by one workgroup; xout must not overlap
- * x or residual). gamma, residual and xout 16-byte aligned. BP_PRO_NORM keeps gamma and the residual rows in LDS
+ * x or residual). With gamma2 (BP_PRO_NORM only) the matmul reads bf16(gamma2 * (t * (1 / sqrt(mean(t^2) + eps))))
+ * of those rows t instead (xout still receives t): a decoder's last post-feed-forward norm and its final norm in the
+ * LM head's launch, bit for bit bp_decode_norm_residual followed by the BP_PRO_NORM launch. gamma, residual, xout
+ * and gamma2 16-byte aligned. BP_PRO_NORM keeps gamma, the residual rows and gamma2 in LDS
  * beside the staged rows at one row, and at more rows while all of it fits 80 KiB (else it reads them from memory;
  * the same result). epilogue 0: y [M, N] = the plain product; 1: the gate|up SiLU product of bp_skinny_mf_silu,
  * y [M, N] with w [2 N, K] interleaved.
@@ -125,6 +128,7 @@ typedef struct BpPrologue {
   const void* gamma;     /* BP_PRO_NORM: bf16 [K] */
   const void* residual;  /* BP_PRO_NORM: bf16 [M, K], or NULL */
   void* xout;            /* bf16 [M, K], or NULL */
+  const void* gamma2;    /* BP_PRO_NORM: bf16 [K]: a second norm of the transformed rows (no residual), or NULL */
 } BpPrologue;
 int bp_skinny_mf_pro(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y, int64_t M,
                      int64_t N, int64_t K, int rb, int waves, int epilogue, const BpPrologue* prologue, void* stream);

@@ -65,6 +65,33 @@ def test_norm_prologue_equals_norm_launch_then_skinny(kind, m, with_residual):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("n,m", [(100352, 1), (2048, 1), (2048, 2), (2048, 5), (6144, 8)])
+def test_two_norm_prologue_equals_norm_launch_then_norm_prologue(kind, n, m):
+    """gamma2: the last post-feed-forward norm (+ residual) and the final norm in the LM head's launch equal the
+    norm launch followed by the one-norm prologue launch, bit for bit (xout: the rows between the two norms)."""
+    g = _gen(30 + m)
+    k, eps = 2048, 1e-6
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    args = (w, None) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
+    x = (torch.randn(m, k, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
+    gamma = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    gamma2 = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    res = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    xn = _norm_rows(x, gamma, res, eps)
+    want = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    S.prologue_mm(xn, args[0], args[1], want, S.PRO_NORM, gamma=gamma2, eps=eps)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    xout = torch.empty(m, k, dtype=torch.bfloat16, device=DEV)
+    S.prologue_mm(x, args[0], args[1], out, S.PRO_NORM, gamma=gamma, residual=res, xout=xout, eps=eps, gamma2=gamma2)
+    torch.cuda.synchronize()
+    assert torch.equal(xout, xn)
+    assert torch.equal(out, want)
+    # the final norm itself against the separate norm launch of xn
+    ref = S.skinny_mm(_norm_rows(xn, gamma2, None, eps), *[a for a in args if a is not None])
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
 def test_norm_prologue_with_the_silu_epilogue(kind):
     """The fused norm before the interleaved gate|up projection equals norm launch + bp_skinny_mf_silu."""
     g = _gen(20)
@@ -141,4 +168,6 @@ def test_prologue_refusals():
     assert call(unit, xp=x.data_ptr() + 2) == -2                                    # unaligned rows
     g = torch.ones(2050, dtype=torch.bfloat16, device=DEV)
     assert call(ctypes.byref(S.BpPrologue(2, 1e-6, g.data_ptr() + 2, None, None))) == -1  # unaligned gamma
+    assert call(ctypes.byref(S.BpPrologue(1, 0.0, None, None, None, g.data_ptr()))) == -1  # gamma2 without a norm
+    assert call(ctypes.byref(S.BpPrologue(2, 1e-6, g.data_ptr(), None, None, g.data_ptr() + 2))) == -1  # unaligned
     torch.cuda.synchronize()
