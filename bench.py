@@ -260,7 +260,7 @@ def int4_figures(device) -> dict:
 
 
 def c1_figures(device) -> dict:
-    """configs[0]-style single linear: y = x W^T, x [1, 2048], W [8192, 2048] bf16 ~ N(0, 0.02^2), over a ring of
+    """One linear at M = 1: y = x W^T, x [1, 2048], W [8192, 2048] bf16 ~ N(0, 0.02^2), over a ring of
     distinct weights (streamed from HBM); the CPU F.linear figure is in cpu_legs."""
     import torch
 
