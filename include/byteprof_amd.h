@@ -322,7 +322,8 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  *                 bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is (each
  *                 call leaves the counter at zero); calls sharing one scratch must not overlap.
  * argmax_rows:    tok[r] = argmax of row r of logits [rows, vocab] (as argmax_next; no position update), with
- *                 bp_decode_argmax_rows_scratch_bytes(rows) bytes of scratch (zero before the first call).
+ *                 bp_decode_argmax_rows_scratch_bytes(rows) bytes of scratch (8-byte aligned, zero before the
+ *                 first call).
  */
 int bp_decode_embed(const int64_t* tok, const void* table, void* x, int hidden, int64_t vocab, void* stream);
 int bp_decode_embed_rows(const int64_t* tok, const void* table, void* x, int rows, int hidden, int64_t vocab,
