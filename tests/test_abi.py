@@ -104,6 +104,11 @@ def test_invalid_arguments_are_rejected_before_any_launch(L):
         assert L.bp_mlstm_lazy_commit(*[p] * 10, 4, 2, dq, 16, 1, 1, 1, 0, 2, 8, None) == -2, dq
     assert L.bp_mlstm_step(*[p] * 12, 2, 320, 16, 0, 2, 0.1, 1e-6, 8, None) == -2
     assert L.bp_mlstm_step(*[p] * 9, None, p, p, 2, 64, 16, 0, 2, 0.1, 1e-6, 8, None) == -1  # no new state
+    # the argmax's partial words are 64-bit: its scratch must be 8-byte aligned
+    odd = ctypes.c_void_p(20)
+    assert L.bp_decode_argmax_next(p, 100, p, p, odd, None) == -1
+    assert L.bp_decode_argmax_rows(p, 100, 2, p, odd, None) == -1
+    assert L.bp_decode_argmax_scratch_bytes() % 8 == 0 and L.bp_decode_argmax_rows_scratch_bytes(3) % 8 == 0
 
 
 # ---- the one-launch linear chain (bp_chain_*) ---------------------------------------------------------------------
