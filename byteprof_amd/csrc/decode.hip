@@ -21,7 +21,6 @@
 
 #include "byteprof_amd.h"
 #include "common.h"
-#include "common.h"
 
 namespace bp {
 namespace {
@@ -686,7 +685,7 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
 }
 
 constexpr int kArgmaxBlocks = 64;    // workgroups of argmax_next
-constexpr long kArgmaxSpin = 1L << 16;  // re-reads of a stale partial word before the fold takes it as it is
+constexpr long kArgmaxSpin = 1L << 16;  // re-reads of a stale partial word before the fold gives up on it
 constexpr int kArgmaxThreads = 256;  // threads per workgroup
 
 // (best value, index) of this thread folded with (v, i).
@@ -706,19 +705,29 @@ __device__ __forceinline__ void wave_take(float& best, int& idx) {
   }
 }
 
-// scratch words (u32) per row: the partials [kArgmaxBlocks] as 64-bit words, then the launch generation and the
-// ticket counter
-constexpr int kArgmaxRowWords = 2 * kArgmaxBlocks + 2;
+// scratch words (u32) per row: the partials [kArgmaxBlocks] as 64-bit words, then the launch generation, the
+// ticket counter, the error word (set to 1 by a fold that gave up on a stale partial) and one word of padding (the
+// next row's partials stay 8-byte aligned)
+constexpr int kArgmaxWordGen = 2 * kArgmaxBlocks;
+constexpr int kArgmaxWordError = kArgmaxWordGen + 2;
+constexpr int kArgmaxRowWords = kArgmaxWordGen + 4;
+static_assert(kArgmaxRowWords == BP_ARGMAX_ROW_WORDS && kArgmaxWordError == BP_ARGMAX_ERROR_WORD, "header layout");
+
+// The 16-bit tag of launch generation gen: never 0 (zeroed words are stale), and consecutive generations differ
+// even where the 32-bit generation wraps (the period 2^15 divides 2^32).
+__device__ __forceinline__ uint32_t argmax_tag(uint32_t gen) { return (gen & 0x7fffu) + 1u; }
 
 // grid = (G, rows), G <= kArgmaxBlocks: for row r of logits [rows, V], G workgroups each take an even share
 // (vec: 16-byte aligned rows, 8 logits per load; the V % 8 tail and, when not vec, every element one at a time);
 // each stores its (value, index) to the row's scratch as one 64-bit word [tag 16 : bf16 value 16 : index 32] with
 // an agent-scope (device-coherent) store, no fence, then takes a ticket; the last workgroup of the row reads the
 // words (re-reading any whose tag is not the launch's), folds them and writes tok[r]; with pos (one row only), it
-// also advances *pos. The tag is the row's generation (advanced by that last workgroup, after every other
-// workgroup read it) mod 65535 + 1: never 0, so zeroed words are stale. The logits are bf16, so a partial's value
+// also advances *pos. The tag is argmax_tag of the row's generation (advanced by that last workgroup, after every
+// other workgroup read it). A word still stale after kArgmaxSpin re-reads sets the row's error word (the token is
+// then not to be trusted; the host reads the word, nothing clears it). The logits are bf16, so a partial's value
 // is exact in 16 bits. better() is a total order, so the result does not depend on the split. Scratch per row:
-// the words, the generation, the counter (all zero before the first launch; the counter is left at zero).
+// the words, the generation, the counter, the error word (all zero before the first launch; the counter is left at
+// zero).
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint16_t* __restrict__ logits, int V,
                                                                      int vec, int64_t* __restrict__ tok,
                                                                      int64_t* __restrict__ pos,
@@ -730,8 +739,9 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint1
   logits += static_cast<int64_t>(row) * V;
   scratch += static_cast<int64_t>(row) * kArgmaxRowWords;
   uint64_t* words = reinterpret_cast<uint64_t*>(scratch);
-  uint32_t* gen_p = scratch + 2 * kArgmaxBlocks;
+  uint32_t* gen_p = scratch + kArgmaxWordGen;
   uint32_t* counter = gen_p + 1;
+  uint32_t* error = scratch + kArgmaxWordError;
   const int b = blockIdx.x, G = gridDim.x;
   // the launch's generation, read before the ticket (only the last workgroup advances it, after every ticket)
   const uint32_t gen = threadIdx.x == 0 ? __hip_atomic_load(as_global(gen_p), __ATOMIC_RELAXED,
@@ -777,7 +787,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint1
   __shared__ uint32_t tag_s;
   if (threadIdx.x == 0) {
     for (int w = 0; w < static_cast<int>(blockDim.x / kWave); ++w) take(best, idx, bv[w], bi[w]);
-    const uint32_t tag = gen % 65535u + 1u;
+    const uint32_t tag = argmax_tag(gen);
     tag_s = tag;
     // best is -inf (no element) or a bf16 logit: its upper 16 bits hold it exactly
     const uint64_t word = (static_cast<uint64_t>(tag) << 48) | (static_cast<uint64_t>(__float_as_uint(best) >> 16)
@@ -792,8 +802,13 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_next_kernel(const uint1
   idx = 0x7fffffff;
   for (int k = threadIdx.x; k < G; k += kWave) {
     uint64_t w = __hip_atomic_load(as_global(words + k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (long spin = 0; static_cast<uint32_t>(w >> 48) != tag && spin < kArgmaxSpin; ++spin)
+    for (long spin = 0; static_cast<uint32_t>(w >> 48) != tag; ++spin) {
+      if (spin == kArgmaxSpin) {
+        __hip_atomic_store(as_global_mut(error), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
       w = __hip_atomic_load(as_global(words + k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     take(best, idx, __uint_as_float(static_cast<uint32_t>(w >> 16) & 0xffff0000u), static_cast<int>(w));
   }
   wave_take(best, idx);

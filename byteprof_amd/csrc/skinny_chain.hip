@@ -9,7 +9,7 @@
 //
 // Hand-off between workgroups (dependent mode): a one-thread kernel ahead of the grid advances the launch
 // generation g (so no workgroup of the grid ever sees it change). Every output is also stored as a 32-bit word
-// [tag : bf16 value] with an agent-scope (device-coherent) store, the tag being g mod 65535 + 1, so a word is either
+// [tag : bf16 value] with an agent-scope (device-coherent) store, the tag being (g mod 2^15) + 1, so a word is either
 // seen whole and current or recognised as stale -- no fences, and nothing is cleared between launches. A producer
 // workgroup issues its stores, then adds 1 to its stage's counter, which therefore only grows: the stage has
 // reported in launch g once counter - (g - 1) x (its workgroups) reaches its workgroup count (unsigned arithmetic,
@@ -97,7 +97,7 @@ __device__ __forceinline__ void chain_body(const BpChainItem& it, int b, int sca
   const int64_t N = it.n;
   const int64_t K = it.K;
   const int64_t n0 = static_cast<int64_t>(b - it.first_wg) * 8 * RB;
-  const uint32_t tag = (gen % 65535u + 1u) << 16;
+  const uint32_t tag = ((gen & 0x7fffu) + 1u) << 16;  // never 0; differs for consecutive generations
 
   const int64_t nseg_all = K / G::kSeg;
   const int64_t nseg = mf_uniform(wave < nseg_all ? (nseg_all - wave + WAVES - 1) / WAVES : 0);

@@ -37,6 +37,7 @@ ROPE_ATTENTION_ROWS = 16  # most rows of one fused q/k-norm + RoPE + cache + att
 VERIFY_ROWS = 16  # rows of the verify-pass buffers (allocated once per decoder, never reallocated)
 PRO_MAX_ROWS = {"bf16": 5, "int8": 4}  # most rows of a linear launch with the sublayer norm as its prologue
 PRO_LDS_BYTES = 80 * 1024  # the launch keeps gamma and the residual rows in LDS while the staged rows and they fit
+ARGMAX_ROW_WORDS, ARGMAX_ERROR_WORD = 132, 130  # u32 words of the argmax scratch per row; its error word
 
 
 class OptimizeError(RuntimeError):
@@ -141,7 +142,7 @@ class OlmoDecoder:
         # the sublayer norms run inside the next linear's launch when its plan keeps whole rows (split 1)
         self.fuse_norms = all(self._plan(n, H, 1)[2] == 1 for n in (3 * H, 2 * F, V))
         self.qkv, self.gu, self.act, self.logits = z(1, 3 * H), z(1, 2 * F), z(1, F), z(1, V)
-        # the argmax's partials and counter: zeroed once, left at zero by every launch
+        # the argmax's partials, counter and error word: zeroed once, the counter left at zero by every launch
         self.argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_scratch_bytes() // 4), dtype=torch.int32)
         self.k_cache = z(cfg.layers, cfg.heads, cfg.max_len, D)
         self.v_cache = z(cfg.layers, cfg.heads, cfg.max_len, D)
@@ -381,6 +382,19 @@ class OlmoDecoder:
         c(L.bp_draft_verify_next(self.v_ids.data_ptr(), self.v_tok.data_ptr(), self.v_out.data_ptr(),
                                  self.v_pos.data_ptr(), s, self.smax, st), "bp_draft_verify_next")
 
+    def argmax_failed(self) -> bool:
+        """Whether an argmax launch since the decoder was made gave up waiting for one of its partials (its token
+        is then not to be trusted); reads the error words of the argmax scratch (synchronises)."""
+        rows = [self.argmax_scratch.view(-1, ARGMAX_ROW_WORDS)]
+        if getattr(self, "smax", 0):
+            rows.append(self.v_argmax_scratch.view(-1, ARGMAX_ROW_WORDS))
+        return any(bool(r[:, ARGMAX_ERROR_WORD].any().item()) for r in rows)
+
+    def check_argmax(self) -> None:
+        """Raises RuntimeError when argmax_failed()."""
+        if self.argmax_failed():
+            raise RuntimeError("an argmax launch gave up waiting for a partial result: its token is not valid")
+
     def weight_bytes(self) -> int:
         """Bytes of the linears' weights (and scales) a step streams."""
         lins = [self.lm_head] + [w[n] for w in self.layers for n in ("qkv", "o", "gate_up", "down")]
@@ -446,6 +460,7 @@ def _loop(dec: OlmoDecoder, group: int, issue: Callable[[int, int], None], prepa
                         break
                 if stop:
                     break
+        dec.check_argmax()
         return torch.cat([inputs[0].to(dev), torch.tensor(new, dtype=torch.long, device=dev)]).unsqueeze(0)
 
     return generate

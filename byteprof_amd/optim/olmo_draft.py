@@ -211,6 +211,7 @@ def make_generate_draft(dec: OlmoDecoder, spec: dict[str, Any] | None = None,
                     break
                 drafter.push(emitted)
                 last = emitted[-1]
+        dec.check_argmax()
         return torch.cat([inputs[0].to(dev), torch.tensor(new, dtype=torch.long, device=dev)]).unsqueeze(0)
 
     generate.drafter = drafter  # type: ignore[attr-defined]

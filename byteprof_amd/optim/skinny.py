@@ -218,6 +218,12 @@ def prologue_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None, ou
     for t in (x, w, out, gamma, residual, xout, gamma2):
         if t is not None and not t.is_contiguous():
             raise ValueError("prologue_mm operands must be contiguous")
+    if xout is not None:
+        # one workgroup writes xout while the others still read x and the residual rows
+        rows = 2 * m * k
+        for t in (x, residual):
+            if t is not None and xout.data_ptr() < t.data_ptr() + rows and t.data_ptr() < xout.data_ptr() + rows:
+                raise ValueError("prologue_mm: xout must not overlap x or residual")
     p = BpPrologue(pro, eps, _lib.ptr(gamma), _lib.ptr(residual), _lib.ptr(xout), _lib.ptr(gamma2))
     sc, sdt = (scale.data_ptr(), _lib.TORCH_DT[scale.dtype]) if scale is not None else (None, 0)
     L = _lib.lib()

@@ -109,8 +109,8 @@ int bp_skinny_mf_static(int wkind, const void* x, const void* w, const void* sca
  *   BP_PRO_NORM:     bf16(residual + bf16(gamma * (x * (1 / sqrt(mean(x^2) + eps))))) per row (residual NULL: the
  *                    plain norm), bit for bit bp_decode_norm_residual's output (its summation order), so that the
  *                    norm of a sublayer's output and the residual add run inside the next linear;
- * and when xout is not NULL the transformed rows [M, K] are written there (by one workgroup; xout must not overlap
- * x or residual). With gamma2 (BP_PRO_NORM only) the matmul reads bf16(gamma2 * (t * (1 / sqrt(mean(t^2) + eps))))
+ * and when xout is not NULL the transformed rows [M, K] are written there (by one workgroup; an xout whose M x K
+ * elements overlap those of x or of residual is refused with BP_E_INVALID_ARG before anything is enqueued). With gamma2 (BP_PRO_NORM only) the matmul reads bf16(gamma2 * (t * (1 / sqrt(mean(t^2) + eps))))
  * of those rows t instead (xout still receives t): a decoder's last post-feed-forward norm and its final norm in the
  * LM head's launch, bit for bit bp_decode_norm_residual followed by the BP_PRO_NORM launch. gamma, residual, xout
  * and gamma2 16-byte aligned. BP_PRO_NORM keeps gamma, the residual rows and gamma2 in LDS
@@ -318,12 +318,16 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  *                 interleaved = 1 reads the pairs (gate_up[2f], gate_up[2f + 1]) instead.
  * argmax_next:    *tok = first index of the largest logit (NaN counts as largest); *pos += 1. Several workgroups
  *                 share the logits and the last to finish writes the result; `scratch` (8-byte aligned) holds
- *                 their partials (tagged with the call's generation, no fences), the generation and a counter:
- *                 bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is (each
- *                 call leaves the counter at zero); calls sharing one scratch must not overlap.
+ *                 their partials (tagged with the call's generation, no fences), the generation, a counter and an
+ *                 error word: bp_decode_argmax_scratch_bytes() bytes, zero before the first call, then reused as is
+ *                 (each call leaves the counter at zero); calls sharing one scratch must not overlap. The error
+ *                 word (u32 at index BP_ARGMAX_ERROR_WORD of a row's scratch) becomes 1 when the last workgroup
+ *                 gave up waiting for a partial (a token written after that is not to be trusted); nothing in the
+ *                 library clears it, so one read after a run covers every call of the run.
  * argmax_rows:    tok[r] = argmax of row r of logits [rows, vocab] (as argmax_next; no position update), with
  *                 bp_decode_argmax_rows_scratch_bytes(rows) bytes of scratch (8-byte aligned, zero before the
- *                 first call).
+ *                 first call): BP_ARGMAX_ROW_WORDS u32 words per row, row r's error word at
+ *                 r * BP_ARGMAX_ROW_WORDS + BP_ARGMAX_ERROR_WORD.
  */
 int bp_decode_embed(const int64_t* tok, const void* table, void* x, int hidden, int64_t vocab, void* stream);
 int bp_decode_embed_rows(const int64_t* tok, const void* table, void* x, int rows, int hidden, int64_t vocab,
@@ -353,6 +357,8 @@ int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* 
                                  float eps, int rows, void* stream);
 int bp_decode_silu_mul(const void* gate_up, void* out, int ffn, void* stream);
 int bp_decode_silu_mul_rows(const void* gate_up, void* out, int ffn, int rows, int interleaved, void* stream);
+#define BP_ARGMAX_ROW_WORDS 132
+#define BP_ARGMAX_ERROR_WORD 130
 size_t bp_decode_argmax_scratch_bytes(void);
 int bp_decode_argmax_next(const void* logits, int vocab, int64_t* tok, int64_t* pos, void* scratch, void* stream);
 size_t bp_decode_argmax_rows_scratch_bytes(int rows);

@@ -111,6 +111,76 @@ def test_invalid_arguments_are_rejected_before_any_launch(L):
     assert L.bp_decode_argmax_scratch_bytes() % 8 == 0 and L.bp_decode_argmax_rows_scratch_bytes(3) % 8 == 0
 
 
+def test_argmax_scratch_holds_an_error_word_per_row(L):
+    """Per row: 64 partial words (64-bit), the generation, the counter, the error word and a pad word, so every
+    row's partials stay 8-byte aligned; the host reads the error word at the place the header names."""
+    from byteprof_amd.optim import olmo
+
+    text = HEADER.read_text()
+    row_words = int(re.search(r"#define BP_ARGMAX_ROW_WORDS (\d+)", text).group(1))
+    error_word = int(re.search(r"#define BP_ARGMAX_ERROR_WORD (\d+)", text).group(1))
+    assert (row_words, error_word) == (olmo.ARGMAX_ROW_WORDS, olmo.ARGMAX_ERROR_WORD) == (132, 130)
+    assert L.bp_decode_argmax_scratch_bytes() == 4 * row_words
+    for rows in (1, 3, 16):
+        assert L.bp_decode_argmax_rows_scratch_bytes(rows) == 4 * row_words * rows
+    assert L.bp_decode_argmax_rows_scratch_bytes(0) == 0
+
+
+def _prologue(**kw):
+    from byteprof_amd.optim.skinny import BpPrologue
+
+    pr = BpPrologue()
+    pr.kind, pr.eps, pr.gamma = 2, 1e-6, 0x100000
+    for key, v in kw.items():
+        setattr(pr, key, v)
+    return pr
+
+
+def test_prologue_refuses_an_xout_overlapping_its_inputs(L):
+    """Workgroup (0, 0) writes xout while the others still read x and the residual rows: an xout whose M x K
+    elements intersect either is refused before anything is enqueued."""
+    x, w, y, res = 0x200000, 0x400000, 0x600000, 0x800000
+    m, n, k = 2, 64, 2048
+    rows = 2 * m * k
+    pro = lambda pr: L.bp_skinny_mf_pro(0, x, w, None, 0, y, m, n, k, 1, 4, 0,  # noqa: E731
+                                        ctypes.byref(pr), None)
+    for xout in (x, x + rows - 16, x - rows + 16):  # the same rows, their last 16 bytes, their first 16 bytes
+        assert pro(_prologue(xout=xout)) == -1, hex(xout)
+        assert pro(_prologue(kind=1, gamma=None, xout=xout)) == -1, hex(xout)
+    for xout in (res, res + rows - 16, res - rows + 16):
+        assert pro(_prologue(residual=res, xout=xout)) == -1, hex(xout)
+
+
+def test_prologue_mm_refuses_an_overlapping_xout_on_the_host():
+    import torch
+
+    from byteprof_amd.optim import skinny as S
+
+    x = torch.zeros(4, 2048, dtype=torch.bfloat16)
+    w = torch.zeros(2048, 2048, dtype=torch.bfloat16)  # a tuned shape whose plan keeps whole rows (split 1)
+    out = torch.zeros(4, 2048, dtype=torch.bfloat16)
+    g = torch.ones(2048, dtype=torch.bfloat16)
+    res = torch.zeros(4, 2048, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="overlap"):
+        S.prologue_mm(x, w, None, out, S.PRO_NORM, gamma=g, residual=res, xout=x, eps=1e-6)
+    with pytest.raises(ValueError, match="overlap"):
+        S.prologue_mm(x, w, None, out, S.PRO_NORM, gamma=g, residual=res, xout=res, eps=1e-6)
+    big = torch.zeros(8, 2048, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="overlap"):  # the last rows of one buffer are the first of the other
+        S.prologue_mm(big[:4], w, None, out, S.PRO_UNIT_RMS, xout=big[3:7])
+
+
+def test_static_scratch_entry_refuses_partials_beyond_its_array(L):
+    """bp_skinny_mf_static's split-K partials live in an 8 MiB device array: a call whose split x M x N x 4
+    bytes exceed it is refused before any HIP call (the pointers are never used)."""
+    p = ctypes.c_void_p(16)
+    assert L.bp_skinny_mf_static_bytes() == 8 << 20
+    assert L.bp_skinny_mf_static(0, p, p, None, 0, p, 16, 100352 * 8, 2048, 1, 4, 2, 0, None) == -3
+    assert L.bp_skinny_mf_static(1, p, p, p, 1, p, 16, 65537, 2048, 1, 4, 2, 0, None) == -3  # 8 MiB + 128 bytes
+    assert L.bp_skinny_mf_static(0, p, p, None, 0, p, 1, 8, 2048, 1, 4, 0, 0, None) == -1    # split 0
+    assert L.bp_skinny_mf_static(0, p, p, None, 0, p, -1, 8, 2048, 1, 4, 1, 0, None) == -1   # negative M
+
+
 # ---- the one-launch linear chain (bp_chain_*) ---------------------------------------------------------------------
 
 

@@ -201,6 +201,37 @@ def test_full_decode_step_set(kind, dependent):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_plain_stage_launches_of_the_set(kind):
+    """The set as the 65 plain stage launches that bench.py times (decode_set.build_stages: one skinny launch per
+    stage over its adjacent weight rows, each on its own unit-RMS input), replayed from a HIP graph: every stage's
+    output against the fp32 product of its input and weights, and each replay equal to the eager pass."""
+    print(f"\n[set] 65 plain stage launches {kind}", flush=True)
+    weights = D.make_weights(kind, DEV, seed=0)
+    ops = D.build_stages(weights, 1, DEV, seed=0)
+    assert len(ops) == 65
+    for op in ops:
+        op()
+    torch.cuda.synchronize()
+    for i, op in enumerate(ops):
+        w = op.args
+        w32 = (w[0].float() * w[1].float()[:, None]) if len(w) > 1 else w[0].float()
+        ref = op.x.float() @ w32.T
+        den = (op.x.float().abs() @ w32.abs().T).clamp(min=1e-30)
+        comp = float(((op.y.float() - ref).abs() / den).max())
+        norm = float((op.y.float() - ref).abs().max() / ref.abs().max())
+        assert comp < 4e-3 and norm < 1e-2, (i, op.name, comp, norm)
+        del w32
+    eager = [op.y.clone() for op in ops]
+    g = D.capture(ops)
+    for _ in range(3):
+        for op in ops:
+            op.y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, op.y) for a, op in zip(eager, ops))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
 def test_stage_graph_of_skinny_launches(kind):
     """The dependent set as 65 stream-ordered skinny launches (one per stage over its adjacent weight rows, the
     renormalisation inside the launch), eager and replayed from a HIP graph: every stage within the gates of its
