@@ -18,6 +18,7 @@ import torch
 from .. import _lib
 from ..optim import skinny
 
+_X_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 DEFAULT_CFG = None  # chosen per shape by byteprof_amd.optim.skinny.get_cfg (tuned table / heuristic)
 
 
@@ -28,10 +29,14 @@ def default_cfg(n_out: int, k: int = 2048) -> tuple[int, int]:
 
 def gemv_int8(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, cfg: tuple[int, ...] | None = None,
               out: torch.Tensor | None = None) -> torch.Tensor:
-    """x: [1, K] bf16, w: [N, K] int8, scale: [N] (bf16 / fp16 / fp32) -> [1, N] bf16."""
+    """x: [1, K] bf16 / fp16 / fp32, w: [N, K] int8, scale: [N] (bf16 / fp16 / fp32) -> [1, N] in x's dtype.
+
+    The kernel's activation operands are bf16: an fp16 or fp32 row is rounded to bf16 on the way in (the
+    reference's GEMV reads x as fp32, triton_int8.py:24; the rounding adds at most 2^-9 of |x| . |w| per output,
+    inside the skinny gates) and the bf16 result is cast to x's dtype, as the reference returns it."""
     N, K = w.shape
-    if x.numel() != K or not x.is_contiguous() or x.dtype != torch.bfloat16 or not x.is_cuda:
-        raise ValueError("x must be a contiguous [1, K] bfloat16 GPU tensor")
+    if x.numel() != K or not x.is_contiguous() or x.dtype not in _X_DTYPES or not x.is_cuda:
+        raise ValueError("x must be a contiguous [1, K] bfloat16, float16 or float32 GPU tensor")
     if not w.is_contiguous() or scale.shape != (N,) or not scale.is_contiguous():
         raise ValueError("w must be a contiguous [N, K] int8 tensor and scale a contiguous [N] tensor")
     y = out if out is not None else torch.empty(1, N, dtype=x.dtype, device=x.device)
@@ -43,7 +48,11 @@ def gemv_int8(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, cfg: tuple[
     if cfg is not None:  # (rows, waves) or (BN, BK, num_warps): the split stays the shape's own (its K order)
         split = skinny.get_cfg("int8", N, K, 1)[2]
         cfg = (int(cfg[0]), int(cfg[-1] if len(cfg) == 2 else cfg[2]), split)
-    skinny._launch("int8", x.reshape(1, K), w, scale, y, cfg)
+    bf = x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16
+    yb = y if bf else torch.empty(1, N, dtype=torch.bfloat16, device=x.device)
+    skinny._launch("int8", x.reshape(1, K).to(torch.bfloat16), w, scale, yb, cfg)
+    if not bf:
+        y.copy_(yb.view_as(y))
     return y
 
 

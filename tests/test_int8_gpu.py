@@ -82,6 +82,35 @@ def test_int8linear_single_row_and_batch_paths_agree_with_bias():
     assert (batch.float() - lin(x).float()).abs().max() < 0.1
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_int8linear_one_row_of_any_float_dtype_takes_the_kernel(dtype, monkeypatch):
+    """One fp32 or fp16 row goes through the fused int8 product, as in the reference, whose GEMV reads x as fp32
+    (integrate.py:40-42, triton_int8.py:24): never through the dequantized weight; the result is in x's dtype and
+    within the int8 tolerance of the oracle on the unrounded activations."""
+    from byteprof_amd.quant.integrate import Int8Linear
+
+    torch.manual_seed(11)
+    n, k = 2048, 2048
+    lin = nn.Linear(k, n, bias=True, dtype=dtype, device="cuda")
+    mod = Int8Linear(lin)
+
+    def refuse(_dtype):
+        raise AssertionError("a one-row GPU call dequantized the weight")
+
+    monkeypatch.setattr(mod, "dequantized", refuse)
+    x = torch.randn(1, 1, k, device="cuda", dtype=dtype)
+    y = mod(x)
+    assert y.shape == (1, 1, n) and y.dtype == dtype
+    ref = _oracle(x.reshape(1, k), mod.q, mod.scale, lin.bias)
+    err = float(abs(y.reshape(1, n).float().cpu().numpy() - ref).max())
+    assert err <= 0.01 * float(abs(ref).max()) + 1e-3, err
+    out = torch.empty(1, n, dtype=dtype, device="cuda")
+    assert gemv_int8(x.reshape(1, k), mod.q, mod.scale, out=out) is out
+    ref_nb = _oracle(x.reshape(1, k), mod.q, mod.scale)
+    err = float(abs(out.float().cpu().numpy() - ref_nb).max())
+    assert err <= 0.01 * float(abs(ref_nb).max()) + 1e-3, err
+
+
 def test_int8linear_empty_input():
     from byteprof_amd.quant.integrate import Int8Linear
 

@@ -169,8 +169,6 @@ def test_mf_silu_equals_mf_then_silu_mul(kind, m, plan):
     L = _lib.lib()
     F, K = 1000, 2048
     rb, waves, xs = plan
-    if xs and L.bp_skinny_mf_stage_bytes(0 if kind == "bf16" else 1, m, K, 1) < 0:
-        pytest.skip("the activations of this row count do not fit the LDS stage")
     rng = np.random.default_rng(m * 7 + waves)
     x = _bf16(ON.bf16_round(rng.standard_normal((m, K)).astype(np.float32)))
     w = _bf16(ON.bf16_round(rng.standard_normal((2 * F, K)).astype(np.float32) * 0.05))
@@ -178,6 +176,13 @@ def test_mf_silu_equals_mf_then_silu_mul(kind, m, plan):
     sc, sdt = (args[1].data_ptr(), _lib.TORCH_DT[torch.float16]) if kind == "int8" else (None, 0)
     kc = 0 if kind == "bf16" else 1
     out = torch.full((m, F), 3.0, dtype=torch.bfloat16, device=DEV)
+    if xs and L.bp_skinny_mf_stage_bytes(kc, m, K, 1) < 0:
+        # the activations of this row count do not fit the LDS stage: refused before anything is enqueued
+        assert L.bp_skinny_mf_silu(kc, x.data_ptr(), args[0].data_ptr(), sc, sdt, out.data_ptr(), m, F, K, rb, waves,
+                                   xs, _st()) == -2
+        torch.cuda.synchronize()
+        assert bool((out == 3.0).all())
+        return
     _lib.check(L.bp_skinny_mf_silu(kc, x.data_ptr(), args[0].data_ptr(), sc, sdt, out.data_ptr(), m, F, K, rb, waves,
                                    xs, _st()), "mf_silu")
     gu = torch.empty(m, 2 * F, dtype=torch.bfloat16, device=DEV)
@@ -201,8 +206,6 @@ def test_splitk_norm_residual_equals_reduce_then_norm(kind, m, plan):
     L = _lib.lib()
     H, F = 2048, 8192
     rb, waves, split, xs = plan
-    if xs and L.bp_skinny_mf_stage_bytes(0 if kind == "bf16" else 1, m, F, split) < 0:
-        pytest.skip("the activations of this row count do not fit the LDS stage")
     rng = np.random.default_rng(m * 11 + waves + split)
     x = _bf16(ON.bf16_round(rng.standard_normal((m, F)).astype(np.float32)))
     w = _bf16(ON.bf16_round(rng.standard_normal((H, F)).astype(np.float32) * 0.02))
@@ -213,6 +216,17 @@ def test_splitk_norm_residual_equals_reduce_then_norm(kind, m, plan):
     kc = 0 if kind == "bf16" else 1
     ws = torch.empty(split * m * H, dtype=torch.float32, device=DEV)
     ra, rbuf = r0.clone(), r0.clone()
+    if xs and L.bp_skinny_mf_stage_bytes(kc, m, F, split) < 0:
+        # the activations of this row count do not fit the LDS stage: both launches are refused before anything is
+        # enqueued
+        assert L.bp_skinny_mf_partials(kc, x.data_ptr(), args[0].data_ptr(), m, H, F, rb, waves, split, xs,
+                                       ws.data_ptr(), ws.numel() * 4, _st()) == -2
+        y = torch.full((m, H), 3.0, dtype=torch.bfloat16, device=DEV)
+        assert L.bp_skinny_mf(kc, x.data_ptr(), args[0].data_ptr(), sc, sdt, y.data_ptr(), m, H, F, rb, waves, split,
+                              xs, ws.data_ptr(), ws.numel() * 4, _st()) == -2
+        torch.cuda.synchronize()
+        assert bool((y == 3.0).all())
+        return
     _lib.check(L.bp_skinny_mf_partials(kc, x.data_ptr(), args[0].data_ptr(), m, H, F, rb, waves, split, xs,
                                        ws.data_ptr(), ws.numel() * 4, _st()), "partials")
     _lib.check(L.bp_decode_splitk_norm_residual_rows(ws.data_ptr(), split, sc, sdt, nw.data_ptr(), ra.data_ptr(),

@@ -92,6 +92,36 @@ def test_two_norm_prologue_equals_norm_launch_then_norm_prologue(kind, n, m):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("with_residual,with_gamma2", [(True, True), (True, False), (False, True), (False, False)])
+def test_norm_prologue_at_k8192_two_rows(kind, with_residual, with_gamma2):
+    """K = 8192 at two rows: the staged rows take 32 KiB; gamma, the residual rows and gamma2 (16 KiB per row or
+    vector) join them in LDS while the total stays within 80 KiB, and are otherwise read from memory (residual +
+    gamma2: 96 KiB). Both ways equal the separate norm launch(es) followed by the plain launch, bit for bit."""
+    g = _gen(40 + 2 * with_residual + with_gamma2)
+    n, k, m, eps = 2048, 8192, 2, 1e-6
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    args = (w, None) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
+    x = (torch.randn(m, k, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
+    gamma = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    gamma2 = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16) if with_gamma2 else None
+    res = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16) if with_residual else None
+    xn = _norm_rows(x, gamma, res, eps)
+    xm = _norm_rows(xn, gamma2, None, eps) if with_gamma2 else xn
+    want = S.skinny_mm(xm, *[a for a in args if a is not None])
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    xout = torch.empty(m, k, dtype=torch.bfloat16, device=DEV)
+    S.prologue_mm(x, args[0], args[1], out, S.PRO_NORM, gamma=gamma, residual=res, xout=xout, eps=eps, gamma2=gamma2)
+    torch.cuda.synchronize()
+    assert torch.equal(xout, xn)
+    assert torch.equal(out, want)
+    # three rows of 8192 do not fit the 32 KiB stage: refused before anything is enqueued
+    x3 = torch.zeros(3, k, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError):
+        S.prologue_mm(x3, args[0], args[1], torch.empty(3, n, dtype=torch.bfloat16, device=DEV), S.PRO_NORM,
+                      gamma=gamma, eps=eps)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
 def test_norm_prologue_with_the_silu_epilogue(kind):
     """The fused norm before the interleaved gate|up projection equals norm launch + bp_skinny_mf_silu."""
     g = _gen(20)
