@@ -13,24 +13,28 @@ execution model is the same sequence with one skinny call per linear (byteprof/o
 benchmark times those calls, tools/skinny_bench.py:45-71): that 113-launch graph is reported beside it.
 
 Printed (one JSON line): GB/s of the step (algorithmic bytes = weights + activations + outputs, each once:
-2,560,237,568 B per step), us per set and % of the 8 TB/s peak; `roofline` for the kernel instantiation with the
-largest time per step (its launches' algorithmic bytes over their average duration from HIP events, HBM traffic per
-launch from the committed rocprofv3 counter summary); `cpu_baseline`: torch F.linear over the set on the host cores
-(the reference's CPU path); secondary figures:
+2,560,237,568 B per step), us per set and % of the 8 TB/s peak; `roofline` for the dominant (kernel instantiation,
+shape) pair, the one with the largest time per step (its launches' algorithmic bytes over their average duration
+from HIP events, HBM traffic per launch from the committed rocprofv3 counter summary), with `shapes` giving the same
+figures for every shape of the set; `copy_ceiling`: a 256 MiB device copy (read + write counted), the ceiling the
+reference reports (tools/skinny_bench.py:74-81); config.floor_us_stream_ordered: 65 empty launches plus the set's
+bytes at the one-launch grid's read rate; `cpu_baseline`: torch F.linear over the set on the host cores (the
+reference's CPU path); secondary figures:
   - graph_113: the 113 linears as one skinny launch each (the reference's sequence);
   - one_launch_set: the same 113 independent linears as one grid (csrc/skinny_chain.hip), with its own roofline;
   - dependent: the set with real data dependencies (each stage reads the unit-RMS renormalisation of the output it
     depends on in a decode step) as 65 stream-ordered skinny launches (the renormalisation inside each launch), as
     one launch of the chain kernel (in-kernel hand-off) and as 65 launches of the chain kernel (those two give
     bitwise equal outputs, checked here);
-  - int8_set: the int8 weight-only set (fp16 scales) in the same execution models, and as 113-launch graphs at
-    M = 4 and 16; bf16 / int8 time ratios;
+  - int8_set: the int8 weight-only set (fp16 scales) in the same execution models (its stage graph with a
+    per-shape roofline), and as 113-launch graphs at M = 4 and 16; bf16 / int8 time ratios;
   - int4: the group-128 int4 kernel on the set's shapes;
   - c1: one 8192 x 2048 linear at M = 1 (GPU, and F.linear on the CPU);
   - mlstm: the fused 16-step mLSTM block;
   - sweep_bf16 / sweep_int8: the verify widths M in {1, 2, 4, 8, 16} x K {2048, 8192} x N {2048, 8192, 100352};
   - decode_loop: the graph-captured greedy decode loop of the OLMo-2-1B shape (bf16, int8) and its drafting loop;
-  - cpu_legs: fp32 F.linear over the set, int8 dequantize-then-F.linear, the fp32 mLSTM recurrence.
+  - cpu_legs: on the host cores, fp32 F.linear over the full 113-linear set, int8 dequantize-then-F.linear over
+    the full set, the 8192 x 2048 linear alone, and the mLSTM block as a torch fp32 step loop.
 Every timed leg is warmed by time (WARM_S seconds of its own launches) first.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
@@ -146,25 +150,40 @@ def per_shape(ops, kind: str, m: int) -> dict:
 
 
 def roofline_of_graph(shapes: dict) -> dict:
-    """The kernel instantiation with the largest total time per step: algorithmic bytes of its launches over their
-    average duration (HIP events over graphs of its launches); HBM traffic per launch from the committed profile
-    when it covers every shape this instantiation serves."""
-    by_kernel: dict[str, list] = {}
-    for key, s in shapes.items():
-        by_kernel.setdefault(s["kernel"], []).append((key, s))
-    name, items = max(by_kernel.items(), key=lambda kv: sum(s["us"] * s["launches"] for _, s in kv[1]))
-    launches = sum(s["launches"] for _, s in items)
-    t = sum(s["us"] * s["launches"] for _, s in items)
-    b = sum(s["bytes"] * s["launches"] for _, s in items)
-    achieved = b / t / 1e3
+    """The dominant (kernel instantiation, shape) pair, the one with the largest time per step: its algorithmic
+    bytes per launch over its average launch duration (HIP events over a graph of the set's launches of that shape),
+    HBM traffic per launch from the committed counter summary; `shapes` lists the same figures for every shape of
+    the set (one entry each)."""
     prof = profiled_traffic(SET_PROFILE)
-    traffic = None
-    if all((name, k) in prof for k, _ in items):
-        traffic = sum(prof[(name, k)] * s["launches"] for k, s in items) / launches
-    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": name,
-            "shapes": [k for k, _ in items], "launches_per_step": launches,
-            "avg_us_per_launch": t / launches, "avg_bytes_per_launch": b / launches}
+    entries = []
+    for key, s in shapes.items():
+        e = {"shape": key, "kernel": s["kernel"], "launches_per_step": s["launches"], "us_per_launch": s["us"],
+             "us_per_step": s["us"] * s["launches"], "bytes_per_launch": s["bytes"], "achieved": s["gbs"],
+             "frac": s["gbs"] / HBM_PEAK_GBS, "traffic": prof.get((s["kernel"], key))}
+        entries.append(e)
+    entries.sort(key=lambda e: -e["us_per_step"])
+    top = entries[0]
+    return {"bound": "hbm", "achieved": top["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": top["frac"],
+            "traffic": top["traffic"], "kernel": top["kernel"], "shape": top["shape"],
+            "launches_per_step": top["launches_per_step"], "avg_us_per_launch": top["us_per_launch"],
+            "bytes_per_launch": top["bytes_per_launch"], "shapes": entries}
+
+
+def copy_ceiling(device, mib: int = 256) -> dict:
+    """GB/s of a large device-to-device copy (read + write counted), timed as a HIP graph of copies: the streaming
+    ceiling the reference reports beside its skinny figures (tools/skinny_bench.py:74-81)."""
+    import torch
+
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device=device)
+    b = torch.empty_like(a)
+    g = graph_of([lambda: b.copy_(a)] * 10)
+    ev_ms, _ = time_runs(g.replay, 7, warm_s=0.2)
+    del g, a, b
+    us = ev_ms * 1e3 / 10
+    gbs = 2 * n / us / 1e3
+    return {"gbs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "us_per_copy": us, "bytes_moved": 2 * n,
+            "method": f"torch copy_ of {mib} MiB (read + write counted), graph of 10 copies, HIP events"}
 
 
 def chain_roofline(lc, ev_ms: float, nbytes: int, tag: str) -> dict:
@@ -492,59 +511,101 @@ def cpu_baseline(weights, budget_s: float = 15.0) -> dict:
             "ms_per_set": sec * 1e3}
 
 
-def cpu_legs(weights8, budget_s: float = 12.0) -> dict:
-    """Further CPU figures on the host cores: fp32 F.linear over the set (fp32 copies of the bf16 weights, a sample
-    of the set's shapes scaled to the whole set by bytes), int8 dequantize-then-F.linear (the reference's int8 CPU
-    path, byteprof/quant/integrate.py:35-45: dequantized weights, then F.linear; same sample), the 8192 x 2048 linear alone (bf16), and the
-    fp32 mLSTM recurrence of the drafting step (the reference's recurrent step restated in numpy, oracle/mlstm.py:
-    T = 16, NH = 4, DQ = DV = 256)."""
-    import numpy as np
+def cpu_fp32_set(weights, budget_s: float = 12.0) -> dict:
+    """torch F.linear in fp32 on the host cores over the full 113-linear decode-step set (fp32 copies of the bf16
+    weights, 5.1 GB), the reference's CPU path at full precision. Bounded: at most 5 passes."""
     import torch
     import torch.nn.functional as F
 
     from byteprof_amd import decode_set as D
-    from byteprof_amd.quant.accounting import Linear, call_bytes
-    from oracle import mlstm as OM
 
     cores = _cores()
     torch.set_num_threads(cores)
     gen = torch.Generator().manual_seed(1)
-    # sample: layer 0's seven linears and the LM head (31% of the set's bytes)
-    names = [f"l0.{nm}" for nm, _, _ in D.LAYER_LINEARS] + ["lm_head"]
-    shapes = {name: (n, k) for name, n, k in D.shapes()}
-    scale_all = D.chain_bytes("bf16") / sum(call_bytes(Linear(*shapes[nm]), None, 1) for nm in names)
+    host = [(weights[name][0].cpu().float(), torch.randn(1, k, generator=gen)) for name, n, k in D.shapes()]
+    sec, passes = _time_passes(lambda: [F.linear(x, w) for w, x in host], budget_s)
+    del host
+    return {"ms_per_set": sec * 1e3, "cores": cores, "linears": len(D.shapes()),
+            "sample": f"the full set, {passes} passes, median"}
+
+
+def cpu_int8_set(weights8, budget_s: float = 12.0) -> dict:
+    """The reference's int8 CPU path over the full 113-linear set: per linear the weights dequantized in the
+    activation dtype, then F.linear (byteprof/quant/integrate.py:35-45), on the host cores; at most 5 passes."""
+    import torch
+    import torch.nn.functional as F
+
+    from byteprof_amd import decode_set as D
+
+    cores = _cores()
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(2)
+    host = [(weights8[name][0].cpu(), weights8[name][1].cpu(), torch.randn(1, k, generator=gen).to(torch.bfloat16))
+            for name, n, k in D.shapes()]
+
+    def one_pass():
+        for q, sc, x in host:
+            F.linear(x, q.to(x.dtype) * sc.to(x.dtype)[:, None])
+
+    sec, passes = _time_passes(one_pass, budget_s)
+    del host
+    return {"ms_per_set": sec * 1e3, "cores": cores, "linears": len(D.shapes()),
+            "sample": f"the full set, {passes} passes, median; fp16 scales, bf16 activations"}
+
+
+def mlstm_torch_fp32(c, n, m, q, k, v, i, f, eps: float):
+    """The fused multistep recurrence of byteprof/optim/mlstm_multistep.py:21-86 as a torch fp32 step loop over the
+    heads at once (DTYPE = DTYPE_STATE = fp32): per step the gates (f_log = log(sigmoid(f)), m_new = max(f_log + m,
+    i), f_act, i_act, max_val), C <- f_act C + i_act k v^T, n <- f_act n + i_act k, h = (q_s C) / (max(|q_s . n|,
+    max_val) + eps) with q_s = q DQ^-1/2. c [NH, DQ, DV], n [NH, DQ], m [NH]; q, k [T, NH, DQ]; v [T, NH, DV];
+    i, f [T, NH]. Returns h [T, NH, DV]."""
+    import torch
+
+    t_steps, _, dq = q.shape
+    scale = dq ** -0.5
+    h = torch.empty(t_steps, v.shape[1], v.shape[2])
+    for t in range(t_steps):
+        f_log = torch.log(torch.sigmoid(f[t]))
+        m_new = torch.maximum(f_log + m, i[t])
+        max_val = torch.exp(-m_new)
+        f_act = torch.exp(f_log + m - m_new)
+        i_act = torch.exp(i[t] - m_new)
+        c = f_act[:, None, None] * c + i_act[:, None, None] * (k[t][:, :, None] * v[t][:, None, :])
+        n = f_act[:, None] * n + i_act[:, None] * k[t]
+        qs = q[t] * scale
+        h_num = torch.bmm(qs[:, None, :], c)[:, 0, :]
+        qn = (qs * n).sum(-1)
+        h[t] = h_num / (torch.maximum(qn.abs(), max_val) + eps)[:, None]
+        m = m_new
+    return h
+
+
+def cpu_legs(weights8, fp32_set: dict | None = None, budget_s: float = 12.0) -> dict:
+    """Further CPU figures on the host cores: fp32 F.linear over the full set (measured by cpu_fp32_set while the
+    bf16 weights exist), the int8 dequantize-then-F.linear set, the 8192 x 2048 linear alone (bf16), and the mLSTM
+    block as a torch fp32 step loop (T = 16, NH = 4, DQ = DV = 256)."""
+    import torch
+    import torch.nn.functional as F
+
+    cores = _cores()
+    torch.set_num_threads(cores)
     out = {"cores": cores, "cpu": _cpu_name()}
-    xs = {nm: torch.randn(1, shapes[nm][1], generator=gen) for nm in names}
-    w32 = {nm: (torch.randn(*shapes[nm], generator=gen) * 0.02) for nm in names}
-    sec, passes = _time_passes(lambda: [F.linear(xs[nm], w32[nm]) for nm in names], budget_s)
-    out["fp32_set"] = {"ms_per_set": sec * scale_all * 1e3, "sample": f"layer 0 + LM head, {passes} passes, scaled "
-                       f"x{scale_all:.2f} to the set by bytes"}
-    del w32
-    q8 = {nm: (weights8[nm][0].cpu(), weights8[nm][1].cpu()) for nm in names}
-    xb = {nm: xs[nm].to(torch.bfloat16) for nm in names}
-
-    def int8_pass():
-        for nm in names:
-            q, s = q8[nm]
-            F.linear(xb[nm], (q.to(torch.bfloat16) * s.to(torch.bfloat16)[:, None]))
-
-    sec8, passes8 = _time_passes(int8_pass, budget_s)
-    scale8 = D.chain_bytes("int8") / sum(call_bytes(Linear(*shapes[nm]), "int8_wo", 1) for nm in names)
-    out["int8_dequant_set"] = {"ms_per_set": sec8 * scale8 * 1e3,
-                               "sample": f"layer 0 + LM head, {passes8} passes, scaled x{scale8:.2f} to the set"}
-    del q8
+    if fp32_set is not None:
+        out["fp32_set"] = fp32_set
+    out["int8_dequant_set"] = cpu_int8_set(weights8, budget_s)
+    gen = torch.Generator().manual_seed(1)
     w1 = (torch.randn(8192, 2048, generator=gen) * 0.02).to(torch.bfloat16)
     x1 = torch.randn(1, 2048, generator=gen).to(torch.bfloat16)
     sec1, _ = _time_passes(lambda: [F.linear(x1, w1) for _ in range(10)], 3.0)
     out["c1_bf16_us"] = sec1 / 10 * 1e6
-    rng = np.random.default_rng(0)
     t, nh, dq, dv = 16, 4, 256, 256
-    args = (rng.standard_normal((nh, dq, dv)) * 0.1, rng.standard_normal((nh, dq)) * 0.1, rng.standard_normal(nh),
-            rng.standard_normal((t, nh, dq)), rng.standard_normal((t, nh, dq)) / 16, rng.standard_normal((t, nh, dv)),
-            rng.standard_normal((t, nh)), rng.standard_normal((t, nh)) + 3.0)
-    secm, _ = _time_passes(lambda: OM.multistep(*args, eps=1e-6, io="f64"), 3.0)
-    out["mlstm_block_us"] = {"value": secm * 1e6, "kind": "port", "threads": 1,
-                             "sample": "oracle.mlstm.multistep, float64 numpy, one 16-step block"}
+    r = lambda *sh: torch.randn(*sh, generator=gen)  # noqa: E731
+    args = (r(nh, dq, dv) * 0.1, r(nh, dq) * 0.1, r(nh), r(t, nh, dq), r(t, nh, dq), r(t, nh, dv), r(t, nh),
+            r(t, nh) + 3.0)
+    secm, passes = _time_passes(lambda: mlstm_torch_fp32(*args, eps=1e-6), 3.0, max_passes=20)
+    out["mlstm_block_us"] = {"value": secm * 1e6, "kind": "reference", "threads": cores,
+                             "sample": f"torch fp32 step loop of the multistep recurrence, one 16-step block, "
+                                       f"{passes} passes, median"}
     return out
 
 
@@ -599,8 +660,10 @@ def main() -> int:
     ms = max(ev_ms, wall_ms)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] {ms * 1e3:.1f} us per set, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
-    log("[bench] per-shape launch times (roofline)")
+    log("[bench] per-shape launch times (roofline) and the device-copy ceiling")
     shapes = per_shape(stages, "bf16", 1)
+    ceiling = copy_ceiling(device)
+    empty_us = D.dispatch_gap_us()
     ops = D.build("bf16", 1, device, seed=0, weights=weights)
     result = {
         "metric": METRIC, "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -612,7 +675,8 @@ def main() -> int:
                    "M": 1, "linears": len(D.shapes()), "launches": len(stages), "bytes_per_step": nbytes,
                    "us_per_set": ms * 1e3,
                    "pct_of_hbm_peak": gbs / HBM_PEAK_GBS * 100, "event_ms": ev_ms, "wall_ms": wall_ms,
-                   "empty_launch_us": D.dispatch_gap_us()},
+                   "empty_launch_us": empty_us},
+        "copy_ceiling": ceiling,
         "roofline": roofline_of_graph(shapes),
         "kernels": shapes,
     }
@@ -627,10 +691,19 @@ def main() -> int:
         extra(result, "graph_113", graph_113)
         extra(result, "one_launch_set", one_launch, "bf16", weights, nbytes, device, 4, "one-launch-bf16")
         extra(result, "dependent", dependent_figures, "bf16", weights, nbytes, device)
+        one = result.get("one_launch_set", {})
+        if "gbs" in one:
+            # what stream-ordered launches allow: every launch's empty-launch cost plus the set's bytes at the best
+            # read rate measured here (the one-launch grid over the same weights)
+            result["config"]["floor_us_stream_ordered"] = len(D.stage_shapes()) * empty_us + nbytes / one["gbs"] / 1e3
     del ops
+    fp32_set = None
     if not a.no_cpu:
         log("[bench] CPU baseline")
         result["cpu_baseline"] = cpu_baseline(weights)
+        if not a.no_extras:
+            log("[bench] CPU fp32 set")
+            fp32_set = cpu_fp32_set(weights)
     del weights
     torch.cuda.empty_cache()
     if not a.no_extras:
@@ -647,7 +720,8 @@ def main() -> int:
             e8, _ = time_runs(g8.replay, 50)
             del g8
             out = {"bytes_per_step": nb8, "scales": "fp16 per output row",
-                   "stage_graph": {**figures(es8, nb8), "launches": len(st8), "kernels": per_shape(st8, "int8", 1)},
+                   "stage_graph": {**figures(es8, nb8), "launches": len(st8),
+                                   "roofline": roofline_of_graph(per_shape(st8, "int8", 1))},
                    "graph_113": {**figures(e8, nb8), "kernels": per_shape(ops8, "int8", 1)},
                    "graph_113_m4": graph_set("int8", w8, 4, device), "graph_113_m16": graph_set("int8", w8, 16, device),
                    "one_launch_set": one_launch("int8", w8, nb8, device, 2, "one-launch-int8"),
@@ -667,7 +741,7 @@ def main() -> int:
 
         extra(result, "int8_set", int8_set)
         if not a.no_cpu:
-            extra(result, "cpu_legs", cpu_legs, w8)
+            extra(result, "cpu_legs", cpu_legs, w8, fp32_set)
         del w8
         torch.cuda.empty_cache()
         extra(result, "int4", int4_figures, device)
