@@ -15,6 +15,8 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load: shares torch's HIP runtime)
 
 LIB_PATH = Path(__file__).resolve().parent / "libbyteprof_amd.so"
+# BYTEPROF_AMD_LIB: another build of the same ABI to load instead (the mutation check, tests/mutation.py)
+LIB_ENV = "BYTEPROF_AMD_LIB"
 
 BP_OK = 0
 BP_E_INVALID_ARG = -1
@@ -110,10 +112,11 @@ def lib() -> ctypes.CDLL:
     global _LIB
     if _LIB is not None:
         return _LIB
-    if not LIB_PATH.exists():
-        raise RuntimeError(f"{LIB_PATH} is not built: run `python -m byteprof_amd.build` "
+    path = Path(os.environ[LIB_ENV]) if os.environ.get(LIB_ENV) else LIB_PATH
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built: run `python -m byteprof_amd.build` "
                            "(or __graft_entry__.build()) first")
-    handle = ctypes.CDLL(str(LIB_PATH))
+    handle = ctypes.CDLL(str(path))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(handle, name)
         fn.restype = res
