@@ -253,8 +253,8 @@ def graph_set(kind: str, weights, m: int, device, seed: int = 0) -> dict:
 
 
 def int4_figures(device) -> dict:
-    """The group-128 int4 kernel (tiles of 32 rows) at M = 1 on the set's shapes: us per call over a ring of
-    distinct weights, bytes stored (codes + bf16 scales + fp16 zeros + activations + outputs)."""
+    """The group-128 int4 kernel at M = 1 on the set's shapes, the weights packed with the tuned tile rows: us per
+    call over a ring of distinct weights, bytes stored (codes + bf16 scales + fp16 zeros + activations + outputs)."""
     import torch
 
     from byteprof_amd.optim import skinny as S
@@ -262,7 +262,7 @@ def int4_figures(device) -> dict:
     out = {}
     for n, k in ((2048, 2048), (8192, 2048), (2048, 8192), (100352, 2048)):
         w = (torch.randn(n, k, device=device) * 0.02).to(torch.bfloat16)
-        packed, sc, z = S.quantize_int4(w)
+        packed, sc, z = S.quantize_int4(w, S.int4_tile_rows(n, k))
         del w
         per = packed.numel() + sc.numel() * 2 + z.numel() * 2
         ring = [(packed, sc, z)] + [(packed.clone(), sc.clone(), z.clone()) for _ in range(max(1, (1 << 29) // per) - 1)]
@@ -272,7 +272,8 @@ def int4_figures(device) -> dict:
         ev_ms, _ = time_runs(g.replay, 5, warm_s=0.2)
         us = ev_ms * 1e3 / len(ring)
         nbytes = per + 2 * (n + k)
-        out[f"{n}x{k}"] = {"us": us, "gbs_stored_bytes": nbytes / us / 1e3, "bytes": nbytes}
+        out[f"{n}x{k}"] = {"us": us, "gbs_stored_bytes": nbytes / us / 1e3, "bytes": nbytes,
+                           "tile_rows": int(packed.shape[2])}
         del g, ring, packed, sc, z
         torch.cuda.empty_cache()
     return out

@@ -54,6 +54,15 @@ __device__ __forceinline__ gptr<T> as_global_mut(T* p) {
   return (gptr<T>)(p);
 }
 
+// The tile of workgroup b of a row of T: the hardware deals a grid's workgroups to the 8 XCDs in turn (b % 8), and
+// this gives each XCD one contiguous run of tiles, so neighbouring tiles that share cache lines (a scale row's 32
+// bytes per 16 rows) meet in one XCD's L2 instead of four.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t T) {
+  const int64_t x = b % kXcds, q = T / kXcds, r = T % kXcds;
+  return x * q + (x < r ? x : r) + b / kXcds;
+}
+
 // Load a scale element of the given dtype code as fp32 (0 = bf16, 1 = fp16, 2 = fp32).
 __device__ __forceinline__ float load_scale(const void* p, int64_t i, int dt) {
   if (dt == 0) return bf16_bits_to_float(as_global(static_cast<const uint16_t*>(p))[i]);

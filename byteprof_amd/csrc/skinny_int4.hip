@@ -65,12 +65,13 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_kernel(const uint16
   const int wave = threadIdx.x / kWave;
   const int rr = lane >> 2;
   const int q = lane & 3;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int64_t tb = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t n0 = tb * R;
   const int64_t G = K / 128;
   const int s = blockIdx.y;
   const int64_t g_lo = s * G / split;
   const int64_t g_hi = (s + 1) * G / split;
-  const uint8_t* tile = w + static_cast<int64_t>(blockIdx.x) * G * R * 64 + rr * 64 + q * 16;
+  const uint8_t* tile = w + tb * G * R * 64 + rr * 64 + q * 16;
 
   // this lane's rows n0 + 16 h + rr (rows past N: clamped for the scale / zero reads, never stored)
   int64_t nrow[RB];
@@ -161,31 +162,36 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_kernel(const uint16
 
 // ---- matrix-core form -----------------------------------------------------------------------------------------
 // v_mfma_f32_16x16x32_bf16 with a block of 16 weight rows as A and the activation rows (up to 16, zero-padded) as
-// the B columns, so the work per group does not grow with M. A block's 1 KiB is loaded in lane order (lane l: bytes
-// 16 l .. 16 l + 15, row l / 4, quarter l % 4: consecutive lanes on consecutive bytes, the fast streaming order),
-// then passed across lanes (ds_bpermute) so that lane l (row / column i = l % 16, K block kb = l / 16) holds bytes
-// 16 kb .. 16 kb + 15 of row i, i.e. codes 16 kb + e (low nibbles) and 64 + 16 kb + e (high nibbles), e < 16; it
-// loads the activations at the same K indices; the four MFMAs of a group take K slots {16 kb + e}, {16 kb + 8 + e}, {64 + 16 kb + e},
-// {64 + 16 kb + 8 + e} (e < 8) of every kb, the same for A and B, so D[r][m] is the group's sum over all 128 codes.
+// the B columns, so the work per group does not grow with M. Lane l (row / column i = l % 16, K block kb = l / 16)
+// loads bytes 16 kb .. 16 kb + 15 of row i of a block's 1 KiB (one load covers the block), i.e. codes 16 kb + e (low
+// nibbles) and 64 + 16 kb + e (high nibbles), e < 16, and the activations at the same K indices; the four MFMAs of a
+// group take K slots {16 kb + e}, {16 kb + 8 + e}, {64 + 16 kb + e}, {64 + 16 kb + 8 + e} (e < 8) of every kb, the
+// same for A and B, so D[r][m] is the group's sum over all 128 codes. (Loading the block in lane order and passing
+// it across lanes with ds_bpermute, consecutive lanes on consecutive bytes, was 1.4 us slower on the LM head.)
 // Codes enter as bf16(128 + code) (v_perm_b32 under 0x43); per group, D (a fresh accumulator) becomes
 // scale (D - (128 + zero) X), X the group's sum of the activation row (four more MFMAs: an all-ones A against the
 // same B operands), and the lane adds it to its rows' sums in group order; the waves'
-// sums meet in LDS in wave order. The groups of a wave are loaded DEPTH ahead of their use. The order of every sum
-// depends on (K, WAVES, split) only: an output row does not depend on M (bitwise).
-// Needs N % 4 == 0 (a lane's four D rows read their scale and zero as one 8- or 16-byte load) and 16-byte aligned x,
-// 8-byte aligned zero, scale aligned to 4 of its elements.
+// sums meet in LDS in wave order. The groups of a wave are loaded DEPTH ahead of their use. A group's scales and
+// zeros for the tile's rows (its record: two 32..128-byte pieces of the [G, N] layout) arrive with the group's
+// loads as one dword per lane (two at 64 rows in fp32) and pass through the wave's own LDS stage to the lanes that
+// use them: loaded per lane, 4 rows at a time, they were twice as many small scattered loads and cost as much as the
+// weights' own stream (the LM head at one row: 32.9 us with them, 23.6 us without). The order of every sum depends
+// on (K, WAVES, split) only: an output row does not depend on M (bitwise).
+// Needs N % 4 == 0 (every dword of a record is whole, and a lane's four D rows read their scales and zeros as one
+// 8- or 16-byte LDS read) and 16-byte aligned x, 8-byte aligned zero, scale aligned to 4 of its elements.
 
-template <int RB>
+template <int RB, int NR>
 struct I4Slot {
-  u32x4 wv[RB];   // bytes 16 l .. 16 l + 15 of each 16-row block (lane order)
-  u32x4 xv[4];    // activations at K 16 kb + 0..7, + 8..15, 64 + 16 kb + 0..7, + 8..15 of the lane's column
-  u32x4 sc[RB];   // scale of the lane's four D rows (fp32 x 4, or 16-bit x 4 in .x, .y)
-  uint2 zr[RB];   // zero (fp16 x 4) of the same rows
+  u32x4 wv[RB];      // bytes 16 l .. 16 l + 15 of each 16-row block (lane order)
+  u32x4 xv[4];       // activations at K 16 kb + 0..7, + 8..15, 64 + 16 kb + 0..7, + 8..15 of the lane's column
+  uint32_t rv[NR];   // dwords 64 c + l of the group's record
 };
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
 }
+
+using u32x2 = unsigned __attribute__((ext_vector_type(2)));
 
 template <int RB, int WAVES, int DEPTH, int SDT>
 __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uint16_t* __restrict__ x,
@@ -201,29 +207,44 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
   __shared__ float red[WAVES][R][16];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: the group loop is scalar
   const int i = lane & 15, kb = lane >> 4;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int64_t tb = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t n0 = tb * R;
   const int64_t G = K / 128;
   const int s = blockIdx.y;
   const int64_t g_lo = s * G / split;
   const int64_t g_hi = (s + 1) * G / split;
   const int64_t first = g_lo + wave;
   const int cnt = first < g_hi ? static_cast<int>((g_hi - first + WAVES - 1) / WAVES) : 0;
-  const uint8_t* tile = w + static_cast<int64_t>(blockIdx.x) * G * R * 64 + lane * 16;
-  const int perm = 4 * (4 * i + kb);  // ds_bpermute address of the lane that loaded row i, quarter kb
+  const uint8_t* tile = w + tb * G * R * 64 + i * 64 + kb * 16;
   const uint16_t* xr = x + static_cast<int64_t>(i < M ? i : M - 1) * K + kb * 16;
-  // first of the lane's four D rows per block (n0 + 16 h + 4 kb + r); past N (all four, as N % 4 == 0): row N - 4,
-  // loaded and never stored
-  int64_t srow[RB];
-#pragma unroll
-  for (int h = 0; h < RB; ++h) {
-    const int64_t r0 = n0 + 16 * h + 4 * kb;
-    srow[h] = r0 < N ? r0 : N - 4;
-  }
   constexpr bool f32 = SDT == BP_DT_F32;  // the scale's dtype (scale_dt == SDT)
 
-  auto load = [&](I4Slot<RB>& sl, int j) {
+  // a group's record: [R scales (scale dtype) | R zeros (fp16)] of the tile's rows, kRecDw dwords; lane l holds
+  // dwords 64 c + l (lanes past the record repeat its last dword); rows past N read row N - 2 of the group (never
+  // stored). Dword 64 c + l sits at rsrc[c] + g * rstride[c] for group g.
+  constexpr int SEB = f32 ? 4 : 2;
+  constexpr int kScDw = R * SEB / 4, kRecDw = kScDw + R / 2;  // dwords of a record's scales / of the whole record
+  constexpr int kRecLoads = (kRecDw + kWave - 1) / kWave;
+  __shared__ __attribute__((aligned(16))) uint32_t stage[WAVES][kRecLoads * kWave];
+  const uint8_t* rsrc[kRecLoads];
+  int64_t rstride[kRecLoads];
+#pragma unroll
+  for (int c = 0; c < kRecLoads; ++c) {
+    const int p = min(c * kWave + lane, kRecDw - 1);
+    if (p < kScDw) {
+      const int64_t r0 = n0 + p * 4 / SEB;
+      rsrc[c] = static_cast<const uint8_t*>(scale) + (r0 < N ? r0 : N - 4 / SEB) * SEB;
+      rstride[c] = N * SEB;
+    } else {
+      const int64_t r0 = n0 + 2 * (p - kScDw);
+      rsrc[c] = reinterpret_cast<const uint8_t*>(zero + (r0 < N ? r0 : N - 2));
+      rstride[c] = N * 2;
+    }
+  }
+
+  auto load = [&](I4Slot<RB, kRecLoads>& sl, int j) {
     const int64_t g = first + static_cast<int64_t>(j) * WAVES;
 #pragma unroll
     for (int h = 0; h < RB; ++h)
@@ -234,16 +255,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
     sl.xv[2] = *reinterpret_cast<const u32x4*>(xg + 64);
     sl.xv[3] = *reinterpret_cast<const u32x4*>(xg + 72);
 #pragma unroll
-    for (int h = 0; h < RB; ++h) {
-      const int64_t e = g * N + srow[h];
-      sl.zr[h] = *reinterpret_cast<const uint2*>(zero + e);
-      if constexpr (f32) {
-        sl.sc[h] = *reinterpret_cast<const u32x4*>(static_cast<const float*>(scale) + e);
-      } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(scale) + e);
-        sl.sc[h] = u32x4{v.x, v.y, 0u, 0u};
-      }
-    }
+    for (int c = 0; c < kRecLoads; ++c) sl.rv[c] = *reinterpret_cast<const uint32_t*>(rsrc[c] + g * rstride[c]);
   };
 
   float acc[RB][4];
@@ -252,21 +264,25 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[h][r] = 0.f;
 
-  auto compute = [&](const I4Slot<RB>& sl) {
+  uint32_t* st = stage[wave];
+  auto compute = [&](const I4Slot<RB, kRecLoads>& sl) {
+    const u32x4* xv = sl.xv;
+    // the record through the wave's stage (the wave's LDS operations run in order: the previous group's reads are
+    // done before these writes land)
+#pragma unroll
+    for (int c = 0; c < kRecLoads; ++c) st[c * kWave + lane] = sl.rv[c];
+    __builtin_amdgcn_wave_barrier();
     // columns past M hold a copy of row M - 1: computed, never stored
     const u32x4 ones = u32x4{kBf16OnePair, kBf16OnePair, kBf16OnePair, kBf16OnePair};
     // X: the group's sum of each column's activations, as the product of an all-ones A with the same B operands
     floatx4 X = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      X = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ones), __builtin_bit_cast(bf16x8, sl.xv[c]),
+      X = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ones), __builtin_bit_cast(bf16x8, xv[c]),
                                                   X, 0, 0, 0);
 #pragma unroll
     for (int h = 0; h < RB; ++h) {
-      const uint32_t d[4] = {static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm, static_cast<int>(sl.wv[h].x))),
-                             static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm, static_cast<int>(sl.wv[h].y))),
-                             static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm, static_cast<int>(sl.wv[h].z))),
-                             static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm, static_cast<int>(sl.wv[h].w)))};
+      const uint32_t d[4] = {sl.wv[h].x, sl.wv[h].y, sl.wv[h].z, sl.wv[h].w};
       // operand c: codes of dwords 2 (c % 2), 2 (c % 2) + 1, low nibbles for c < 2, high for c >= 2
       u32x4 a[4];
 #pragma unroll
@@ -281,9 +297,19 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[c]),
-                                                    __builtin_bit_cast(bf16x8, sl.xv[c]), D, 0, 0, 0);
-      const uint32_t zw[2] = {sl.zr[h].x, sl.zr[h].y};
-      const uint32_t sw[4] = {sl.sc[h].x, sl.sc[h].y, sl.sc[h].z, sl.sc[h].w};
+                                                    __builtin_bit_cast(bf16x8, xv[c]), D, 0, 0, 0);
+      // the lane's four D rows 16 h + 4 kb + r of the group: their scales and zeros from the record
+      const int rr = 16 * h + 4 * kb;
+      const u32x2 zq = *reinterpret_cast<const u32x2*>(st + kScDw + rr / 2);
+      uint32_t sw[4];
+      if constexpr (f32) {
+        const u32x4 sq = *reinterpret_cast<const u32x4*>(st + rr);
+        sw[0] = sq.x, sw[1] = sq.y, sw[2] = sq.z, sw[3] = sq.w;
+      } else {
+        const u32x2 sq = *reinterpret_cast<const u32x2*>(st + rr / 2);
+        sw[0] = sq.x, sw[1] = sq.y, sw[2] = 0u, sw[3] = 0u;
+      }
+      const uint32_t zw[2] = {zq.x, zq.y};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float z = half_bits_to_float(r % 2 == 0 ? zw[r / 2] & 0xffffu : zw[r / 2] >> 16);
@@ -296,26 +322,24 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
   };
 
   if (cnt > 0) {
-    // whole rounds of DEPTH groups with every load unconditional (so the waits count exactly), then the rest
-    I4Slot<RB> sl[DEPTH];
+    // rounds of DEPTH groups with every load unconditional, so the waits count exactly (a load past the wave's last
+    // group reloads it, unused), and no peeled rest: the slots are not live after the loop, so the first round's
+    // loads land in the registers the loop uses
+    I4Slot<RB, kRecLoads> sl[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       load(sl[d], d < cnt ? d : cnt - 1);
       __builtin_amdgcn_sched_barrier(0);  // the slots' loads in slot order
     }
-    int j0 = 0;
-    for (; j0 + DEPTH <= cnt; j0 += DEPTH) {
+    for (int j0 = 0; j0 < cnt; j0 += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
         const int j = j0 + d;
-        compute(sl[d]);
-        load(sl[d], j + DEPTH < cnt ? j + DEPTH : cnt - 1);  // past the last group: the last again (not used)
+        if (j < cnt) compute(sl[d]);
+        load(sl[d], j + DEPTH < cnt ? j + DEPTH : cnt - 1);
         __builtin_amdgcn_sched_barrier(0);  // keeps the pipeline's order: group j's arithmetic before j + 1's
       }
     }
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d)
-      if (j0 + d < cnt) compute(sl[d]);
   }
 
   // the waves' sums in wave order
@@ -383,8 +407,8 @@ Int4Fn int4_rows(int rb, int waves) {
 
 }  // namespace
 
-// Matrix-core kernel for (tile rows, waves, scale dtype), or null; groups in flight per wave: 4 at 16 and 32 tile
-// rows, 2 at 64.
+// Matrix-core kernel for (tile rows, waves, scale dtype), or null; groups in flight per wave: 4 at 16 tile rows, 3
+// at 32, 2 at 64.
 Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt) {
   switch (tile_rows) {
     case 16: return int4_mf_dtype<1, 4>(waves, scale_dt);

@@ -301,9 +301,23 @@ def skinny_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None = Non
 INT4_ROWS_PER_LAUNCH = 16  # activation rows per launch of the int4 kernel
 
 
+INT4_TILES = (16, 32, 64)  # tile rows of the int4 matrix-core kernel on gfx950
+
+
+def int4_tile_rows(n: int, k: int) -> int:
+    """Tile rows to pack an int4 weight [N, K] with: the tuned table entry 'int4|N|K' (the tile rows whose plan is
+    fastest at M = 1), else by N: more rows per workgroup for larger N (one wave per 64-row tile streams the LM head
+    fastest; 16-row tiles keep small matrices on enough workgroups)."""
+    entry = _TABLE.get(("int4", n, k))
+    if entry is not None and int(entry.get("tile_rows", 32)) in INT4_TILES:
+        return int(entry.get("tile_rows", 32))
+    return 64 if n >= 32768 else 16 if n <= 4096 else 32
+
+
 def int4_cfg(n: int, k: int, tile_rows: int, cfg=None) -> tuple[int, int]:
-    """(waves, split) of an int4 launch: the tuned table entry 'int4|N|K', else a heuristic; a user cfg is
-    (waves, split) or the reference's (BN, BK, warps, stages[, split])."""
+    """(waves, split) of an int4 launch on weights packed in tiles of tile_rows: the tuned table entry 'int4|N|K'
+    for those tile rows, else a heuristic; a user cfg is (waves, split) or the reference's (BN, BK, warps,
+    stages[, split])."""
     if cfg is not None:
         if len(cfg) == 2:
             waves, split = int(cfg[0]), int(cfg[1])
@@ -312,14 +326,17 @@ def int4_cfg(n: int, k: int, tile_rows: int, cfg=None) -> tuple[int, int]:
         else:
             raise ValueError(f"int4 cfg must be (waves, split) or (BN, BK, warps, stages[, split]), got {cfg!r}")
     else:
-        entry = _TABLE.get(("int4", n, k))
-        if entry is not None:
-            waves, split = int(entry["waves"]), int(entry.get("split", 1))
+        entry = _TABLE.get(("int4", n, k)) or {}
+        plan = entry.get("tiles", {}).get(str(tile_rows))
+        if plan is None and entry and int(entry.get("tile_rows", 32)) == tile_rows:
+            plan = entry
+        if plan is not None:
+            waves, split = int(plan["waves"]), int(plan.get("split", 1))
         else:
             groups = k // GROUP
-            waves = 1
-            while waves * 2 <= min(groups, 4):
-                waves *= 2
+            waves = 1 if tile_rows == 64 else 4 if tile_rows == 16 else 8
+            while waves > 1 and waves > groups:
+                waves //= 2
             split = 1
     waves = max(w for w in (1, 2, 4, 8) if w <= max(waves, 1))
     return waves, max(1, split)

@@ -21,10 +21,14 @@ SCHEMES = {"bf16_wo": "bf16", "int8_wo": "int8", "int4_wo": "int4"}
 class SkinnyLinear(WeightOnlyLinear):
     empty_returns_empty = True
 
-    def __init__(self, lin: nn.Linear, scheme: str):
+    def __init__(self, lin: nn.Linear, scheme: str, tile_rows: int | None = None):
+        """tile_rows: int4_wo's row tiles (16, 32 or 64; the reference packs 32); None picks the tuned tile rows
+        of the weight's shape (skinny.int4_tile_rows)."""
         if scheme not in SCHEMES:
             raise ValueError(f"unknown scheme {scheme!r}")
-        super().__init__(lin, SCHEMES[scheme])
+        if tile_rows is not None and tile_rows not in skinny.INT4_TILES:
+            raise ValueError(f"int4 tile rows must be one of {skinny.INT4_TILES}, got {tile_rows}")
+        super().__init__(lin, SCHEMES[scheme], tile_rows)
         self.scheme = scheme
 
     def _kind(self) -> str:

@@ -23,14 +23,15 @@ from . import skinny
 KINDS = ("bf16", "int8", "int4")
 
 
-def _stored(kind: str, w: torch.Tensor) -> dict[str, torch.Tensor]:
-    """The buffers of a weight-only format for weights w [N, K]."""
+def _stored(kind: str, w: torch.Tensor, tile_rows: int | None = None) -> dict[str, torch.Tensor]:
+    """The buffers of a weight-only format for weights w [N, K]; int4 tiles of tile_rows rows (16, 32 or 64: the
+    format's row-tile parameter, byteprof/optim/skinny.py:188-198; None: the tuned choice for the shape)."""
     if kind == "int8":
         from ..quant.hip_int8 import quantize_rowwise_int8
 
         q, scale = quantize_rowwise_int8(w)
         return {"q": q, "scale": scale}
-    packed, scale, zero = skinny.quantize_int4(w)
+    packed, scale, zero = skinny.quantize_int4(w, tile_rows or skinny.int4_tile_rows(*w.shape))
     return {"q": packed, "scale": scale, "zero": zero}
 
 
@@ -40,7 +41,7 @@ class WeightOnlyLinear(nn.Module):
 
     empty_returns_empty = False  # an input of zero rows returns an empty output without a call
 
-    def __init__(self, lin: nn.Linear, kind: str):
+    def __init__(self, lin: nn.Linear, kind: str, tile_rows: int | None = None):
         super().__init__()
         if kind not in KINDS:
             raise ValueError(f"unknown weight kind {kind!r}")
@@ -54,7 +55,7 @@ class WeightOnlyLinear(nn.Module):
         src = lin.weight.data
         # callers read weight.dtype (and Bolmo's cache setup reads it); the bf16 weights themselves are not kept
         self.weight = nn.Parameter(src.new_empty(0), requires_grad=False)
-        stored = _stored(kind, src)
+        stored = _stored(kind, src, tile_rows)
         for name in ("q", "scale", "zero"):
             if name in stored:
                 self.register_buffer(name, stored[name])

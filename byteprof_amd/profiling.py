@@ -200,7 +200,7 @@ def main(argv=None) -> int:
             elif a.kind == "int8":
                 ring.append(quantize_rowwise_int8(w, torch.float16))
             else:
-                ring.append(S.quantize_int4(w))
+                ring.append(S.quantize_int4(w, S.int4_tile_rows(a.n, a.k)))
             del w
         x = torch.randn(a.m, a.k, device=device).to(torch.bfloat16)
         y = torch.empty(a.m, a.n, dtype=torch.bfloat16, device=device)

@@ -236,44 +236,53 @@ def tune_shape(kind: str, n: int, k: int, device, log=print) -> dict:
     return {"waves": waves, "split": split, "rb": rb, "xs": xs, "us": us, **({"rb_pro": rb_pro} if rb_pro else {})}
 
 
-def tune_int4(n: int, k: int, device, log=print) -> dict | None:
-    """int4 (tile rows 32, the quantizer's default): (waves, split) by the M = 1 time (split > 1 kept only if it
-    wins by more than 3%), then the time of every row bucket at that K order."""
+def tune_int4(n: int, k: int, device, log=print, tiles=S.INT4_TILES) -> dict | None:
+    """int4: per tile rows (16, 32, 64: a packing choice), (waves, split) by the M = 1 time (split > 1 kept only if
+    it wins by more than 3%); the tile rows of the fastest plan are the entry's, with the time of every row bucket
+    at that plan's K order."""
     if k % S.GROUP:
         return None
     groups = k // S.GROUP
     per = n * k // 2
     count = max(2, min(64, RING_BYTES // per))
-    g = torch.Generator(device=device).manual_seed(n * 17 + k)
-    ring = []
-    for _ in range(count):
-        w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
-        ring.append(S.quantize_int4(w))
-        del w
     x16 = torch.randn(16, k, device=device).to(torch.bfloat16)
     y = torch.empty(16, n, dtype=torch.bfloat16, device=device)
-    results = {}
     x1, y1 = x16[:1].contiguous(), y[:1]
-    for w in INT4_WAVES:
-        if w > groups:
-            continue
-        for sp in SPLITS:
-            if sp > 1 and sp * w > groups:
+    plans, best_tile, us = {}, None, {}
+    for tr in tiles:
+        g = torch.Generator(device=device).manual_seed(n * 17 + k)
+        ring = []
+        for _ in range(count):
+            w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+            ring.append(S.quantize_int4(w, tr))
+            del w
+        results = {}
+        for w in INT4_WAVES:
+            if w > groups:
                 continue
-            results[(w, sp)] = _time_calls([lambda a=a: S.skinny_mm(x1, *a, out=y1, cfg=(w, sp)) for a in ring])
-    best = min(results, key=results.get)
-    if best[1] > 1:
-        no_split = min((c for c in results if c[1] == 1), key=results.get)
-        if results[no_split] <= results[best] * 1.03:
-            best = no_split
-    us = {}
-    for bm in (1, 2, 4, 8, 16):
-        xb, yb = x16[:bm].contiguous(), y[:bm]
-        us[str(bm)] = round(_time_calls([lambda a=a: S.skinny_mm(xb, *a, out=yb, cfg=best) for a in ring]), 3)
-    log(f"  int4 {n}x{k}: waves={best[0]} split={best[1]}: us {us} (M=1: {per / us['1'] / 1e3:.0f} GB/s of codes)")
-    del ring
-    torch.cuda.empty_cache()
-    return {"waves": best[0], "split": best[1], "us": us}
+            for sp in SPLITS:
+                if sp > 1 and sp * w > groups:
+                    continue
+                results[(w, sp)] = _time_calls([lambda a=a: S.skinny_mm(x1, *a, out=y1, cfg=(w, sp)) for a in ring])
+        best = min(results, key=results.get)
+        if best[1] > 1:
+            no_split = min((c for c in results if c[1] == 1), key=results.get)
+            if results[no_split] <= results[best] * 1.03:
+                best = no_split
+        plans[str(tr)] = {"waves": best[0], "split": best[1], "us1": round(results[best], 3)}
+        log(f"  int4 {n}x{k} tile {tr}: waves={best[0]} split={best[1]}: {results[best]:.3f} us at M=1")
+        if best_tile is None or results[best] < plans[str(best_tile)]["us1"]:
+            best_tile = tr
+            us = {}
+            for bm in (1, 2, 4, 8, 16):
+                xb, yb = x16[:bm].contiguous(), y[:bm]
+                us[str(bm)] = round(_time_calls([lambda a=a: S.skinny_mm(xb, *a, out=yb, cfg=best) for a in ring]), 3)
+        del ring
+        torch.cuda.empty_cache()
+    top = plans[str(best_tile)]
+    log(f"  int4 {n}x{k}: tile rows {best_tile}, waves={top['waves']} split={top['split']}: us {us} "
+        f"(M=1: {per / us['1'] / 1e3:.0f} GB/s of codes)")
+    return {"tile_rows": best_tile, "waves": top["waves"], "split": top["split"], "us": us, "tiles": plans}
 
 
 def main(argv=None) -> int:
@@ -294,7 +303,9 @@ def main(argv=None) -> int:
                        "staged in LDS, 2: the general segment loop instead of the straight-line kernel of the "
                        "segment count), per row bucket (1, 8, 16, 32, 64), rb_pro = rb of launches with a norm "
                        "prologue (buckets 1 and 8), us = measured time per call by row count (ring of distinct "
-                       "weights, HIP graph); int4|N|K: waves and split of the int4 kernel (tile rows 32).")
+                       "weights, HIP graph); int4|N|K: tile_rows = the rows per tile to pack the weight "
+                       "with, waves and split of the int4 kernel at those tile rows, us per row count, and tiles = the "
+                       "best (waves, split) and its M = 1 time for each tile rows.")
     log = lambda m: print(m, flush=True)  # noqa: E731
     if a.pro_only:
         for kind in a.kinds.split(","):

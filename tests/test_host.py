@@ -325,8 +325,12 @@ def test_int4_skinny_linear_holds_the_packed_format():
     from byteprof_amd.optim.skinny_linear import SkinnyLinear
 
     lin = torch.nn.Linear(256, 40, bias=False, dtype=torch.bfloat16)
-    m = SkinnyLinear(lin, "int4_wo")
+    m = SkinnyLinear(lin, "int4_wo", tile_rows=32)  # the reference's packing
     assert m.q.shape == (2, 2, 32, 64) and m.scale.shape == (2, 40) and m.zero.shape == (2, 40)
+    tuned = S.int4_tile_rows(40, 256)
+    assert SkinnyLinear(lin, "int4_wo").q.shape == (-(-40 // tuned), 2, tuned, 64)
+    with pytest.raises(ValueError):
+        SkinnyLinear(lin, "int4_wo", tile_rows=48)
     assert m.weight.numel() == 0 and m.weight.dtype == torch.bfloat16
     x = torch.randn(3, 256, dtype=torch.bfloat16)
     y = m(x)  # CPU input: dequantized F.linear, as the reference
@@ -426,8 +430,11 @@ def test_tuned_table_entries_resolve_to_compiled_plans():
         kind, n, k = key.split("|")
         n, k = int(n), int(k)
         if kind == "int4":
-            waves, split = S.int4_cfg(n, k, 32)
+            assert S.int4_tile_rows(n, k) == e["tile_rows"] in S.INT4_TILES
+            waves, split = S.int4_cfg(n, k, e["tile_rows"])
             assert (waves, split) == (e["waves"], e["split"]) and waves in (1, 2, 4, 8) and 1 <= split <= k // 128
+            for rows, plan in e["tiles"].items():
+                assert S.int4_cfg(n, k, int(rows)) == (plan["waves"], plan["split"])
             continue
         assert e["waves"] in (1, 2, 4, 8) and e["split"] >= 1
         for bucket in ("1", "8", "16", "32", "64"):

@@ -57,9 +57,10 @@ def test_tuned_plan_is_one_k_order_and_matches_the_oracle(kind):
 def test_int4_tuned_plan_matches_the_oracle():
     n, k = 512, 1024
     e = T.tune_int4(n, k, DEV, log=lambda m: None)
-    assert e["waves"] in (1, 2, 4, 8) and 1 <= e["split"] <= k // S.GROUP
+    assert e["waves"] in (1, 2, 4, 8) and 1 <= e["split"] <= k // S.GROUP and e["tile_rows"] in S.INT4_TILES
+    assert set(e["tiles"]) == {str(t) for t in S.INT4_TILES}
     w = (torch.randn(n, k, generator=torch.Generator(device=DEV).manual_seed(4), device=DEV) * 0.02).to(torch.bfloat16)
-    packed, scale, zero = S.quantize_int4(w)
+    packed, scale, zero = S.quantize_int4(w, e["tile_rows"])
     w_np = S.dequantize("int4", packed, scale, zero).cpu().numpy()
     for m in (1, 4, 16):
         x = randn_x(m, k, seed=m)
