@@ -167,6 +167,7 @@ def main(argv=None) -> int:
     ap.add_argument("--n", type=int, default=100352, help="skinny: output rows")
     ap.add_argument("--k", type=int, default=2048, help="skinny: input length")
     ap.add_argument("--m", type=int, default=16, help="skinny: activation rows")
+    ap.add_argument("--ring-mib", type=int, default=1024, help="skinny: MiB of distinct weights in the ring")
     ap.add_argument("--tokens", type=int, default=128, help="decode: new tokens")
     ap.add_argument("--draft", action="store_true", help="decode: also the drafting loop (oracle drafter)")
     ap.add_argument("--mib", type=int, default=256)
@@ -193,7 +194,8 @@ def main(argv=None) -> int:
 
         per = a.n * a.k * {"bf16": 2, "int8": 1, "int4": 0.5}[a.kind]
         ring = []
-        for r in range(max(2, int((1 << 30) // per))):  # >= 1 GiB of distinct weights: streamed from HBM every call
+        # distinct weights past the caches (256 MiB of MALL): streamed from HBM every call
+        for r in range(max(2, int((a.ring_mib << 20) // per))):
             w = (torch.randn(a.n, a.k, device=device) * 0.02).to(torch.bfloat16)
             if a.kind == "bf16":
                 ring.append((w,))
