@@ -77,5 +77,35 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+TIMELINE_LIB_PATH = PKG / "libbyteprof_amd_timeline.so"
+TIMELINE_SOURCES = ("mlstm.hip",)  # the units with timeline stamps (compiled with -DBP_TIMELINE)
+
+
+def build_timeline(verbose: bool = False) -> Path:
+    """The timeline library: the units of TIMELINE_SOURCES compiled with -DBP_TIMELINE, linked with the normal
+    objects of the others (build() first). Same C ABI plus the timeline readers; for profiling only."""
+    cc = hipcc()
+    objs = []
+    for src, extra, obj in units():
+        if src.name in TIMELINE_SOURCES:
+            tl_obj = obj.with_name(obj.stem + "_timeline.o")
+            cmd = [cc, *common_flags(), *extra, "-DBP_TIMELINE", "-c", str(src), "-o", str(tl_obj)]
+            if verbose:
+                print(" ".join(cmd))
+            _run(cmd)
+            objs.append(tl_obj)
+        else:
+            if not obj.exists():
+                raise RuntimeError(f"{obj} is missing: run build() first")
+            objs.append(obj)
+    tmp = TIMELINE_LIB_PATH.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *[str(o) for o in objs]])
+    os.replace(tmp, TIMELINE_LIB_PATH)
+    return TIMELINE_LIB_PATH
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--timeline" in sys.argv:
+        print(build_timeline(verbose="-v" in sys.argv))
+    else:
+        print(build(verbose="-v" in sys.argv))

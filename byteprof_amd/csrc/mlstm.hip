@@ -26,6 +26,31 @@
 
 #include <type_traits>
 
+// Timeline builds (-DBP_TIMELINE, `python -m byteprof_amd.build --timeline`, a separate library): thread 0 of
+// every workgroup of the multistep kernel stamps s_memrealtime (100 MHz) at the kernel's stages into
+// bp_mlstm_timeline[workgroup][8], which bp_mlstm_timeline_read() copies out: 0 entry, 1 every load of the first
+// group landed (an explicit wait for all loads, which a normal build leaves to the first use), 2 the gate chain
+// (m_t and the activations) done, 3 the 16 positions' state updates done, 4 the in-wave reductions done, 5 the
+// cross-wave sums combined (after the barrier), 6 the outputs stored (after the barrier), 7 the end. Normal builds
+// compile none of it.
+#ifdef BP_TIMELINE
+__device__ unsigned long long bp_mlstm_timeline[1024][8];
+extern "C" int bp_mlstm_timeline_read(void* dst, size_t bytes) {
+  if (bytes < sizeof(bp_mlstm_timeline)) return BP_E_INVALID_ARG;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(bp_mlstm_timeline), sizeof(bp_mlstm_timeline)) == hipSuccess
+             ? BP_OK
+             : BP_E_INVALID_ARG;
+}
+#define BP_TL(k)                                                 \
+  do {                                                           \
+    if (threadIdx.x == 0) tl_[k] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define BP_TL(k) \
+  do {           \
+  } while (0)
+#endif
+
 namespace bp {
 namespace {
 
@@ -63,6 +88,31 @@ __device__ __forceinline__ float raw_value(uint32_t r) {
   if constexpr (IO == BP_DT_BF16) return bf16_bits_to_float(r);
   else if constexpr (IO == BP_DT_F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
   else return __uint_as_float(r);
+}
+
+// log(sigmoid(f)) = -log(1 + exp(-f)), with HIP's fast exp and log (the hardware's exp2 / log2, ~1 ulp); the
+// activations use __expf too (the lazy commit the same, so a step and a multistep-then-commit agree bit for bit):
+// the gate chain heads every position's dependent work, and the library expf / logf / division were most of it.
+__device__ __forceinline__ float log_sigmoid(float f) { return -__logf(1.f + __expf(-f)); }
+
+// One step of the gate chain's scan: compose each lane's max-plus map (A, B) with the one D lanes below it
+// (row_shr:D; the group's G <= 16 lanes are in the first row, and lanes below D read the identity (-inf, 0)).
+template <int D, int G>
+__device__ __forceinline__ void scan_step(float& A, float& B) {
+  if constexpr (D < G) {
+    const float Ad = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(-__builtin_huge_valf()), __float_as_int(A), 0x110 + D, 0xF, 0xF,
+                                    false));
+    const float Bd = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(B), 0x110 + D, 0xF, 0xF, false));
+    A = fmaxf(A, B + Ad);
+    B = B + Bd;
+  }
+}
+
+// bf16(lo) | bf16(hi) << 16, both rounded to nearest even (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 __device__ __forceinline__ float load_gate(const void* p, int64_t i, int dt) {
@@ -110,6 +160,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
   const int wave = tid / kWave;
   const int nthreads = blockDim.x;
   const int nwaves = nthreads / kWave;
+#ifdef BP_TIMELINE
+  unsigned long long tl_[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+  BP_TL(0);
 
   // This thread's block of the start state, loaded first (the loop keeps a copy of the start n, whose wait then
   // covers only these loads).
@@ -152,6 +206,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
   };
   __builtin_assume(T >= 1);  // the host handles T = 0 without a launch
   issue_group(0);
+#ifdef BP_TIMELINE
+  __builtin_amdgcn_s_waitcnt(0);
+  BP_TL(1);
+#endif
 
   for (int t0 = 0; t0 < T; t0 += G) {
     const int gcount = T - t0 < G ? T - t0 : G;
@@ -166,26 +224,26 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
       // Gate activations: lane g < gcount handles position t0 + g; the max-plus chain of m runs through the lanes.
       const float fv = gate_value(fr, gate_dt);
       const float iv = gate_value(ir, gate_dt);
-      const float fl = logf(1.f / (1.f + expf(-fv)));
-      float m_old_l = 0.f, m_new_l = 0.f;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        if (FULL || g < gcount) {
-          // lane g's values, broadcast through a scalar register (g is a constant of the unrolled loop)
-          const float fg_g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fl), g));
-          const float ig_g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(iv), g));
-          const float mn = fmaxf(fg_g + m_prev, ig_g);
-          if (lane == g) {
-            m_old_l = m_prev;
-            m_new_l = mn;
-          }
-          m_prev = mn;
-        }
-      }
-      const float fa_l = round_io<IO>(expf(fl + m_old_l - m_new_l));
-      const float ia_l = round_io<IO>(expf(iv - m_new_l));
-      mv_l = round_io<IO>(expf(-m_new_l));
+      const float fl = log_sigmoid(fv);
+      // m over the group as an inclusive scan across lanes 0 .. G - 1 of the max-plus maps x -> max(i_t, fl_t + x):
+      // a map is (A, B) = x -> max(A, B + x); (A2, B2) after (A1, B1) is (max(A2, B2 + A1), B2 + B1); lanes past
+      // gcount hold the identity (-inf, 0). log2(G) steps of row shifts instead of G dependent broadcasts.
+      const bool pos = FULL || lane < gcount;
+      float A = pos ? iv : -__builtin_huge_valf();
+      float B = pos ? fl : 0.f;
+      scan_step<1, G>(A, B);
+      scan_step<2, G>(A, B);
+      scan_step<4, G>(A, B);
+      scan_step<8, G>(A, B);
+      const float m_new_l = fmaxf(A, B + m_prev);  // m of position t0 + lane
+      const float m_old_l = __int_as_float(  // m of the position before
+          __builtin_amdgcn_update_dpp(__float_as_int(m_prev), __float_as_int(m_new_l), 0x111, 0xF, 0xF, false));
+      m_prev = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_new_l), gcount - 1));
+      const float fa_l = round_io<IO>(__expf(fl + m_old_l - m_new_l));
+      const float ia_l = round_io<IO>(__expf(iv - m_new_l));
+      mv_l = round_io<IO>(__expf(-m_new_l));
       const float v_l = raw_value<IO>(vr);
+      BP_TL(2);
 
       // Advance the state over the group's positions, keeping the per-thread partial dot products.
 #pragma unroll
@@ -203,29 +261,51 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
 #pragma unroll
           for (int j = 0; j < DPT; ++j) {
             const float kk = raw_value<IO>(kv[g][j]);
-            const float qs = raw_value<IO>(qv[g][j]) * qk_scale;
             const float ik = ia * kk;
+            if constexpr (IO == BP_DT_BF16) {
+              // bf16 io: the rounded state enters the dot products as packed bf16 pairs (one conversion per two
+              // columns) against q unscaled, (q, 0) for the even column and (0, q) for the odd one (v_dot2_f32_bf16:
+              // exact products, the same sums up to the order of rounding); qk_scale is applied to the sums
+              const uint32_t qlo = qv[g][j], qhi = qv[g][j] << 16;
 #pragma unroll
-            for (int b = 0; b < BV; ++b) {
-              C[j][b] = fmaf(ik, vv[b], fa * C[j][b]);
-              hp[g * BV + b] = fmaf(qs, round_io<IO>(C[j][b]), hp[g * BV + b]);
+              for (int b = 0; b < BV; b += 2) {
+                C[j][b] = fmaf(ik, vv[b], fa * C[j][b]);
+                C[j][b + 1] = fmaf(ik, vv[b + 1], fa * C[j][b + 1]);
+                const uint32_t pk = pack_bf16x2(C[j][b], C[j][b + 1]);
+                hp[g * BV + b] = dot2_bf16(pk, qlo, hp[g * BV + b]);
+                hp[g * BV + b + 1] = dot2_bf16(pk, qhi, hp[g * BV + b + 1]);
+              }
+              nn[j] = fmaf(fa, nn[j], ik);
+              qp[g] = dot2_bf16(pack_bf16x2(nn[j], 0.f), qlo, qp[g]);
+            } else {
+              const float qs = raw_value<IO>(qv[g][j]) * qk_scale;
+#pragma unroll
+              for (int b = 0; b < BV; ++b) {
+                C[j][b] = fmaf(ik, vv[b], fa * C[j][b]);
+                hp[g * BV + b] = fmaf(qs, round_io<IO>(C[j][b]), hp[g * BV + b]);
+              }
+              nn[j] = fmaf(fa, nn[j], ik);
+              qp[g] = fmaf(qs, round_io<IO>(nn[j]), qp[g]);
             }
-            nn[j] = fmaf(fa, nn[j], ik);
-            qp[g] = fmaf(qs, round_io<IO>(nn[j]), qp[g]);
           }
         }
+        // one position's broadcasts (scalar registers) at a time: hoisted for all positions they spill
+        __builtin_amdgcn_sched_barrier(0);
       }
     };
     if (gcount == G) advance(std::true_type{});
     else advance(std::false_type{});
+    BP_TL(3);
 
     if (t0 + G < T) issue_group(t0 + G);  // the next group's loads, in flight during the reductions
 
     wave_transpose_reduce<G * BV>(hp, lane);  // lane l: wave total of index l = g * BV + b
     wave_transpose_reduce<G>(qp, lane);       // lane l: wave total of position l / (64 / G)
+    BP_TL(4);
     red_h[wave][lane] = hp[0];
     if ((lane & (kWave / G - 1)) == 0) red_q[wave][lane / (kWave / G)] = qp[0];
     __syncthreads();
+    BP_TL(5);
     if (wave == 0) {
       const int g = lane / BV;
       float hs = red_h[0][lane];
@@ -235,6 +315,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
         qn += red_q[w][g];
       }
       const float mv = __shfl(mv_l, g);
+      if constexpr (IO == BP_DT_BF16) {
+        hs *= qk_scale;
+        qn *= qk_scale;
+      }
       if (g < gcount) {
         const float out = hs / (fmaxf(fabsf(qn), mv) + eps);
         store_io<IO>(h, static_cast<int64_t>(t0 + g) * str_h + static_cast<int64_t>(hd) * DV + v0 + (lane % BV),
@@ -242,6 +326,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
       }
     }
     __syncthreads();
+    BP_TL(6);
   }
   // copies of the start n and m (stored last, so no wait for their loads delays the gate chain)
   if (blockIdx.x == 0 && nstart != nullptr) {
@@ -261,6 +346,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_multistep_kernel(
     }
     if (blockIdx.x == 0 && tid == 0) m_out[hd] = m_prev;
   }
+  BP_TL(7);
+#ifdef BP_TIMELINE
+  const int wg = blockIdx.y * gridDim.x + blockIdx.x;
+  if (threadIdx.x == 0 && wg < 1024)
+    for (int e = 0; e < 8; ++e) bp_mlstm_timeline[wg][e] = tl_[e];
+#endif
 }
 
 // Lazy commit of a verify round: the state after positions 0 .. L (L read from device memory, so a captured graph
@@ -298,10 +389,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlstm_lazy_commit_kernel(
     const int64_t off = static_cast<int64_t>(t) * str_if + hd;
     const float fv = load_gate(fg, off, gate_dt);
     const float iv = load_gate(ig, off, gate_dt);
-    const float fl = logf(1.f / (1.f + expf(-fv)));
+    const float fl = log_sigmoid(fv);
     const float mn = fmaxf(fl + m_prev, iv);
-    const float fa = round_io<IO>(expf(fl + m_prev - mn));
-    const float ia = round_io<IO>(expf(iv - mn));
+    const float fa = round_io<IO>(__expf(fl + m_prev - mn));
+    const float ia = round_io<IO>(__expf(iv - mn));
     m_prev = mn;
     float vv[BV];
 #pragma unroll

@@ -18,6 +18,9 @@
                                                                          skinny_mm over a ring of distinct weights
   python -m byteprof_amd.profiling mlstm [--replays R]                    the fused mLSTM multistep (4 heads,
                                                                          256 x 256, 16 steps), R launches
+  python -m byteprof_amd.profiling mlstm-timeline [--replays R]           the same from the timeline library
+                                                                         (build --timeline): per-stage times of
+                                                                         the workgroups of one launch, R times
   python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
   python -m byteprof_amd.profiling summarize TRACE_DB [--fetch DB --write DB --fetch-copy DB --write-copy DB
                                              --copy-mib 256]               text summary of rocprofv3 databases
@@ -30,6 +33,7 @@ The copy is the calibration reference for the FETCH_SIZE / WRITE_SIZE counters: 
 from __future__ import annotations
 
 import argparse
+import os
 import sys
 
 import torch
@@ -146,9 +150,60 @@ def _set_launches(kind: str) -> dict[tuple[str, str], int]:
     return out
 
 
+MLSTM_STAGES = ("entry -> first group's loads landed", "gate chain (m_t, activations)", "16 positions' updates",
+                "in-wave reductions", "cross-wave combine (LDS, barrier)", "outputs stored (barrier)", "end")
+
+
+def mlstm_timeline(a, device) -> int:
+    """Per-stage times of the fused mLSTM multistep's workgroups from the timeline library's s_memrealtime stamps
+    (thread 0 of each workgroup; 100 MHz, 10 ns resolution): medians over the workgroups of one launch of a graph
+    of 64 launches, the spread of the workgroups' starts and the launch's span, and the graph's time per launch."""
+    import ctypes
+    import statistics
+
+    import numpy as np
+
+    from . import _lib
+    from . import decode_set as D
+    from .optim import draft_fused
+
+    lib = _lib.lib()
+    if not hasattr(lib, "bp_mlstm_timeline_read"):
+        print(f"{os.environ[_lib.LIB_ENV]} has no timeline: build it with python -m byteprof_amd.build --timeline",
+              file=sys.stderr)
+        return 1
+    read = lib.bp_mlstm_timeline_read
+    read.restype, read.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t]
+    g = torch.Generator(device=device).manual_seed(0)
+    t, nh, dq, dv = 16, 4, 256, 256
+    r = lambda *shape: torch.randn(*shape, generator=g, device=device)  # noqa: E731
+    q, k, v = (r(t, nh, d).to(torch.bfloat16) for d in (dq, dq, dv))
+    i, f = r(t, nh, 1), r(t, nh, 1) + 3.0
+    state = (r(1, nh, dq, dv) * 0.1, r(1, nh, dq) * 0.1, r(1, nh, 1))
+    h = torch.empty(t, nh, dv, dtype=torch.bfloat16, device=device)
+    ns, ms = torch.empty(nh, dq, device=device), torch.empty(nh, device=device)
+    gr = D.capture([lambda: draft_fused.multistep_fw(state, q, k, v, i, f, h, ns, ms, eps=1e-6)] * 64)
+    D.time_replays(gr, 3, 1)
+    us = statistics.median(D.time_replays(gr, 10, 5)) * 1000 / 64
+    print(f"mLSTM multistep (NH {nh}, {dq} x {dv}, T {t}, bf16), timeline library: {us:.3f} us per launch in a graph "
+          f"of 64 launches")
+    buf = np.zeros((1024, 8), np.uint64)
+    wgs = nh * dv // draft_fused.BV
+    for rep in range(a.replays):
+        gr.replay()
+        torch.cuda.synchronize()
+        _lib.check(read(buf.ctypes.data, buf.nbytes), "bp_mlstm_timeline_read")
+        ts = (buf[:wgs].astype(np.int64) - int(buf[:wgs, 0].min())) * 10  # ns from the first workgroup's start
+        med = [float(np.median(ts[:, e + 1] - ts[:, e])) for e in range(7)]
+        print(f"launch {rep}: {wgs} workgroups, starts spread over {ts[:, 0].max()} ns, span {ts[:, 7].max()} ns; "
+              "per-workgroup medians (ns): " + "; ".join(f"{n} {m:.0f}" for n, m in zip(MLSTM_STAGES, med)))
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=("set", "set113", "chain", "stages", "decode", "skinny", "mlstm", "copy",
+    ap.add_argument("what", choices=("set", "set113", "chain", "stages", "decode", "skinny", "mlstm",
+                                     "mlstm-timeline", "copy",
                                      "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
@@ -187,6 +242,10 @@ def main(argv=None) -> int:
     from . import _lib
     from . import decode_set as D
 
+    if a.what == "mlstm-timeline" and not os.environ.get(_lib.LIB_ENV):
+        from . import build as B
+
+        os.environ[_lib.LIB_ENV] = str(B.TIMELINE_LIB_PATH)  # before the first load
     _lib.lib()
     if a.what == "skinny":
         from .optim import skinny as S
@@ -214,6 +273,8 @@ def main(argv=None) -> int:
         print(f"skinny_mm {a.kind} {a.n}x{a.k} at M={a.m} (tuned plan): {a.replays} passes "
               f"over {len(ring)} weights", flush=True)
         return 0
+    if a.what == "mlstm-timeline":
+        return mlstm_timeline(a, device)
     if a.what == "mlstm":
         from .optim import draft_fused
 
