@@ -78,26 +78,28 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
 
 
 TIMELINE_LIB_PATH = PKG / "libbyteprof_amd_timeline.so"
-TIMELINE_SOURCES = ("mlstm.hip",)  # the units with timeline stamps (compiled with -DBP_TIMELINE)
+# the units with timeline stamps (compiled with -DBP_TIMELINE)
+TIMELINE_SOURCES = ("mlstm.hip", "skinny_mf.hip", "skinny_mf_n4.hip", "skinny_mf_n8.hip", "skinny_mf_n16.hip")
 
 
 def build_timeline(verbose: bool = False) -> Path:
     """The timeline library: the units of TIMELINE_SOURCES compiled with -DBP_TIMELINE, linked with the normal
     objects of the others (build() first). Same C ABI plus the timeline readers; for profiling only."""
     cc = hipcc()
-    objs = []
+    objs, cmds = [], []
     for src, extra, obj in units():
         if src.name in TIMELINE_SOURCES:
             tl_obj = obj.with_name(obj.stem + "_timeline.o")
-            cmd = [cc, *common_flags(), *extra, "-DBP_TIMELINE", "-c", str(src), "-o", str(tl_obj)]
-            if verbose:
-                print(" ".join(cmd))
-            _run(cmd)
+            cmds.append([cc, *common_flags(), *extra, "-DBP_TIMELINE", "-c", str(src), "-o", str(tl_obj)])
             objs.append(tl_obj)
         else:
             if not obj.exists():
                 raise RuntimeError(f"{obj} is missing: run build() first")
             objs.append(obj)
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+        for cmd, _ in zip(cmds, ex.map(_run, cmds)):
+            if verbose:
+                print(" ".join(cmd))
     tmp = TIMELINE_LIB_PATH.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *[str(o) for o in objs]])
     os.replace(tmp, TIMELINE_LIB_PATH)

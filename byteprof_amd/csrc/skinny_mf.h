@@ -236,10 +236,11 @@ struct MfMain {
 
   // wrow[rb]: the lane's weight row of block rb, advanced to the lane's byte offset in a segment.
   // (VEC = false: wrow[rb] is the row start and kl the lane's K offset in a segment, for bounded element loads.)
-  template <class Hook = MfNoHook>
+  template <class Hook = MfNoHook, class First = MfNoHook>
   __device__ __forceinline__ static void run(const uint8_t* const (&wrow)[RB], const XS& xs, const void* ph,
                                              int64_t K, int64_t kl, int64_t s_first, int64_t stride, int64_t nseg,
-                                             floatx4 (&acc)[RB][MB], const Hook& hook = Hook()) {
+                                             floatx4 (&acc)[RB][MB], const Hook& hook = Hook(),
+                                             const First& first = First()) {
     Slot buf[D];
     auto issue = [&](Slot& sl, int64_t idx) {
       const bool live = idx < nseg;
@@ -267,6 +268,7 @@ struct MfMain {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         if (base + d < nseg) compute_slot(buf[d], xs, s_first + (base + d) * stride, acc);
+        if (d == 0 && base == 0) first();
         issue(buf[d], base + d + D);
       }
     }
@@ -282,9 +284,10 @@ struct MfFixed {
   using Ops = MfMain<KIND, MB, RB, 1, true, XMEM, XS>;
   static constexpr int kD = D < NSEG ? D : NSEG;  // segments in flight
 
-  template <class Hook = MfNoHook>
+  template <class Hook = MfNoHook, class First = MfNoHook>
   __device__ __forceinline__ static void run(const uint8_t* const (&wrow)[RB], const XS& xs, int64_t s_first,
-                                             int64_t stride, floatx4 (&acc)[RB][MB], const Hook& hook = Hook()) {
+                                             int64_t stride, floatx4 (&acc)[RB][MB], const Hook& hook = Hook(),
+                                             const First& first = First()) {
     typename Ops::Slot buf[kD];
 #pragma unroll
     for (int i = 0; i < kD; ++i) Ops::load_slot(buf[i], wrow, xs, s_first + i * stride);
@@ -292,6 +295,7 @@ struct MfFixed {
 #pragma unroll
     for (int i = 0; i < NSEG; ++i) {
       Ops::compute_slot(buf[i % kD], xs, s_first + i * stride, acc);
+      if (i == 0) first();
       if (i + kD < NSEG) Ops::load_slot(buf[i % kD], wrow, xs, s_first + (i + kD) * stride);
     }
   }

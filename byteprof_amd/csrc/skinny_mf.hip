@@ -56,6 +56,17 @@ __global__ void mf_fill_zero_kernel(uint16_t* __restrict__ y, int64_t count) {
     y[i] = 0;
 }
 
+#ifdef BP_TIMELINE
+// Timeline builds: the stamps of the last launch's workgroups (MfPro::tl), read by bp_mf_timeline_read.
+__device__ unsigned long long mf_timeline[kMfTimelineWgs * 8];
+
+unsigned long long* mf_timeline_buffer() {
+  void* p = nullptr;
+  return hipGetSymbolAddress(&p, HIP_SYMBOL(mf_timeline)) == hipSuccess ? static_cast<unsigned long long*>(p)
+                                                                          : nullptr;
+}
+#endif
+
 constexpr int64_t kMaxStageBytes = 32 * 1024;  // LDS for staged activations (dynamic shared memory)
 constexpr int64_t kMaxProLdsBytes = 80 * 1024;  // with a norm prologue's gamma and residual rows as well
 
@@ -140,6 +151,9 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
       lds += gl;
     }
   }
+#ifdef BP_TIMELINE
+  pro.tl = mf_timeline_buffer();
+#endif
   // every wave has the same segment count when the split ranges and the waves divide the segments evenly
   const int nseg_wave = !general && nseg % split == 0 && (nseg / split) % waves == 0
                             ? static_cast<int>(nseg / split / waves)
@@ -186,6 +200,17 @@ void* static_scratch() {
 }  // namespace bp
 
 extern "C" {
+
+#ifdef BP_TIMELINE
+// Timeline builds only: the per-workgroup stamps of the last matrix-core launch, [16384][8] uint64.
+int bp_mf_timeline_read(void* dst, size_t bytes) {
+  if (dst == nullptr || bytes < sizeof(unsigned long long) * bp::kMfTimelineWgs * 8) return BP_E_INVALID_ARG;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(bp::mf_timeline), sizeof(unsigned long long) * bp::kMfTimelineWgs * 8) ==
+                 hipSuccess
+             ? BP_OK
+             : BP_E_INVALID_ARG;
+}
+#endif
 
 size_t bp_skinny_mf_static_bytes(void) { return bp::kStaticScratchBytes; }
 

@@ -23,7 +23,24 @@ struct MfPro {
   uint16_t* xout;            // [M, K] or null: the transformed rows, written by workgroup (0, 0)
   int gl;                    // BP_PRO_NORM: 1 when gamma and the residual rows are staged in LDS (the launch sized it)
   const uint16_t* gamma2;    // BP_PRO_NORM: [K] or null: a second norm (no residual) of the transformed rows
+  unsigned long long* tl;    // timeline builds (-DBP_TIMELINE): per-workgroup stamps [kMfTimelineWgs][8], or null
 };
+
+// Timeline builds: thread 0 of each workgroup (linear index below kMfTimelineWgs) stores s_memrealtime (100 MHz)
+// at 0 entry, 1 the first segments' loads issued (after the activation staging, if any), 2 the first segment's
+// MFMAs issued (its data arrived), 3 the last segment's MFMAs issued, 4 the waves' tiles in LDS (after the barrier),
+// 5 the outputs stored, 6 the end. Normal builds compile none of it.
+constexpr int kMfTimelineWgs = 16384;
+#ifdef BP_TIMELINE
+#define MF_TL(k)                                                        \
+  do {                                                                  \
+    if (threadIdx.x == 0) tl_[k] = __builtin_amdgcn_s_memrealtime();    \
+  } while (0)
+#else
+#define MF_TL(k) \
+  do {           \
+  } while (0)
+#endif
 
 using MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, uint16_t*, float*, int, int64_t, int64_t,
                       int, MfPro);
@@ -168,6 +185,13 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
   __shared__ float pro_sums[PRO ? 8 * MB : 1];  // the prologue's per-row sums of squares
   extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];
 
+#ifdef BP_TIMELINE
+  unsigned long long tl_[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const auto first = [&]() { MF_TL(2); };
+#else
+  const MfNoHook first;
+#endif
+  MF_TL(0);
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform (a scalar value): the segment count below decides whether MFMAs run, and MFMAs ignore EXEC, so the
   // compiler must see those branches as uniform and make them scalar branches
@@ -175,6 +199,38 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
   const MfLane ln(lane);
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 8 * RB;
   const int sp = blockIdx.y;
+  constexpr int kRows = 8 * RB;
+  // The epilogue's operands, ready before the weight stream. Left to the compiler, the output pointers' kernel-
+  // argument loads sink into the epilogue and the int8 scales are loaded there: both then wait behind the
+  // saturated weight stream (~1.3 us per workgroup, the tail of every launch). So y and ws are pinned in scalar
+  // registers here, and an int8 launch at split 1 loads the scales of the rows this thread stores (every pass of
+  // the epilogue loop gives thread t row t % 8RB, or rows 2 (t % 4RB) and + 1 with the SiLU epilogue, as 8RB
+  // divides the thread count) as raw halves, unconditionally (a 16-bit scale read twice).
+  uint16_t* yk = y;
+  float* wsk = ws;
+  asm volatile("" : "+s"(yk), "+s"(wsk));
+  uint32_t sraw[EPI == 0 ? 1 : 2][2];
+  if constexpr (KIND == kInt8) {
+    // unconditional loads (a conditional one would be waited for where the branches meet); without scales to read
+    // (split > 1: the reduce applies them; the partials launch passes none) they read x[0], unused
+    const bool have = split == 1 && scale != nullptr;
+    const int rr0 = EPI == 0 ? static_cast<int>(threadIdx.x % kRows) : 2 * static_cast<int>(threadIdx.x % (kRows / 2));
+    const bool f32 = scale_dt == BP_DT_F32;
+    const auto p = as_global(have ? static_cast<const uint16_t*>(scale) : x);
+#pragma unroll
+    for (int u = 0; u < (EPI == 0 ? 1 : 2); ++u) {
+      const int64_t n = std::min<int64_t>(n0 + rr0 + u, N - 1);
+      const int64_t e = !have ? 0 : f32 ? 2 * n : n;
+      sraw[u][0] = p[e];
+      sraw[u][1] = p[e + (have && f32 ? 1 : 0)];
+    }
+  }
+  // the prefetched scale of the thread's row u
+  const auto row_scale = [&](int u) -> float {
+    if (scale_dt == BP_DT_F32) return __uint_as_float(sraw[u][0] | (sraw[u][1] << 16));
+    if (scale_dt == BP_DT_BF16) return bf16_bits_to_float(sraw[u][0]);
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(sraw[u][0])));
+  };
   const int64_t nseg_all = (K + G::kSeg - 1) / G::kSeg;
   // split 1 (every decode-step launch) needs no division
   const int64_t s_lo = split == 1 ? 0 : sp * nseg_all / split;
@@ -280,20 +336,23 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
         }
         __syncthreads();
       }
+      MF_TL(1);
     };
     if constexpr (NSEG > 0)
-      MfFixed<KIND, MB, RB, D, NSEG, false, MfXLds<KIND, MB>>::run(wrow, xs, s_first, WAVES, acc, commit);
+      MfFixed<KIND, MB, RB, D, NSEG, false, MfXLds<KIND, MB>>::run(wrow, xs, s_first, WAVES, acc, commit, first);
     else
       MfMain<KIND, MB, RB, D, true, false, MfXLds<KIND, MB>>::run(wrow, xs, x, K, kl, s_first, WAVES, nseg, acc,
-                                                                 commit);
+                                                                 commit, first);
   } else if constexpr (VEC) {
     MfXGlobal<KIND, MB, true> xs;
     xs.init(x, M, K, ln);
+    const auto issued = [&]() { MF_TL(1); };
     if constexpr (NSEG > 0)
-      MfFixed<KIND, MB, RB, D, NSEG, true, MfXGlobal<KIND, MB, true>>::run(wrow, xs, s_first, WAVES, acc);
+      MfFixed<KIND, MB, RB, D, NSEG, true, MfXGlobal<KIND, MB, true>>::run(wrow, xs, s_first, WAVES, acc, issued,
+                                                                           first);
     else
       MfMain<KIND, MB, RB, D, true, true, MfXGlobal<KIND, MB, true>>::run(wrow, xs, x, K, kl, s_first, WAVES, nseg,
-                                                                          acc);
+                                                                          acc, issued, first);
   } else {
     // element loads with bounds (K not a multiple of the segment or unaligned operands): same segments, same order
     MfXGlobal<KIND, MB, false> xs;
@@ -301,11 +360,12 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
     MfMain<KIND, MB, RB, 1, false, true, MfXGlobal<KIND, MB, false>>::run(wrow, xs, x, K, kl, s_first, WAVES, nseg,
                                                                           acc);
   }
+  MF_TL(3);
   mf_fold_halves<RB, MB>(acc);
   mf_store_red<WAVES, RB, MB>(red, acc, wave, lane);
   __syncthreads();
+  MF_TL(4);
 
-  constexpr int kRows = 8 * RB;
   if constexpr (EPI == 0) {
     const int cols = M < 8 * MB ? M : 8 * MB;
     for (int e = threadIdx.x; e < kRows * cols; e += WAVES * kWave) {
@@ -315,10 +375,10 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
       if (n >= N) continue;
       float t = mf_total<WAVES, RB, MB>(red, rr, m);
       if (split == 1) {
-        if constexpr (KIND == kInt8) t *= load_scale(scale, n, scale_dt);
-        y[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);
+        if constexpr (KIND == kInt8) t *= row_scale(0);
+        yk[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);
       } else {
-        ws[(static_cast<int64_t>(sp) * M + m) * N + n] = t;
+        wsk[(static_cast<int64_t>(sp) * M + m) * N + n] = t;
       }
     }
   } else {
@@ -331,14 +391,22 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
       float gv = mf_total<WAVES, RB, MB>(red, rr, m);
       float uv = mf_total<WAVES, RB, MB>(red, rr + 1, m);
       if constexpr (KIND == kInt8) {
-        gv *= load_scale(scale, n, scale_dt);
-        uv *= load_scale(scale, n + 1, scale_dt);
+        gv *= row_scale(0);
+        uv *= row_scale(EPI == 0 ? 0 : 1);
       }
       const float gb = round_to_bf16(gv);
       const float a = round_to_bf16(gb / (1.f + expf(-gb)));
-      y[static_cast<int64_t>(m) * (N / 2) + n / 2] = float_to_bf16_bits(a * round_to_bf16(uv));
+      yk[static_cast<int64_t>(m) * (N / 2) + n / 2] = float_to_bf16_bits(a * round_to_bf16(uv));
     }
   }
+  MF_TL(5);
+#ifdef BP_TIMELINE
+  __builtin_amdgcn_s_waitcnt(0);  // the stores done
+  MF_TL(6);
+  const int64_t wg = static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+  if (threadIdx.x == 0 && pro.tl != nullptr && wg < kMfTimelineWgs)
+    for (int e = 0; e < 8; ++e) pro.tl[wg * 8 + e] = tl_[e];
+#endif
 }
 
 

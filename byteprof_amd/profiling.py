@@ -21,6 +21,10 @@
   python -m byteprof_amd.profiling mlstm-timeline [--replays R]           the same from the timeline library
                                                                          (build --timeline): per-stage times of
                                                                          the workgroups of one launch, R times
+  python -m byteprof_amd.profiling skinny-timeline [--kind bf16|int8] [--n N] [--k K] [--m M] [--replays R]
+                                                                         skinny_mm (tuned plan) from the timeline
+                                                                         library: per-stage times of the matrix-core
+                                                                         kernel's workgroups, R launches
   python -m byteprof_amd.profiling copy [--mib 256] [--reps 5]             a device-to-device copy of known size
   python -m byteprof_amd.profiling summarize TRACE_DB [--fetch DB --write DB --fetch-copy DB --write-copy DB
                                              --copy-mib 256]               text summary of rocprofv3 databases
@@ -200,10 +204,65 @@ def mlstm_timeline(a, device) -> int:
     return 0
 
 
+MF_STAGES = ("entry -> first loads issued", "-> first segment's MFMAs", "-> last segment's MFMAs",
+             "-> tiles in LDS (barrier)", "-> outputs issued", "-> stores done")
+
+
+def skinny_timeline(a, device) -> int:
+    """Per-stage times of the matrix-core skinny kernel's workgroups (the timeline library's s_memrealtime stamps,
+    thread 0 of each workgroup, 100 MHz): skinny_mm with the tuned plan over a ring of distinct weights (streamed
+    from HBM) in one HIP graph, replayed R times; after each replay, the last launch's workgroups: the spread of
+    their starts, the launch's span and the per-workgroup medians of each stage."""
+    import ctypes
+
+    import numpy as np
+
+    from . import _lib
+    from .optim import skinny as S
+    from .quant.hip_int8 import quantize_rowwise_int8
+
+    lib = _lib.lib()
+    if not hasattr(lib, "bp_mf_timeline_read"):
+        print(f"{os.environ.get(_lib.LIB_ENV)} has no timeline: build it with python -m byteprof_amd.build "
+              "--timeline", file=sys.stderr)
+        return 1
+    read = lib.bp_mf_timeline_read
+    read.restype, read.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t]
+    per = a.n * a.k * (2 if a.kind == "bf16" else 1)
+    ring = []
+    for _ in range(max(2, int((a.ring_mib << 20) // per))):
+        w = (torch.randn(a.n, a.k, device=device) * 0.02).to(torch.bfloat16)
+        ring.append((w,) if a.kind == "bf16" else quantize_rowwise_int8(w, torch.float16))
+        del w
+    x = torch.randn(a.m, a.k, device=device).to(torch.bfloat16)
+    y = torch.empty(a.m, a.n, dtype=torch.bfloat16, device=device)
+    rb, waves, split, xs = S._resolve(a.kind, a.n, a.k, a.m, None)
+    wgs = -(-a.n // (8 * rb)) * split
+    from . import decode_set as D
+
+    g = D.capture([lambda args=args: S.skinny_mm(x, *args, out=y) for args in ring])
+    D.time_replays(g, 2, 1)
+    us = float(np.median(D.time_replays(g, 5, 3))) * 1000 / len(ring)
+    print(f"skinny_mm {a.kind} {a.n}x{a.k} at M={a.m}: plan rb {rb} waves {waves} split {split} xstage {xs}, "
+          f"{wgs} workgroups; a graph of the ring of {len(ring)} weights: {us:.2f} us per launch (timeline build)")
+    buf = np.zeros((16384, 8), np.uint64)
+    n = min(wgs, buf.shape[0])
+    for r in range(a.replays):
+        g.replay()  # the stamps are the ring's last launch's, right after the launch before it
+        torch.cuda.synchronize()
+        _lib.check(read(buf.ctypes.data, buf.nbytes), "bp_mf_timeline_read")
+        ts = (buf[:n].astype(np.int64) - int(buf[:n, 0].min())) * 10  # ns from the first workgroup's entry
+        med = [float(np.median(ts[:, e + 1] - ts[:, e])) for e in range(6)]
+        print(f"launch {r}: starts spread over {ts[:, 0].max()} ns, span {ts[:, 6].max()} ns, workgroup median "
+              f"{np.median(ts[:, 6] - ts[:, 0]):.0f} ns; stage medians (ns): "
+              + "; ".join(f"{s} {m:.0f}" for s, m in zip(MF_STAGES, med)))
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("what", choices=("set", "set113", "chain", "stages", "decode", "skinny", "mlstm",
-                                     "mlstm-timeline", "copy",
+                                     "mlstm-timeline", "skinny-timeline", "copy",
                                      "summarize"))
     ap.add_argument("db", nargs="?", help="summarize: kernel-trace database")
     ap.add_argument("--fetch", help="summarize: FETCH_SIZE database of the workload")
@@ -242,7 +301,7 @@ def main(argv=None) -> int:
     from . import _lib
     from . import decode_set as D
 
-    if a.what == "mlstm-timeline" and not os.environ.get(_lib.LIB_ENV):
+    if a.what in ("mlstm-timeline", "skinny-timeline") and not os.environ.get(_lib.LIB_ENV):
         from . import build as B
 
         os.environ[_lib.LIB_ENV] = str(B.TIMELINE_LIB_PATH)  # before the first load
@@ -275,6 +334,8 @@ def main(argv=None) -> int:
         return 0
     if a.what == "mlstm-timeline":
         return mlstm_timeline(a, device)
+    if a.what == "skinny-timeline":
+        return skinny_timeline(a, device)
     if a.what == "mlstm":
         from .optim import draft_fused
 
