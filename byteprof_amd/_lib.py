@@ -36,6 +36,7 @@ SIGNATURES: dict[str, tuple] = {
     "bp_skinny_mf_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "bp_skinny_mf_k_segment": (_c_int, [_c_int]),
     "bp_skinny_mf_stage_bytes": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
+    "bp_skinny_mf_stage_bytes_rows": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int, _c_int]),
     "bp_skinny_mf": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
                               _c_int, _c_vp, _c_size, _c_vp]),
     "bp_skinny_mf_partials": (_c_int, [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,

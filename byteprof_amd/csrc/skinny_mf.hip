@@ -18,22 +18,29 @@ int splitk_reduce_launch(const float* ws, uint16_t* y, const void* scale, int sc
                          int split, hipStream_t st);
 
 // Launches whose waves have 4, 8 or 16 segments each are instantiated in skinny_mf_n4 / n8 / n16.hip.
-extern template MfFn mf_pick_n<4>(int, int, int, int, bool, int, bool, bool);
-extern template MfFn mf_pick_n<8>(int, int, int, int, bool, int, bool, bool);
-extern template MfFn mf_pick_n<16>(int, int, int, int, bool, int, bool, bool);
-template MfFn mf_pick_n<0>(int, int, int, int, bool, int, bool, bool);
+extern template MfFn mf_pick_n<4>(int, int, int, int, bool, int, bool, bool, int);
+extern template MfFn mf_pick_n<8>(int, int, int, int, bool, int, bool, bool, int);
+extern template MfFn mf_pick_n<16>(int, int, int, int, bool, int, bool, bool, int);
+template MfFn mf_pick_n<0>(int, int, int, int, bool, int, bool, bool, int);
 
 namespace {
 
 // The kernel of a launch: the straight-line variant when every wave has exactly 4, 8 or 16 segments (nseg_wave),
 // else the general one.
-MfFn mf_pick(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro = false, int nseg_wave = 0) {
+MfFn mf_pick(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro = false, int nseg_wave = 0,
+             int wr = 1) {
   switch (vec ? nseg_wave : 0) {
-    case 4: return mf_pick_n<4>(wkind, mb, rb, waves, vec, epi, xl, pro);
-    case 8: return mf_pick_n<8>(wkind, mb, rb, waves, vec, epi, xl, pro);
-    case 16: return mf_pick_n<16>(wkind, mb, rb, waves, vec, epi, xl, pro);
-    default: return mf_pick_n<0>(wkind, mb, rb, waves, vec, epi, xl, pro);
+    case 4: return mf_pick_n<4>(wkind, mb, rb, waves, vec, epi, xl, pro, wr);
+    case 8: return mf_pick_n<8>(wkind, mb, rb, waves, vec, epi, xl, pro, wr);
+    case 16: return mf_pick_n<16>(wkind, mb, rb, waves, vec, epi, xl, pro, wr);
+    default: return mf_pick_n<0>(wkind, mb, rb, waves, vec, epi, xl, pro, wr);
   }
+}
+
+// Row groups of a launch's xstage flags (BP_XS_ROWS2 / BP_XS_ROWS4, with BP_XS_STAGE), 1 without.
+int mf_row_groups(int xstage) {
+  if (!(xstage & BP_XS_STAGE)) return 1;
+  return (xstage & BP_XS_ROWS4) ? 4 : (xstage & BP_XS_ROWS2) ? 2 : 1;
 }
 
 int mf_blocks(int64_t M) { return M <= 8 ? 1 : M <= 16 ? 2 : M <= 32 ? 4 : 8; }
@@ -68,16 +75,18 @@ unsigned long long* mf_timeline_buffer() {
 #endif
 
 constexpr int64_t kMaxStageBytes = 32 * 1024;  // LDS for staged activations (dynamic shared memory)
+constexpr int64_t kMaxStageBytesRows = 64 * 1024;  // with row groups (one copy serves 2-4x the rows)
 constexpr int64_t kMaxProLdsBytes = 80 * 1024;  // with a norm prologue's gamma and residual rows as well
 
-// LDS bytes of the staged activations of a launch (the largest K range of a workgroup), or -1 when they do not fit.
-int64_t mf_stage_bytes(int wkind, int64_t M, int64_t K, int split) {
+// LDS bytes of the staged activations of a launch (the largest K range of a workgroup), or -1 when they do not fit
+// (limit: kMaxStageBytes, with row groups kMaxStageBytesRows).
+int64_t mf_stage_bytes(int wkind, int64_t M, int64_t K, int split, int wr = 1) {
   const int64_t seg = wkind == kBf16 ? 64 : 128;
   const int64_t nseg = (K + seg - 1) / seg;
   const int64_t per = (nseg + split - 1) / split;
   const int64_t rows = M < 8 * mf_blocks(M) ? M : 8 * mf_blocks(M);
   const int64_t bytes = rows * per * seg * 2;
-  return bytes <= kMaxStageBytes ? bytes : -1;
+  return bytes <= (wr > 1 ? kMaxStageBytesRows : kMaxStageBytes) ? bytes : -1;
 }
 
 // mode 0: y (split > 1: partials then the reduce); 1: partials only (split >= 2, y unused); 2: SiLU epilogue.
@@ -103,6 +112,7 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   }
   // xstage bit 1: the general segment loop even where the straight-line kernel of the count applies
   const bool general = (xstage & BP_XS_GENERAL) != 0;
+  int wr = mf_row_groups(xstage);
   xstage &= BP_XS_STAGE;
   const int64_t seg = wkind == kBf16 ? 64 : 128;
   // the vector loads read whole segments: K a multiple of the segment, 16-byte aligned operands
@@ -112,6 +122,7 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
     rb = 1;
     waves = 4;
     xstage = 0;
+    wr = 1;
   }
   const int64_t nseg = (K + seg - 1) / seg;
   if (split > nseg) split = static_cast<int>(nseg);
@@ -133,13 +144,14 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
       return BP_E_INVALID_ARG;
     if (!vec || split != 1 || M > 16 || mode == 1) return BP_E_UNSUPPORTED;
     xstage = 1;
+    wr = 1;
     pro = MfPro{prologue->kind, prologue->eps, static_cast<const uint16_t*>(prologue->gamma),
                 static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout), 0,
                 static_cast<const uint16_t*>(prologue->gamma2)};
   }
   int64_t lds = 0;
   if (xstage) {
-    lds = mf_stage_bytes(wkind, M, K, split);
+    lds = mf_stage_bytes(wkind, M, K, split, wr);
     if (lds < 0) return BP_E_UNSUPPORTED;
   }
   if (pro.kind == BP_PRO_NORM) {
@@ -155,16 +167,31 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   pro.tl = mf_timeline_buffer();
 #endif
   // every wave has the same segment count when the split ranges and the waves divide the segments evenly
-  const int nseg_wave = !general && nseg % split == 0 && (nseg / split) % waves == 0
-                            ? static_cast<int>(nseg / split / waves)
-                            : 0;
-  MfFn fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0, pro.kind != 0, nseg_wave);
+  int nseg_wave = !general && nseg % split == 0 && (nseg / split) % waves == 0
+                      ? static_cast<int>(nseg / split / waves)
+                      : 0;
+  if (wr > 1 && nseg_wave == 16) nseg_wave = 0;  // the row-group kernels run the general loop there
+  MfFn fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0, pro.kind != 0, nseg_wave,
+                    wr);
+  if (fn == nullptr && wr > 1) {
+    // row groups are a plan, not a K order: without a compiled row-group kernel (rows outside 9..16, rb or waves
+    // outside its menu), the same sums from one row group, staged where the rows fit in the plain limit
+    wr = 1;
+    if (xstage && pro.kind == 0) {
+      lds = mf_stage_bytes(wkind, M, K, split, 1);
+      if (lds < 0) {
+        xstage = 0;
+        lds = 0;
+      }
+    }
+    fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0, pro.kind != 0, nseg_wave);
+  }
   if (fn == nullptr) return BP_E_UNSUPPORTED;
   if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
     return BP_E_WORKSPACE;
-  const int64_t tiles = (N + 8 * rb - 1) / (8 * rb);
+  const int64_t tiles = (N + 8 * rb * wr - 1) / (8 * rb * wr);
   if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
-  fn<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(split)), waves * kWave, static_cast<size_t>(lds),
+  fn<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(split)), waves * wr * kWave, static_cast<size_t>(lds),
        st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), scale, scale_dt,
              static_cast<uint16_t*>(y), static_cast<float*>(ws), static_cast<int>(M), N, K, split, pro);
   const int rc = mf_status();
@@ -232,7 +259,12 @@ int bp_skinny_mf_static(int wkind, const void* x, const void* w, const void* sca
 
 int bp_skinny_mf_supported(int wkind, int M, int rb, int waves, int xstage) {
   if (M < 1 || M > 64) return 0;
-  return bp::mf_pick(wkind, bp::mf_blocks(M), rb, waves, true, 0, (xstage & BP_XS_STAGE) != 0) != nullptr ? 1 : 0;
+  const int wr = bp::mf_row_groups(xstage);
+  // the row-group kernels exist for the straight-line counts 4 and 8 and the general loop; report the general one
+  return bp::mf_pick(wkind, bp::mf_blocks(M), rb, waves, true, 0, (xstage & BP_XS_STAGE) != 0, false, 0, wr) !=
+                 nullptr
+             ? 1
+             : 0;
 }
 
 int bp_skinny_mf_k_segment(int wkind) { return wkind == bp::kBf16 ? 64 : wkind == bp::kInt8 ? 128 : 0; }
@@ -240,6 +272,11 @@ int bp_skinny_mf_k_segment(int wkind) { return wkind == bp::kBf16 ? 64 : wkind =
 int64_t bp_skinny_mf_stage_bytes(int wkind, int64_t M, int64_t K, int split) {
   if ((wkind != bp::kBf16 && wkind != bp::kInt8) || M < 1 || M > 64 || K < 1 || split < 1) return -1;
   return bp::mf_stage_bytes(wkind, M, K, split);
+}
+
+int64_t bp_skinny_mf_stage_bytes_rows(int wkind, int64_t M, int64_t K, int split, int xstage) {
+  if ((wkind != bp::kBf16 && wkind != bp::kInt8) || M < 1 || M > 64 || K < 1 || split < 1) return -1;
+  return bp::mf_stage_bytes(wkind, M, K, split, bp::mf_row_groups(xstage | BP_XS_STAGE));
 }
 
 int bp_skinny_mf(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y, int64_t M,

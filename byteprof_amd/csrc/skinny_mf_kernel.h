@@ -45,9 +45,10 @@ constexpr int kMfTimelineWgs = 16384;
 using MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, uint16_t*, float*, int, int64_t, int64_t,
                       int, MfPro);
 
-// The kernel of a launch whose waves have NSEG segments each (0: any count), or null when none is compiled.
+// The kernel of a launch whose waves have NSEG segments each (0: any count), or null when none is compiled; wr:
+// row groups over the staged activations (1, or 2 / 4 with xl).
 template <int NSEG>
-MfFn mf_pick_n(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro);
+MfFn mf_pick_n(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro, int wr);
 
 #ifdef BP_MF_INSTANTIATE
 namespace {
@@ -171,17 +172,22 @@ __device__ void mf_prologue(uint16_t* xs, int rows, int K, MfPro pro, bool write
 // BP_PRO_NORM, gamma and the residual rows are loaded into LDS ahead of the weights too where the launch sized the
 // LDS for them (pro.gl: 2 K (1 + rows) more bytes, always at one row, else within 80 KiB in all). NSEG > 0 (VEC only): every wave of the launch has exactly NSEG segments (the
 // host checks K / (segment x split x waves) == NSEG), run as straight-line code (MfFixed); 0: any count (MfMain).
-template <int KIND, int MB, int RB, int WAVES, bool VEC, int EPI, bool XL, bool PRO, int NSEG>
-__global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t* __restrict__ x,
+// WR > 1 (XL only, no prologue): WR row groups of 8 RB rows, each with its own WAVES waves splitting K as above, over
+// the one LDS copy of the activation rows: the workgroup reads its activation operands once for 8 RB WR rows (the
+// bytes per weight row fall by WR), every row's sum in the same order as with WR = 1.
+template <int KIND, int MB, int RB, int WAVES, bool VEC, int EPI, bool XL, bool PRO, int NSEG, int WR = 1>
+__global__ __launch_bounds__(WAVES * WR * kWave) void skinny_mf_kernel(const uint16_t* __restrict__ x,
                                                                   const uint8_t* __restrict__ w,
                                                                   const void* __restrict__ scale, int scale_dt,
                                                                   uint16_t* __restrict__ y, float* __restrict__ ws,
                                                                   int M, int64_t N, int64_t K, int split, MfPro pro) {
   using G = MfGeom<KIND>;
   static_assert(NSEG == 0 || VEC, "the fixed segment count needs vector loads");
+  static_assert(WR == 1 || (XL && !PRO), "row groups share the staged activations (no prologue)");
+  constexpr int NT = WAVES * WR * kWave;
   constexpr int D = VEC ? mf_depth<KIND, MB, RB, !XL>() : 1;
   constexpr int kInFlight = NSEG > 0 && NSEG < D ? NSEG : D;  // weight segments issued before the staging commit
-  __shared__ MfRed<WAVES, RB, MB> red;
+  __shared__ MfRed<WAVES, RB, MB> red[WR];
   __shared__ float pro_sums[PRO ? 8 * MB : 1];  // the prologue's per-row sums of squares
   extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];
 
@@ -196,16 +202,20 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
   // wave-uniform (a scalar value): the segment count below decides whether MFMAs run, and MFMAs ignore EXEC, so the
   // compiler must see those branches as uniform and make them scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wk = WR == 1 ? wave : wave % WAVES;  // the wave's K share
+  const int wr = WR == 1 ? 0 : wave / WAVES;     // its row group
   const MfLane ln(lane);
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 8 * RB;
+  constexpr int kRows = 8 * RB;       // a row group's rows
+  constexpr int kRowsW = kRows * WR;  // the workgroup's rows
+  const int64_t nw0 = static_cast<int64_t>(blockIdx.x) * kRowsW;
+  const int64_t n0 = nw0 + wr * kRows;
   const int sp = blockIdx.y;
-  constexpr int kRows = 8 * RB;
   // The epilogue's operands, ready before the weight stream. Left to the compiler, the output pointers' kernel-
   // argument loads sink into the epilogue and the int8 scales are loaded there: both then wait behind the
   // saturated weight stream (~1.3 us per workgroup, the tail of every launch). So y and ws are pinned in scalar
   // registers here, and an int8 launch at split 1 loads the scales of the rows this thread stores (every pass of
-  // the epilogue loop gives thread t row t % 8RB, or rows 2 (t % 4RB) and + 1 with the SiLU epilogue, as 8RB
-  // divides the thread count) as raw halves, unconditionally (a 16-bit scale read twice).
+  // the epilogue loop gives thread t the workgroup's row t % 8RB WR, or rows 2 (t % 4RB WR) and + 1 with the SiLU
+  // epilogue, as 8 RB WR divides the thread count) as raw halves, unconditionally (a 16-bit scale read twice).
   uint16_t* yk = y;
   float* wsk = ws;
   asm volatile("" : "+s"(yk), "+s"(wsk));
@@ -214,12 +224,13 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
     // unconditional loads (a conditional one would be waited for where the branches meet); without scales to read
     // (split > 1: the reduce applies them; the partials launch passes none) they read x[0], unused
     const bool have = split == 1 && scale != nullptr;
-    const int rr0 = EPI == 0 ? static_cast<int>(threadIdx.x % kRows) : 2 * static_cast<int>(threadIdx.x % (kRows / 2));
+    const int rr0 =
+        EPI == 0 ? static_cast<int>(threadIdx.x % kRowsW) : 2 * static_cast<int>(threadIdx.x % (kRowsW / 2));
     const bool f32 = scale_dt == BP_DT_F32;
     const auto p = as_global(have ? static_cast<const uint16_t*>(scale) : x);
 #pragma unroll
     for (int u = 0; u < (EPI == 0 ? 1 : 2); ++u) {
-      const int64_t n = std::min<int64_t>(n0 + rr0 + u, N - 1);
+      const int64_t n = std::min<int64_t>(nw0 + rr0 + u, N - 1);
       const int64_t e = !have ? 0 : f32 ? 2 * n : n;
       sraw[u][0] = p[e];
       sraw[u][1] = p[e + (have && f32 ? 1 : 0)];
@@ -235,7 +246,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
   // split 1 (every decode-step launch) needs no division
   const int64_t s_lo = split == 1 ? 0 : sp * nseg_all / split;
   const int64_t s_hi = split == 1 ? nseg_all : (sp + 1) * nseg_all / split;
-  const int64_t s_first = s_lo + wave;
+  const int64_t s_first = s_lo + wk;
   const int64_t nseg = NSEG > 0 ? NSEG : mf_uniform(s_first < s_hi ? (s_hi - s_first + WAVES - 1) / WAVES : 0);
 
   // the lane's weight rows (rows past N read row N - 1; their outputs are never stored), advanced to the lane's
@@ -254,7 +265,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
     for (int b = 0; b < MB; ++b) acc[rb][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   if constexpr (XL) {
-    constexpr int kNT = WAVES * kWave;
+    constexpr int kNT = NT;
     constexpr int kPer = 4;
     const int mrows = M < 8 * MB ? M : 8 * MB;
     const int kn = static_cast<int>((s_hi - s_lo) * G::kSeg);
@@ -362,18 +373,18 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
   }
   MF_TL(3);
   mf_fold_halves<RB, MB>(acc);
-  mf_store_red<WAVES, RB, MB>(red, acc, wave, lane);
+  mf_store_red<WAVES, RB, MB>(red[wr], acc, wk, lane);
   __syncthreads();
   MF_TL(4);
 
   if constexpr (EPI == 0) {
     const int cols = M < 8 * MB ? M : 8 * MB;
-    for (int e = threadIdx.x; e < kRows * cols; e += WAVES * kWave) {
-      const int m = e / kRows;
-      const int rr = e % kRows;
-      const int64_t n = n0 + rr;
+    for (int e = threadIdx.x; e < kRowsW * cols; e += NT) {
+      const int m = e / kRowsW;
+      const int rw = e % kRowsW;  // the workgroup's row: row group rw / 8RB, row rw % 8RB of it
+      const int64_t n = nw0 + rw;
       if (n >= N) continue;
-      float t = mf_total<WAVES, RB, MB>(red, rr, m);
+      float t = mf_total<WAVES, RB, MB>(red[rw / kRows], rw % kRows, m);
       if (split == 1) {
         if constexpr (KIND == kInt8) t *= row_scale(0);
         yk[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);
@@ -383,13 +394,13 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_mf_kernel(const uint16_t
     }
   } else {
     const int cols = M < 8 * MB ? M : 8 * MB;
-    for (int e = threadIdx.x; e < (kRows / 2) * cols; e += WAVES * kWave) {
-      const int m = e / (kRows / 2);
-      const int rr = 2 * (e % (kRows / 2));
-      const int64_t n = n0 + rr;  // the gate row; n + 1 the up row
+    for (int e = threadIdx.x; e < (kRowsW / 2) * cols; e += NT) {
+      const int m = e / (kRowsW / 2);
+      const int rw = 2 * (e % (kRowsW / 2));
+      const int64_t n = nw0 + rw;  // the gate row; n + 1 the up row
       if (n + 1 >= N) continue;
-      float gv = mf_total<WAVES, RB, MB>(red, rr, m);
-      float uv = mf_total<WAVES, RB, MB>(red, rr + 1, m);
+      float gv = mf_total<WAVES, RB, MB>(red[rw / kRows], rw % kRows, m);
+      float uv = mf_total<WAVES, RB, MB>(red[rw / kRows], rw % kRows + 1, m);
       if constexpr (KIND == kInt8) {
         gv *= row_scale(0);
         uv *= row_scale(EPI == 0 ? 0 : 1);
@@ -474,9 +485,41 @@ MfFn pick_pro(int mb, int rb, int waves) {
   }
 }
 
+// Row groups (WR 2 / 4): the staged-activation kernels at 9..16 rows (MB 2), both epilogues, waves x WR <= 16.
+template <int NSEG, int KIND, int RB, int EPI, int WR>
+MfFn pick_wr_waves(int waves) {
+  switch (waves) {
+    case 2: return &skinny_mf_kernel<KIND, 2, RB, 2, true, EPI, true, false, NSEG, WR>;
+    case 4: return &skinny_mf_kernel<KIND, 2, RB, 4, true, EPI, true, false, NSEG, WR>;
+    case 8:
+      if constexpr (WR == 2) return &skinny_mf_kernel<KIND, 2, RB, 8, true, EPI, true, false, NSEG, WR>;
+      return nullptr;
+    default: return nullptr;
+  }
+}
+
+template <int NSEG, int KIND, int EPI, int WR>
+MfFn pick_wr_rb(int rb, int waves) {
+  switch (rb) {
+    case 1: return pick_wr_waves<NSEG, KIND, 1, EPI, WR>(waves);
+    case 2: return pick_wr_waves<NSEG, KIND, 2, EPI, WR>(waves);
+    case 4: return pick_wr_waves<NSEG, KIND, 4, EPI, WR>(waves);
+    default: return nullptr;
+  }
+}
+
 template <int NSEG, int KIND>
-MfFn mf_pick_kind(int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro) {
+MfFn mf_pick_kind(int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro, int wr) {
   if (NSEG > 0 && !vec) return nullptr;
+  if (wr != 1) {
+    if constexpr (NSEG == 16) {
+      return nullptr;  // K ranges of 16 segments a wave do not stage at 16 rows
+    } else {
+      if (!vec || !xl || pro || mb != 2 || (wr != 2 && wr != 4)) return nullptr;
+      if (epi == 0) return wr == 2 ? pick_wr_rb<NSEG, KIND, 0, 2>(rb, waves) : pick_wr_rb<NSEG, KIND, 0, 4>(rb, waves);
+      return wr == 2 ? pick_wr_rb<NSEG, KIND, 1, 2>(rb, waves) : pick_wr_rb<NSEG, KIND, 1, 4>(rb, waves);
+    }
+  }
   if (pro)
     return vec && xl ? (epi == 0 ? pick_pro<NSEG, KIND, 0>(mb, rb, waves) : pick_pro<NSEG, KIND, 1>(mb, rb, waves))
                      : nullptr;
@@ -488,9 +531,9 @@ MfFn mf_pick_kind(int mb, int rb, int waves, bool vec, int epi, bool xl, bool pr
 }  // namespace
 
 template <int NSEG>
-MfFn mf_pick_n(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro) {
-  if (wkind == kBf16) return mf_pick_kind<NSEG, kBf16>(mb, rb, waves, vec, epi, xl, pro);
-  if (wkind == kInt8) return mf_pick_kind<NSEG, kInt8>(mb, rb, waves, vec, epi, xl, pro);
+MfFn mf_pick_n(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro, int wr) {
+  if (wkind == kBf16) return mf_pick_kind<NSEG, kBf16>(mb, rb, waves, vec, epi, xl, pro, wr);
+  if (wkind == kInt8) return mf_pick_kind<NSEG, kInt8>(mb, rb, waves, vec, epi, xl, pro, wr);
   return nullptr;
 }
 

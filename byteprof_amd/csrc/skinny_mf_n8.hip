@@ -3,5 +3,5 @@
 #include "skinny_mf_kernel.h"
 
 namespace bp {
-template MfFn mf_pick_n<8>(int, int, int, int, bool, int, bool, bool);
+template MfFn mf_pick_n<8>(int, int, int, int, bool, int, bool, bool, int);
 }  // namespace bp

@@ -35,6 +35,8 @@ ROWS_PER_LAUNCH = MAX_M
 
 _KIND_CODE = {"bf16": 0, "int8": 1}
 XS_STAGE, XS_GENERAL = 1, 2  # BP_XS_STAGE, BP_XS_GENERAL: activations staged in LDS; the general segment loop
+XS_ROWS2, XS_ROWS4 = 4, 8     # BP_XS_ROWS2 / 4: with XS_STAGE at 9..16 rows, 2 / 4 row groups over one staged copy
+XS_ROWS = XS_ROWS2 | XS_ROWS4
 _RB_MENU = (1, 2, 4)        # 8-row weight blocks per workgroup
 _WAVES_MENU = (1, 2, 4, 8)
 _BUCKETS = (1, 8, 16, 32, 64)  # row buckets of the tuned plans (8-row activation blocks per launch: 1, 1, 2, 4, 8)
@@ -132,11 +134,13 @@ def _resolve(kind: str, n: int, k: int, m: int, cfg, pro: bool = False) -> tuple
     rb = max(r for r in _RB_MENU if r <= max(rows // 8, 1))
     waves = max(w for w in _WAVES_MENU if w <= max(waves, 1))
     split = max(1, min(int(split), -(-k // k_segment(kind))))
-    if xs & XS_STAGE and (m > 16 or _stage_bytes(kind, m, k, split) < 0):
-        xs &= ~XS_STAGE
-    while rb > 1 and not _supported(kind, m, rb, waves, xs & XS_STAGE):
+    if xs & XS_STAGE and (m > 16 or _stage_bytes(kind, m, k, split, xs) < 0):
+        xs &= ~(XS_STAGE | XS_ROWS)
+    if not xs & XS_STAGE or not 8 < m <= 16 or not _supported(kind, m, rb, waves, xs & (XS_STAGE | XS_ROWS)):
+        xs &= ~XS_ROWS  # row groups: staged 9..16-row launches of a compiled (rb, waves)
+    while rb > 1 and not _supported(kind, m, rb, waves, xs & (XS_STAGE | XS_ROWS)):
         rb //= 2
-    if not _supported(kind, m, rb, waves, xs & XS_STAGE):
+    if not _supported(kind, m, rb, waves, xs & (XS_STAGE | XS_ROWS)):
         raise ValueError(f"no compiled kernel for {kind} at {m} rows, {8 * rb} weight rows, {waves} waves")
     return rb, waves, split, xs
 
@@ -160,8 +164,12 @@ def kernel_name(kind: str, n: int, k: int, m: int, cfg=None) -> str:
     segments per wave)."""
     rb, waves, split, xs = _resolve(kind, n, k, m, cfg)
     mb = 1 if m <= 8 else 2 if m <= 16 else 4 if m <= 32 else 8
+    wr = 4 if xs & XS_ROWS4 else 2 if xs & XS_ROWS2 else 1
+    nseg = segments_per_wave(kind, k, waves, split, xs)
+    if wr > 1 and nseg == 16:
+        nseg = 0  # the row-group kernels run the general loop there
     return (f"skinny_mf_kernel<{_KIND_CODE[kind]}, {mb}, {rb}, {waves}, true, 0, "
-            f"{'true' if xs & XS_STAGE else 'false'}, false, {segments_per_wave(kind, k, waves, split, xs)}>")
+            f"{'true' if xs & XS_STAGE else 'false'}, false, {nseg}" + (f", {wr}>" if wr > 1 else ">"))
 
 
 @functools.lru_cache(maxsize=None)
@@ -170,7 +178,9 @@ def _supported(kind: str, m: int, rb: int, waves: int, xs: int = 0) -> bool:
 
 
 @functools.lru_cache(maxsize=None)
-def _stage_bytes(kind: str, m: int, k: int, split: int) -> int:
+def _stage_bytes(kind: str, m: int, k: int, split: int, xs: int = 0) -> int:
+    if xs & XS_ROWS:
+        return int(_lib.lib().bp_skinny_mf_stage_bytes_rows(_KIND_CODE[kind], m, k, split, xs))
     return int(_lib.lib().bp_skinny_mf_stage_bytes(_KIND_CODE[kind], m, k, split))
 
 

@@ -13,11 +13,13 @@ loop), and at one row with a norm prologue (split 1). It keeps the fastest one-r
 split > 1 must win by more than 3%; when that order has no split, the split-1 order within 5% of it whose plain and
 prologue launches are fastest together (the decode step runs the prologue form); then, among the orders within 2%
 of that, the fastest at 16 rows. Then, at that K order, it picks the weight blocks per workgroup and
-the flags for each bucket (1; 8: four and eight rows together; 16, 32, 64). Last, for launches with a norm
-prologue (bp_skinny_mf_pro: the decode loops' q|k|v, gate|up and LM head launches), the weight blocks per workgroup
-at the same K order, for buckets 1 and 8 (rb_pro; `--pro-only` retunes just those in an existing table).
+the flags for each bucket (1; 8: four and eight rows together; 16: nine and sixteen rows, the row groups over one
+staged copy among its plans; 32, 64; `--plans-only 16` retunes just those buckets in an existing table). Last, for
+launches with a norm prologue (bp_skinny_mf_pro: the decode loops' q|k|v, gate|up and LM head launches), the weight
+blocks per workgroup at the same K order, for buckets 1 and 8 (rb_pro; `--pro-only` retunes just those).
 
 Usage: python -m byteprof_amd.tune [--shapes N:K,...] [--kinds bf16,int8,int4] [--out path] [--pro-only]
+                                   [--plans-only BUCKETS]
 """
 
 from __future__ import annotations
@@ -102,13 +104,14 @@ def _plans(kind: str, m: int, k: int, waves: int, split: int):
     """(rb, xstage flags) of every compiled plan at this K order: staged activations or not, and where the
     straight-line kernel of the segment count applies, that kernel or the general loop (XS_GENERAL)."""
     fixed = S.segments_per_wave(kind, k, waves, split) > 0
+    rows = (S.XS_STAGE | S.XS_ROWS2, S.XS_STAGE | S.XS_ROWS4) if 8 < m <= 16 else ()
     for rb in RBS:
-        for xs in (0, S.XS_STAGE, S.XS_GENERAL, S.XS_STAGE | S.XS_GENERAL):
-            if xs & S.XS_STAGE and (m > 16 or S._stage_bytes(kind, m, k, split) < 0):
+        for xs in (0, S.XS_STAGE, S.XS_GENERAL, S.XS_STAGE | S.XS_GENERAL, *rows):
+            if xs & S.XS_STAGE and (m > 16 or S._stage_bytes(kind, m, k, split, xs) < 0):
                 continue
             if xs & S.XS_GENERAL and not fixed:
                 continue
-            if S._supported(kind, m, rb, waves, xs & S.XS_STAGE):
+            if S._supported(kind, m, rb, waves, xs & (S.XS_STAGE | S.XS_ROWS)):
                 yield rb, xs
 
 
@@ -187,6 +190,33 @@ def _pro_time(kind: str, ring, x, n: int, k: int, waves: int) -> float | None:
     return best
 
 
+# the row buckets of a plan and the row counts its choice is timed at (16: a drafting verify round's 9 rows too)
+BUCKET_ROWS = ((1, [1]), (8, [4, 8]), (16, [9, 16]), (32, [32]), (64, [64]))
+
+
+def retune_plans(kind: str, n: int, k: int, entry: dict, buckets, device, log=print) -> dict:
+    """The plans (rb, xstage flags) of the given row buckets at the entry's K order (its waves and split), with
+    their times; the rest of the entry is kept."""
+    waves, split = int(entry["waves"]), int(entry.get("split", 1))
+    ring = _ring(kind, n, k, device)
+    x = torch.randn(64, k, device=device).to(torch.bfloat16)
+    y = torch.empty(64, n, dtype=torch.bfloat16, device=device)
+    out = {**entry, "rb": dict(entry.get("rb", {})), "xs": dict(entry.get("xs", {})), "us": dict(entry.get("us", {}))}
+    for bucket, rows in BUCKET_ROWS:
+        if bucket not in buckets:
+            continue
+        _, rb, xs = _best_plan(kind, ring, x, y, waves, split, rows)
+        out["rb"][str(bucket)], out["xs"][str(bucket)] = rb, xs
+        for m in rows:
+            out["us"][str(m)] = round(_time_calls(_launcher(kind, ring, x[:m].contiguous(), y[:m], rb, waves, split,
+                                                            xs)), 3)
+        log(f"  {kind} {n}x{k} bucket {bucket}: rb {rb} xs {xs}: " + ", ".join(f"M={m} {out['us'][str(m)]} us"
+                                                                           for m in rows))
+    del ring
+    torch.cuda.empty_cache()
+    return out
+
+
 def tune_shape(kind: str, n: int, k: int, device, log=print) -> dict:
     ring = _ring(kind, n, k, device)
     nseg = -(-k // S.k_segment(kind))
@@ -221,7 +251,7 @@ def tune_shape(kind: str, n: int, k: int, device, log=print) -> dict:
     best = min(near, key=lambda o: orders[o][1])
     waves, split = best
     rb, xs, us = {}, {}, {}
-    for bucket, rows in ((1, [1]), (8, [4, 8]), (16, [16]), (32, [32]), (64, [64])):
+    for bucket, rows in BUCKET_ROWS:
         t, rb[str(bucket)], xs[str(bucket)] = _best_plan(kind, ring, x, y, waves, split, rows)
         for m in rows:
             us[str(m)] = round(_time_calls(_launcher(kind, ring, x[:m].contiguous(), y[:m], rb[str(bucket)], waves,
@@ -290,6 +320,9 @@ def main(argv=None) -> int:
     ap.add_argument("--shapes", default=None, help="N:K,N:K,... (default: the decode-step set shapes)")
     ap.add_argument("--kinds", default="bf16,int8")
     ap.add_argument("--out", default=str(S._CFG_FILE))
+    ap.add_argument("--plans-only", default=None,
+                    help="comma-separated row buckets: only (re)tune those buckets' plans (rb, xstage) of the table's "
+                         "existing bf16 / int8 entries (the K orders kept)")
     ap.add_argument("--pro-only", action="store_true",
                     help="only (re)tune rb_pro of the table's existing bf16 / int8 entries (the K orders kept)")
     a = ap.parse_args(argv)
@@ -307,6 +340,18 @@ def main(argv=None) -> int:
                        "with, waves and split of the int4 kernel at those tile rows, us per row count, and tiles = the "
                        "best (waves, split) and its M = 1 time for each tile rows.")
     log = lambda m: print(m, flush=True)  # noqa: E731
+    if a.plans_only:
+        buckets = {int(b) for b in a.plans_only.split(",")}
+        for kind in a.kinds.split(","):
+            for n, k in shapes:
+                key = f"{kind}|{n}|{k}"
+                if kind == "int4" or key not in table:
+                    continue
+                print(f"[tune] {key} plans of buckets {sorted(buckets)}", flush=True)
+                table[key] = retune_plans(kind, n, k, table[key], buckets, device, log=log)
+                out.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
+        print(f"[tune] wrote {out}")
+        return 0
     if a.pro_only:
         for kind in a.kinds.split(","):
             for n, k in shapes:

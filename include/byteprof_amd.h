@@ -59,8 +59,11 @@ size_t bp_skinny_workspace_bytes(int64_t M, int64_t N, int split);
  * bp_skinny_workspace_bytes), xstage: flags BP_XS_STAGE (each workgroup copies its activation rows and K range to
  * LDS first; up to M = 16 and bp_skinny_mf_stage_bytes() >= 0; else the activation operands are loaded with the
  * weights) and BP_XS_GENERAL (the general segment loop; without it, a launch whose waves have exactly 4, 8 or 16
- * segments each runs a straight-line kernel for that count). The K order of every sum depends only on (K, waves,
- * split): output row i is bitwise independent of M (1..64), rb and xstage. K not a multiple of the 128-byte segment
+ * segments each runs a straight-line kernel for that count); with BP_XS_STAGE at 9..16 rows, BP_XS_ROWS2 /
+ * BP_XS_ROWS4 make the workgroup 2 / 4 row groups of rb blocks, each with its own `waves` waves, over one LDS copy of
+ * the activation rows (the activation bytes per weight row fall 2 / 4x; up to 64 KiB of LDS,
+ * bp_skinny_mf_stage_bytes_rows(); waves x groups <= 16; not with 16 segments a wave). The K order of every sum
+ * depends only on (K, waves, split): output row i is bitwise independent of M (1..64), rb and xstage. K not a multiple of the 128-byte segment
  * (64 bf16 / 128 int8 elements) or x, w not 16-byte aligned: an element-load variant with the same segments (rb 1,
  * 4 waves, xstage 0).
  * Replaces: byteprof/optim/skinny.py:36-90 (_skinny_kernel MODE 0 / 1, _split_reduce) and :111-133 (_launch) via
@@ -69,10 +72,15 @@ size_t bp_skinny_workspace_bytes(int64_t M, int64_t N, int split);
  */
 #define BP_XS_STAGE 1
 #define BP_XS_GENERAL 2
+#define BP_XS_ROWS2 4
+#define BP_XS_ROWS4 8
 int bp_skinny_mf_supported(int wkind, int M, int rb, int waves, int xstage);
 int bp_skinny_mf_k_segment(int wkind);
 /* LDS bytes a launch with BP_XS_STAGE uses, or -1 when its activations do not fit (then the flag must be off). */
 int64_t bp_skinny_mf_stage_bytes(int wkind, int64_t M, int64_t K, int split);
+/* The same for a launch with BP_XS_STAGE and the row-group flags of xstage (their larger LDS limit). No counterpart in
+ * the reference (its kernel stages nothing). */
+int64_t bp_skinny_mf_stage_bytes_rows(int wkind, int64_t M, int64_t K, int split, int xstage);
 int bp_skinny_mf(int wkind, const void* x, const void* w, const void* scale, int scale_dtype, void* y, int64_t M,
                  int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* workspace,
                  size_t workspace_bytes, void* stream);

@@ -438,11 +438,16 @@ def test_tuned_table_entries_resolve_to_compiled_plans():
             continue
         assert e["waves"] in (1, 2, 4, 8) and e["split"] >= 1
         for bucket in ("1", "8", "16", "32", "64"):
-            assert int(e["rb"][bucket]) in (1, 2, 4) and int(e["xs"][bucket]) in (0, 1, 2, 3)
+            xs = int(e["xs"][bucket])
+            assert int(e["rb"][bucket]) in (1, 2, 4) and xs in (0, 1, 2, 3, 5, 9)
+            # row groups: staged 9..16-row plans only
+            assert not xs & S.XS_ROWS or (bucket == "16" and xs & S.XS_STAGE)
         for m in (1, 5, 8, 9, 16, 17, 33, 64):
             rb, waves, split, xs = S._resolve(kind, n, k, m, None)
             assert (waves, split) == (e["waves"], e["split"])
-            assert S._supported(kind, m, rb, waves, xs & S.XS_STAGE)
+            assert S._supported(kind, m, rb, waves, xs & (S.XS_STAGE | S.XS_ROWS))
+            if m in (9, 16):  # the table's plan is the one launched (no silent fallback)
+                assert (rb, xs) == (int(e["rb"]["16"]), int(e["xs"]["16"])), (kind, n, k, m)
         # rb_pro (norm-prologue launches): only where the order keeps whole rows, for buckets 1 and 8, compiled,
         # and the one picked for those launches (same K order)
         assert set(e.get("rb_pro", {})) <= {"1", "8"} and (not e.get("rb_pro") or e["split"] == 1)
