@@ -173,18 +173,23 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   if (wr > 1 && nseg_wave == 16) nseg_wave = 0;  // the row-group kernels run the general loop there
   MfFn fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0, pro.kind != 0, nseg_wave,
                     wr);
-  if (fn == nullptr && wr > 1) {
-    // row groups are a plan, not a K order: without a compiled row-group kernel (rows outside 9..16, rb or waves
-    // outside its menu), the same sums from one row group, staged where the rows fit in the plain limit
+  if (fn == nullptr && wr == 4) {
+    // row groups are a plan, not a K order: without a compiled kernel of 4 groups, 2 (the same LDS)
+    wr = 2;
+    fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0, pro.kind != 0, nseg_wave, wr);
+  }
+  if (fn == nullptr && wr > 1 && pro.kind == 0) {
+    // without a row-group kernel (rows outside 9..16, rb or waves outside its menu), the same sums from one group,
+    // staged where the rows fit in the plain limit
     wr = 1;
-    if (xstage && pro.kind == 0) {
+    if (xstage) {
       lds = mf_stage_bytes(wkind, M, K, split, 1);
       if (lds < 0) {
         xstage = 0;
         lds = 0;
       }
     }
-    fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0, pro.kind != 0, nseg_wave);
+    fn = mf_pick(wkind, mf_blocks(M), rb, waves, vec, mode == 2 ? 1 : 0, xstage != 0, false, nseg_wave);
   }
   if (fn == nullptr) return BP_E_UNSUPPORTED;
   if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))

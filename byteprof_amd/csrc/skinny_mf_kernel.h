@@ -184,7 +184,8 @@ __global__ __launch_bounds__(WAVES * WR * kWave) void skinny_mf_kernel(const uin
   using G = MfGeom<KIND>;
   static_assert(NSEG == 0 || VEC, "the fixed segment count needs vector loads");
   static_assert(WR == 1 || (XL && !PRO), "row groups share the staged activations (no prologue)");
-  constexpr int NT = WAVES * WR * kWave;
+  constexpr int NW = WAVES * WR;  // the workgroup's waves
+  constexpr int NT = NW * kWave;
   constexpr int D = VEC ? mf_depth<KIND, MB, RB, !XL>() : 1;
   constexpr int kInFlight = NSEG > 0 && NSEG < D ? NSEG : D;  // weight segments issued before the staging commit
   __shared__ MfRed<WAVES, RB, MB> red[WR];
@@ -282,7 +283,7 @@ __global__ __launch_bounds__(WAVES * WR * kWave) void skinny_mf_kernel(const uin
       // rows past the register pass (kPer pieces per thread): straight into LDS, 64 pieces of 16 bytes per load
       // (piece e at element 8 e of the staged rows), ahead of the weight loads as well
       const int pieces = mrows * (kn / 8);
-      for (int c = kPer * WAVES + wave; c * kWave < pieces; c += WAVES) {
+      for (int c = kPer * NW + wave; c * kWave < pieces; c += NW) {
         const int e = c * kWave + lane;
         if (e < pieces)
           __builtin_amdgcn_global_load_lds(
@@ -295,7 +296,7 @@ __global__ __launch_bounds__(WAVES * WR * kWave) void skinny_mf_kernel(const uin
         // LDS: gamma [kn], then the residual rows [kn] each
         if (mrows == 1) {
           uint16_t* dst2 = dst + (pro.residual != nullptr ? 2 : 1) * kn;  // gamma2 after gamma and the residual
-          for (int j = wave; j * 512 < kn; j += WAVES) {
+          for (int j = wave; j * 512 < kn; j += NW) {
             const int e = j * 512 + 8 * lane;
             if (e < kn) {
               __builtin_amdgcn_global_load_lds(as_global(pro.gamma + e),
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(WAVES * WR * kWave) void skinny_mf_kernel(const uin
           }
         } else {
           const int nres = pro.residual != nullptr ? mrows : 0;
-          for (int j = wave; j * 512 < kn; j += WAVES) {
+          for (int j = wave; j * 512 < kn; j += NW) {
             const int e = j * 512 + 8 * lane;
             if (e < kn) {
               __builtin_amdgcn_global_load_lds(as_global(pro.gamma + e),
