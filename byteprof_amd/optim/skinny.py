@@ -161,7 +161,7 @@ def segments_per_wave(kind: str, k: int, waves: int, split: int, xs: int = 0) ->
 def kernel_name(kind: str, n: int, k: int, m: int, cfg=None) -> str:
     """Name of the kernel instantiation a skinny_mm launch of m rows runs, as the profiler reports it (template
     arguments: kind, activation blocks, weight blocks, waves, vector loads, epilogue, staged activations, prologue,
-    segments per wave)."""
+    segments per wave, row groups)."""
     rb, waves, split, xs = _resolve(kind, n, k, m, cfg)
     mb = 1 if m <= 8 else 2 if m <= 16 else 4 if m <= 32 else 8
     wr = 4 if xs & XS_ROWS4 else 2 if xs & XS_ROWS2 else 1
@@ -169,7 +169,7 @@ def kernel_name(kind: str, n: int, k: int, m: int, cfg=None) -> str:
     if wr > 1 and nseg == 16:
         nseg = 0  # the row-group kernels run the general loop there
     return (f"skinny_mf_kernel<{_KIND_CODE[kind]}, {mb}, {rb}, {waves}, true, 0, "
-            f"{'true' if xs & XS_STAGE else 'false'}, false, {nseg}" + (f", {wr}>" if wr > 1 else ">"))
+            f"{'true' if xs & XS_STAGE else 'false'}, false, {nseg}, {wr}>")
 
 
 @functools.lru_cache(maxsize=None)
