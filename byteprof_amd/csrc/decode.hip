@@ -638,6 +638,62 @@ __global__ __launch_bounds__(kBlock) void norm_residual_kernel(const uint16_t* _
   norm_row_out(norm_xs, w, residual != nullptr ? residual + row : nullptr, out + row, n, eps);
 }
 
+// norm_residual_kernel's arithmetic, bit for bit, for rows of n % 8 == 0 elements with 16-byte aligned x, w,
+// residual and out: a thread owns pieces of 8 elements (one 16-byte load each of x, w and the residual, every load
+// issued before the barrier), so the launch makes one memory round trip before its sum of squares instead of two.
+constexpr int kNormVecThreads = 256;
+constexpr int kNormVecPer = kNormMax / 8 / kNormVecThreads;  // pieces per thread at the longest row
+
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+__global__ __launch_bounds__(kNormVecThreads) void norm_residual_vec_kernel(const uint16_t* __restrict__ x,
+                                                                            const uint16_t* __restrict__ w,
+                                                                            const uint16_t* residual, uint16_t* out,
+                                                                            int n, float eps) {
+  extern __shared__ uint16_t norm_xs[];
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * n;
+  const int pieces = n / 8;
+  const bool res = residual != nullptr;
+  uint4 xv[kNormVecPer], wv[kNormVecPer], rv[kNormVecPer];
+#pragma unroll
+  for (int j = 0; j < kNormVecPer; ++j) {
+    const int p = static_cast<int>(threadIdx.x) + j * kNormVecThreads;
+    if (p < pieces) {
+      xv[j] = *reinterpret_cast<const uint4*>(x + row + 8 * p);
+      wv[j] = *reinterpret_cast<const uint4*>(w + 8 * p);
+      rv[j] = res ? *reinterpret_cast<const uint4*>(residual + row + 8 * p) : uint4{0u, 0u, 0u, 0u};
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kNormVecPer; ++j) {
+    const int p = static_cast<int>(threadIdx.x) + j * kNormVecThreads;
+    if (p < pieces) *reinterpret_cast<uint4*>(norm_xs + 8 * p) = xv[j];
+  }
+  __syncthreads();
+  const float ss = wave_sumsq_lds(norm_xs, n);
+  const float r = 1.f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int j = 0; j < kNormVecPer; ++j) {
+    const int p = static_cast<int>(threadIdx.x) + j * kNormVecThreads;
+    if (p < pieces) {
+      const uint32_t xa[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+      const uint32_t wa[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+      const uint32_t ra[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y0 = round_to_bf16(bf16_lo(wa[e]) * (bf16_lo(xa[e]) * r));
+        const float y1 = round_to_bf16(bf16_hi(wa[e]) * (bf16_hi(xa[e]) * r));
+        const uint32_t o0 = float_to_bf16_bits(res ? bf16_lo(ra[e]) + y0 : y0);
+        const uint32_t o1 = float_to_bf16_bits(res ? bf16_hi(ra[e]) + y1 : y1);
+        o[e] = o0 | (o1 << 16);
+      }
+      *reinterpret_cast<uint4*>(out + row + 8 * p) = uint4{o[0], o[1], o[2], o[3]};
+    }
+  }
+}
+
 // The split-K reduce of a projection's partials (ws [split][rows][n], added in split order, the int8 scale applied
 // to the sum, rounded to bf16: splitk_reduce_kernel's arithmetic) feeding norm_residual_kernel's arithmetic in the
 // same workgroup (grid = rows, n <= kNormMax): out = bf16(residual + bf16(w * y * rsqrt(mean(y^2) + eps))), equal
@@ -936,9 +992,17 @@ int bp_decode_norm_residual_rows(const void* x, const void* weight, const void* 
                                  float eps, int rows, void* stream) {
   if (x == nullptr || weight == nullptr || out == nullptr || n <= 0 || rows <= 0) return BP_E_INVALID_ARG;
   if (n > bp::kNormMax) return BP_E_UNSUPPORTED;
-  bp::norm_residual_kernel<<<rows, bp::kBlock, static_cast<size_t>(n) * 2, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight),
-      static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), n, eps);
+  using bp::aligned16;
+  if (n % 8 == 0 && aligned16(x) && aligned16(weight) && aligned16(out) &&
+      (residual == nullptr || aligned16(residual)))
+    bp::norm_residual_vec_kernel<<<rows, bp::kNormVecThreads, static_cast<size_t>(n) * 2,
+                                   static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight),
+        static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), n, eps);
+  else
+    bp::norm_residual_kernel<<<rows, bp::kBlock, static_cast<size_t>(n) * 2, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight),
+        static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), n, eps);
   return bp::status();
 }
 

@@ -35,7 +35,7 @@ from . import skinny as S
 MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
 ROPE_ATTENTION_ROWS = 16  # most rows of one fused q/k-norm + RoPE + cache + attention launch
 VERIFY_ROWS = 16  # rows of the verify-pass buffers (allocated once per decoder, never reallocated)
-PRO_MAX_ROWS = {"bf16": 5, "int8": 4}  # most rows of a linear launch with the sublayer norm as its prologue
+PRO_MAX_ROWS = {"bf16": 3, "int8": 1}  # most rows of a linear launch with the sublayer norm as its prologue
 PRO_LDS_BYTES = 80 * 1024  # the launch keeps gamma and the residual rows in LDS while the staged rows and they fit
 ARGMAX_ROW_WORDS, ARGMAX_ERROR_WORD = 132, 130  # u32 words of the argmax scratch per row; its error word
 
@@ -287,9 +287,10 @@ class OlmoDecoder:
         """Whether the launch of an n x k linear at rows rows takes a norm prologue: a plan that keeps whole rows
         (split 1), the rows x k activations staged in LDS (32 KiB), gamma with the residual rows in LDS beside them
         (one row, or PRO_LDS_BYTES in all: past it the prologue would read them from memory element by element, which
-        made 7-row verify rounds 870 -> 1206 us), and at most PRO_MAX_ROWS rows: measured on the OLMo-2-1B shape, the
-        prologue beats a separate norm launch at 1..5 rows for bf16 (5-row round 838 -> 817 us; 7 rows: no gain) and
-        at 1..4 for int8 (5 rows: 685 -> 736 us, 7 rows: 724 -> 809 us)."""
+        made 7-row verify rounds 870 -> 1206 us), and at most PRO_MAX_ROWS rows: measured on the OLMo-2-1B shape
+        against the one-round-trip norm launch, the prologue wins at 1..3 rows for bf16 (2 / 3-row rounds 731 / 755
+        -> 724 / 749 us; 5 rows loses, 791-808 -> 829 us) and at one row only for int8 (2 / 3 rows: 575 / 586-599
+        without it, 587-597 / 631-634 with it); at one row it saves the norm launch of every sublayer."""
         _, _, split, _ = self._plan(n, k, rows)
         if split != 1 or rows > PRO_MAX_ROWS[self.kind]:
             return False
@@ -303,7 +304,7 @@ class OlmoDecoder:
         length L (drafts ids[1 + j] equal to the prediction of row j) and the next round's inputs: ids[0] <- the
         token after the accepted prefix, pos += L + 1. Every row is computed as the one-token step at its position
         computes it (the linears' rows do not depend on the row count). Each sublayer norm runs inside the next
-        linear's launch where _pro_fits allows (up to 5 bf16 / 4 int8 rows), else as its own launch (the
+        linear's launch where _pro_fits allows (up to 3 bf16 rows / one int8 row), else as its own launch (the
         same bits either way); the residual stream alternates between vx and vh where a prologue writes it."""
         if not 1 <= s <= getattr(self, "smax", 0):
             raise ValueError(f"s must be in 1..{getattr(self, 'smax', 0)} (verify_buffers)")

@@ -53,7 +53,7 @@ def _ocfg(cfg: OG.OlmoConfig) -> OO.Config:
 def test_norm_residual_matches_the_oracle():
     rng = np.random.default_rng(0)
     L = _lib.lib()
-    for n in (256, 2048, 3000, 8192, 10000):  # registers up to 8192, two passes above
+    for n in (256, 1004, 2048, 3000, 8192, 10000):  # n % 8 != 0 (1004) takes the scalar kernel
         print(f"\n[olmo] norm n={n}", flush=True)
         x, w, r = (ON.bf16_round(rng.standard_normal(n).astype(np.float32) * s) for s in (3.0, 1.0, 2.0))
         tx, tw, tr = _bf16(x), _bf16(w), _bf16(r)
@@ -64,6 +64,37 @@ def test_norm_residual_matches_the_oracle():
         _lib.check(L.bp_decode_norm_residual(tx.data_ptr(), tw.data_ptr(), tr.data_ptr(), tr.data_ptr(), n, 1e-6,
                                              st), "n")  # in place on the residual
         assert _ulps(_np(tr), ON.bf16_round(r + OO.rmsnorm(x, w, 1e-6))).max() <= 1
+
+
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_norm_residual_vector_and_scalar_kernels_agree_bit_for_bit(with_residual):
+    """Rows of n % 8 == 0 elements at 16-byte aligned addresses take the vector kernel, other rows the scalar one:
+    the same arithmetic in the same order, so the same bits (9 rows of 2048, in place on the residual; the scalar
+    kernel reached by offsetting every operand by one element)."""
+    L = _lib.lib()
+    rng = np.random.default_rng(3)
+    S, n = 9, 2048
+    x = _bf16(ON.bf16_round(rng.standard_normal((S, n)).astype(np.float32) * 2)).reshape(-1)
+    w = _bf16(ON.bf16_round(1 + 0.1 * rng.standard_normal(n).astype(np.float32)))
+    r = _bf16(ON.bf16_round(rng.standard_normal((S, n)).astype(np.float32))).reshape(-1)
+    outs = []
+    for off in (0, 1):
+        bufs = [torch.zeros(t.numel() + 8, dtype=torch.bfloat16, device=DEV) for t in (x, w, r)]
+        for b, t in zip(bufs, (x, w, r)):
+            b[off:off + t.numel()] = t
+        bx, bw, br = (b[off:] for b in bufs)
+        if with_residual:
+            dst, res = br, br.data_ptr()
+        else:
+            dst, res = torch.zeros_like(br), None
+        _lib.check(L.bp_decode_norm_residual_rows(bx.data_ptr(), bw.data_ptr(), res, dst.data_ptr(), n, 1e-6, S,
+                                                  _lib.stream_ptr(x.device)), "rows")
+        outs.append(dst[:S * n].clone())
+    assert torch.equal(outs[0], outs[1])
+    ref = np.stack([OO.rmsnorm(row, _np(w), 1e-6) for row in _np(x).reshape(S, n)])
+    if with_residual:
+        ref = ON.bf16_round(_np(r).reshape(S, n) + ref)
+    assert _ulps(_np(outs[0]).reshape(S, n), ref).max() <= 1
 
 
 @pytest.mark.parametrize("pos", [0, 5, 63])
