@@ -53,7 +53,7 @@ def _ocfg(cfg: OG.OlmoConfig) -> OO.Config:
 def test_norm_residual_matches_the_oracle():
     rng = np.random.default_rng(0)
     L = _lib.lib()
-    for n in (256, 1004, 2048, 3000, 8192, 10000):  # n % 8 != 0 (1004) takes the scalar kernel
+    for n in (8, 256, 1004, 2048, 3000, 8192, 10000, 16384):  # n % 8 != 0 (1004) takes the scalar kernel
         print(f"\n[olmo] norm n={n}", flush=True)
         x, w, r = (ON.bf16_round(rng.standard_normal(n).astype(np.float32) * s) for s in (3.0, 1.0, 2.0))
         tx, tw, tr = _bf16(x), _bf16(w), _bf16(r)
