@@ -97,6 +97,9 @@ __device__ __forceinline__ u32x4 mf_load_w16(const uint8_t* __restrict__ wrow, i
   }
 }
 
+// Word 3 of a gfx9 buffer resource for raw dword access (data format 32, no swizzle, no index stride).
+constexpr int kBufferWord3 = 0x00020000;
+
 // Activation operands read from global memory (rows past M read row 0; their columns are never stored).
 template <int KIND, int MB, bool VEC>
 struct MfXGlobal {
@@ -117,6 +120,32 @@ struct MfXGlobal {
   // operand `part` of segment s for activation block b
   __device__ __forceinline__ u32x4 load(int64_t s, int b, int part) const {
     return mf_load_x8<VEC>(row[b], s * G::kSeg + kl + 8 * part, K);
+  }
+};
+
+// The vector form: one buffer resource over the M x K activations (the launch takes it for K < 2^24: with up to 64
+// rows, 2 M K < 2^31 bytes).
+// A lane of a row past M has an offset past the resource, so its loads return zeros without a memory request:
+// the padding rows of the last activation block (7 of 8 at 9 rows) cost no memory traffic.
+template <int KIND, int MB>
+struct MfXGlobal<KIND, MB, true> {
+  using G = MfGeom<KIND>;
+  static constexpr uint32_t kPast = 0x80000000u;  // beyond any resource: 2 M K < 2^31
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t off[MB];  // byte offset of the lane's row at its K offset within a segment, or kPast
+
+  __device__ __forceinline__ void init(const uint16_t* __restrict__ x, int M, int64_t K, const MfLane& ln) {
+    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, static_cast<int>(2 * M * K), kBufferWord3);
+    const int64_t kl = static_cast<int64_t>(G::kLaneK) * ln.slot();
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      const int m = 8 * b + ln.r;
+      off[b] = m < M ? static_cast<uint32_t>(2 * (m * K + kl)) : kPast;
+    }
+  }
+  __device__ __forceinline__ u32x4 load(int64_t s, int b, int part) const {
+    const uint32_t o = off[b] + static_cast<uint32_t>(2 * (s * G::kSeg + 8 * part));
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0));
   }
 };
 

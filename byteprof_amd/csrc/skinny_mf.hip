@@ -89,6 +89,8 @@ int64_t mf_stage_bytes(int wkind, int64_t M, int64_t K, int split, int wr = 1) {
   return bytes <= (wr > 1 ? kMaxStageBytesRows : kMaxStageBytes) ? bytes : -1;
 }
 
+constexpr int64_t kMaxVecK = int64_t{1} << 24;  // 2 x 64 rows x K bytes of activations < 2^31
+
 // mode 0: y (split > 1: partials then the reduce); 1: partials only (split >= 2, y unused); 2: SiLU epilogue.
 int mf_launch(int wkind, const void* x, const void* w, const void* scale, int scale_dt, void* y, int64_t M,
               int64_t N, int64_t K, int rb, int waves, int split, int xstage, void* ws, size_t ws_bytes, void* stream,
@@ -115,9 +117,11 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
   int wr = mf_row_groups(xstage);
   xstage &= BP_XS_STAGE;
   const int64_t seg = wkind == kBf16 ? 64 : 128;
-  // the vector loads read whole segments: K a multiple of the segment, 16-byte aligned operands
+  // the vector loads read whole segments: K a multiple of the segment, 16-byte aligned operands, and K below
+  // 2^24, so that up to 64 activation rows lie within one buffer resource (2 M K < 2^31 bytes) whatever M is: the
+  // choice, and with it the K order, does not depend on M
   const bool vec = K % seg == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(w) % 16 == 0;
+                   reinterpret_cast<uintptr_t>(w) % 16 == 0 && K < kMaxVecK;
   if (!vec) {
     rb = 1;
     waves = 4;

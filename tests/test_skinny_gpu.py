@@ -137,6 +137,18 @@ def test_unaligned_operands_use_the_element_path(kind):
     check_against_oracle(S.skinny_mm(x, *args), x, w_np)
 
 
+@pytest.mark.parametrize("kind", KINDS)
+def test_k_past_the_buffer_range_takes_the_element_path(kind):
+    """K >= 2^24: 64 activation rows would not fit one buffer resource, so every row count takes the element-load
+    kernel (the same K order for one row and for three)."""
+    n, k = 8, (1 << 24) + 128
+    _, args = make_weights(kind, n, k, seed=11)
+    x = randn_x(3, k, seed=12)
+    y = S.skinny_mm(x, *args)
+    assert torch.equal(S.skinny_mm(x[1:2].contiguous(), *args), y[1:2])
+    check_against_oracle(y, x, oracle_weights(kind, args))
+
+
 def test_exact_fixture():
     """Tiny operands whose exact bf16 products are committed (tests/golden/skinny_kat.json): the kernel's fp32
     accumulation may move a result by at most one bf16 step from the exactly rounded value."""
