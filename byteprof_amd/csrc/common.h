@@ -54,6 +54,12 @@ __device__ __forceinline__ gptr<T> as_global_mut(T* p) {
   return (gptr<T>)(p);
 }
 
+// A raw buffer resource over `bytes` bytes at p (gfx9 word 3: 32-bit data format, no swizzle, no index stride).
+// A load at an offset past `bytes` returns zeros without a memory request.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
 // The tile of workgroup b of a row of T: the hardware deals a grid's workgroups to the 8 XCDs in turn (b % 8), and
 // this gives each XCD one contiguous run of tiles, so neighbouring tiles that share cache lines (a scale row's 32
 // bytes per 16 rows) meet in one XCD's L2 instead of four.

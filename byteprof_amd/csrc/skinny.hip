@@ -66,10 +66,11 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(packed) % 16 != 0 ||
       reinterpret_cast<uintptr_t>(zero) % 2 != 0)
     return BP_E_UNSUPPORTED;
-  // the matrix-core kernel where a lane's four rows can read their scale and zero as one vector each
+  // the matrix-core kernel where a lane's four rows can read their scale and zero as one vector each, and the
+  // activations of up to 16 rows fit one buffer resource (K < 2^24); the choice does not depend on M
   const int64_t sc_align = scale_dt == BP_DT_F32 ? 16 : 8;
   const bool mf = N % 4 == 0 && reinterpret_cast<uintptr_t>(zero) % 8 == 0 &&
-                  reinterpret_cast<uintptr_t>(scale) % sc_align == 0;
+                  reinterpret_cast<uintptr_t>(scale) % sc_align == 0 && K < (int64_t{1} << 24);
   Int4Fn fn = mf ? int4_mf_pick(tile_rows, waves, scale_dt) : int4_pick(row_bucket(M), tile_rows, waves);
   if (fn == nullptr) return BP_E_UNSUPPORTED;
   const int64_t groups = K / 128;

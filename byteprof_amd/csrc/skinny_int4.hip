@@ -218,7 +218,10 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
   const int64_t first = g_lo + wave;
   const int cnt = first < g_hi ? static_cast<int>((g_hi - first + WAVES - 1) / WAVES) : 0;
   const uint8_t* tile = w + tb * G * R * 64 + i * 64 + kb * 16;
-  const uint16_t* xr = x + static_cast<int64_t>(i < M ? i : M - 1) * K + kb * 16;
+  // the activations through one buffer resource (the launch takes this kernel for K < 2^24: 2 M K < 2^31 bytes);
+  // a column past M has an offset past it, so its loads return zeros without a memory request
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(x, static_cast<int>(2 * M * K));
+  const uint32_t xoff = i < M ? static_cast<uint32_t>(2 * (i * K + kb * 16)) : 0x80000000u;
   constexpr bool f32 = SDT == BP_DT_F32;  // the scale's dtype (scale_dt == SDT)
 
   // a group's record: [R scales (scale dtype) | R zeros (fp16)] of the tile's rows, kRecDw dwords; lane l holds
@@ -249,11 +252,11 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
 #pragma unroll
     for (int h = 0; h < RB; ++h)
       sl.wv[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + (g * R + 16 * h) * 64));
-    const uint16_t* xg = xr + g * 128;
-    sl.xv[0] = *reinterpret_cast<const u32x4*>(xg);
-    sl.xv[1] = *reinterpret_cast<const u32x4*>(xg + 8);
-    sl.xv[2] = *reinterpret_cast<const u32x4*>(xg + 64);
-    sl.xv[3] = *reinterpret_cast<const u32x4*>(xg + 72);
+    const uint32_t xo = xoff + static_cast<uint32_t>(256 * g);
+    sl.xv[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
+    sl.xv[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16, 0, 0));
+    sl.xv[2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 128, 0, 0));
+    sl.xv[3] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 144, 0, 0));
 #pragma unroll
     for (int c = 0; c < kRecLoads; ++c) sl.rv[c] = *reinterpret_cast<const uint32_t*>(rsrc[c] + g * rstride[c]);
   };
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
 #pragma unroll
     for (int c = 0; c < kRecLoads; ++c) st[c * kWave + lane] = sl.rv[c];
     __builtin_amdgcn_wave_barrier();
-    // columns past M hold a copy of row M - 1: computed, never stored
+    // columns past M hold zeros: computed, never stored
     const u32x4 ones = u32x4{kBf16OnePair, kBf16OnePair, kBf16OnePair, kBf16OnePair};
     // X: the group's sum of each column's activations, as the product of an all-ones A with the same B operands
     floatx4 X = {0.f, 0.f, 0.f, 0.f};

@@ -97,9 +97,6 @@ __device__ __forceinline__ u32x4 mf_load_w16(const uint8_t* __restrict__ wrow, i
   }
 }
 
-// Word 3 of a gfx9 buffer resource for raw dword access (data format 32, no swizzle, no index stride).
-constexpr int kBufferWord3 = 0x00020000;
-
 // Activation operands read from global memory (rows past M read row 0; their columns are never stored).
 template <int KIND, int MB, bool VEC>
 struct MfXGlobal {
@@ -135,7 +132,7 @@ struct MfXGlobal<KIND, MB, true> {
   uint32_t off[MB];  // byte offset of the lane's row at its K offset within a segment, or kPast
 
   __device__ __forceinline__ void init(const uint16_t* __restrict__ x, int M, int64_t K, const MfLane& ln) {
-    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, static_cast<int>(2 * M * K), kBufferWord3);
+    rs = buffer_rsrc(x, static_cast<int>(2 * M * K));
     const int64_t kl = static_cast<int64_t>(G::kLaneK) * ln.slot();
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
