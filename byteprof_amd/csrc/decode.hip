@@ -111,30 +111,32 @@ struct HeadAttention {
   static constexpr int RPW = kWave / LPR;           // rows per wave instruction
   static constexpr int STEP = kAttnWaves * RPW;     // rows per workgroup-wide batch
   static constexpr int BATCH = kAttnUnroll * STEP;  // rows per round of loads
-  const uint16_t* K;
-  const uint16_t* V;
+  // the rows 0 .. T-1 of K and V as buffer resources: a row at or past T has an offset past its resource, so its
+  // load returns zeros without a memory request (and without a branch around the load)
+  __amdgpu_buffer_rsrc_t krs, vrs;
   int T, s, slot;
   u32x4 k0[kAttnUnroll], v0[kAttnUnroll];
 
-  __device__ __forceinline__ HeadAttention(const uint16_t* K_, const uint16_t* V_, int T_) : K(K_), V(V_), T(T_) {
+  __device__ __forceinline__ HeadAttention(const uint16_t* K_, const uint16_t* V_, int T_)
+      : krs(buffer_rsrc(K_, 2 * T_ * D)), vrs(buffer_rsrc(V_, 2 * T_ * D)), T(T_) {
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     s = lane % LPR;
     slot = wave * RPW + lane / LPR;  // this lane's row within a batch
   }
 
-  __device__ __forceinline__ void load_batch(const uint16_t* base, int t0, u32x4 (&out)[kAttnUnroll]) const {
+  __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rs, int t0, u32x4 (&out)[kAttnUnroll]) const {
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
       const int t = t0 + u * STEP + slot;
-      out[u] = u32x4{0u, 0u, 0u, 0u};
-      if (t < T) out[u] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(t) * D + 8 * s);
+      const uint32_t off = t < T ? static_cast<uint32_t>(2 * (t * D + 8 * s)) : 0x80000000u;
+      out[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     }
   }
 
   // Issues the loads of the first batch of K and V rows.
   __device__ __forceinline__ void prefetch() {
-    load_batch(K, 0, k0);
-    load_batch(V, 0, v0);
+    load_batch(krs, 0, k0);
+    load_batch(vrs, 0, v0);
   }
 
   __device__ __forceinline__ void scores(const u32x4 (&kv)[kAttnUnroll], int t0, const float (&qv)[8],
@@ -193,7 +195,7 @@ struct HeadAttention {
     scores(k0, 0, qv, ksub, sub_lo, scale, sc, m);
     for (int t0 = BATCH; t0 < T; t0 += BATCH) {
       u32x4 kv[kAttnUnroll];
-      load_batch(K, t0, kv);
+      load_batch(krs, t0, kv);
       scores(kv, t0, qv, ksub, sub_lo, scale, sc, m);
     }
     m = wave_max(m);
@@ -219,7 +221,7 @@ struct HeadAttention {
     values(v0, 0, vsub, sub_lo, sc, inv, acc);
     for (int t0 = BATCH; t0 < T; t0 += BATCH) {
       u32x4 vv[kAttnUnroll];
-      load_batch(V, t0, vv);
+      load_batch(vrs, t0, vv);
       values(vv, t0, vsub, sub_lo, sc, inv, acc);
     }
     // the wave's row groups (lanes s, s + LPR, s + 2 LPR, ...) added by butterflies over the group bits
@@ -507,16 +509,20 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_rows_kernel(const
     v_b[p] = qj[2 * H + b];
   }
 
-  // sums of squares of q (row r) and k (rows 0 .. r), each in qk_rms's order
+  // sums of squares of q (row r) and k (rows 0 .. r), each in qk_rms's order; the k rows through a buffer resource
+  // over the launch's rows, rows past r at an offset past it (zeros, no memory request; their sums are unused)
   float sq = 0.f;
   float sk[kRowsMax];
 #pragma unroll
   for (int j = 0; j < kRowsMax; ++j) sk[j] = 0.f;
+  const __amdgpu_buffer_rsrc_t qkv_rs = buffer_rsrc(qkv, 2 * static_cast<int>(gridDim.y) * row3);
   for (int i = 8 * threadIdx.x; i < H; i += 8 * kAttnThreads) {
     u32x4 kx[kRowsMax];
 #pragma unroll
-    for (int j = 0; j < kRowsMax; ++j)
-      kx[j] = *reinterpret_cast<const u32x4*>(qkv + static_cast<int64_t>(j <= r ? j : r) * row3 + H + i);
+    for (int j = 0; j < kRowsMax; ++j) {
+      const uint32_t off = j <= r ? static_cast<uint32_t>(2 * (j * row3 + H + i)) : 0x80000000u;
+      kx[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qkv_rs, off, 0, 0));
+    }
     const u32x4 qa = *reinterpret_cast<const u32x4*>(qkv + static_cast<int64_t>(r) * row3 + i);
     const uint32_t qd[4] = {qa.x, qa.y, qa.z, qa.w};
 #pragma unroll
