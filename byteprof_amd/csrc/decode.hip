@@ -977,6 +977,8 @@ int bp_decode_rope_attention_rows(const void* qkv, const void* q_norm_w, const v
       max_len > bp::kAttnMaxLen)
     return BP_E_UNSUPPORTED;
   if (!bp::aligned16(qkv) || !bp::aligned16(k_cache) || !bp::aligned16(v_cache)) return BP_E_INVALID_ARG;
+  // the verify launch reads its rows of q|k|v through one buffer resource (under 2^31 bytes)
+  if (static_cast<int64_t>(rows) * 3 * heads * head_dim * 2 >= (int64_t{1} << 31)) return BP_E_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define BP_ROPE_ATT(L)                                                                                           \
   bp::launch_rope_attention<L>(qkv, q_norm_w, k_norm_w, inv_freq, pos, k_cache, v_cache, out, heads, rows, max_len, \

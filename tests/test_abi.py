@@ -109,6 +109,11 @@ def test_invalid_arguments_are_rejected_before_any_launch(L):
     assert L.bp_decode_argmax_next(p, 100, p, p, odd, None) == -1
     assert L.bp_decode_argmax_rows(p, 100, 2, p, odd, None) == -1
     assert L.bp_decode_argmax_scratch_bytes() % 8 == 0 and L.bp_decode_argmax_rows_scratch_bytes(3) % 8 == 0
+    # the verify attention's q|k|v rows must fit one buffer resource (2^31 bytes): 16 rows x 3 x 2^25 x 2 bytes
+    ra = lambda heads, rows: L.bp_decode_rope_attention_rows(p, p, p, p, p, p, p, p, heads, 128, rows, 64,  # noqa: E731
+                                                             1e-6, 0.1, None)
+    assert ra(1 << 18, 16) == -2
+    assert ra(0, 16) == -1
 
 
 def test_argmax_scratch_holds_an_error_word_per_row(L):
