@@ -147,7 +147,7 @@ struct MfXGlobal<KIND, MB, true> {
 };
 
 // Activation operands read from an LDS copy xs[m][k] of the workgroup's activation rows (row stride `stride`
-// elements; segment s at element s * kSeg - k_base; rows past M read row 0, as from memory).
+// elements; segment s at element s * kSeg - k_base; rows past M read row 0 of the copy, never stored).
 template <int KIND, int MB>
 struct MfXLds {
   using G = MfGeom<KIND>;
