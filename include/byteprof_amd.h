@@ -64,7 +64,8 @@ size_t bp_skinny_workspace_bytes(int64_t M, int64_t N, int split);
  * the activation rows (the activation bytes per weight row fall 2 / 4x; up to 64 KiB of LDS,
  * bp_skinny_mf_stage_bytes_rows(); waves x groups <= 16; not with 16 segments a wave). The K order of every sum
  * depends only on (K, waves, split): output row i is bitwise independent of M (1..64), rb and xstage. K not a multiple of the 128-byte segment
- * (64 bf16 / 128 int8 elements) or x, w not 16-byte aligned: an element-load variant with the same segments (rb 1,
+ * (64 bf16 / 128 int8 elements), x, w not 16-byte aligned, or K >= 2^24 (the vector loads read the activations
+ * through one buffer resource, under 2^31 bytes at 64 rows): an element-load variant with the same segments (rb 1,
  * 4 waves, xstage 0).
  * Replaces: byteprof/optim/skinny.py:36-90 (_skinny_kernel MODE 0 / 1, _split_reduce) and :111-133 (_launch) via
  *           skinny_mm (skinny.py:136-166) for every BM bucket (16, 32, 64); at M = 1 with int8 weights, the one-row
@@ -200,7 +201,8 @@ int bp_chain_run(int wkind, int scale_dtype, const void* dev_items, const void* 
  * waves: 1, 2, 4 or 8 (groups dealt to the waves); split: as for the other skinny kernels (the scale is applied per
  * group, so the reduce adds the partial sums as they are). The K order depends only on (K, waves, split) and on
  * which of two kernels runs: the matrix-core kernel (the activation rows as MFMA columns: nearly the same time at
- * any M) when N % 4 == 0, zero is 8-byte aligned and scale aligned to four of its elements; else a VALU kernel.
+ * any M) when N % 4 == 0, zero is 8-byte aligned, scale aligned to four of its elements and K < 2^24 (its
+ * activations through one buffer resource); else a VALU kernel.
  * Replaces: byteprof/optim/skinny.py:46-63 (_skinny_kernel MODE 3) via skinny_mm (skinny.py:136-166).
  */
 int bp_skinny_int4_config_supported(int mt, int tile_rows, int waves);
@@ -313,7 +315,8 @@ int bp_draft_commit(const void* c_hist, void* c_cur, const void* n_hist, void* n
  * attention:      per head, positions 0 .. *pos: out = bf16(softmax_fp32(bf16(bf16(q . k) * scale)) as bf16 . v);
  *                 head_dim a multiple of 8 dividing 256, max_len <= 4096; caches 16-byte aligned.
  * rope_attention: qk_rope_cache and attention in one launch (one workgroup per head), equal bit for bit to the
- *                 two launches; qkv 16-byte aligned. rope_attention_rows: rows (<= 16) consecutive positions
+ *                 two launches; qkv 16-byte aligned. rope_attention_rows: rows (<= 16, and rows x 3 x heads x
+ *                 head_dim x 2 bytes of q|k|v under 2^31, else BP_E_UNSUPPORTED) consecutive positions
  *                 *pos .. *pos + rows - 1 (>= 0) in one launch (one workgroup per head and row), equal bit for bit
  *                 to qk_rope_cache_rows + attention_rows.
  * norm_residual:  out = bf16(residual + bf16(w * x * rsqrt(mean(x^2) + eps))), the mean square summed in one fixed
