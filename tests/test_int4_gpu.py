@@ -52,6 +52,17 @@ def test_tile_heights(tile_rows, n, k):
         check_against_oracle(S.skinny_mm(x[:m].contiguous(), *args), x[:m], w_np)
 
 
+def test_k_past_the_buffer_range_takes_the_valu_kernel():
+    """K >= 2^24: the matrix-core kernel reads its activations through one buffer resource (under 2^31 bytes at 16
+    rows), so such K takes the VALU kernel at every row count (the same K order for one row and for three)."""
+    n, k = 16, (1 << 24) + 128
+    args, w_np = make_int4(n, k, seed=21, tile_rows=16)
+    x = randn_x(3, k, seed=22)
+    y = S.skinny_mm(x, *args)
+    assert torch.equal(S.skinny_mm(x[1:2].contiguous(), *args), y[1:2])
+    check_against_oracle(y, x, w_np)
+
+
 @pytest.mark.parametrize("cfg", [(1, 1), (2, 1), (4, 1), (8, 1), (2, 3), (8, 2), (32, 128, 4, 3, 5)])
 def test_configurations_match(cfg):
     args, w_np = make_int4(192, 2048, seed=5)
