@@ -48,8 +48,8 @@ MUTANTS = [
     ("int4 group scale ignored", "csrc/skinny_int4.hip",
      "acc[h][r] += sc * (D[r] - (128.f + z) * X[r]);", "acc[h][r] += (D[r] - (128.f + z) * X[r]);"),
     ("int8 channel scale ignored", "csrc/skinny_mf_kernel.h",
-     "if constexpr (KIND == kInt8) t *= load_scale(scale, n, scale_dt);\n        y[",
-     "if constexpr (KIND == kInt8) t *= 1.f;\n        y["),
+     "if constexpr (KIND == kInt8) t *= row_scale(0);\n        yk[",
+     "if constexpr (KIND == kInt8) t *= 1.f;\n        yk["),
     ("split-K reduce skips the last split", "csrc/skinny.hip",
      "for (int s = 1; s < split; ++s) t += ws[s * total + idx];",
      "for (int s = 1; s < split - 1; ++s) t += ws[s * total + idx];"),
@@ -67,8 +67,11 @@ MUTANTS = [
     ("store not masked on rows >= M", "csrc/skinny_mf_kernel.h",
      "not run: every form of it writes rows past y's [M, N]", None),
     ("output rows reversed", "csrc/skinny_mf_kernel.h",
-     "y[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);",
-     "y[static_cast<int64_t>(m) * N + (N - 1 - n)] = float_to_bf16_bits(t);"),
+     "yk[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);",
+     "yk[static_cast<int64_t>(m) * N + (N - 1 - n)] = float_to_bf16_bits(t);"),
+    ("activation operands one piece late (buffer offsets)", "csrc/skinny_mf.h",
+     "const uint32_t o = off[b] + static_cast<uint32_t>(2 * (s * G::kSeg + 8 * part));",
+     "const uint32_t o = off[b] + static_cast<uint32_t>(2 * (s * G::kSeg + 8 * part + 8));"),
     ("int4 pack: high nibble from the low code", "optim/skinny.py",
      "g[:, :, :, 0] | (g[:, :, :, 1] << 4)", "g[:, :, :, 0] | (g[:, :, :, 0] << 4)"),
     ("MFMA halves folded from the wrong lanes", "csrc/skinny_mf.h",

@@ -456,3 +456,18 @@ def test_tuned_table_entries_resolve_to_compiled_plans():
                 rb, waves, split, _ = S._resolve(kind, n, k, m, None, pro=True)
                 assert rb == int(e["rb_pro"][bucket]) and (waves, split) == (e["waves"], e["split"])
                 assert S._supported(kind, m, rb, waves, True)
+
+
+def test_every_mutant_plants_its_text_once():
+    """The mutation check (tests/mutation.py) plants each bug by replacing one exact piece of source text: every
+    piece must still occur exactly once, or the mutant would silently stop being built."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("mutation", Path(__file__).with_name("mutation.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    pkg = Path(__file__).resolve().parent.parent / "byteprof_amd"
+    for name, rel, old, new in mod.MUTANTS:
+        if new is None:
+            continue
+        assert (pkg / rel).read_text().count(old) == 1, name
