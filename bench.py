@@ -32,7 +32,7 @@ reference's CPU path); secondary figures:
   - c1: one 8192 x 2048 linear at M = 1 (GPU, and F.linear on the CPU);
   - mlstm: the fused 16-step mLSTM block;
   - sweep_bf16 / sweep_int8: the verify widths M in {1, 2, 4, 8, 16} x K {2048, 8192} x N {2048, 8192, 100352};
-  - decode_loop: the graph-captured greedy decode loop of the OLMo-2-1B shape (bf16, int8) and its drafting loop;
+  - decode_loop: the graph-captured greedy decode loop of the OLMo-2-1B shape (bf16, int8, int4) and its drafting loop;
   - cpu_legs: on the host cores, fp32 F.linear over the full 113-linear set, int8 dequantize-then-F.linear over
     the full set, the 8192 x 2048 linear alone, and the mLSTM block as a torch fp32 step loop.
 Every timed leg is warmed by time (WARM_S seconds of its own launches) first.
@@ -403,7 +403,8 @@ def decode_loop(device, new_tokens: int = 128) -> dict:
     """The graph-captured greedy decode loop (byteprof_amd/optim/olmo.py) on the OLMo-2-1B shape with synthetic
     weights: per kind, the GPU time of one captured decode step (replays timed with events), the loop's time per
     token (two-step graph replays kept one ahead of the host; a generate of 1 + N tokens minus one of 1, over N) and the
-    eager loop's, with the weight bytes a step streams."""
+    eager loop's, with the weight bytes a step streams; the drafting rounds for bf16 and int8 (the int4 decoder steps
+    one token at a time)."""
     import torch
 
     from byteprof_amd.optim import olmo as OG
@@ -412,9 +413,10 @@ def decode_loop(device, new_tokens: int = 128) -> dict:
     prompt = torch.tensor([[11, 2027, 5, 99999, 42, 3, 3, 1000]])
     out = {"model": "OLMo-2-1B shape (16 x 2048, FFN 8192, 16 heads, vocab 100352), synthetic weights",
            "prompt_tokens": prompt.shape[1], "new_tokens": new_tokens}
-    for kind in ("bf16", "int8"):
+    for kind in ("bf16", "int8", "int4"):
         dec = OG.OlmoDecoder(cfg, OG.random_weights(cfg, device, seed=4), kind)
-        out["launches_per_step"] = dec.launches_per_step
+        if kind != "int4":
+            out["launches_per_step"] = dec.launches_per_step
         graph = OG.make_generate_graph(dec)
         graph(prompt, max_new_tokens=4)  # captures the step
         warm(lambda: graph(prompt, max_new_tokens=8), 0.3)
@@ -454,7 +456,11 @@ def decode_loop(device, new_tokens: int = 128) -> dict:
         nb = dec.weight_bytes()
         out[kind] = {"us_per_token_loop": loop_us, "us_per_step_graph": step_us, "us_per_token_eager": eager_us,
                      "weight_bytes_per_step": nb, "weight_gbs_graph_step": nb / step_us / 1e3,
-                     "tokens_per_s_loop": 1e6 / loop_us, "draft": draft_figures(dec, prompt, ref, new_tokens)}
+                     "tokens_per_s_loop": 1e6 / loop_us}
+        if kind == "int4":
+            out[kind]["launches_per_step"] = dec.launches_per_step
+        else:
+            out[kind]["draft"] = draft_figures(dec, prompt, ref, new_tokens)
         del dec, graph, eager, g
         torch.cuda.empty_cache()
     return out

@@ -95,12 +95,14 @@ def random_weights(cfg: OlmoConfig, device, seed: int = 0, std: float | None = N
 
 class OlmoDecoder:
     """One OLMo-2 decode step on the GPU, reading the token id and the position from device memory (tok, pos) and
-    leaving the next token in tok and pos + 1 in pos. kind: 'bf16' or 'int8' (every linear quantized per row,
-    fp16 scales; embeddings and norm weights stay bf16)."""
+    leaving the next token in tok and pos + 1 in pos. kind: 'bf16', 'int8' (every linear quantized per row, fp16
+    scales) or 'int4' (group-128 codes with per-group scale and zero, tile-major at the tuned tile rows: the int4_wo
+    format of skinny_mm; its steps run the norms and the SiLU product as launches of their own, and drafting verify
+    passes take bf16 or int8 only); embeddings and norm weights stay bf16."""
 
     def __init__(self, cfg: OlmoConfig, weights: dict[str, torch.Tensor], kind: str = "bf16"):
-        if kind not in ("bf16", "int8"):
-            raise ValueError("kind must be 'bf16' or 'int8'")
+        if kind not in ("bf16", "int8", "int4"):
+            raise ValueError("kind must be 'bf16', 'int8' or 'int4'")
         if cfg.hidden % cfg.heads or cfg.head_dim % 8 or 256 % cfg.head_dim or cfg.max_len > 4096:
             raise ValueError("head_dim must be a multiple of 8 dividing 256 and max_len at most 4096")
         self.cfg, self.kind = cfg, kind
@@ -112,6 +114,8 @@ class OlmoDecoder:
 
         def lin(w: torch.Tensor) -> tuple:
             w = w.contiguous()
+            if kind == "int4":
+                return S.quantize_int4(w, S.int4_tile_rows(*w.shape))
             return (w,) if kind == "bf16" else quantize_rowwise_int8(w, torch.float16)
 
         bf = torch.bfloat16
@@ -139,8 +143,9 @@ class OlmoDecoder:
         self.tok, self.pos = z(1, dtype=torch.int64), z(1, dtype=torch.int64)
         self.x, self.xn, self.attn, self.o, self.dn = z(1, H), z(1, H), z(1, H), z(1, H), z(1, H)
         self.h = z(1, H)  # the residual stream after the attention half of a layer (fused-norm step)
-        # the sublayer norms run inside the next linear's launch when its plan keeps whole rows (split 1)
-        self.fuse_norms = all(self._plan(n, H, 1)[2] == 1 for n in (3 * H, 2 * F, V))
+        # the sublayer norms run inside the next linear's launch when its plan keeps whole rows (split 1); the int4
+        # kernel has no prologue
+        self.fuse_norms = kind != "int4" and all(self._plan(n, H, 1)[2] == 1 for n in (3 * H, 2 * F, V))
         self.qkv, self.gu, self.act, self.logits = z(1, 3 * H), z(1, 2 * F), z(1, F), z(1, V)
         # the argmax's partials, counter and error word: zeroed once, the counter left at zero by every launch
         self.argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_scratch_bytes() // 4), dtype=torch.int32)
@@ -224,7 +229,12 @@ class OlmoDecoder:
                                   self.argmax_scratch.data_ptr(), st), "bp_decode_argmax_next")
 
     def _plan(self, n: int, k: int, rows: int) -> tuple[int, int, int, int]:
-        """(weight blocks per workgroup, waves, split, staging) of the skinny launch skinny_mm makes."""
+        """(weight blocks per workgroup, waves, split, staging) of the skinny launch skinny_mm makes (int4: the tile
+        rows' 16-row blocks, waves, split, no staging)."""
+        if self.kind == "int4":
+            tile = S.int4_tile_rows(n, k)
+            waves, split = S.int4_cfg(n, k, tile)
+            return tile // 16, waves, min(split, k // 128), 0
         return S._resolve(self.kind, n, k, rows, None)
 
     def _gate_up_silu(self, x: torch.Tensor, gw: tuple, act: torch.Tensor, gu: torch.Tensor, rows: int) -> None:
@@ -234,7 +244,7 @@ class OlmoDecoder:
         F, H = self.cfg.ffn, self.cfg.hidden
         rb, waves, split, xs = self._plan(2 * F, H, rows)
         L, st = _lib.lib(), _lib.stream_ptr(self.device)
-        if split == 1 and rows <= 16:
+        if split == 1 and rows <= 16 and self.kind != "int4":
             sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
             _lib.check(L.bp_skinny_mf_silu(S._KIND_CODE[self.kind], x.data_ptr(), gw[0].data_ptr(), sc, sdt,
                                            act.data_ptr(), rows, F, H, rb, waves, xs, st), "bp_skinny_mf_silu")
@@ -251,7 +261,10 @@ class OlmoDecoder:
         extra = lambda n, k: int(self._plan(n, k, 1)[2] > 1)  # noqa: E731  (the split reduce)
         if self.fuse_norms:
             return 3 + (5 + extra(H, H) + extra(H, F)) * self.cfg.layers
-        per_layer = 7 + extra(3 * H, H) + extra(H, H) + extra(H, F) + 2 * extra(2 * F, H)
+        # gate|up: the SiLU epilogue in the launch, else the product's own launch (after a split's reduce; int4
+        # always)
+        silu = 1 + extra(2 * F, H) if self.kind == "int4" else 2 * extra(2 * F, H)
+        per_layer = 7 + extra(3 * H, H) + extra(H, H) + extra(H, F) + silu
         return 4 + per_layer * self.cfg.layers + extra(V, H)
 
     def _down_splitk(self, s: int) -> tuple[int, int, int, int] | None:
@@ -267,6 +280,8 @@ class OlmoDecoder:
         out [VERIFY_ROWS + 1] receives the row tokens and, at VERIFY_ROWS (= self.smax), the accepted length."""
         if not 1 <= smax <= VERIFY_ROWS:
             raise ValueError(f"verify passes take 1..{VERIFY_ROWS} rows, asked for {smax}")
+        if self.kind == "int4":
+            raise OptimizeError("drafting verify passes take bf16 or int8 weights (the int4 decoder steps one token)")
         if getattr(self, "smax", 0):
             return
         cfg, dev = self.cfg, self.device

@@ -21,6 +21,7 @@ from byteprof_amd.optim.skinny import skinny_mm
 from byteprof_amd.quant.hip_int8 import quantize_rowwise_int8
 from oracle import numerics as ON
 from oracle import olmo as OO
+from oracle import skinny as OS
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -306,22 +307,31 @@ def _small_decoder(kind: str, seed: int = 1, cfg: OG.OlmoConfig = SMALL):
     oc = _ocfg(cfg)
     W = OO.random_weights(oc, seed=seed, std=2.0 / np.sqrt(cfg.hidden))
     dec = OG.OlmoDecoder(cfg, {k: _bf16(v) for k, v in W.items()}, kind)
-    if kind == "int8":  # the oracle runs on the weights the kernels see: q * scale
+    if kind != "bf16":  # the oracle runs on the weights the kernels see: q * scale, or (code - zero) * scale
+        deq = _deq if kind == "int8" else _deq4
         for i, lw in enumerate(dec.layers):
             p = f"l{i}."
-            qkv = _deq(lw["qkv"])
+            qkv = deq(lw["qkv"])
             H = cfg.hidden
             W[p + "q"], W[p + "k"], W[p + "v"] = qkv[:H], qkv[H:2 * H], qkv[2 * H:]
-            gu = _deq(lw["gate_up"])
+            gu = deq(lw["gate_up"])
             W[p + "gate"], W[p + "up"] = gu[0::2], gu[1::2]
-            W[p + "o"] = _deq(lw["o"])
-            W[p + "down"] = _deq(lw["down"])
-        W["lm_head"] = _deq(dec.lm_head)
+            W[p + "o"] = deq(lw["o"])
+            W[p + "down"] = deq(lw["down"])
+        W["lm_head"] = deq(dec.lm_head)
     return dec, W, oc
 
 
+def _deq4(args) -> np.ndarray:
+    """(code - zero) * scale of int4 group-128 weights, exact in float32 (a 4-bit code, an fp16 zero and a bf16
+    scale)."""
+    packed, scale, zero = args
+    return OS.dequantize_int4(packed.cpu().numpy(), scale.float().cpu().numpy(),
+                              zero.float().cpu().numpy()).astype(np.float32)
+
+
 @pytest.mark.parametrize("shape", ["small", "fused"])
-@pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
 def test_decode_steps_match_the_oracle(kind, shape):
     dec, W, oc = _small_decoder(kind, cfg=SMALL if shape == "small" else FUSED_SMALL)
     prompt = [3, 17, 99, 250, 7]
@@ -383,7 +393,7 @@ def test_generate_contract():
         assert torch.equal(gen(torch.tensor([[7, 8, 9]]), max_new_tokens=n).cpu(), full[:, :3 + n].cpu()), n
 
 
-@pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
 def test_graph_loop_equals_the_eager_loop_olmo2_1b(kind):
     cfg = OG.OLMO2_1B
     print(f"\n[olmo] 1B {kind}", flush=True)
@@ -397,6 +407,20 @@ def test_graph_loop_equals_the_eager_loop_olmo2_1b(kind):
     assert len(set(a[0, 8:].tolist())) > 1
     del dec
     torch.cuda.empty_cache()
+
+
+def test_int4_decoder_steps_one_token_and_refuses_verify_passes():
+    """The int4 decoder: separate norm and SiLU launches (the int4 kernel has no prologue or epilogue), counted by
+    launches_per_step; a drafting verify pass is refused."""
+    dec, _, _ = _small_decoder("int4")
+    assert not dec.fuse_norms
+    cfg = SMALL
+    per_layer = 8 + sum(int(dec._plan(n, k, 1)[2] > 1) for n, k in
+                        ((3 * cfg.hidden, cfg.hidden), (cfg.hidden, cfg.hidden), (cfg.hidden, cfg.ffn),
+                         (2 * cfg.ffn, cfg.hidden)))
+    assert dec.launches_per_step == 4 + per_layer * cfg.layers + int(dec._plan(cfg.vocab, cfg.hidden, 1)[2] > 1)
+    with pytest.raises(OG.OptimizeError):
+        dec.verify_buffers(9)
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8"])
