@@ -13,7 +13,7 @@ namespace bp {
 using Int4Fn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
                         int64_t, int64_t, int);
 Int4Fn int4_pick(int mt, int tile_rows, int waves);
-Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt);
+Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt, int epi);
 
 namespace {
 
@@ -49,10 +49,13 @@ int grid_for(int64_t count) {
   return static_cast<int>(b < 2048 ? (b < 1 ? 1 : b) : 2048);
 }
 
+// epi 0: y [M, N] (split > 1: partials then the reduce); 1: the gate|up SiLU product y [M, N / 2] of interleaved
+// rows (split 1, the matrix-core kernel only).
 int skinny_int4_launch(const void* x, const void* packed, const void* scale, int scale_dt, const void* zero, void* y,
                        int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int split, void* ws,
-                       size_t ws_bytes, void* stream) {
+                       size_t ws_bytes, void* stream, int epi = 0) {
   if (M < 0 || N < 0 || K < 0 || M > 16 || K % 128 != 0) return BP_E_INVALID_ARG;
+  if (epi != 0 && (split != 1 || N % 2 != 0)) return BP_E_UNSUPPORTED;
   if (M == 0 || N == 0) return BP_OK;
   if (x == nullptr || packed == nullptr || y == nullptr || scale == nullptr || zero == nullptr)
     return BP_E_INVALID_ARG;
@@ -60,7 +63,9 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
   if (split < 1 || split > 1024) return BP_E_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (K == 0) {
-    fill_zero_bf16_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<uint16_t*>(y), M * N);
+    // silu(0) * 0 = 0: zeros either way
+    const int64_t count = epi != 0 ? M * (N / 2) : M * N;
+    fill_zero_bf16_kernel<<<grid_for(count), 256, 0, st>>>(static_cast<uint16_t*>(y), count);
     return launch_status();
   }
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(packed) % 16 != 0 ||
@@ -71,7 +76,8 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
   const int64_t sc_align = scale_dt == BP_DT_F32 ? 16 : 8;
   const bool mf = N % 4 == 0 && reinterpret_cast<uintptr_t>(zero) % 8 == 0 &&
                   reinterpret_cast<uintptr_t>(scale) % sc_align == 0 && K < (int64_t{1} << 24);
-  Int4Fn fn = mf ? int4_mf_pick(tile_rows, waves, scale_dt) : int4_pick(row_bucket(M), tile_rows, waves);
+  if (epi != 0 && !mf) return BP_E_UNSUPPORTED;
+  Int4Fn fn = mf ? int4_mf_pick(tile_rows, waves, scale_dt, epi) : int4_pick(row_bucket(M), tile_rows, waves);
   if (fn == nullptr) return BP_E_UNSUPPORTED;
   const int64_t groups = K / 128;
   if (split > groups) split = static_cast<int>(groups);
@@ -111,6 +117,13 @@ int bp_skinny_int4(const void* x, const void* packed, const void* scale, int sca
                    size_t workspace_bytes, void* stream) {
   return bp::skinny_int4_launch(x, packed, scale, scale_dtype, zero, y, M, N, K, tile_rows, waves, split, workspace,
                                 workspace_bytes, stream);
+}
+
+int bp_skinny_int4_silu(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero,
+                        void* out, int64_t M, int64_t ffn, int64_t K, int tile_rows, int waves, void* stream) {
+  if (ffn < 0) return BP_E_INVALID_ARG;
+  return bp::skinny_int4_launch(x, packed, scale, scale_dtype, zero, out, M, 2 * ffn, K, tile_rows, waves, 1, nullptr,
+                                0, stream, 1);
 }
 
 int bp_version(void) { return 100; }

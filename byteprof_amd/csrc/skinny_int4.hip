@@ -193,7 +193,7 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
 
 using u32x2 = unsigned __attribute__((ext_vector_type(2)));
 
-template <int RB, int WAVES, int DEPTH, int SDT>
+template <int RB, int WAVES, int DEPTH, int SDT, int EPI = 0>
 __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uint16_t* __restrict__ x,
                                                                        const uint8_t* __restrict__ w,
                                                                        const void* __restrict__ scale, int scale_dt,
@@ -351,38 +351,66 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][16 * h + 4 * kb + r][i] = acc[h][r];
   __syncthreads();
-  for (int e = threadIdx.x; e < R * 16; e += WAVES * kWave) {
-    const int row = e / 16;
-    const int m = e % 16;
-    const int64_t n = n0 + row;
-    if (m >= M || n >= N) continue;
+  const auto total = [&](int row, int m) {
     float t = red[0][row][m];
 #pragma unroll
     for (int v = 1; v < WAVES; ++v) t += red[v][row][m];
-    if (split == 1)
-      y[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);
-    else
-      ws[(static_cast<int64_t>(s) * M + m) * N + n] = t;
+    return t;
+  };
+  if constexpr (EPI == 0) {
+    for (int e = threadIdx.x; e < R * 16; e += WAVES * kWave) {
+      const int row = e / 16;
+      const int m = e % 16;
+      const int64_t n = n0 + row;
+      if (m >= M || n >= N) continue;
+      const float t = total(row, m);
+      if (split == 1)
+        y[static_cast<int64_t>(m) * N + n] = float_to_bf16_bits(t);
+      else
+        ws[(static_cast<int64_t>(s) * M + m) * N + n] = t;
+    }
+  } else {
+    // the gate|up SiLU product (split 1): rows 2f and 2f + 1 of the tile are the gate and up rows of output f,
+    // y [M, N / 2]; the arithmetic of bp_decode_silu_mul_rows on the rounded sums
+    for (int e = threadIdx.x; e < (R / 2) * 16; e += WAVES * kWave) {
+      const int row = 2 * (e / 16);
+      const int m = e % 16;
+      const int64_t n = n0 + row;
+      if (m >= M || n + 1 >= N) continue;
+      const float gb = round_to_bf16(total(row, m));
+      const float a = round_to_bf16(gb / (1.f + expf(-gb)));
+      y[static_cast<int64_t>(m) * (N / 2) + n / 2] = float_to_bf16_bits(a * round_to_bf16(total(row + 1, m)));
+    }
   }
 }
 
-template <int RB, int DEPTH, int SDT>
+template <int RB, int DEPTH, int SDT, int EPI>
 Int4Fn int4_mf_waves(int waves) {
   switch (waves) {
-    case 1: return &skinny_int4_mf_kernel<RB, 1, DEPTH, SDT>;
-    case 2: return &skinny_int4_mf_kernel<RB, 2, DEPTH, SDT>;
-    case 4: return &skinny_int4_mf_kernel<RB, 4, DEPTH, SDT>;
-    case 8: return &skinny_int4_mf_kernel<RB, 8, DEPTH, SDT>;
+    case 1: return &skinny_int4_mf_kernel<RB, 1, DEPTH, SDT, EPI>;
+    case 2: return &skinny_int4_mf_kernel<RB, 2, DEPTH, SDT, EPI>;
+    case 4: return &skinny_int4_mf_kernel<RB, 4, DEPTH, SDT, EPI>;
+    case 8: return &skinny_int4_mf_kernel<RB, 8, DEPTH, SDT, EPI>;
     default: return nullptr;
   }
 }
 
-template <int RB, int DEPTH>
+template <int RB, int DEPTH, int EPI>
 Int4Fn int4_mf_dtype(int waves, int scale_dt) {
   switch (scale_dt) {
-    case BP_DT_BF16: return int4_mf_waves<RB, DEPTH, BP_DT_BF16>(waves);
-    case BP_DT_F16: return int4_mf_waves<RB, DEPTH, BP_DT_F16>(waves);
-    case BP_DT_F32: return int4_mf_waves<RB, DEPTH, BP_DT_F32>(waves);
+    case BP_DT_BF16: return int4_mf_waves<RB, DEPTH, BP_DT_BF16, EPI>(waves);
+    case BP_DT_F16: return int4_mf_waves<RB, DEPTH, BP_DT_F16, EPI>(waves);
+    case BP_DT_F32: return int4_mf_waves<RB, DEPTH, BP_DT_F32, EPI>(waves);
+    default: return nullptr;
+  }
+}
+
+template <int EPI>
+Int4Fn int4_mf_tile(int tile_rows, int waves, int scale_dt) {
+  switch (tile_rows) {
+    case 16: return int4_mf_dtype<1, 4, EPI>(waves, scale_dt);
+    case 32: return int4_mf_dtype<2, 3, EPI>(waves, scale_dt);
+    case 64: return int4_mf_dtype<4, 2, EPI>(waves, scale_dt);
     default: return nullptr;
   }
 }
@@ -410,15 +438,10 @@ Int4Fn int4_rows(int rb, int waves) {
 
 }  // namespace
 
-// Matrix-core kernel for (tile rows, waves, scale dtype), or null; groups in flight per wave: 4 at 16 tile rows, 3
-// at 32, 2 at 64.
-Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt) {
-  switch (tile_rows) {
-    case 16: return int4_mf_dtype<1, 4>(waves, scale_dt);
-    case 32: return int4_mf_dtype<2, 3>(waves, scale_dt);
-    case 64: return int4_mf_dtype<4, 2>(waves, scale_dt);
-    default: return nullptr;
-  }
+// Matrix-core kernel for (tile rows, waves, scale dtype, epilogue: 0 the product, 1 the gate|up SiLU product), or
+// null; groups in flight per wave: 4 at 16 tile rows, 3 at 32, 2 at 64.
+Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt, int epi) {
+  return epi == 0 ? int4_mf_tile<0>(tile_rows, waves, scale_dt) : int4_mf_tile<1>(tile_rows, waves, scale_dt);
 }
 
 // Kernel for (activation-row bucket, tile rows, waves), or null.

@@ -97,8 +97,8 @@ class OlmoDecoder:
     """One OLMo-2 decode step on the GPU, reading the token id and the position from device memory (tok, pos) and
     leaving the next token in tok and pos + 1 in pos. kind: 'bf16', 'int8' (every linear quantized per row, fp16
     scales) or 'int4' (group-128 codes with per-group scale and zero, tile-major at the tuned tile rows: the int4_wo
-    format of skinny_mm; its steps run the norms and the SiLU product as launches of their own, and drafting verify
-    passes take bf16 or int8 only); embeddings and norm weights stay bf16."""
+    format of skinny_mm; its steps run the norms as launches of their own, and drafting verify passes take bf16 or
+    int8 only); embeddings and norm weights stay bf16."""
 
     def __init__(self, cfg: OlmoConfig, weights: dict[str, torch.Tensor], kind: str = "bf16"):
         if kind not in ("bf16", "int8", "int4"):
@@ -244,6 +244,12 @@ class OlmoDecoder:
         F, H = self.cfg.ffn, self.cfg.hidden
         rb, waves, split, xs = self._plan(2 * F, H, rows)
         L, st = _lib.lib(), _lib.stream_ptr(self.device)
+        if self.kind == "int4" and split == 1 and rows <= 16 and F % 2 == 0:
+            packed, scale, zero = gw
+            _lib.check(L.bp_skinny_int4_silu(x.data_ptr(), packed.data_ptr(), scale.data_ptr(),
+                                             _lib.TORCH_DT[scale.dtype], zero.data_ptr(), act.data_ptr(), rows, F, H,
+                                             16 * rb, waves, st), "bp_skinny_int4_silu")
+            return
         if split == 1 and rows <= 16 and self.kind != "int4":
             sc, sdt = (gw[1].data_ptr(), _lib.TORCH_DT[gw[1].dtype]) if self.kind == "int8" else (None, 0)
             _lib.check(L.bp_skinny_mf_silu(S._KIND_CODE[self.kind], x.data_ptr(), gw[0].data_ptr(), sc, sdt,
@@ -261,10 +267,8 @@ class OlmoDecoder:
         extra = lambda n, k: int(self._plan(n, k, 1)[2] > 1)  # noqa: E731  (the split reduce)
         if self.fuse_norms:
             return 3 + (5 + extra(H, H) + extra(H, F)) * self.cfg.layers
-        # gate|up: the SiLU epilogue in the launch, else the product's own launch (after a split's reduce; int4
-        # always)
-        silu = 1 + extra(2 * F, H) if self.kind == "int4" else 2 * extra(2 * F, H)
-        per_layer = 7 + extra(3 * H, H) + extra(H, H) + extra(H, F) + silu
+        # gate|up: the SiLU epilogue in the launch, else the product's own launch after a split's reduce
+        per_layer = 7 + extra(3 * H, H) + extra(H, H) + extra(H, F) + 2 * extra(2 * F, H)
         return 4 + per_layer * self.cfg.layers + extra(V, H)
 
     def _down_splitk(self, s: int) -> tuple[int, int, int, int] | None:

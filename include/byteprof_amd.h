@@ -209,6 +209,15 @@ int bp_skinny_int4_config_supported(int mt, int tile_rows, int waves);
 int bp_skinny_int4(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero, void* y,
                    int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int split, void* workspace,
                    size_t workspace_bytes, void* stream);
+/* bp_skinny_int4 of an interleaved gate|up weight ([2 ffn, K] packed: row 2f the gate row f, row 2f + 1 the up row
+ * f) with the SiLU product as the epilogue: out [M, ffn] = bf16(bf16(silu(bf16(g))) * bf16(u)), equal bit for bit to
+ * bp_skinny_int4 (same tile rows and waves, split 1) followed by bp_decode_silu_mul_rows (interleaved). The
+ * matrix-core kernel only (ffn even, zero 8-byte aligned, scale aligned to four of its elements, K < 2^24), else
+ * BP_E_UNSUPPORTED.
+ * Replaces: the gate / up projections and act_fn(gate) * up of HF Olmo2MLP (with int4_wo weights) in the decode step
+ *           that byteprof/optim/olmo.py:122-219 captures. */
+int bp_skinny_int4_silu(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero,
+                        void* out, int64_t M, int64_t ffn, int64_t K, int tile_rows, int waves, void* stream);
 
 /*
  * Fixed-order reduction of split-K partial sums: y[M, N] = bf16(scale[n] * sum_{s < split} ws[s, M, N]);

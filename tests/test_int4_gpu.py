@@ -52,6 +52,37 @@ def test_tile_heights(tile_rows, n, k):
         check_against_oracle(S.skinny_mm(x[:m].contiguous(), *args), x[:m], w_np)
 
 
+@pytest.mark.parametrize("tile_rows", [16, 32, 64])
+@pytest.mark.parametrize("scale_dtype", [None, torch.float16, torch.float32])
+def test_silu_epilogue_equals_the_product_then_silu_mul(tile_rows, scale_dtype):
+    """bp_skinny_int4_silu on an interleaved gate|up weight: bit for bit bp_skinny_int4 (same tile rows and waves)
+    followed by bp_decode_silu_mul_rows, for 1..16 rows and a ragged last tile; the sums checked against the
+    oracle."""
+    from byteprof_amd import _lib
+
+    L = _lib.lib()
+    for ffn, k in ((512, 1024), (1000, 512)):
+        args, w_np = make_int4(2 * ffn, k, seed=ffn, tile_rows=tile_rows, scale_dtype=scale_dtype)
+        packed, scale, zero = args
+        for waves in (1, 4):
+            for m in (1, 5, 16):
+                x = randn_x(m, k, seed=m + ffn)
+                gu = torch.empty(m, 2 * ffn, dtype=torch.bfloat16, device="cuda")
+                _lib.check(L.bp_skinny_int4(x.data_ptr(), packed.data_ptr(), scale.data_ptr(),
+                                            _lib.TORCH_DT[scale.dtype], zero.data_ptr(), gu.data_ptr(), m, 2 * ffn, k,
+                                            tile_rows, waves, 1, None, 0, _lib.stream_ptr(x.device)), "int4")
+                ref = torch.empty(m, ffn, dtype=torch.bfloat16, device="cuda")
+                _lib.check(L.bp_decode_silu_mul_rows(gu.data_ptr(), ref.data_ptr(), ffn, m, 1,
+                                                     _lib.stream_ptr(x.device)), "silu")
+                out = torch.full((m, ffn), float("nan"), dtype=torch.bfloat16, device="cuda")
+                _lib.check(L.bp_skinny_int4_silu(x.data_ptr(), packed.data_ptr(), scale.data_ptr(),
+                                                 _lib.TORCH_DT[scale.dtype], zero.data_ptr(), out.data_ptr(), m, ffn,
+                                                 k, tile_rows, waves, _lib.stream_ptr(x.device)), "int4 silu")
+                assert torch.equal(out, ref), (ffn, k, waves, m)
+                if m == 16:
+                    check_against_oracle(gu, x, w_np)
+
+
 def test_k_past_the_buffer_range_takes_the_valu_kernel():
     """K >= 2^24: the matrix-core kernel reads its activations through one buffer resource (under 2^31 bytes at 16
     rows), so such K takes the VALU kernel at every row count (the same K order for one row and for three)."""

@@ -410,14 +410,14 @@ def test_graph_loop_equals_the_eager_loop_olmo2_1b(kind):
 
 
 def test_int4_decoder_steps_one_token_and_refuses_verify_passes():
-    """The int4 decoder: separate norm and SiLU launches (the int4 kernel has no prologue or epilogue), counted by
-    launches_per_step; a drafting verify pass is refused."""
+    """The int4 decoder: separate norm launches (the int4 kernel has no prologue), the SiLU product in the gate|up
+    launch where it keeps whole rows, counted by launches_per_step; a drafting verify pass is refused."""
     dec, _, _ = _small_decoder("int4")
     assert not dec.fuse_norms
     cfg = SMALL
-    per_layer = 8 + sum(int(dec._plan(n, k, 1)[2] > 1) for n, k in
-                        ((3 * cfg.hidden, cfg.hidden), (cfg.hidden, cfg.hidden), (cfg.hidden, cfg.ffn),
-                         (2 * cfg.ffn, cfg.hidden)))
+    per_layer = 7 + sum(int(dec._plan(n, k, 1)[2] > 1) for n, k in
+                        ((3 * cfg.hidden, cfg.hidden), (cfg.hidden, cfg.hidden), (cfg.hidden, cfg.ffn))) + \
+        2 * int(dec._plan(2 * cfg.ffn, cfg.hidden, 1)[2] > 1)
     assert dec.launches_per_step == 4 + per_layer * cfg.layers + int(dec._plan(cfg.vocab, cfg.hidden, 1)[2] > 1)
     with pytest.raises(OG.OptimizeError):
         dec.verify_buffers(9)
