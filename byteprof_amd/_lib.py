@@ -57,6 +57,8 @@ SIGNATURES: dict[str, tuple] = {
                                 _c_int, _c_vp, _c_size, _c_vp]),
     "bp_skinny_int4_silu": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                      _c_int, _c_vp]),
+    "bp_skinny_int4_pro": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
+                                    _c_int, _c_int, _c_vp, _c_vp]),
     "bp_splitk_reduce": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_int, _c_vp]),
     "bp_mlstm_multistep": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                     _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,

@@ -54,6 +54,13 @@ __device__ __forceinline__ gptr<T> as_global_mut(T* p) {
   return (gptr<T>)(p);
 }
 
+// Whether the byte ranges [a, a + na) and [b, b + nb) intersect (a null pointer is an empty range).
+inline bool ranges_overlap(const void* a, int64_t na, const void* b, int64_t nb) {
+  if (a == nullptr || b == nullptr || na <= 0 || nb <= 0) return false;
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + static_cast<uintptr_t>(nb) && pb < pa + static_cast<uintptr_t>(na);
+}
+
 // A raw buffer resource over `bytes` bytes at p (gfx9 word 3: 32-bit data format, no swizzle, no index stride).
 // A load at an offset past `bytes` returns zeros without a memory request.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, int bytes) {

@@ -6,6 +6,7 @@
 
 #include "byteprof_amd.h"
 #include "common.h"
+#include "skinny_mf_kernel.h"  // MfPro
 
 namespace bp {
 
@@ -13,7 +14,9 @@ namespace bp {
 using Int4Fn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
                         int64_t, int64_t, int);
 Int4Fn int4_pick(int mt, int tile_rows, int waves);
-Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt, int epi);
+using Int4MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
+                          int64_t, int64_t, int, MfPro);
+Int4MfFn int4_mf_pick(int tile_rows, int waves, int scale_dt, int epi, bool pro);
 
 namespace {
 
@@ -49,13 +52,35 @@ int grid_for(int64_t count) {
   return static_cast<int>(b < 2048 ? (b < 1 ? 1 : b) : 2048);
 }
 
+constexpr int64_t kInt4ProMaxK = 8192;  // the prologue's LDS: the row, gamma, the residual row and gamma2 (64 KiB)
+
 // epi 0: y [M, N] (split > 1: partials then the reduce); 1: the gate|up SiLU product y [M, N / 2] of interleaved
-// rows (split 1, the matrix-core kernel only).
+// rows (split 1, the matrix-core kernel only). prologue (kind != 0): a transform of the one activation row first
+// (split 1, the matrix-core kernel, bf16 scales, K <= 8192), as bp_skinny_mf_pro's.
 int skinny_int4_launch(const void* x, const void* packed, const void* scale, int scale_dt, const void* zero, void* y,
                        int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int split, void* ws,
-                       size_t ws_bytes, void* stream, int epi = 0) {
+                       size_t ws_bytes, void* stream, int epi = 0, const BpPrologue* prologue = nullptr) {
   if (M < 0 || N < 0 || K < 0 || M > 16 || K % 128 != 0) return BP_E_INVALID_ARG;
   if (epi != 0 && (split != 1 || N % 2 != 0)) return BP_E_UNSUPPORTED;
+  MfPro pro{0, 0.f, nullptr, nullptr, nullptr, 0, nullptr, nullptr};
+  if (prologue != nullptr && prologue->kind != 0) {
+    if (prologue->kind != BP_PRO_UNIT_RMS && prologue->kind != BP_PRO_NORM) return BP_E_INVALID_ARG;
+    if (prologue->kind == BP_PRO_NORM && prologue->gamma == nullptr) return BP_E_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(prologue->gamma) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(prologue->residual) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(prologue->xout) % 16 != 0 || reinterpret_cast<uintptr_t>(prologue->gamma2) % 16 != 0)
+      return BP_E_INVALID_ARG;
+    if (prologue->gamma2 != nullptr && prologue->kind != BP_PRO_NORM) return BP_E_INVALID_ARG;
+    // workgroup (0, 0) writes xout while the others still read x and the residual row
+    const int64_t rows_bytes = 2 * M * K;
+    if (ranges_overlap(prologue->xout, rows_bytes, x, rows_bytes) ||
+        (prologue->kind == BP_PRO_NORM && ranges_overlap(prologue->xout, rows_bytes, prologue->residual, rows_bytes)))
+      return BP_E_INVALID_ARG;
+    if (M > 1 || split != 1 || K > kInt4ProMaxK) return BP_E_UNSUPPORTED;
+    pro = MfPro{prologue->kind, prologue->eps, static_cast<const uint16_t*>(prologue->gamma),
+                static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout), 1,
+                static_cast<const uint16_t*>(prologue->gamma2), nullptr};
+  }
   if (M == 0 || N == 0) return BP_OK;
   if (x == nullptr || packed == nullptr || y == nullptr || scale == nullptr || zero == nullptr)
     return BP_E_INVALID_ARG;
@@ -63,6 +88,7 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
   if (split < 1 || split > 1024) return BP_E_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (K == 0) {
+    if (pro.kind != 0) return BP_E_UNSUPPORTED;
     // silu(0) * 0 = 0: zeros either way
     const int64_t count = epi != 0 ? M * (N / 2) : M * N;
     fill_zero_bf16_kernel<<<grid_for(count), 256, 0, st>>>(static_cast<uint16_t*>(y), count);
@@ -76,9 +102,10 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
   const int64_t sc_align = scale_dt == BP_DT_F32 ? 16 : 8;
   const bool mf = N % 4 == 0 && reinterpret_cast<uintptr_t>(zero) % 8 == 0 &&
                   reinterpret_cast<uintptr_t>(scale) % sc_align == 0 && K < (int64_t{1} << 24);
-  if (epi != 0 && !mf) return BP_E_UNSUPPORTED;
-  Int4Fn fn = mf ? int4_mf_pick(tile_rows, waves, scale_dt, epi) : int4_pick(row_bucket(M), tile_rows, waves);
-  if (fn == nullptr) return BP_E_UNSUPPORTED;
+  if ((epi != 0 || pro.kind != 0) && !mf) return BP_E_UNSUPPORTED;
+  Int4MfFn mf_fn = mf ? int4_mf_pick(tile_rows, waves, scale_dt, epi, pro.kind != 0) : nullptr;
+  Int4Fn fn = mf ? nullptr : int4_pick(row_bucket(M), tile_rows, waves);
+  if (mf_fn == nullptr && fn == nullptr) return BP_E_UNSUPPORTED;
   const int64_t groups = K / 128;
   if (split > groups) split = static_cast<int>(groups);
   if (split > 1 && (ws == nullptr || ws_bytes < static_cast<size_t>(split) * M * N * sizeof(float)))
@@ -86,9 +113,17 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
   const int64_t tiles = (N + tile_rows - 1) / tile_rows;
   if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
   dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(split));
-  fn<<<grid, waves * kWave, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(packed), scale,
-                                     scale_dt, static_cast<const uint16_t*>(zero), static_cast<uint16_t*>(y),
-                                     static_cast<float*>(ws), static_cast<int>(M), N, K, split);
+  if (mf_fn != nullptr) {
+    const size_t lds = pro.kind != 0 ? static_cast<size_t>(4 * K * 2) : 0;
+    mf_fn<<<grid, waves * kWave, lds, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(packed),
+                                            scale, scale_dt, static_cast<const uint16_t*>(zero),
+                                            static_cast<uint16_t*>(y), static_cast<float*>(ws), static_cast<int>(M),
+                                            N, K, split, pro);
+  } else {
+    fn<<<grid, waves * kWave, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(packed), scale,
+                                       scale_dt, static_cast<const uint16_t*>(zero), static_cast<uint16_t*>(y),
+                                       static_cast<float*>(ws), static_cast<int>(M), N, K, split);
+  }
   const int rc = launch_status();
   if (rc != BP_OK || split == 1) return rc;
   splitk_reduce_kernel<<<grid_for(M * N), 256, 0, st>>>(static_cast<const float*>(ws), static_cast<uint16_t*>(y),
@@ -117,6 +152,14 @@ int bp_skinny_int4(const void* x, const void* packed, const void* scale, int sca
                    size_t workspace_bytes, void* stream) {
   return bp::skinny_int4_launch(x, packed, scale, scale_dtype, zero, y, M, N, K, tile_rows, waves, split, workspace,
                                 workspace_bytes, stream);
+}
+
+int bp_skinny_int4_pro(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero, void* y,
+                       int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int epilogue,
+                       const BpPrologue* prologue, void* stream) {
+  if (prologue == nullptr || epilogue < 0 || epilogue > 1) return BP_E_INVALID_ARG;
+  return bp::skinny_int4_launch(x, packed, scale, scale_dtype, zero, y, M, epilogue ? 2 * N : N, K, tile_rows, waves,
+                                1, nullptr, 0, stream, epilogue, prologue);
 }
 
 int bp_skinny_int4_silu(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero,

@@ -32,11 +32,14 @@
 
 #include "byteprof_amd.h"
 #include "common.h"
+#include "skinny_mf_kernel.h"  // MfPro and mf_prologue: the norm prologue the matrix-core kernels share
 
 namespace bp {
 
 using Int4Fn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
                         int64_t, int64_t, int);
+using Int4MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, const uint16_t*, uint16_t*, float*, int,
+                          int64_t, int64_t, int, MfPro);
 
 namespace {
 
@@ -193,14 +196,18 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
 
 using u32x2 = unsigned __attribute__((ext_vector_type(2)));
 
-template <int RB, int WAVES, int DEPTH, int SDT, int EPI = 0>
+// PRO (one activation row, split 1): the row staged in LDS with gamma, the residual row and gamma2 (dynamic shared
+// memory, 4 K bf16), transformed by mf_prologue (the norm kernel's arithmetic: the product equals a norm launch
+// followed by the plain kernel, bit for bit) while the first groups' weights are in flight; the B operands are then
+// read from LDS.
+template <int RB, int WAVES, int DEPTH, int SDT, int EPI = 0, bool PRO = false>
 __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uint16_t* __restrict__ x,
                                                                        const uint8_t* __restrict__ w,
                                                                        const void* __restrict__ scale, int scale_dt,
                                                                        const uint16_t* __restrict__ zero,
                                                                        uint16_t* __restrict__ y,
                                                                        float* __restrict__ ws, int M, int64_t N,
-                                                                       int64_t K, int split) {
+                                                                       int64_t K, int split, MfPro pro) {
   using floatx4 = float __attribute__((ext_vector_type(4)));
   using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
   constexpr int R = 16 * RB;
@@ -247,16 +254,20 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
     }
   }
 
+  extern __shared__ __attribute__((aligned(16))) uint16_t i4_xs[];  // PRO: [x row | gamma | residual | gamma2]
+  __shared__ float pro_sums[PRO ? 8 : 1];
   auto load = [&](I4Slot<RB, kRecLoads>& sl, int j) {
     const int64_t g = first + static_cast<int64_t>(j) * WAVES;
 #pragma unroll
     for (int h = 0; h < RB; ++h)
       sl.wv[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + (g * R + 16 * h) * 64));
-    const uint32_t xo = xoff + static_cast<uint32_t>(256 * g);
-    sl.xv[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
-    sl.xv[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16, 0, 0));
-    sl.xv[2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 128, 0, 0));
-    sl.xv[3] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 144, 0, 0));
+    if constexpr (!PRO) {
+      const uint32_t xo = xoff + static_cast<uint32_t>(256 * g);
+      sl.xv[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
+      sl.xv[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16, 0, 0));
+      sl.xv[2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 128, 0, 0));
+      sl.xv[3] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 144, 0, 0));
+    }
 #pragma unroll
     for (int c = 0; c < kRecLoads; ++c) sl.rv[c] = *reinterpret_cast<const uint32_t*>(rsrc[c] + g * rstride[c]);
   };
@@ -268,8 +279,19 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
     for (int r = 0; r < 4; ++r) acc[h][r] = 0.f;
 
   uint32_t* st = stage[wave];
-  auto compute = [&](const I4Slot<RB, kRecLoads>& sl) {
+  auto compute = [&](const I4Slot<RB, kRecLoads>& sl, int j) {
     const u32x4* xv = sl.xv;
+    u32x4 xl[4];
+    if constexpr (PRO) {
+      // the transformed row from LDS (column 0; the other columns zeros, never stored)
+      const uint16_t* src = i4_xs + (first + static_cast<int64_t>(j) * WAVES) * 128 + kb * 16;
+      const u32x4 zv = u32x4{0u, 0u, 0u, 0u};
+      xl[0] = i == 0 ? *reinterpret_cast<const u32x4*>(src) : zv;
+      xl[1] = i == 0 ? *reinterpret_cast<const u32x4*>(src + 8) : zv;
+      xl[2] = i == 0 ? *reinterpret_cast<const u32x4*>(src + 64) : zv;
+      xl[3] = i == 0 ? *reinterpret_cast<const u32x4*>(src + 72) : zv;
+      xv = xl;
+    }
     // the record through the wave's stage (the wave's LDS operations run in order: the previous group's reads are
     // done before these writes land)
 #pragma unroll
@@ -324,21 +346,57 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
     }
   };
 
-  if (cnt > 0) {
-    // rounds of DEPTH groups with every load unconditional, so the waits count exactly (a load past the wave's last
-    // group reloads it, unused), and no peeled rest: the slots are not live after the loop, so the first round's
-    // loads land in the registers the loop uses
-    I4Slot<RB, kRecLoads> sl[DEPTH];
+  // rounds of DEPTH groups with every load unconditional, so the waits count exactly (a load past the wave's last
+  // group reloads it, unused), and no peeled rest: the slots are not live after the loop, so the first round's
+  // loads land in the registers the loop uses
+  I4Slot<RB, kRecLoads> sl[DEPTH];
+  if constexpr (PRO) {
+    // the row, gamma, the residual row and gamma2 straight into LDS (64 lanes x 16 bytes per load), ahead of the
+    // first groups' weights; every wave takes part in the prologue's barriers, groups or not
+    const int kn = static_cast<int>(K);
+    uint16_t* gl = i4_xs + kn;
+    uint16_t* dst2 = gl + (pro.residual != nullptr ? 2 : 1) * kn;
+    for (int c = wave; c * 512 < kn; c += WAVES) {
+      const int e = c * 512 + 8 * lane;
+      if (e < kn) {
+        __builtin_amdgcn_global_load_lds(as_global(x + e), (__attribute__((address_space(3))) void*)(i4_xs + c * 512),
+                                         16, 0, 0);
+        if (pro.kind == BP_PRO_NORM) {
+          __builtin_amdgcn_global_load_lds(as_global(pro.gamma + e),
+                                           (__attribute__((address_space(3))) void*)(gl + c * 512), 16, 0, 0);
+          if (pro.residual != nullptr)
+            __builtin_amdgcn_global_load_lds(as_global(pro.residual + e),
+                                             (__attribute__((address_space(3))) void*)(gl + kn + c * 512), 16, 0, 0);
+          if (pro.gamma2 != nullptr)
+            __builtin_amdgcn_global_load_lds(as_global(pro.gamma2 + e),
+                                             (__attribute__((address_space(3))) void*)(dst2 + c * 512), 16, 0, 0);
+        }
+      }
+    }
+    if (cnt > 0) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        load(sl[d], d < cnt ? d : cnt - 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the staged operands (and the first groups) have landed
+    __syncthreads();
+    mf_prologue<WAVES * kWave>(i4_xs, 1, kn, pro, blockIdx.x == 0 && blockIdx.y == 0,
+                               pro.kind == BP_PRO_NORM ? gl : nullptr, pro_sums);
+  } else if (cnt > 0) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       load(sl[d], d < cnt ? d : cnt - 1);
       __builtin_amdgcn_sched_barrier(0);  // the slots' loads in slot order
     }
+  }
+  if (cnt > 0) {
     for (int j0 = 0; j0 < cnt; j0 += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
         const int j = j0 + d;
-        if (j < cnt) compute(sl[d]);
+        if (j < cnt) compute(sl[d], j);
         load(sl[d], j + DEPTH < cnt ? j + DEPTH : cnt - 1);
         __builtin_amdgcn_sched_barrier(0);  // keeps the pipeline's order: group j's arithmetic before j + 1's
       }
@@ -384,33 +442,38 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
   }
 }
 
-template <int RB, int DEPTH, int SDT, int EPI>
-Int4Fn int4_mf_waves(int waves) {
+template <int RB, int DEPTH, int SDT, int EPI, bool PRO>
+Int4MfFn int4_mf_waves(int waves) {
   switch (waves) {
-    case 1: return &skinny_int4_mf_kernel<RB, 1, DEPTH, SDT, EPI>;
-    case 2: return &skinny_int4_mf_kernel<RB, 2, DEPTH, SDT, EPI>;
-    case 4: return &skinny_int4_mf_kernel<RB, 4, DEPTH, SDT, EPI>;
-    case 8: return &skinny_int4_mf_kernel<RB, 8, DEPTH, SDT, EPI>;
+    case 1: return &skinny_int4_mf_kernel<RB, 1, DEPTH, SDT, EPI, PRO>;
+    case 2: return &skinny_int4_mf_kernel<RB, 2, DEPTH, SDT, EPI, PRO>;
+    case 4: return &skinny_int4_mf_kernel<RB, 4, DEPTH, SDT, EPI, PRO>;
+    case 8: return &skinny_int4_mf_kernel<RB, 8, DEPTH, SDT, EPI, PRO>;
     default: return nullptr;
   }
 }
 
-template <int RB, int DEPTH, int EPI>
-Int4Fn int4_mf_dtype(int waves, int scale_dt) {
+// the prologue variants for bf16 scales only (quantize_int4 keeps the weights' dtype, bf16 in a decoder)
+template <int RB, int DEPTH, int EPI, bool PRO>
+Int4MfFn int4_mf_dtype(int waves, int scale_dt) {
   switch (scale_dt) {
-    case BP_DT_BF16: return int4_mf_waves<RB, DEPTH, BP_DT_BF16, EPI>(waves);
-    case BP_DT_F16: return int4_mf_waves<RB, DEPTH, BP_DT_F16, EPI>(waves);
-    case BP_DT_F32: return int4_mf_waves<RB, DEPTH, BP_DT_F32, EPI>(waves);
+    case BP_DT_BF16: return int4_mf_waves<RB, DEPTH, BP_DT_BF16, EPI, PRO>(waves);
+    case BP_DT_F16:
+      if constexpr (!PRO) return int4_mf_waves<RB, DEPTH, BP_DT_F16, EPI, false>(waves);
+      return nullptr;
+    case BP_DT_F32:
+      if constexpr (!PRO) return int4_mf_waves<RB, DEPTH, BP_DT_F32, EPI, false>(waves);
+      return nullptr;
     default: return nullptr;
   }
 }
 
-template <int EPI>
-Int4Fn int4_mf_tile(int tile_rows, int waves, int scale_dt) {
+template <int EPI, bool PRO>
+Int4MfFn int4_mf_tile(int tile_rows, int waves, int scale_dt) {
   switch (tile_rows) {
-    case 16: return int4_mf_dtype<1, 4, EPI>(waves, scale_dt);
-    case 32: return int4_mf_dtype<2, 3, EPI>(waves, scale_dt);
-    case 64: return int4_mf_dtype<4, 2, EPI>(waves, scale_dt);
+    case 16: return int4_mf_dtype<1, 4, EPI, PRO>(waves, scale_dt);
+    case 32: return int4_mf_dtype<2, 3, EPI, PRO>(waves, scale_dt);
+    case 64: return int4_mf_dtype<4, 2, EPI, PRO>(waves, scale_dt);
     default: return nullptr;
   }
 }
@@ -438,10 +501,14 @@ Int4Fn int4_rows(int rb, int waves) {
 
 }  // namespace
 
-// Matrix-core kernel for (tile rows, waves, scale dtype, epilogue: 0 the product, 1 the gate|up SiLU product), or
-// null; groups in flight per wave: 4 at 16 tile rows, 3 at 32, 2 at 64.
-Int4Fn int4_mf_pick(int tile_rows, int waves, int scale_dt, int epi) {
-  return epi == 0 ? int4_mf_tile<0>(tile_rows, waves, scale_dt) : int4_mf_tile<1>(tile_rows, waves, scale_dt);
+// Matrix-core kernel for (tile rows, waves, scale dtype, epilogue: 0 the product, 1 the gate|up SiLU product,
+// prologue), or null; groups in flight per wave: 4 at 16 tile rows, 3 at 32, 2 at 64.
+Int4MfFn int4_mf_pick(int tile_rows, int waves, int scale_dt, int epi, bool pro) {
+  if (pro)
+    return epi == 0 ? int4_mf_tile<0, true>(tile_rows, waves, scale_dt)
+                    : int4_mf_tile<1, true>(tile_rows, waves, scale_dt);
+  return epi == 0 ? int4_mf_tile<0, false>(tile_rows, waves, scale_dt)
+                  : int4_mf_tile<1, false>(tile_rows, waves, scale_dt);
 }
 
 // Kernel for (activation-row bucket, tile rows, waves), or null.

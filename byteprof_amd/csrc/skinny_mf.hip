@@ -45,13 +45,6 @@ int mf_row_groups(int xstage) {
 
 int mf_blocks(int64_t M) { return M <= 8 ? 1 : M <= 16 ? 2 : M <= 32 ? 4 : 8; }
 
-// Whether the byte ranges [a, a + na) and [b, b + nb) intersect (a null pointer is an empty range).
-bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
-  if (a == nullptr || b == nullptr || na <= 0 || nb <= 0) return false;
-  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
-  return pa < pb + static_cast<uintptr_t>(nb) && pb < pa + static_cast<uintptr_t>(na);
-}
-
 int mf_status() {
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? BP_OK : static_cast<int>(e);
@@ -143,8 +136,8 @@ int mf_launch(int wkind, const void* x, const void* w, const void* scale, int sc
     if (prologue->gamma2 != nullptr && prologue->kind != BP_PRO_NORM) return BP_E_INVALID_ARG;
     // workgroup (0, 0) writes xout while the others still read x and the residual rows
     const int64_t rows_bytes = 2 * M * K;
-    if (overlaps(prologue->xout, rows_bytes, x, rows_bytes) ||
-        (prologue->kind == BP_PRO_NORM && overlaps(prologue->xout, rows_bytes, prologue->residual, rows_bytes)))
+    if (ranges_overlap(prologue->xout, rows_bytes, x, rows_bytes) ||
+        (prologue->kind == BP_PRO_NORM && ranges_overlap(prologue->xout, rows_bytes, prologue->residual, rows_bytes)))
       return BP_E_INVALID_ARG;
     if (!vec || split != 1 || M > 16 || mode == 1) return BP_E_UNSUPPORTED;
     xstage = 1;

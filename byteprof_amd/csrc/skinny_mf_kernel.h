@@ -50,9 +50,6 @@ using MfFn = void (*)(const uint16_t*, const uint8_t*, const void*, int, uint16_
 template <int NSEG>
 MfFn mf_pick_n(int wkind, int mb, int rb, int waves, bool vec, int epi, bool xl, bool pro, int wr);
 
-#ifdef BP_MF_INSTANTIATE
-namespace {
-
 // In place, row by row:
 //   BP_PRO_UNIT_RMS: x <- bf16(x * (1 / sqrt(mean(x^2)))) (an all-zero row is left as is);
 //   BP_PRO_NORM:     x <- bf16(residual + bf16(gamma * (x * (1 / sqrt(mean(x^2) + eps))))) (no residual: the plain
@@ -162,6 +159,9 @@ __device__ void mf_prologue(uint16_t* xs, int rows, int K, MfPro pro, bool write
   }
   __syncthreads();
 }
+
+#ifdef BP_MF_INSTANTIATE
+namespace {
 
 // EPI: 0 = y[m][n] (split 1) or fp32 partials ws[split][m][n]; 1 = the SiLU product of interleaved gate|up rows
 // (rows 2f / 2f + 1 the gate / up rows of output f): y[m][f] = bf16(bf16(silu(bf16(g))) * bf16(u)).

@@ -36,6 +36,7 @@ MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
 ROPE_ATTENTION_ROWS = 16  # most rows of one fused q/k-norm + RoPE + cache + attention launch
 VERIFY_ROWS = 16  # rows of the verify-pass buffers (allocated once per decoder, never reallocated)
 PRO_MAX_ROWS = {"bf16": 3, "int8": 1}  # most rows of a linear launch with the sublayer norm as its prologue
+INT4_PRO_MAX_K = 8192  # widest row the int4 kernel's norm prologue stages (with gamma, residual and gamma2: 64 KiB)
 PRO_LDS_BYTES = 80 * 1024  # the launch keeps gamma and the residual rows in LDS while the staged rows and they fit
 ARGMAX_ROW_WORDS, ARGMAX_ERROR_WORD = 132, 130  # u32 words of the argmax scratch per row; its error word
 
@@ -144,8 +145,9 @@ class OlmoDecoder:
         self.x, self.xn, self.attn, self.o, self.dn = z(1, H), z(1, H), z(1, H), z(1, H), z(1, H)
         self.h = z(1, H)  # the residual stream after the attention half of a layer (fused-norm step)
         # the sublayer norms run inside the next linear's launch when its plan keeps whole rows (split 1); the int4
-        # kernel has no prologue
-        self.fuse_norms = kind != "int4" and all(self._plan(n, H, 1)[2] == 1 for n in (3 * H, 2 * F, V))
+        # kernel's prologue stages the row, gamma, the residual row and gamma2 in LDS (K <= 8192, bf16 scales)
+        self.fuse_norms = all(self._plan(n, H, 1)[2] == 1 for n in (3 * H, 2 * F, V)) and (
+            kind != "int4" or (H <= INT4_PRO_MAX_K and self.lm_head[1].dtype == torch.bfloat16))
         self.qkv, self.gu, self.act, self.logits = z(1, 3 * H), z(1, 2 * F), z(1, F), z(1, V)
         # the argmax's partials, counter and error word: zeroed once, the counter left at zero by every launch
         self.argmax_scratch = z(-(-_lib.lib().bp_decode_argmax_scratch_bytes() // 4), dtype=torch.int32)
@@ -198,7 +200,8 @@ class OlmoDecoder:
         """out = linear(bf16(residual + bf16(gamma * rmsnorm(x)))) in one launch (with gamma2: linear of the
         gamma2-norm of that); xout receives the normalised rows (the new residual stream)."""
         S.prologue_mm(x, args[0], args[1] if len(args) > 1 else None, out, S.PRO_NORM, gamma=gamma,
-                      residual=residual, xout=xout, eps=self.cfg.eps, silu=silu, gamma2=gamma2)
+                      residual=residual, xout=xout, eps=self.cfg.eps, silu=silu, gamma2=gamma2,
+                      zero=args[2] if len(args) > 2 else None)
 
     def _step_separate(self) -> None:
         """The step with a norm launch after o and after down (plans that split K)."""

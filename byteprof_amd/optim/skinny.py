@@ -213,16 +213,26 @@ PRO_UNIT_RMS, PRO_NORM = 1, 2  # BP_PRO_UNIT_RMS, BP_PRO_NORM
 def prologue_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None, out: torch.Tensor, pro: int,
                 gamma: torch.Tensor | None = None, residual: torch.Tensor | None = None,
                 xout: torch.Tensor | None = None, eps: float = 0.0, silu: bool = False, cfg=None,
-                gamma2: torch.Tensor | None = None) -> None:
-    """out = (transform of x) . W^T in one launch (bp_skinny_mf_pro): pro PRO_UNIT_RMS renormalises each row of x
-    to unit RMS, PRO_NORM takes bf16(residual + bf16(gamma * rmsnorm(x))) (the decode norm kernel's arithmetic),
-    then with gamma2 the plain norm of that with weight gamma2; xout, when given, receives the rows before the
-    second norm. silu: w is the interleaved gate|up weight [2 F, K] and out [M,
-    F] the SiLU product. The shape's plan must have split 1 (rows x K of x are staged in LDS; M <= 16)."""
+                gamma2: torch.Tensor | None = None, zero: torch.Tensor | None = None) -> None:
+    """out = (transform of x) . W^T in one launch (bp_skinny_mf_pro; int4 weights with zero: bp_skinny_int4_pro):
+    pro PRO_UNIT_RMS renormalises each row of x to unit RMS, PRO_NORM takes bf16(residual + bf16(gamma *
+    rmsnorm(x))) (the decode norm kernel's arithmetic), then with gamma2 the plain norm of that with weight gamma2;
+    xout, when given, receives the rows before the second norm. silu: w is the interleaved gate|up weight [2 F, K]
+    and out [M, F] the SiLU product. The shape's plan must have split 1 (rows x K of x are staged in LDS; M <= 16;
+    int4: M 1, K <= 8192, bf16 scales)."""
     m, k = x.shape
-    n = w.shape[0] // (2 if silu else 1)
-    kind = "bf16" if scale is None else "int8"
-    rb, waves, split, _ = _resolve(kind, w.shape[0], k, m, cfg, pro=True)
+    if w.dtype == torch.uint8:
+        kind = "int4"
+        if zero is None or scale is None:
+            raise ValueError("int4 weights need scale and zero")
+        tile = int(w.shape[2])
+        n = scale.shape[1] // (2 if silu else 1)
+        waves, split = int4_cfg(scale.shape[1], k, tile, cfg)
+        split = min(split, k // GROUP)
+    else:
+        n = w.shape[0] // (2 if silu else 1)
+        kind = "bf16" if scale is None else "int8"
+        rb, waves, split, _ = _resolve(kind, w.shape[0], k, m, cfg, pro=True)
     if split != 1:
         raise ValueError(f"a prologue needs whole rows per workgroup: the {w.shape[0]}x{k} plan splits K {split} ways")
     for t in (x, w, out, gamma, residual, xout, gamma2):
@@ -237,6 +247,11 @@ def prologue_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None, ou
     p = BpPrologue(pro, eps, _lib.ptr(gamma), _lib.ptr(residual), _lib.ptr(xout), _lib.ptr(gamma2))
     sc, sdt = (scale.data_ptr(), _lib.TORCH_DT[scale.dtype]) if scale is not None else (None, 0)
     L = _lib.lib()
+    if kind == "int4":
+        rc = L.bp_skinny_int4_pro(x.data_ptr(), w.data_ptr(), sc, sdt, zero.data_ptr(), out.data_ptr(), m, n, k, tile,
+                                  waves, int(silu), ctypes.byref(p), _lib.stream_ptr(x.device))
+        _lib.check(rc, "bp_skinny_int4_pro")
+        return
     rc = L.bp_skinny_mf_pro(_KIND_CODE[kind], x.data_ptr(), w.data_ptr(), sc, sdt, out.data_ptr(), m, n, k, rb, waves,
                             int(silu), ctypes.byref(p), _lib.stream_ptr(x.device))
     _lib.check(rc, "bp_skinny_mf_pro")

@@ -410,11 +410,18 @@ def test_graph_loop_equals_the_eager_loop_olmo2_1b(kind):
 
 
 def test_int4_decoder_steps_one_token_and_refuses_verify_passes():
-    """The int4 decoder: separate norm launches (the int4 kernel has no prologue), the SiLU product in the gate|up
-    launch where it keeps whole rows, counted by launches_per_step; a drafting verify pass is refused."""
+    """The int4 decoder: the sublayer norms inside the next linears (bp_skinny_int4_pro) where every plan keeps whole
+    rows, else separate norm launches with the SiLU product in the gate|up launch where it keeps whole rows; both
+    counted by launches_per_step; a drafting verify pass is refused."""
     dec, _, _ = _small_decoder("int4")
-    assert not dec.fuse_norms
     cfg = SMALL
+    H, F = cfg.hidden, cfg.ffn
+    whole = all(dec._plan(n, H, 1)[2] == 1 for n in (3 * H, 2 * F, cfg.vocab))
+    assert dec.fuse_norms == whole
+    if whole:
+        assert dec.launches_per_step == 3 + (5 + sum(int(dec._plan(n, k, 1)[2] > 1) for n, k in
+                                                     ((H, H), (H, F)))) * cfg.layers
+    dec.fuse_norms = False
     per_layer = 7 + sum(int(dec._plan(n, k, 1)[2] > 1) for n, k in
                         ((3 * cfg.hidden, cfg.hidden), (cfg.hidden, cfg.hidden), (cfg.hidden, cfg.ffn))) + \
         2 * int(dec._plan(2 * cfg.ffn, cfg.hidden, 1)[2] > 1)
@@ -423,7 +430,7 @@ def test_int4_decoder_steps_one_token_and_refuses_verify_passes():
         dec.verify_buffers(9)
 
 
-@pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
 def test_fused_norm_step_equals_the_separate_norm_step(kind):
     """The step with the sublayer norms inside the next linears (83 launches; the last two norms inside the LM
     head's) gives the logits and tokens of the step with separate norm launches (116 launches), bit for bit, step

@@ -201,3 +201,93 @@ def test_prologue_refusals():
     assert call(ctypes.byref(S.BpPrologue(1, 0.0, None, None, None, g.data_ptr()))) == -1  # gamma2 without a norm
     assert call(ctypes.byref(S.BpPrologue(2, 1e-6, g.data_ptr(), None, None, g.data_ptr() + 2))) == -1  # unaligned
     torch.cuda.synchronize()
+
+
+def _int4_pro(x, args, out, tile, waves, silu, kind, gamma=None, res=None, xout=None, gamma2=None, eps=1e-6):
+    packed, scale, zero = args
+    p = S.BpPrologue(kind, eps, _lib.ptr(gamma), _lib.ptr(res), _lib.ptr(xout), _lib.ptr(gamma2))
+    m, k = x.shape
+    return _lib.lib().bp_skinny_int4_pro(x.data_ptr(), packed.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype],
+                                         zero.data_ptr(), out.data_ptr(), m, out.shape[1], k, tile, waves, int(silu),
+                                         __import__("ctypes").byref(p), _lib.stream_ptr(x.device))
+
+
+def _int4_plain(x, args, n, tile, waves, silu):
+    """bp_skinny_int4 (split 1), then bp_decode_silu_mul_rows for the gate|up product."""
+    L = _lib.lib()
+    packed, scale, zero = args
+    m, k = x.shape
+    y = torch.empty(m, 2 * n if silu else n, dtype=torch.bfloat16, device=DEV)
+    _lib.check(L.bp_skinny_int4(x.data_ptr(), packed.data_ptr(), scale.data_ptr(), _lib.TORCH_DT[scale.dtype],
+                                zero.data_ptr(), y.data_ptr(), m, y.shape[1], k, tile, waves, 1, None, 0,
+                                _lib.stream_ptr(x.device)), "bp_skinny_int4")
+    if not silu:
+        return y
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    _lib.check(L.bp_decode_silu_mul_rows(y.data_ptr(), out.data_ptr(), n, m, 1, _lib.stream_ptr(x.device)), "silu")
+    return out
+
+
+@pytest.mark.parametrize("tile", [16, 32, 64])
+@pytest.mark.parametrize("k", [2048, 384, 8192])
+def test_int4_norm_prologue_equals_norm_launch_then_int4(tile, k):
+    """bp_skinny_int4_pro (one row): the row, gamma, the residual row and gamma2 staged in LDS, then the int4 matrix-
+    core kernel; equal bit for bit to the norm launch(es) followed by bp_skinny_int4 at the same tile rows and waves
+    (with the SiLU epilogue: then bp_decode_silu_mul_rows), with and without the residual and gamma2; K 384 leaves
+    a partial 512-element staging chunk, K 8192 fills the 64 KiB; xout receives the rows before the second norm."""
+    g = _gen(60 + tile + k)
+    n, eps = 1000, 1e-6
+    w = (torch.randn(2 * n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    args = S.quantize_int4(w, tile)
+    x = (torch.randn(1, k, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
+    gamma = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    gamma2 = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    res = torch.randn(1, k, generator=g, device=DEV).to(torch.bfloat16)
+    print(f"\n[int4 pro] tile={tile} k={k}", flush=True)
+    for r, g2 in ((res, None), (None, None), (res, gamma2), (None, gamma2)):
+        xn = _norm_rows(x, gamma, r, eps)
+        xm = _norm_rows(xn, g2, None, eps) if g2 is not None else xn
+        for silu in (False, True):
+            nn = n if silu else 2 * n
+            for waves in (1, 4):
+                want = _int4_plain(xm, args, nn, tile, waves, silu)
+                out = torch.full((1, nn), float("nan"), dtype=torch.bfloat16, device=DEV)
+                xout = torch.empty(1, k, dtype=torch.bfloat16, device=DEV)
+                _lib.check(_int4_pro(x, args, out, tile, waves, silu, S.PRO_NORM, gamma, r, xout, g2, eps),
+                           "bp_skinny_int4_pro")
+                torch.cuda.synchronize()
+                assert torch.equal(xout, xn), (r is None, g2 is None, silu, waves)
+                assert torch.equal(out, want), (r is None, g2 is None, silu, waves)
+
+
+def test_int4_unit_rms_prologue_and_refusals():
+    """BP_PRO_UNIT_RMS with int4 weights: xout within one bf16 rounding of x / rms(x) (float64), the product equal
+    to bp_skinny_int4 of xout bit for bit; two rows, fp16 scales, K past 8192, split plans and an xout overlapping
+    x are refused before anything runs."""
+    g = _gen(77)
+    n, k = 2048, 2048
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    args = S.quantize_int4(w, 32)
+    x = (torch.randn(1, k, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
+    out = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    xout = torch.empty(1, k, dtype=torch.bfloat16, device=DEV)
+    _lib.check(_int4_pro(x, args, out, 32, 4, False, S.PRO_UNIT_RMS, xout=xout), "bp_skinny_int4_pro")
+    torch.cuda.synchronize()
+    xd = x.double()
+    want_rows = xd / xd.pow(2).mean().sqrt()
+    assert ((xout.double() - want_rows).abs() <= want_rows.abs() * 2.0 ** -8 + 1e-30).all()
+    assert torch.equal(out, _int4_plain(xout, args, n, 32, 4, False))
+    gamma = torch.ones(k, dtype=torch.bfloat16, device=DEV)
+    x2 = torch.zeros(2, k, dtype=torch.bfloat16, device=DEV)
+    assert _int4_pro(x2, args, torch.empty(2, n, dtype=torch.bfloat16, device=DEV), 32, 4, False, S.PRO_NORM,
+                     gamma) == _lib.BP_E_UNSUPPORTED
+    a16 = (args[0], args[1].to(torch.float16), args[2])
+    assert _int4_pro(x, a16, out, 32, 4, False, S.PRO_NORM, gamma) == _lib.BP_E_UNSUPPORTED
+    wk = (torch.randn(256, 8320, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    xk = torch.zeros(1, 8320, dtype=torch.bfloat16, device=DEV)
+    gk = torch.ones(8320, dtype=torch.bfloat16, device=DEV)
+    assert _int4_pro(xk, S.quantize_int4(wk, 16), torch.empty(1, 256, dtype=torch.bfloat16, device=DEV), 16, 4,
+                     False, S.PRO_NORM, gk) == _lib.BP_E_UNSUPPORTED
+    big = torch.zeros(2, k, dtype=torch.bfloat16, device=DEV)
+    assert _int4_pro(big[:1], args, out, 32, 4, False, S.PRO_NORM, gamma, xout=big[:1]) == _lib.BP_E_INVALID_ARG
+    torch.cuda.synchronize()
