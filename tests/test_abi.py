@@ -156,6 +156,29 @@ def test_prologue_refuses_an_xout_overlapping_its_inputs(L):
         assert pro(_prologue(residual=res, xout=xout)) == -1, hex(xout)
 
 
+def test_int4_prologue_refusals_before_any_launch(L):
+    """bp_skinny_int4_pro checks its arguments before any HIP call (the pointers are never used): no prologue, an
+    unknown kind or epilogue, NORM without gamma, unaligned norm operands, gamma2 with the unit-RMS kind and an xout
+    overlapping x or the residual row are invalid; two rows, K past 8192 and K not a multiple of 128 are refused."""
+    x, pk, sc, z, y, res = 0x200000, 0x400000, 0x600000, 0x800000, 0xa00000, 0xc00000
+    n, k = 64, 2048
+    call = lambda pr, m=1, k_=k, epi=0: L.bp_skinny_int4_pro(  # noqa: E731
+        x, pk, sc, 0, z, y, m, n, k_, 16, 4, epi, None if pr is None else ctypes.byref(pr), None)
+    assert call(None) == -1
+    assert call(_prologue(), epi=2) == -1
+    assert call(_prologue(kind=7)) == -1
+    assert call(_prologue(gamma=None)) == -1
+    assert call(_prologue(gamma=0x100008)) == -1
+    assert call(_prologue(residual=res + 8)) == -1
+    assert call(_prologue(kind=1, gamma=None, gamma2=0x100000)) == -1
+    for xout in (x, x + 2 * k - 16, res):
+        assert call(_prologue(residual=res, xout=xout)) == -1, hex(xout)
+    assert call(_prologue(), m=2) == -2
+    assert call(_prologue(), k_=8320) == -2
+    assert call(_prologue(), k_=2000) == -1
+    assert call(_prologue(), m=0) == 0  # nothing to do
+
+
 def test_prologue_mm_refuses_an_overlapping_xout_on_the_host():
     import torch
 
