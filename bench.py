@@ -403,8 +403,7 @@ def decode_loop(device, new_tokens: int = 128) -> dict:
     """The graph-captured greedy decode loop (byteprof_amd/optim/olmo.py) on the OLMo-2-1B shape with synthetic
     weights: per kind, the GPU time of one captured decode step (replays timed with events), the loop's time per
     token (two-step graph replays kept one ahead of the host; a generate of 1 + N tokens minus one of 1, over N) and the
-    eager loop's, with the weight bytes a step streams; the drafting rounds for bf16 and int8 (the int4 decoder steps
-    one token at a time)."""
+    eager loop's, with the weight bytes a step streams; the drafting rounds of each."""
     import torch
 
     from byteprof_amd.optim import olmo as OG
@@ -459,8 +458,7 @@ def decode_loop(device, new_tokens: int = 128) -> dict:
                      "tokens_per_s_loop": 1e6 / loop_us}
         if kind == "int4":
             out[kind]["launches_per_step"] = dec.launches_per_step
-        else:
-            out[kind]["draft"] = draft_figures(dec, prompt, ref, new_tokens)
+        out[kind]["draft"] = draft_figures(dec, prompt, ref, new_tokens)
         del dec, graph, eager, g
         torch.cuda.empty_cache()
     return out

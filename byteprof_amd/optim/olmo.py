@@ -13,10 +13,11 @@ followed by the new tokens, [1, L + n].
 
 The model is the OLMo-2 architecture with synthetic weights (the checkpoint is not available here): an
 `OlmoDecoder` holds the weights of transformers' Olmo2ForCausalLM layout with q|k|v and gate|up fused into one
-linear each (one launch instead of three or two; the outputs are the same rows), bf16 or int8 (per-row scales).
-The gate and up rows are interleaved (row 2n gate n, row 2n + 1 up n) so that one launch computes the projection
-and the SiLU product (bp_skinny_mf_silu). Every linear runs on the skinny matrix-core kernel, whose rows do not
-depend on how many rows share a launch: a verify pass of s rows computes each row exactly as the one-token step.
+linear each (one launch instead of three or two; the outputs are the same rows), bf16, int8 (per-row scales) or
+int4 (group-128 codes). The gate and up rows are interleaved (row 2n gate n, row 2n + 1 up n) so that one launch
+computes the projection and the SiLU product (bp_skinny_mf_silu, bp_skinny_int4_silu). Every linear runs on a
+matrix-core kernel whose rows do not depend on how many rows share a launch: a verify pass of s rows computes each
+row exactly as the one-token step.
 The prompt is fed one position at a time through the same step (the reference prefills with one batched
 forward; the cache contents and the first new token are the same up to rounding).
 """
@@ -35,7 +36,7 @@ from . import skinny as S
 MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
 ROPE_ATTENTION_ROWS = 16  # most rows of one fused q/k-norm + RoPE + cache + attention launch
 VERIFY_ROWS = 16  # rows of the verify-pass buffers (allocated once per decoder, never reallocated)
-PRO_MAX_ROWS = {"bf16": 3, "int8": 1}  # most rows of a linear launch with the sublayer norm as its prologue
+PRO_MAX_ROWS = {"bf16": 3, "int8": 1, "int4": 1}  # most rows of a linear launch with the norm as its prologue
 INT4_PRO_MAX_K = 8192  # widest row the int4 kernel's norm prologue stages (with gamma, residual and gamma2: 64 KiB)
 PRO_LDS_BYTES = 80 * 1024  # the launch keeps gamma and the residual rows in LDS while the staged rows and they fit
 ARGMAX_ROW_WORDS, ARGMAX_ERROR_WORD = 132, 130  # u32 words of the argmax scratch per row; its error word
@@ -277,6 +278,8 @@ class OlmoDecoder:
     def _down_splitk(self, s: int) -> tuple[int, int, int, int] | None:
         """The down projection's plan at s rows when it is split-K (its partials then feed the norm's launch)."""
         H, F = self.cfg.hidden, self.cfg.ffn
+        if self.kind == "int4":  # no partials entry for int4 weights: skinny_mm reduces, a norm launch follows
+            return None
         plan = self._plan(H, F, s)
         return plan if plan[2] > 1 and H <= 8192 else None
 
@@ -287,8 +290,6 @@ class OlmoDecoder:
         out [VERIFY_ROWS + 1] receives the row tokens and, at VERIFY_ROWS (= self.smax), the accepted length."""
         if not 1 <= smax <= VERIFY_ROWS:
             raise ValueError(f"verify passes take 1..{VERIFY_ROWS} rows, asked for {smax}")
-        if self.kind == "int4":
-            raise OptimizeError("drafting verify passes take bf16 or int8 weights (the int4 decoder steps one token)")
         if getattr(self, "smax", 0):
             return
         cfg, dev = self.cfg, self.device
@@ -316,6 +317,8 @@ class OlmoDecoder:
         _, _, split, _ = self._plan(n, k, rows)
         if split != 1 or rows > PRO_MAX_ROWS[self.kind]:
             return False
+        if self.kind == "int4":  # the int4 kernel's one-row prologue (row, gamma, residual, gamma2 in LDS)
+            return k <= INT4_PRO_MAX_K and self.lm_head[1].dtype == torch.bfloat16
         st = S._stage_bytes(self.kind, rows, k, 1)
         return st >= 0 and (rows == 1 or st + 2 * k * (norms + rows) <= PRO_LDS_BYTES)
 
@@ -326,8 +329,8 @@ class OlmoDecoder:
         length L (drafts ids[1 + j] equal to the prediction of row j) and the next round's inputs: ids[0] <- the
         token after the accepted prefix, pos += L + 1. Every row is computed as the one-token step at its position
         computes it (the linears' rows do not depend on the row count). Each sublayer norm runs inside the next
-        linear's launch where _pro_fits allows (up to 3 bf16 rows / one int8 row), else as its own launch (the
-        same bits either way); the residual stream alternates between vx and vh where a prologue writes it."""
+        linear's launch where _pro_fits allows (up to 3 bf16 rows / one int8 or int4 row), else as its own launch
+        (the same bits either way); the residual stream alternates between vx and vh where a prologue writes it."""
         if not 1 <= s <= getattr(self, "smax", 0):
             raise ValueError(f"s must be in 1..{getattr(self, 'smax', 0)} (verify_buffers)")
         cfg, L = self.cfg, _lib.lib()

@@ -309,7 +309,7 @@ def test_verify_next_accepts_the_matching_prefix_and_advances():
         assert int(pos) == 100 + want_len + 1
 
 
-@pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
 def test_verify_rows_match_the_oracle(kind):
     """A verify pass of s rows, teacher-forced after a 5-token prompt: row r's logits against the oracle's decode
     step at that position (within the decode gate), for s = 1 .. 9, and the round's end (accepted length, next
@@ -346,7 +346,7 @@ def _greedy_reference(dec, prompt, n):
     return graph(prompt, max_new_tokens=n)
 
 
-@pytest.mark.parametrize("kind", ["bf16", "int8"])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
 def test_draft_loop_reproduces_the_graph_loop_olmo2_1b(kind):
     cfg = OG.OLMO2_1B
     print(f"\n[draft] 1B {kind}", flush=True)

@@ -409,10 +409,10 @@ def test_graph_loop_equals_the_eager_loop_olmo2_1b(kind):
     torch.cuda.empty_cache()
 
 
-def test_int4_decoder_steps_one_token_and_refuses_verify_passes():
+def test_int4_decoder_launch_counts():
     """The int4 decoder: the sublayer norms inside the next linears (bp_skinny_int4_pro) where every plan keeps whole
     rows, else separate norm launches with the SiLU product in the gate|up launch where it keeps whole rows; both
-    counted by launches_per_step; a drafting verify pass is refused."""
+    counted by launches_per_step."""
     dec, _, _ = _small_decoder("int4")
     cfg = SMALL
     H, F = cfg.hidden, cfg.ffn
@@ -426,8 +426,6 @@ def test_int4_decoder_steps_one_token_and_refuses_verify_passes():
                         ((3 * cfg.hidden, cfg.hidden), (cfg.hidden, cfg.hidden), (cfg.hidden, cfg.ffn))) + \
         2 * int(dec._plan(2 * cfg.ffn, cfg.hidden, 1)[2] > 1)
     assert dec.launches_per_step == 4 + per_layer * cfg.layers + int(dec._plan(cfg.vocab, cfg.hidden, 1)[2] > 1)
-    with pytest.raises(OG.OptimizeError):
-        dec.verify_buffers(9)
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
