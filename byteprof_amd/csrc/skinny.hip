@@ -52,11 +52,14 @@ int grid_for(int64_t count) {
   return static_cast<int>(b < 2048 ? (b < 1 ? 1 : b) : 2048);
 }
 
-constexpr int64_t kInt4ProMaxK = 8192;  // the prologue's LDS: the row, gamma, the residual row and gamma2 (64 KiB)
+// the prologue's LDS: the rows, gamma, the residual rows and gamma2, (2 M + 2) K bf16 within 64 KiB (K <= 8192 at
+// one row, 2048 at up to 7); the per-row sums of squares hold up to 8 rows
+constexpr int64_t kInt4ProLdsBytes = 64 * 1024;
+constexpr int64_t kInt4ProMaxRows = 8;
 
 // epi 0: y [M, N] (split > 1: partials then the reduce); 1: the gate|up SiLU product y [M, N / 2] of interleaved
-// rows (split 1, the matrix-core kernel only). prologue (kind != 0): a transform of the one activation row first
-// (split 1, the matrix-core kernel, bf16 scales, K <= 8192), as bp_skinny_mf_pro's.
+// rows (split 1, the matrix-core kernel only). prologue (kind != 0): a transform of the activation rows first
+// (split 1, the matrix-core kernel, bf16 scales, M <= 8 and (2 M + 2) K x 2 bytes <= 64 KiB), as bp_skinny_mf_pro's.
 int skinny_int4_launch(const void* x, const void* packed, const void* scale, int scale_dt, const void* zero, void* y,
                        int64_t M, int64_t N, int64_t K, int tile_rows, int waves, int split, void* ws,
                        size_t ws_bytes, void* stream, int epi = 0, const BpPrologue* prologue = nullptr) {
@@ -76,7 +79,7 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
     if (ranges_overlap(prologue->xout, rows_bytes, x, rows_bytes) ||
         (prologue->kind == BP_PRO_NORM && ranges_overlap(prologue->xout, rows_bytes, prologue->residual, rows_bytes)))
       return BP_E_INVALID_ARG;
-    if (M > 1 || split != 1 || K > kInt4ProMaxK) return BP_E_UNSUPPORTED;
+    if (M > kInt4ProMaxRows || split != 1 || (2 * M + 2) * K * 2 > kInt4ProLdsBytes) return BP_E_UNSUPPORTED;
     pro = MfPro{prologue->kind, prologue->eps, static_cast<const uint16_t*>(prologue->gamma),
                 static_cast<const uint16_t*>(prologue->residual), static_cast<uint16_t*>(prologue->xout), 1,
                 static_cast<const uint16_t*>(prologue->gamma2), nullptr};
@@ -114,7 +117,7 @@ int skinny_int4_launch(const void* x, const void* packed, const void* scale, int
   if (tiles > 0x7fffffff) return BP_E_INVALID_ARG;
   dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(split));
   if (mf_fn != nullptr) {
-    const size_t lds = pro.kind != 0 ? static_cast<size_t>(4 * K * 2) : 0;
+    const size_t lds = pro.kind != 0 ? static_cast<size_t>((2 * M + 2) * K * 2) : 0;
     mf_fn<<<grid, waves * kWave, lds, st>>>(static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(packed),
                                             scale, scale_dt, static_cast<const uint16_t*>(zero),
                                             static_cast<uint16_t*>(y), static_cast<float*>(ws), static_cast<int>(M),

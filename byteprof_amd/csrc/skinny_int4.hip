@@ -196,8 +196,8 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
 
 using u32x2 = unsigned __attribute__((ext_vector_type(2)));
 
-// PRO (one activation row, split 1): the row staged in LDS with gamma, the residual row and gamma2 (dynamic shared
-// memory, 4 K bf16), transformed by mf_prologue (the norm kernel's arithmetic: the product equals a norm launch
+// PRO (up to 8 activation rows, split 1): the rows staged in LDS with gamma, the residual rows and gamma2 (dynamic
+// shared memory, (2 M + 2) K bf16), transformed by mf_prologue (the norm kernel's arithmetic: the product equals a norm launch
 // followed by the plain kernel, bit for bit) while the first groups' weights are in flight; the B operands are then
 // read from LDS.
 template <int RB, int WAVES, int DEPTH, int SDT, int EPI = 0, bool PRO = false>
@@ -283,13 +283,15 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
     const u32x4* xv = sl.xv;
     u32x4 xl[4];
     if constexpr (PRO) {
-      // the transformed row from LDS (column 0; the other columns zeros, never stored)
-      const uint16_t* src = i4_xs + (first + static_cast<int64_t>(j) * WAVES) * 128 + kb * 16;
+      // the transformed rows from LDS (columns past M zeros, never stored)
+      const bool live = i < M;
+      const uint16_t* src =
+          i4_xs + (live ? i : 0) * K + (first + static_cast<int64_t>(j) * WAVES) * 128 + kb * 16;
       const u32x4 zv = u32x4{0u, 0u, 0u, 0u};
-      xl[0] = i == 0 ? *reinterpret_cast<const u32x4*>(src) : zv;
-      xl[1] = i == 0 ? *reinterpret_cast<const u32x4*>(src + 8) : zv;
-      xl[2] = i == 0 ? *reinterpret_cast<const u32x4*>(src + 64) : zv;
-      xl[3] = i == 0 ? *reinterpret_cast<const u32x4*>(src + 72) : zv;
+      xl[0] = live ? *reinterpret_cast<const u32x4*>(src) : zv;
+      xl[1] = live ? *reinterpret_cast<const u32x4*>(src + 8) : zv;
+      xl[2] = live ? *reinterpret_cast<const u32x4*>(src + 64) : zv;
+      xl[3] = live ? *reinterpret_cast<const u32x4*>(src + 72) : zv;
       xv = xl;
     }
     // the record through the wave's stage (the wave's LDS operations run in order: the previous group's reads are
@@ -351,22 +353,26 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
   // loads land in the registers the loop uses
   I4Slot<RB, kRecLoads> sl[DEPTH];
   if constexpr (PRO) {
-    // the row, gamma, the residual row and gamma2 straight into LDS (64 lanes x 16 bytes per load), ahead of the
+    // the rows, gamma, the residual rows and gamma2 straight into LDS (64 lanes x 16 bytes per load), ahead of the
     // first groups' weights; every wave takes part in the prologue's barriers, groups or not
     const int kn = static_cast<int>(K);
-    uint16_t* gl = i4_xs + kn;
-    uint16_t* dst2 = gl + (pro.residual != nullptr ? 2 : 1) * kn;
+    uint16_t* gl = i4_xs + M * kn;
+    uint16_t* dst2 = gl + (pro.residual != nullptr ? 1 + M : 1) * kn;
     for (int c = wave; c * 512 < kn; c += WAVES) {
       const int e = c * 512 + 8 * lane;
       if (e < kn) {
-        __builtin_amdgcn_global_load_lds(as_global(x + e), (__attribute__((address_space(3))) void*)(i4_xs + c * 512),
-                                         16, 0, 0);
+        for (int m = 0; m < M; ++m)
+          __builtin_amdgcn_global_load_lds(as_global(x + static_cast<int64_t>(m) * kn + e),
+                                           (__attribute__((address_space(3))) void*)(i4_xs + m * kn + c * 512), 16,
+                                           0, 0);
         if (pro.kind == BP_PRO_NORM) {
           __builtin_amdgcn_global_load_lds(as_global(pro.gamma + e),
                                            (__attribute__((address_space(3))) void*)(gl + c * 512), 16, 0, 0);
           if (pro.residual != nullptr)
-            __builtin_amdgcn_global_load_lds(as_global(pro.residual + e),
-                                             (__attribute__((address_space(3))) void*)(gl + kn + c * 512), 16, 0, 0);
+            for (int m = 0; m < M; ++m)
+              __builtin_amdgcn_global_load_lds(
+                  as_global(pro.residual + static_cast<int64_t>(m) * kn + e),
+                  (__attribute__((address_space(3))) void*)(gl + (1 + m) * kn + c * 512), 16, 0, 0);
           if (pro.gamma2 != nullptr)
             __builtin_amdgcn_global_load_lds(as_global(pro.gamma2 + e),
                                              (__attribute__((address_space(3))) void*)(dst2 + c * 512), 16, 0, 0);
@@ -382,7 +388,7 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_int4_mf_kernel(const uin
     }
     __builtin_amdgcn_s_waitcnt(0);  // the staged operands (and the first groups) have landed
     __syncthreads();
-    mf_prologue<WAVES * kWave>(i4_xs, 1, kn, pro, blockIdx.x == 0 && blockIdx.y == 0,
+    mf_prologue<WAVES * kWave>(i4_xs, M, kn, pro, blockIdx.x == 0 && blockIdx.y == 0,
                                pro.kind == BP_PRO_NORM ? gl : nullptr, pro_sums);
   } else if (cnt > 0) {
 #pragma unroll

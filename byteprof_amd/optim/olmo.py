@@ -37,7 +37,8 @@ MAX_CACHE_LEN = 1024  # the reference's static cache length (olmo.py:16)
 ROPE_ATTENTION_ROWS = 16  # most rows of one fused q/k-norm + RoPE + cache + attention launch
 VERIFY_ROWS = 16  # rows of the verify-pass buffers (allocated once per decoder, never reallocated)
 PRO_MAX_ROWS = {"bf16": 3, "int8": 1, "int4": 1}  # most rows of a linear launch with the norm as its prologue
-INT4_PRO_MAX_K = 8192  # widest row the int4 kernel's norm prologue stages (with gamma, residual and gamma2: 64 KiB)
+INT4_PRO_LDS_BYTES = 64 * 1024  # the int4 kernel's norm prologue: rows, gamma, residual rows, gamma2, (2 M + 2) K bf16
+INT4_PRO_MAX_K = INT4_PRO_LDS_BYTES // 8  # widest row it stages at one row
 PRO_LDS_BYTES = 80 * 1024  # the launch keeps gamma and the residual rows in LDS while the staged rows and they fit
 ARGMAX_ROW_WORDS, ARGMAX_ERROR_WORD = 132, 130  # u32 words of the argmax scratch per row; its error word
 
@@ -313,12 +314,13 @@ class OlmoDecoder:
         made 7-row verify rounds 870 -> 1206 us), and at most PRO_MAX_ROWS rows: measured on the OLMo-2-1B shape
         against the one-round-trip norm launch, the prologue wins at 1..3 rows for bf16 (2 / 3-row rounds 731 / 755
         -> 724 / 749 us; 5 rows loses, 791-808 -> 829 us) and at one row only for int8 (2 / 3 rows: 575 / 586-599
-        without it, 587-597 / 631-634 with it); at one row it saves the norm launch of every sublayer."""
+        without it, 587-597 / 631-634 with it) and for int4 (2 / 3 / 5 / 7 rows: 601 / 617 / 642 / 681 us without it,
+        619 / 654 / 746 / 867 with it); at one row it saves the norm launch of every sublayer."""
         _, _, split, _ = self._plan(n, k, rows)
         if split != 1 or rows > PRO_MAX_ROWS[self.kind]:
             return False
-        if self.kind == "int4":  # the int4 kernel's one-row prologue (row, gamma, residual, gamma2 in LDS)
-            return k <= INT4_PRO_MAX_K and self.lm_head[1].dtype == torch.bfloat16
+        if self.kind == "int4":  # the int4 kernel's prologue (rows, gamma, residual rows, gamma2 in LDS)
+            return (2 * rows + 2) * k * 2 <= INT4_PRO_LDS_BYTES and self.lm_head[1].dtype == torch.bfloat16
         st = S._stage_bytes(self.kind, rows, k, 1)
         return st >= 0 and (rows == 1 or st + 2 * k * (norms + rows) <= PRO_LDS_BYTES)
 

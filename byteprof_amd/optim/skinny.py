@@ -219,7 +219,7 @@ def prologue_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None, ou
     rmsnorm(x))) (the decode norm kernel's arithmetic), then with gamma2 the plain norm of that with weight gamma2;
     xout, when given, receives the rows before the second norm. silu: w is the interleaved gate|up weight [2 F, K]
     and out [M, F] the SiLU product. The shape's plan must have split 1 (rows x K of x are staged in LDS; M <= 16;
-    int4: M 1, K <= 8192, bf16 scales)."""
+    int4: M <= 8 and (2 M + 2) K bf16 within 64 KiB, bf16 scales)."""
     m, k = x.shape
     if w.dtype == torch.uint8:
         kind = "int4"

@@ -218,12 +218,12 @@ int bp_skinny_int4(const void* x, const void* packed, const void* scale, int sca
  *           that byteprof/optim/olmo.py:122-219 captures. */
 int bp_skinny_int4_silu(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero,
                         void* out, int64_t M, int64_t ffn, int64_t K, int tile_rows, int waves, void* stream);
-/* bp_skinny_int4 (epilogue 0: y [1, N]) or bp_skinny_int4_silu (epilogue 1: y [1, N] of an interleaved [2 N, K]
- * weight) with a prologue on the one activation row, as bp_skinny_mf_pro's: BP_PRO_NORM (residual add, xout, gamma,
+/* bp_skinny_int4 (epilogue 0: y [M, N]) or bp_skinny_int4_silu (epilogue 1: y [M, N] of an interleaved [2 N, K]
+ * weight) with a prologue on the activation rows, as bp_skinny_mf_pro's: BP_PRO_NORM (residual add, xout, gamma,
  * an optional gamma2) or BP_PRO_UNIT_RMS; equal bit for bit to bp_decode_norm_residual_rows (or its unit-RMS form)
- * followed by the plain launch with the same tile rows and waves. M 1, split 1, bf16 scales and K <= 8192 (the row,
- * gamma, the residual row and gamma2 staged in 64 KiB of LDS), else BP_E_UNSUPPORTED; xout may not overlap x or the
- * residual row (BP_E_INVALID_ARG).
+ * followed by the plain launch with the same tile rows and waves. M <= 8, split 1, bf16 scales and (2 M + 2) K x 2
+ * bytes <= 64 KiB (the rows, gamma, the residual rows and gamma2 staged in LDS: K <= 8192 at one row, 2048 at up to
+ * 7), else BP_E_UNSUPPORTED; xout may not overlap x or the residual rows (BP_E_INVALID_ARG).
  * Replaces: the RMSNorm / residual add before the next linear of HF Olmo2DecoderLayer (with int4_wo weights) in the
  *           decode step that byteprof/optim/olmo.py:122-219 captures. */
 int bp_skinny_int4_pro(const void* x, const void* packed, const void* scale, int scale_dtype, const void* zero, void* y,

@@ -159,7 +159,8 @@ def test_prologue_refuses_an_xout_overlapping_its_inputs(L):
 def test_int4_prologue_refusals_before_any_launch(L):
     """bp_skinny_int4_pro checks its arguments before any HIP call (the pointers are never used): no prologue, an
     unknown kind or epilogue, NORM without gamma, unaligned norm operands, gamma2 with the unit-RMS kind and an xout
-    overlapping x or the residual row are invalid; two rows, K past 8192 and K not a multiple of 128 are refused."""
+    overlapping x or the residual row are invalid; nine rows, rows whose staging passes 64 KiB of LDS and K not a
+    multiple of 128 are refused."""
     x, pk, sc, z, y, res = 0x200000, 0x400000, 0x600000, 0x800000, 0xa00000, 0xc00000
     n, k = 64, 2048
     call = lambda pr, m=1, k_=k, epi=0: L.bp_skinny_int4_pro(  # noqa: E731
@@ -173,7 +174,9 @@ def test_int4_prologue_refusals_before_any_launch(L):
     assert call(_prologue(kind=1, gamma=None, gamma2=0x100000)) == -1
     for xout in (x, x + 2 * k - 16, res):
         assert call(_prologue(residual=res, xout=xout)) == -1, hex(xout)
-    assert call(_prologue(), m=2) == -2
+    assert call(_prologue(), m=9) == -2
+    assert call(_prologue(), m=2, k_=8192) == -2  # (2 M + 2) K bf16 past 64 KiB
+    assert call(_prologue(), m=7, k_=2176) == -2
     assert call(_prologue(), k_=8320) == -2
     assert call(_prologue(), k_=2000) == -1
     assert call(_prologue(), m=0) == 0  # nothing to do

@@ -229,21 +229,22 @@ def _int4_plain(x, args, n, tile, waves, silu):
 
 
 @pytest.mark.parametrize("tile", [16, 32, 64])
-@pytest.mark.parametrize("k", [2048, 384, 8192])
-def test_int4_norm_prologue_equals_norm_launch_then_int4(tile, k):
-    """bp_skinny_int4_pro (one row): the row, gamma, the residual row and gamma2 staged in LDS, then the int4 matrix-
-    core kernel; equal bit for bit to the norm launch(es) followed by bp_skinny_int4 at the same tile rows and waves
-    (with the SiLU epilogue: then bp_decode_silu_mul_rows), with and without the residual and gamma2; K 384 leaves
-    a partial 512-element staging chunk, K 8192 fills the 64 KiB; xout receives the rows before the second norm."""
-    g = _gen(60 + tile + k)
+@pytest.mark.parametrize("k,m", [(2048, 1), (384, 1), (8192, 1), (2048, 3), (2048, 7), (384, 8)])
+def test_int4_norm_prologue_equals_norm_launch_then_int4(tile, k, m):
+    """bp_skinny_int4_pro: the rows, gamma, the residual rows and gamma2 staged in LDS, then the int4 matrix-core
+    kernel; equal bit for bit to the norm launch(es) followed by bp_skinny_int4 at the same tile rows and waves (with
+    the SiLU epilogue: then bp_decode_silu_mul_rows), with and without the residual and gamma2; K 384 leaves a
+    partial 512-element staging chunk, K 8192 at one row and 2048 at seven rows fill the 64 KiB; xout receives the
+    rows before the second norm."""
+    g = _gen(60 + tile + k + m)
     n, eps = 1000, 1e-6
     w = (torch.randn(2 * n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
     args = S.quantize_int4(w, tile)
-    x = (torch.randn(1, k, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
+    x = (torch.randn(m, k, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
     gamma = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
     gamma2 = (1.0 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
-    res = torch.randn(1, k, generator=g, device=DEV).to(torch.bfloat16)
-    print(f"\n[int4 pro] tile={tile} k={k}", flush=True)
+    res = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    print(f"\n[int4 pro] tile={tile} k={k} m={m}", flush=True)
     for r, g2 in ((res, None), (None, None), (res, gamma2), (None, gamma2)):
         xn = _norm_rows(x, gamma, r, eps)
         xm = _norm_rows(xn, g2, None, eps) if g2 is not None else xn
@@ -251,8 +252,8 @@ def test_int4_norm_prologue_equals_norm_launch_then_int4(tile, k):
             nn = n if silu else 2 * n
             for waves in (1, 4):
                 want = _int4_plain(xm, args, nn, tile, waves, silu)
-                out = torch.full((1, nn), float("nan"), dtype=torch.bfloat16, device=DEV)
-                xout = torch.empty(1, k, dtype=torch.bfloat16, device=DEV)
+                out = torch.full((m, nn), float("nan"), dtype=torch.bfloat16, device=DEV)
+                xout = torch.empty(m, k, dtype=torch.bfloat16, device=DEV)
                 _lib.check(_int4_pro(x, args, out, tile, waves, silu, S.PRO_NORM, gamma, r, xout, g2, eps),
                            "bp_skinny_int4_pro")
                 torch.cuda.synchronize()
@@ -262,8 +263,8 @@ def test_int4_norm_prologue_equals_norm_launch_then_int4(tile, k):
 
 def test_int4_unit_rms_prologue_and_refusals():
     """BP_PRO_UNIT_RMS with int4 weights: xout within one bf16 rounding of x / rms(x) (float64), the product equal
-    to bp_skinny_int4 of xout bit for bit; two rows, fp16 scales, K past 8192, split plans and an xout overlapping
-    x are refused before anything runs."""
+    to bp_skinny_int4 of xout bit for bit; nine rows, fp16 scales, staging past 64 KiB of LDS and an xout
+    overlapping x are refused before anything runs."""
     g = _gen(77)
     n, k = 2048, 2048
     w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
@@ -278,8 +279,8 @@ def test_int4_unit_rms_prologue_and_refusals():
     assert ((xout.double() - want_rows).abs() <= want_rows.abs() * 2.0 ** -8 + 1e-30).all()
     assert torch.equal(out, _int4_plain(xout, args, n, 32, 4, False))
     gamma = torch.ones(k, dtype=torch.bfloat16, device=DEV)
-    x2 = torch.zeros(2, k, dtype=torch.bfloat16, device=DEV)
-    assert _int4_pro(x2, args, torch.empty(2, n, dtype=torch.bfloat16, device=DEV), 32, 4, False, S.PRO_NORM,
+    x9 = torch.zeros(9, k, dtype=torch.bfloat16, device=DEV)
+    assert _int4_pro(x9, args, torch.empty(9, n, dtype=torch.bfloat16, device=DEV), 32, 4, False, S.PRO_NORM,
                      gamma) == _lib.BP_E_UNSUPPORTED
     a16 = (args[0], args[1].to(torch.float16), args[2])
     assert _int4_pro(x, a16, out, 32, 4, False, S.PRO_NORM, gamma) == _lib.BP_E_UNSUPPORTED
