@@ -238,6 +238,14 @@ def prologue_mm(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor | None, ou
     for t in (x, w, out, gamma, residual, xout, gamma2):
         if t is not None and not t.is_contiguous():
             raise ValueError("prologue_mm operands must be contiguous")
+    wk = w.shape[1] * GROUP if kind == "int4" else w.shape[1]
+    if x.dtype != torch.bfloat16 or wk != k:
+        raise ValueError(f"prologue_mm: x must be bf16 [M, {wk}]")
+    if out.shape != (m, n) or out.dtype != torch.bfloat16:
+        raise ValueError(f"prologue_mm: out must be a bf16 [{m}, {n}] tensor")
+    for t, rows in ((gamma, None), (gamma2, None), (residual, m), (xout, m)):
+        if t is not None and (t.dtype != torch.bfloat16 or t.numel() != (k if rows is None else rows * k)):
+            raise ValueError("prologue_mm: gamma / gamma2 must be bf16 [K], residual / xout bf16 [M, K]")
     if xout is not None:
         # one workgroup writes xout while the others still read x and the residual rows
         rows = 2 * m * k

@@ -199,6 +199,15 @@ def test_prologue_mm_refuses_an_overlapping_xout_on_the_host():
     big = torch.zeros(8, 2048, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="overlap"):  # the last rows of one buffer are the first of the other
         S.prologue_mm(big[:4], w, None, out, S.PRO_UNIT_RMS, xout=big[3:7])
+    # operands whose shapes do not match the launch are refused before any pointer reaches the library
+    with pytest.raises(ValueError, match="out must"):
+        S.prologue_mm(x, w, None, out[:3], S.PRO_NORM, gamma=g, eps=1e-6)
+    with pytest.raises(ValueError, match="gamma"):
+        S.prologue_mm(x, w, None, out, S.PRO_NORM, gamma=g[:1024], eps=1e-6)
+    with pytest.raises(ValueError, match="residual"):
+        S.prologue_mm(x, w, None, out, S.PRO_NORM, gamma=g, residual=res[:2], eps=1e-6)
+    with pytest.raises(ValueError, match="x must"):
+        S.prologue_mm(x[:, :1024].contiguous(), w, None, out, S.PRO_UNIT_RMS)
 
 
 def test_static_scratch_entry_refuses_partials_beyond_its_array(L):
